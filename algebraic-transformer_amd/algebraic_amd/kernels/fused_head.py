@@ -1,0 +1,97 @@
+"""Fused tied-embedding algebraic likelihood head on MI355X: drop-in for
+``algebraic.kernels.fused_head``.
+
+Mirrors ``fused_head(h, embed, targets, *, kind, n, c, block_n, block_v)``
+(src/algebraic/kernels/fused_head.py:260-275) and its custom VJP (232-257) over torch
+tensors on the GPU. The logits are never materialised: the forward is one tiled
+``E h^T`` MFMA pass with the row statistics fused into its epilogue; the backward
+recomputes the tiles, forms the bf16 logit gradient in a bounded workspace and runs the two
+gradient GEMMs in HIP (including the embedding gradient the reference leaves to XLA,
+fused_head.py:215). Returns ``(objective, telemetry)``: the mean target-miss probability
+(whose gradient is the exact NLL gradient) and the per-token target probability, which
+receives no gradient. ``kind="ce"`` (the softmax control arm) raises NotImplementedError.
+"""
+
+import torch
+
+from .. import _lib
+
+
+def _root(value, n):
+    out = float(value)
+    while n > 1:
+        out = out ** 0.5
+        n //= 2
+    return out
+
+
+class _HeadFn(torch.autograd.Function):
+
+    @staticmethod
+    def forward(ctx, h, embed, targets, n, c):
+        N, d = h.shape
+        V = embed.shape[0]
+        lib = _lib.load()
+        dev = h.device
+        st = _lib.stream_of(h)
+        h = h.contiguous()
+        e = embed.detach().to(h.dtype).contiguous()        # fused_head.py:168
+        t = targets.to(device=dev, dtype=torch.int32).contiguous()
+        ws_bytes = lib.alg_head_workspace_size(N, d, V, 0)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        stat = torch.empty(N, dtype=torch.float32, device=dev)
+        zt = torch.empty(N, dtype=torch.float32, device=dev)
+        pt = torch.empty(N, dtype=torch.float32, device=dev)
+        obj = torch.empty((), dtype=torch.float32, device=dev)
+        _lib.check(lib.alg_head_fwd(st, N, d, V, _lib.ptr(h), _lib.ptr(e), _lib.ptr(t), n, c, _lib.ptr(stat),
+                                    _lib.ptr(zt), _lib.ptr(pt), _lib.ptr(obj), _lib.ptr(ws), ws_bytes),
+                   "fused_head forward")
+        ctx.n, ctx.c = n, c
+        ctx.embed_dtype = embed.dtype
+        ctx.save_for_backward(h, e, t, stat)
+        ctx.mark_non_differentiable(pt)
+        return obj, pt
+
+    @staticmethod
+    def backward(ctx, g_obj, g_tel):
+        h, e, t, stat = ctx.saved_tensors
+        N, d = h.shape
+        V = e.shape[0]
+        lib = _lib.load()
+        dev = h.device
+        st = _lib.stream_of(h)
+        g = (g_obj if g_obj is not None else torch.zeros((), device=dev)).to(torch.float32).reshape(1).contiguous()
+        ws_bytes = lib.alg_head_workspace_size(N, d, V, 1)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        dh = torch.empty_like(h)
+        de_f32 = ctx.embed_dtype == torch.float32
+        dE = torch.empty((V, d), dtype=torch.float32 if de_f32 else torch.bfloat16, device=dev)
+        _lib.check(lib.alg_head_bwd(st, N, d, V, _lib.ptr(h), _lib.ptr(e), _lib.ptr(t), _lib.ptr(stat), _lib.ptr(g),
+                                    ctx.n, ctx.c, _lib.ptr(dh), _lib.ptr(dE),
+                                    _lib.DTYPE_F32 if de_f32 else _lib.DTYPE_BF16, _lib.ptr(ws), ws_bytes),
+                   "fused_head backward")
+        return dh, dE.to(ctx.embed_dtype), None, None, None
+
+
+def fused_head(h, embed, targets, *, kind="ce", n=16, c=16.0, block_n=128, block_v=512):
+    """Fused tied-embedding projection and likelihood objective (fused_head.py:260-275).
+
+    ``h`` (N, d) bfloat16 hidden states, ``embed`` (V, d), ``targets`` (N,). Returns
+    ``(objective, telemetry)``; the telemetry carries no gradient.
+    """
+    if kind not in ("ce", "alg_ce"):
+        raise ValueError(kind)
+    if kind == "alg_ce" and (n & (n - 1)):
+        raise ValueError("n must be a power of two")
+    N = h.shape[0]
+    bn = min(block_n, N)
+    if N % bn:
+        raise ValueError(f"token count {N} must be divisible by block {bn}")
+    if kind == "ce":
+        raise NotImplementedError("kind='ce' is the softmax control arm; only kind='alg_ce' is built for MI355X")
+    if h.dtype != torch.bfloat16:
+        raise NotImplementedError(f"hidden dtype {h.dtype}: the gfx950 head takes bfloat16 hidden states")
+    if not h.is_cuda:
+        raise RuntimeError("fused_head needs GPU tensors (no CPU fallback)")
+    obj, tel = _HeadFn.apply(h, embed, targets, int(n), float(c))
+    return obj, tel.detach()

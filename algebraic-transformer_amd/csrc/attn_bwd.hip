@@ -1,0 +1,420 @@
+// Causal algebraic attention backward for gfx950.
+//
+// Replaces src/algebraic/kernels/flash.py:333-361 (tile gradients), 515-627 (fused and
+// resident backward schedules), 630-645 (di), 694-726 (sink VJP) and
+// src/algebraic/kernels/head_resident.py:91-119.
+//
+// Three launches:
+//   pre   di = sum_d dO*o per row (from the rounded output in range, the f32 output when
+//         shifted; flash.py:633), zero the f32 dQ accumulator, per-(b,h,block) partial sums
+//         of mass*di for the sink gradient (flash.py:694-705, 721-723).
+//   main  one workgroup = 4 waves = 128 keys of one (b,h); dK/dV accumulate in registers
+//         while the kernel streams 64-query tiles of Q and dO through LDS. Scores are
+//         formed as S = Q K^T so a lane owns one key column; P^T and dS^T feed dV += P^T dO
+//         and dK += dS^T Q directly as MFMA A operands, with dO/Q fragments transposed by
+//         ds_read_b64_tr_b16. dS is staged in LDS ([key][query]) and each wave forms one
+//         quarter of the tile's dQ = dS K over the workgroup's 128 keys, added to the f32
+//         accumulator with one atomic per element per key block (no per-key-block dQ
+//         partials in HBM, unlike flash.py:537-544).
+//   post  dq = round(round(n * acc) * dq_scale) and the per-head sink gradient.
+#include "attn_common.h"
+
+namespace alg {
+
+constexpr int BWD_BK = 128;  // keys per workgroup
+// Queries per streamed tile: 64, or 32 where 64 would not fit in LDS (f32 with D=128).
+template <typename T, int D>
+constexpr int bwd_bq() { return (sizeof(T) == 4 && D == 128) ? 32 : 64; }
+constexpr int PRE_ROWS = 256;  // rows per pre-kernel workgroup
+
+// ---------------------------------------------------------------------------
+// pre: di, dq_acc = 0, sink partials
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void attn_bwd_pre_kernel(AttnBwdParams p, int D) {
+  const int bh = blockIdx.x;
+  const int head = bh % p.H;
+  const int T_ = p.T;
+  bool shifted = p.mode == MODE_SHIFTED;
+  if (p.flag) shifted = *p.flag == 0;
+  const bool precise = shifted && p.o_precise != nullptr;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row0 = blockIdx.y * PRE_ROWS;
+  const int n = 1 << p.log2n;
+  float b = p.sink ? p.sink[head] : 0.0f;
+  if (p.mode == MODE_CLIPPED && !p.flag) b = fminf(b, p.clamp);
+  const float rb = rho_exact(b);
+  const bool inv_stat = !shifted && (p.mode != MODE_CLIPPED || p.inv_stat);
+  const float rbn = ipow_rt(rb, n);
+  float part = 0.0f;
+  for (int r = row0 + wave; r < min(row0 + PRE_ROWS, T_); r += 4) {
+    const size_t off = ((size_t)bh * T_ + r) * D;
+    const T* dO = reinterpret_cast<const T*>(p.dO) + off;
+    float s = 0.0f;
+    for (int d = lane; d < D; d += 64) {
+      const float o = precise ? p.o_precise[off + d] : (float)reinterpret_cast<const T*>(p.o)[off + d];
+      s += (float)dO[d] * o;
+      p.dq_acc[off + d] = 0.0f;
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
+    if (lane == 0) {
+      p.di[(size_t)bh * T_ + r] = s;
+      const float st = p.stat[(size_t)bh * T_ + r];
+      const float mass = inv_stat ? rbn * st : ipow_rt(rb * st, n);
+      part += mass * s;
+    }
+  }
+  __shared__ float red[4];
+  if (lane == 0) red[wave] = part;
+  __syncthreads();
+  if (threadIdx.x == 0) p.sink_part[(size_t)bh * gridDim.y + blockIdx.y] = red[0] + red[1] + red[2] + red[3];
+}
+
+// ---------------------------------------------------------------------------
+// main
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void load_tile(T* dst, int pitch, const T* src, int r0, int nrows, int T_, int D) {
+  constexpr int CH = 16 / sizeof(T);
+  const int cpr = D / CH;
+  for (int c = threadIdx.x; c < nrows * cpr; c += blockDim.x) {
+    const int row = c / cpr, col = (c - row * cpr) * CH;
+    uint4 val = make_uint4(0, 0, 0, 0);
+    if (r0 + row < T_) val = *reinterpret_cast<const uint4*>(src + (size_t)(r0 + row) * D + col);
+    *reinterpret_cast<uint4*>(dst + row * pitch + col) = val;
+  }
+}
+
+template <typename T, int D, int MODE>
+__global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
+  static_assert(D == 64 || D == 128, "head_dim");
+  constexpr bool BF = sizeof(T) == 2;
+  constexpr int PITCH = D + (BF ? 8 : 4);
+  constexpr int BWD_BQ = bwd_bq<T, D>();
+  constexpr int SPITCH = BWD_BQ + (BF ? 8 : 4);
+  constexpr int NDB = D / 32;
+  __shared__ __attribute__((aligned(16))) T Ks[BWD_BK * PITCH];
+  __shared__ __attribute__((aligned(16))) T Qs[BWD_BQ * PITCH];
+  __shared__ __attribute__((aligned(16))) T dOs[BWD_BQ * PITCH];
+  __shared__ __attribute__((aligned(16))) T dSs[BWD_BK * SPITCH];
+  __shared__ __attribute__((aligned(16))) float st_s[BWD_BQ];
+  __shared__ __attribute__((aligned(16))) float di_s[BWD_BQ];
+
+  if (p.flag) {
+    const bool in_range = *p.flag != 0;
+    if ((MODE == MODE_SHIFTED) == in_range) return;
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
+  const int T_ = p.T;
+  const int bh = blockIdx.x;
+  const int k0 = blockIdx.y * BWD_BK;  // blockIdx.y = 0 has the most causal work
+  const size_t base = (size_t)bh * T_ * D;
+  const T* Q = reinterpret_cast<const T*>(p.q) + base;
+  const T* K = reinterpret_cast<const T*>(p.k) + base;
+  const T* V = reinterpret_cast<const T*>(p.v) + base;
+  const T* dO = reinterpret_cast<const T*>(p.dO) + base;
+  const float* stat = p.stat + (size_t)bh * T_;
+  const float* di = p.di + (size_t)bh * T_;
+  float* dq_acc = p.dq_acc + base;
+  const int wk0 = k0 + wave * 32;    // this wave's first key
+  const int mykey = wk0 + l32;
+  const int log2n = p.log2n;
+
+  load_tile<T>(Ks, PITCH, K, k0, BWD_BK, T_, D);
+
+  // K and V fragments as B operands of S = Q K^T and dP = dO V^T.
+  constexpr int NF = BF ? D / 16 : D / 8;
+  typedef typename std::conditional<BF, bf16x8, floatx4>::type Frag;
+  Frag kf[NF], vf[NF];
+#pragma unroll
+  for (int s = 0; s < NF; ++s) {
+    if constexpr (BF) {
+      bf16x8 z = {};
+      const size_t o = (size_t)mykey * D + 16 * s + 8 * h;
+      kf[s] = mykey < T_ ? ld8(reinterpret_cast<const bf16*>(K) + o) : z;
+      vf[s] = mykey < T_ ? ld8(reinterpret_cast<const bf16*>(V) + o) : z;
+    } else {
+      floatx4 z = {};
+      const size_t o = (size_t)mykey * D + 8 * s + 4 * h;
+      kf[s] = mykey < T_ ? *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(K) + o) : z;
+      vf[s] = mykey < T_ ? *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(V) + o) : z;
+    }
+  }
+  floatx16 dk[NDB], dv[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) { dk[db] = floatx16{}; dv[db] = floatx16{}; }
+
+  const int nq = ceil_div(T_, BWD_BQ);
+  const int qstart = k0 / BWD_BQ;
+  for (int qt = qstart; qt < nq; ++qt) {
+    const int qbase = qt * BWD_BQ;
+    __syncthreads();
+    load_tile<T>(Qs, PITCH, Q, qbase, BWD_BQ, T_, D);
+    load_tile<T>(dOs, PITCH, dO, qbase, BWD_BQ, T_, D);
+    if (threadIdx.x < BWD_BQ) {
+      const int q = qbase + threadIdx.x;
+      st_s[threadIdx.x] = q < T_ ? stat[q] : 0.0f;
+      di_s[threadIdx.x] = q < T_ ? di[q] : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int sub = 0; sub < BWD_BQ / 32; ++sub) {
+      const int sq0 = qbase + sub * 32;
+      T* dsrow = dSs + (wave * 32 + l32) * SPITCH + sub * 32;
+      if (sq0 + 31 < wk0 || wk0 >= T_) {  // all queries precede all keys of this wave
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          if constexpr (BF) { bf16x4 z = {}; *reinterpret_cast<bf16x4*>(dsrow + 8 * g + 4 * h) = z; }
+          else { floatx4 z = {}; *reinterpret_cast<floatx4*>(dsrow + 8 * g + 4 * h) = z; }
+        }
+        continue;
+      }
+      const T* qrow = Qs + (sub * 32 + l32) * PITCH;
+      const T* dorow = dOs + (sub * 32 + l32) * PITCH;
+      floatx16 s = {}, dp = {};
+#pragma unroll
+      for (int st = 0; st < NF; ++st) {
+        if constexpr (BF) {
+          bf16x8 qa = *reinterpret_cast<const bf16x8*>(qrow + 16 * st + 8 * h);
+          s = mfma_bf16(qa, kf[st], s);
+          bf16x8 da = *reinterpret_cast<const bf16x8*>(dorow + 16 * st + 8 * h);
+          dp = mfma_bf16(da, vf[st], dp);
+        } else {
+          floatx4 qa = *reinterpret_cast<const floatx4*>(qrow + 8 * st + 4 * h);
+          floatx4 da = *reinterpret_cast<const floatx4*>(dorow + 8 * st + 4 * h);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            s = mfma_f32(qa[u], kf[st][u], s);
+            dp = mfma_f32(da[u], vf[st][u], dp);
+          }
+        }
+      }
+      const bool diag = wk0 + 31 > sq0;
+      float pv[16], dsv[16];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const floatx4 stq = *reinterpret_cast<const floatx4*>(st_s + sub * 32 + 8 * g + 4 * h);
+        const floatx4 diq = *reinterpret_cast<const floatx4*>(di_s + sub * 32 + 8 * g + 4 * h);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 4 * g + e;
+          float x = s[i];
+          float r, pw;
+          if constexpr (MODE == MODE_INRANGE) {
+            float t = rho_fast(x, r);
+            for (int k2 = 0; k2 < log2n; ++k2) t = t * t;
+            pw = t * stq[e];
+          } else if constexpr (MODE == MODE_CLIPPED) {
+            x = fminf(x, p.clamp);
+            float t = rho_fast(x, r);
+            if (p.inv_stat) {
+              for (int k2 = 0; k2 < log2n; ++k2) t = t * t;
+              pw = t * stq[e];
+            } else {
+              t = t * stq[e];
+              for (int k2 = 0; k2 < log2n; ++k2) t = t * t;
+              pw = t;
+            }
+          } else {
+            const int q = sq0 + 8 * g + 4 * h + e;
+            if (diag && mykey > q) x = 0.0f;
+            float t = p.fast_rho ? rho_fast(x, r) : rho_exact(x, r);
+            t = t * stq[e];
+            for (int k2 = 0; k2 < log2n; ++k2) t = t * t;
+            pw = t;
+          }
+          float dsx = pw * (dp[i] - diq[e]) * r;
+          if constexpr (MODE == MODE_CLIPPED) dsx = s[i] < p.clamp ? dsx : 0.0f;
+          if (diag) {
+            const int q = sq0 + 8 * g + 4 * h + e;
+            if (mykey > q) { pw = 0.0f; dsx = 0.0f; }
+          }
+          pv[i] = pw;
+          dsv[i] = dsx;
+        }
+      }
+      if constexpr (BF) {
+        bf16x8 pa0, pa1, da0, da1;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          pa0[j] = f2bf(pv[j]); pa1[j] = f2bf(pv[8 + j]);
+          da0[j] = f2bf(dsv[j]); da1[j] = f2bf(dsv[8 + j]);
+        }
+        const bf16* qt_ = reinterpret_cast<const bf16*>(Qs);
+        const bf16* dot_ = reinterpret_cast<const bf16*>(dOs);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          const int r0 = sub * 32 + 4 * h;
+          bf16x8 ob0 = lds_tr_frag(dot_, PITCH, r0, r0 + 8, db * 32, lane);
+          bf16x8 ob1 = lds_tr_frag(dot_, PITCH, r0 + 16, r0 + 24, db * 32, lane);
+          dv[db] = mfma_bf16(pa0, ob0, dv[db]);
+          dv[db] = mfma_bf16(pa1, ob1, dv[db]);
+          bf16x8 qb0 = lds_tr_frag(qt_, PITCH, r0, r0 + 8, db * 32, lane);
+          bf16x8 qb1 = lds_tr_frag(qt_, PITCH, r0 + 16, r0 + 24, db * 32, lane);
+          dk[db] = mfma_bf16(da0, qb0, dk[db]);
+          dk[db] = mfma_bf16(da1, qb1, dk[db]);
+        }
+        // Stage dS (rounded, as the dq/dk operands are) in LDS as [key][query].
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          bf16x4 v4;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v4[e] = f2bf(dsv[4 * g + e]);
+          *reinterpret_cast<bf16x4*>(dsrow + 8 * g + 4 * h) = v4;
+        }
+      } else {
+        const float* qt_ = reinterpret_cast<const float*>(Qs);
+        const float* dot_ = reinterpret_cast<const float*>(dOs);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int qr = sub * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+            dv[db] = mfma_f32(pv[i], dot_[qr * PITCH + db * 32 + l32], dv[db]);
+            dk[db] = mfma_f32(dsv[i], qt_[qr * PITCH + db * 32 + l32], dk[db]);
+          }
+        }
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          floatx4 v4;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v4[e] = dsv[4 * g + e];
+          *reinterpret_cast<floatx4*>(dsrow + 8 * g + 4 * h) = v4;
+        }
+      }
+    }
+    __syncthreads();
+    // dQ tile = dS K over this workgroup's keys; each wave takes 32 queries x DBW blocks.
+    {
+      constexpr int NQH = BWD_BQ / 32;         // 32-query slices of the tile
+      constexpr int WPH = 4 / NQH;             // waves per slice
+      constexpr int DBW = NDB / WPH;           // 32-wide d blocks per wave
+      static_assert(DBW >= 1, "tile shape");
+      const int qs = wave / WPH;
+      const int db0 = (wave % WPH) * DBW;
+      floatx16 dqa[DBW];
+#pragma unroll
+      for (int j = 0; j < DBW; ++j) dqa[j] = floatx16{};
+      if constexpr (BF) {
+        const bf16* ds_ = reinterpret_cast<const bf16*>(dSs);
+        const bf16* k_ = reinterpret_cast<const bf16*>(Ks);
+#pragma unroll
+        for (int ks = 0; ks < BWD_BK / 16; ++ks) {
+          const int klo = ks * 16 + 8 * h;
+          bf16x8 a = lds_tr_frag(ds_, SPITCH, klo, klo + 4, qs * 32, lane);
+#pragma unroll
+          for (int j = 0; j < DBW; ++j) {
+            bf16x8 bk = lds_tr_frag(k_, PITCH, klo, klo + 4, (db0 + j) * 32, lane);
+            dqa[j] = mfma_bf16(a, bk, dqa[j]);
+          }
+        }
+      } else {
+        const float* ds_ = reinterpret_cast<const float*>(dSs);
+        const float* k_ = reinterpret_cast<const float*>(Ks);
+#pragma unroll 8
+        for (int ks = 0; ks < BWD_BK / 2; ++ks) {
+          const int key = 2 * ks + h;
+          const float a = ds_[key * SPITCH + qs * 32 + l32];
+#pragma unroll
+          for (int j = 0; j < DBW; ++j) dqa[j] = mfma_f32(a, k_[key * PITCH + (db0 + j) * 32 + l32], dqa[j]);
+        }
+      }
+      {
+#pragma unroll
+        for (int j = 0; j < DBW; ++j) {
+          const int d = (db0 + j) * 32 + l32;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int q = qbase + qs * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+            if (q < T_) atomicAdd(dq_acc + (size_t)q * D + d, dqa[j][i]);
+          }
+        }
+      }
+    }
+  }
+
+  // dK = n * acc, dV = acc (flash.py:591-597), rounded to the input dtype.
+  const float slope = (float)(1 << log2n);
+  T* DK = reinterpret_cast<T*>(p.dk) + base;
+  T* DV = reinterpret_cast<T*>(p.dv) + base;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int key = wk0 + 8 * (i >> 2) + 4 * h + (i & 3);
+      if (key < T_) {
+        const size_t o = (size_t)key * D + db * 32 + l32;
+        DK[o] = (T)(dk[db][i] * slope);
+        DV[o] = (T)(dv[db][i]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// post: dq and the per-head sink gradient
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void attn_bwd_post_kernel(AttnBwdParams p, size_t total, int nblk) {
+  const float slope = (float)(1 << p.log2n);
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    const T dqs = (T)(p.dq_acc[i] * slope);       // kernel output dq_s (flash.py:592)
+    reinterpret_cast<T*>(p.dq)[i] = (T)((float)dqs * p.dq_scale);  // chain rule through q_s
+  }
+  if (blockIdx.x == 0 && p.dbeta) {
+    bool shifted = p.mode == MODE_SHIFTED;
+    if (p.flag) shifted = *p.flag == 0;
+    for (int hh = threadIdx.x; hh < p.H; hh += blockDim.x) {
+      if (!p.sink) { p.dbeta[hh] = 0.0f; continue; }
+      float s = 0.0f;
+      for (int b = 0; b < p.B; ++b)
+        for (int k = 0; k < nblk; ++k) s += p.sink_part[(size_t)(b * p.H + hh) * nblk + k];
+      float beta = p.sink[hh];
+      const bool clipped = !shifted && p.mode == MODE_CLIPPED && !p.flag;
+      float bb = clipped ? fminf(beta, p.clamp) : beta;
+      float r;
+      rho_exact(bb, r);
+      float sl = (float)(1 << p.log2n) * r;
+      if (clipped && !(beta < p.clamp)) sl = 0.0f;  // flash.py:703-704
+      p.dbeta[hh] = -s * sl;
+    }
+  }
+}
+
+template <typename T, int D>
+static hipError_t launch_bwd_main(const AttnBwdParams& p, int mode, hipStream_t st) {
+  dim3 grid(p.B * p.H, ceil_div(p.T, BWD_BK)), block(256);
+  switch (mode) {
+    case MODE_INRANGE: hipLaunchKernelGGL((attn_bwd_kernel<T, D, MODE_INRANGE>), grid, block, 0, st, p); break;
+    case MODE_CLIPPED: hipLaunchKernelGGL((attn_bwd_kernel<T, D, MODE_CLIPPED>), grid, block, 0, st, p); break;
+    case MODE_SHIFTED: hipLaunchKernelGGL((attn_bwd_kernel<T, D, MODE_SHIFTED>), grid, block, 0, st, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+int attn_bwd_sink_blocks(int T) { return ceil_div(T, PRE_ROWS); }
+
+// modes: list of main-kernel variants to launch (each exits early unless the guard selects it).
+hipError_t launch_attn_bwd(const AttnBwdParams& p, int D, bool bf16_io, const int* modes, int nmodes,
+                           hipStream_t st) {
+  const int nblk = attn_bwd_sink_blocks(p.T);
+  dim3 pgrid(p.B * p.H, nblk);
+  if (bf16_io) hipLaunchKernelGGL((attn_bwd_pre_kernel<bf16>), pgrid, dim3(256), 0, st, p, D);
+  else hipLaunchKernelGGL((attn_bwd_pre_kernel<float>), pgrid, dim3(256), 0, st, p, D);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  for (int m = 0; m < nmodes; ++m) {
+    if (bf16_io) e = D == 64 ? launch_bwd_main<bf16, 64>(p, modes[m], st) : launch_bwd_main<bf16, 128>(p, modes[m], st);
+    else e = D == 64 ? launch_bwd_main<float, 64>(p, modes[m], st) : launch_bwd_main<float, 128>(p, modes[m], st);
+    if (e != hipSuccess) return e;
+  }
+  const size_t total = (size_t)p.B * p.H * p.T * D;
+  const int blocks = (int)std::min<size_t>((total + 255) / 256, 4096);
+  if (bf16_io) hipLaunchKernelGGL((attn_bwd_post_kernel<bf16>), dim3(blocks), dim3(256), 0, st, p, total, nblk);
+  else hipLaunchKernelGGL((attn_bwd_post_kernel<float>), dim3(blocks), dim3(256), 0, st, p, total, nblk);
+  return hipGetLastError();
+}
+
+}  // namespace alg

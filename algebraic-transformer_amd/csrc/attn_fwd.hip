@@ -1,0 +1,263 @@
+// Causal algebraic attention forward for gfx950.
+//
+// Replaces the Pallas forward kernels src/algebraic/kernels/flash.py:189-326 and
+// src/algebraic/kernels/head_resident.py:25-89 (same maths, MI355X tiling).
+//
+// Work decomposition: one workgroup = 4 waves = 128 query rows of one (b, h); each wave owns
+// 32 consecutive queries and streams K/V through LDS in 64-key tiles. Scores are formed
+// transposed, S^T = K Q^T (32x32x16 bf16 MFMA, or 32x32x2 f32 MFMA for f32 inputs), so
+// every lane owns one query column: the per-row weight sum is a per-lane running sum,
+// reduced across the two lane halves once at the end, and the running maximum of the
+// shifted variant is per lane as well. The weight tile P^T feeds the PV product directly
+// as the B operand of O^T = V^T P^T; V^T fragments come from the row-major LDS tile with
+// ds_read_b64_tr_b16. Causal tiles above the diagonal are skipped per wave; only tiles
+// crossing it evaluate the mask.
+#include "attn_common.h"
+
+namespace alg {
+
+constexpr int FWD_BQ = 128;  // queries per workgroup
+constexpr int FWD_BK = 64;   // keys per LDS tile
+
+template <typename T>
+__device__ __forceinline__ void load_rows(T* dst, int pitch, const T* src, int r0, int nrows, int T_, int D) {
+  constexpr int CH = 16 / sizeof(T);
+  const int cpr = D / CH;
+  for (int c = threadIdx.x; c < nrows * cpr; c += blockDim.x) {
+    const int row = c / cpr, col = (c - row * cpr) * CH;
+    uint4 val = make_uint4(0, 0, 0, 0);
+    if (r0 + row < T_) val = *reinterpret_cast<const uint4*>(src + (size_t)(r0 + row) * D + col);
+    *reinterpret_cast<uint4*>(dst + row * pitch + col) = val;
+  }
+}
+
+template <typename T, int D, int MODE>
+__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
+  static_assert(D == 64 || D == 128, "head_dim");
+  constexpr bool BF = sizeof(T) == 2;
+  constexpr int PITCH = D + (BF ? 8 : 4);
+  constexpr int NDB = D / 32;  // 32-wide d blocks of the O^T accumulator
+  __shared__ __attribute__((aligned(16))) T Ks[FWD_BK * PITCH];
+  __shared__ __attribute__((aligned(16))) T Vs[FWD_BK * PITCH];
+
+  if (p.flag) {  // device-side guard dispatch (lax.cond at flash.py:853-856)
+    const bool in_range = *p.flag != 0;
+    if ((MODE == MODE_SHIFTED) == in_range) return;
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
+  const int T_ = p.T;
+  const int nqb = ceil_div(T_, FWD_BQ);
+  const int bh = blockIdx.x;
+  const int qb = nqb - 1 - blockIdx.y;  // heaviest causal rows first
+  const int head = bh % p.H;
+  const size_t base = (size_t)bh * T_ * D;
+  const T* Q = reinterpret_cast<const T*>(p.q) + base;
+  const T* K = reinterpret_cast<const T*>(p.k) + base;
+  const T* V = reinterpret_cast<const T*>(p.v) + base;
+  const int q0 = qb * FWD_BQ + wave * 32;
+  const int myq = q0 + l32;
+  const bool wave_live = q0 < T_;
+
+  // Query fragments (B operand of S^T = K Q^T), held for the whole kernel.
+  constexpr int NQF = BF ? D / 16 : D / 8;
+  typedef typename std::conditional<BF, bf16x8, floatx4>::type QFrag;
+  QFrag qf[NQF];
+#pragma unroll
+  for (int s = 0; s < NQF; ++s) {
+    if constexpr (BF) {
+      bf16x8 z = {};
+      qf[s] = myq < T_ ? ld8(reinterpret_cast<const bf16*>(Q) + (size_t)myq * D + 16 * s + 8 * h) : z;
+    } else {
+      floatx4 z = {};
+      qf[s] = myq < T_ ? *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(Q) + (size_t)myq * D + 8 * s + 4 * h) : z;
+    }
+  }
+
+  const int log2n = p.log2n;
+  const bool has_sink = p.sink != nullptr;
+  const float beta = has_sink ? p.sink[head] : 0.0f;
+  floatx16 oacc[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) oacc[db] = floatx16{};
+  float lsum = 0.0f;
+  // Shifted state (flash.py:209-214): m = sink or NEG, l = 1 (sink) or 0; the sink's unit
+  // mass sits in lane half 0 so the half-sum reduction counts it once.
+  float m_run = has_sink ? beta : -1e4f;
+  if (MODE == MODE_SHIFTED && has_sink && h == 0) lsum = 1.0f;
+  bool first = true;
+
+  const int q_last = min(qb * FWD_BQ + FWD_BQ, T_) - 1;
+  const int ntiles = q_last / FWD_BK + 1;
+  for (int kt = 0; kt < ntiles; ++kt) {
+    __syncthreads();
+    load_rows<T>(Ks, PITCH, K, kt * FWD_BK, FWD_BK, T_, D);
+    load_rows<T>(Vs, PITCH, V, kt * FWD_BK, FWD_BK, T_, D);
+    __syncthreads();
+    if (!wave_live) continue;
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      const int kb = kt * FWD_BK + sub * 32;
+      if (kb > q0 + 31 || kb >= T_) continue;  // wave-uniform: tile fully masked
+      const T* krow = Ks + (sub * 32 + l32) * PITCH;
+      floatx16 s = {};
+#pragma unroll
+      for (int st = 0; st < NQF; ++st) {
+        if constexpr (BF) {
+          bf16x8 kf = *reinterpret_cast<const bf16x8*>(krow + 16 * st + 8 * h);
+          s = mfma_bf16(kf, qf[st], s);
+        } else {
+          floatx4 kf = *reinterpret_cast<const floatx4*>(krow + 8 * st + 4 * h);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) s = mfma_f32(kf[u], qf[st][u], s);
+        }
+      }
+      const bool diag = kb + 31 > q0;
+      float w[16];
+      if constexpr (MODE != MODE_SHIFTED) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          float x = s[i];
+          if constexpr (MODE == MODE_CLIPPED) x = fminf(x, p.clamp);
+          float t = rho_fast(x);
+          for (int e = 0; e < log2n; ++e) t = t * t;
+          w[i] = t;
+        }
+        if (diag) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int key = kb + 8 * (i >> 2) + 4 * h + (i & 3);
+            if (key > myq) w[i] = 0.0f;
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) lsum += w[i];
+      } else {
+        // Running maximum over this 32-key block (flash.py:235-259).
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = kb + 8 * (i >> 2) + 4 * h + (i & 3);
+          if (!diag || key <= myq) tmax = fmaxf(tmax, s[i]);
+        }
+        tmax = fmaxf(tmax, xor32(tmax));
+        float m_new = fmaxf(m_run, tmax);
+        float m_prev = m_run;
+        if (!has_sink && first) { m_new = tmax; m_prev = tmax; }
+        const float shift = rho_exact(-m_new);
+        const float alpha = ipow_rt(rho_exact(m_prev) * shift, 1 << log2n);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = kb + 8 * (i >> 2) + 4 * h + (i & 3);
+          const bool valid = !diag || key <= myq;
+          const float x = valid ? s[i] : 0.0f;
+          const float r0 = p.fast_rho ? rho_fast(x) : rho_exact(x);
+          float t = r0 * shift;
+          for (int e = 0; e < log2n; ++e) t = t * t;
+          w[i] = valid ? t : 0.0f;
+        }
+        float ts = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) ts += w[i];
+        lsum = alpha * lsum + ts;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) oacc[db] = oacc[db] * alpha;
+        m_run = m_new;
+      }
+      first = false;
+      // O^T += V^T P^T over the 32 keys of this block.
+      if constexpr (BF) {
+        bf16x8 pf0, pf1;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) { pf0[j] = f2bf(w[j]); pf1[j] = f2bf(w[8 + j]); }
+        const bf16* vt = reinterpret_cast<const bf16*>(Vs);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          bf16x8 v0 = lds_tr_frag(vt, PITCH, sub * 32 + 4 * h, sub * 32 + 8 + 4 * h, db * 32, lane);
+          oacc[db] = mfma_bf16(v0, pf0, oacc[db]);
+          bf16x8 v1 = lds_tr_frag(vt, PITCH, sub * 32 + 16 + 4 * h, sub * 32 + 24 + 4 * h, db * 32, lane);
+          oacc[db] = mfma_bf16(v1, pf1, oacc[db]);
+        }
+      } else {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int krow_i = sub * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+            const float a = reinterpret_cast<const float*>(Vs)[krow_i * PITCH + db * 32 + l32];
+            oacc[db] = mfma_f32(a, w[i], oacc[db]);
+          }
+        }
+      }
+    }
+  }
+  if (!wave_live) return;
+
+  // Finalize (flash.py:271-284).
+  float Z = lsum + xor32(lsum);
+  float stat;
+  if constexpr (MODE != MODE_SHIFTED) {
+    if (has_sink) {
+      float b = beta;
+      if constexpr (MODE == MODE_CLIPPED) b = fminf(b, p.clamp);
+      float t = rho_fast(b);
+      for (int e = 0; e < log2n; ++e) t = t * t;
+      Z += t;
+    }
+    const float inv = 1.0f / Z;
+    stat = (MODE == MODE_CLIPPED && !p.inv_stat) ? inv_root(Z, 1 << log2n) : inv;
+    Z = inv;  // reuse as the output scale
+  } else {
+    stat = rho_exact(-m_run) * inv_root(Z, 1 << log2n);
+    Z = 1.0f / Z;
+  }
+  const float scale = Z;
+  if (myq < T_) {
+    T* O = reinterpret_cast<T*>(p.o) + base + (size_t)myq * D;
+    float* OP = p.o_precise ? p.o_precise + base + (size_t)myq * D : nullptr;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = db * 32 + 8 * g + 4 * h;
+        floatx4 val;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) val[e] = oacc[db][4 * g + e] * scale;
+        if constexpr (BF) {
+          bf16x4 ob;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) ob[e] = f2bf(val[e]);
+          *reinterpret_cast<bf16x4*>(O + d0) = ob;
+        } else {
+          *reinterpret_cast<floatx4*>(O + d0) = val;
+        }
+        if (OP) *reinterpret_cast<floatx4*>(OP + d0) = val;
+      }
+    }
+    if (h == 0) p.stat[(size_t)bh * T_ + myq] = stat;
+  }
+}
+
+template <typename T, int D>
+static hipError_t launch_fwd_mode(const AttnFwdParams& p, int mode, hipStream_t st) {
+  dim3 grid(p.B * p.H, ceil_div(p.T, FWD_BQ)), block(256);
+  switch (mode) {
+    case MODE_INRANGE: hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_INRANGE>), grid, block, 0, st, p); break;
+    case MODE_CLIPPED: hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_CLIPPED>), grid, block, 0, st, p); break;
+    case MODE_SHIFTED: hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_SHIFTED>), grid, block, 0, st, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_attn_fwd(const AttnFwdParams& p, int D, bool bf16_io, int mode, hipStream_t st) {
+  if (bf16_io) {
+    if (D == 64) return launch_fwd_mode<bf16, 64>(p, mode, st);
+    if (D == 128) return launch_fwd_mode<bf16, 128>(p, mode, st);
+  } else {
+    if (D == 64) return launch_fwd_mode<float, 64>(p, mode, st);
+    if (D == 128) return launch_fwd_mode<float, 128>(p, mode, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace alg

@@ -1,0 +1,130 @@
+// Attention prologue and range guard for gfx950 (src/algebraic/kernels/flash.py:823-849).
+//
+//   prep      q_s = round(q * alpha) (flash.py:833); per-workgroup maxima of ||q_s||^2,
+//             ||k||^2 (f32 row sums) and |v| (flash.py:841-849). NaN propagates, so a NaN
+//             input fails the guard as the reference's comparisons do.
+//   finalize  one workgroup reduces the maxima, writes sink/c broadcast to (H,)
+//             (flash.py:826-828) and the guard flag (1 = in range) that the forward and
+//             backward kernels read on the device (the lax.cond of flash.py:853-856).
+#include "attn_prep.h"
+
+namespace alg {
+
+__device__ __forceinline__ float nanmax(float a, float b) { return (a > b || a != a) ? a : b; }
+
+
+
+template <typename T>
+__global__ __launch_bounds__(256) void attn_prep_kernel(PrepParams p) {
+  constexpr int CH = 16 / sizeof(T);
+  const int lpr = p.D / CH;                 // lanes per row
+  const int rpw = 64 / lpr;                 // rows per wave per step
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane / lpr, li = lane - sub * lpr;
+  float mq = 0.0f, mk = 0.0f, mv = 0.0f;
+  const size_t step = (size_t)gridDim.x * 4 * rpw;
+  for (size_t r0 = ((size_t)blockIdx.x * 4 + wave) * rpw; r0 < p.rows; r0 += step) {
+    const size_t r = r0 + sub;
+    const bool ok = r < p.rows;
+    const size_t off = r * p.D + li * CH;
+    float sq = 0.0f, sk = 0.0f, av = 0.0f;
+    if (ok) {
+      T qv[CH], kv[CH], vv[CH];
+      *reinterpret_cast<uint4*>(qv) = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.q) + off);
+      T out[CH];
+#pragma unroll
+      for (int j = 0; j < CH; ++j) {
+        out[j] = (T)((float)qv[j] * p.alpha);
+        const float f = (float)out[j];
+        sq += f * f;
+      }
+      *reinterpret_cast<uint4*>(reinterpret_cast<T*>(p.q_s) + off) = *reinterpret_cast<uint4*>(out);
+      if (p.want_guard) {
+        *reinterpret_cast<uint4*>(kv) = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.k) + off);
+        *reinterpret_cast<uint4*>(vv) = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.v) + off);
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+          const float kf = (float)kv[j];
+          sk += kf * kf;
+          av = nanmax(av, __builtin_fabsf((float)vv[j]));
+        }
+      }
+    }
+    // Row sums across the lanes of one row.
+    for (int m = 1; m < lpr; m <<= 1) {
+      sq += __shfl_xor(sq, m, 64);
+      sk += __shfl_xor(sk, m, 64);
+    }
+    mq = nanmax(mq, sq);
+    mk = nanmax(mk, sk);
+    mv = nanmax(mv, av);
+  }
+  for (int m = 32; m >= 1; m >>= 1) {
+    mq = nanmax(mq, __shfl_xor(mq, m, 64));
+    mk = nanmax(mk, __shfl_xor(mk, m, 64));
+    mv = nanmax(mv, __shfl_xor(mv, m, 64));
+  }
+  __shared__ float red[4][3];
+  if (lane == 0) { red[wave][0] = mq; red[wave][1] = mk; red[wave][2] = mv; }
+  __syncthreads();
+  if (threadIdx.x < 3) {
+    float m = red[0][threadIdx.x];
+    for (int w = 1; w < 4; ++w) m = nanmax(m, red[w][threadIdx.x]);
+    p.part[blockIdx.x * 3 + threadIdx.x] = m;
+  }
+}
+
+
+
+__global__ __launch_bounds__(256) void attn_guard_kernel(GuardParams g) {
+  __shared__ float red[256][3];
+  float mq = 0.0f, mk = 0.0f, mv = 0.0f;
+  if (g.want_guard) {
+    for (int i = threadIdx.x; i < g.nblocks; i += 256) {
+      mq = nanmax(mq, g.part[3 * i]);
+      mk = nanmax(mk, g.part[3 * i + 1]);
+      mv = nanmax(mv, g.part[3 * i + 2]);
+    }
+  }
+  red[threadIdx.x][0] = mq; red[threadIdx.x][1] = mk; red[threadIdx.x][2] = mv;
+  for (int hh = threadIdx.x; hh < g.H; hh += 256) {
+    if (g.sink_logit && g.sink_out) {
+      const float s = g.sink_logit[g.sink_count == 1 ? 0 : hh];
+      g.sink_out[hh] = s / g.c;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0 && g.flag) {
+    for (int i = 1; i < 256; ++i) {
+      mq = nanmax(mq, red[i][0]);
+      mk = nanmax(mk, red[i][1]);
+      mv = nanmax(mv, red[i][2]);
+    }
+    bool ok = (mq * mk <= g.q2k2_bound) && (mv <= g.v_bound);
+    if (g.sink_logit) {
+      float ms = 0.0f;
+      for (int hh = 0; hh < g.H; ++hh) ms = nanmax(ms, __builtin_fabsf(g.sink_logit[g.sink_count == 1 ? 0 : hh] / g.c));
+      ok = ok && (ms <= g.sink_bound);
+    }
+    *g.flag = g.want_guard ? (ok ? 1 : 0) : 1;
+  }
+}
+
+int attn_prep_blocks(size_t rows) {
+  size_t b = (rows + 63) / 64;
+  return (int)(b < 1024 ? (b ? b : 1) : 1024);
+}
+
+hipError_t launch_attn_prep(const PrepParams& p, bool bf16_io, GuardParams g, hipStream_t st) {
+  const int nb = attn_prep_blocks(p.rows);
+  if (bf16_io) hipLaunchKernelGGL((attn_prep_kernel<bf16>), dim3(nb), dim3(256), 0, st, p);
+  else hipLaunchKernelGGL((attn_prep_kernel<float>), dim3(nb), dim3(256), 0, st, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  g.part = p.part;
+  g.nblocks = nb;
+  hipLaunchKernelGGL(attn_guard_kernel, dim3(1), dim3(256), 0, st, g);
+  return hipGetLastError();
+}
+
+}  // namespace alg

@@ -1,0 +1,282 @@
+// C ABI entry points of libalgebraic_hip.so (declared in include/algebraic_hip.h).
+//
+// Host-side validation mirrors the reference's ValueErrors where the reference raises
+// (src/algebraic/kernels/flash.py:740-743, 796-797; fused_head.py:163-164, 269-272);
+// everything else is shape/pointer checking before any launch, so a bad call returns an
+// error instead of launching a kernel whose grid does not match its operands.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/algebraic_hip.h"
+#include "launchers.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_status(hipError_t e, const char* where) {
+  if (e == hipSuccess) return ALG_OK;
+  return fail(ALG_ERR_HIP, "%s: %s", where, hipGetErrorString(e));
+}
+
+int log2_pow2(int n) {
+  if (n < 1 || (n & (n - 1))) return -1;
+  int k = 0;
+  while ((1 << k) < n) ++k;
+  return k;
+}
+
+double root_pow2(double v, int n) {
+  while (n > 1) { v = std::sqrt(v); n /= 2; }
+  return v;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+int check_attn_shape(int dtype, int B, int H, int T, int D) {
+  if (dtype != ALG_DTYPE_BF16 && dtype != ALG_DTYPE_F32) return fail(ALG_ERR_INVALID, "dtype must be bf16 or f32");
+  if (B <= 0 || H <= 0 || T <= 0) return fail(ALG_ERR_INVALID, "B, H, T must be positive (got %d, %d, %d)", B, H, T);
+  if (D != 64 && D != 128) return fail(ALG_ERR_UNSUPPORTED, "head_dim %d: gfx950 kernels are built for D in {64, 128}", D);
+  if ((double)B * H * T * D > 4.0e9) return fail(ALG_ERR_INVALID, "tensor too large");
+  return ALG_OK;
+}
+
+int check_n(int n) {
+  const int k = log2_pow2(n);
+  if (k < 1 || k > 6) return fail(ALG_ERR_INVALID, "asinh kernel needs n to be a power of two in [2, 64] (got %d)", n);
+  return ALG_OK;
+}
+
+// Workspace layout for attention: [dq_acc f32 B*H*T*D][sink partials B*H*nblk][prep partials 3*1024]
+struct AttnWs {
+  size_t dq_acc, sink_part, prep_part, total;
+};
+AttnWs attn_ws(int B, int H, int T, int D) {
+  AttnWs w;
+  w.dq_acc = 0;
+  w.sink_part = align256((size_t)B * H * T * D * sizeof(float));
+  w.prep_part = w.sink_part + align256((size_t)B * H * alg::attn_bwd_sink_blocks(T) * sizeof(float));
+  w.total = w.prep_part + align256(3 * 1024 * sizeof(float));
+  return w;
+}
+
+// Workspace layout for the head: [partials f32 nvt*N][obj parts][dZ^T bf16 V*Npad (pass 1)]
+struct HeadWs {
+  size_t partial, obj_part, dzt, total;
+  int Npad;
+};
+HeadWs head_ws(int N, int d, int V, int pass) {
+  (void)d;
+  HeadWs w;
+  w.Npad = ((N + 127) / 128) * 128;
+  w.partial = 0;
+  w.obj_part = align256((size_t)alg::head_vocab_tiles(V) * N * sizeof(float));
+  w.dzt = w.obj_part + align256((size_t)alg::head_stat_blocks(N) * sizeof(float));
+  w.total = pass == 0 ? w.dzt : w.dzt + align256((size_t)V * w.Npad * 2);
+  return w;
+}
+
+int check_head(int N, int d, int V, int n, float c) {
+  if (N <= 0 || d <= 0 || V <= 0) return fail(ALG_ERR_INVALID, "N, d, V must be positive (got %d, %d, %d)", N, d, V);
+  if (d % 128) return fail(ALG_ERR_UNSUPPORTED, "d_model %d: gfx950 head kernels need d %% 128 == 0", d);
+  if ((double)N * d > 2.0e9 || (double)V * d > 2.0e9 || (double)V * ((N + 127) / 128 * 128) > 4.0e9)
+    return fail(ALG_ERR_INVALID, "head too large");
+  const int k = log2_pow2(n);
+  if (k < 0 || k > 6) return fail(ALG_ERR_INVALID, "n must be a power of two in [1, 64] (got %d)", n);
+  if (!(c > 0.0f) || !std::isfinite(c)) return fail(ALG_ERR_INVALID, "c must be positive and finite");
+  return ALG_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* alg_last_error(void) { return g_err.c_str(); }
+const char* alg_version(void) { return "algebraic_hip 0.1 gfx950"; }
+
+size_t alg_attn_workspace_size(int B, int H, int T, int D) {
+  if (B <= 0 || H <= 0 || T <= 0 || D <= 0) return 0;
+  return attn_ws(B, H, T, D).total;
+}
+
+int alg_attn_prepare(alg_stream_t stream, int dtype, int B, int H, int T, int D, const void* q, const void* k,
+                     const void* v, const float* sink_logit, int sink_count, float c, int n, int range_guard,
+                     void* q_s, float* sink_scaled, int* guard_flag, void* workspace, size_t workspace_bytes) {
+  int rc = check_attn_shape(dtype, B, H, T, D);
+  if (rc) return rc;
+  if ((rc = check_n(n))) return rc;
+  if (!(c > 0.0f) || !std::isfinite(c)) return fail(ALG_ERR_INVALID, "asinh scale c must be positive and finite");
+  if (!q || !q_s || !guard_flag) return fail(ALG_ERR_INVALID, "q, q_s and guard_flag are required");
+  if (range_guard && (!k || !v)) return fail(ALG_ERR_INVALID, "range_guard needs k and v");
+  if (sink_logit && sink_count != 1 && sink_count != H) return fail(ALG_ERR_INVALID, "sink_count must be 1 or H");
+  if (sink_logit && !sink_scaled) return fail(ALG_ERR_INVALID, "sink_scaled output required with a sink");
+  const AttnWs ws = attn_ws(B, H, T, D);
+  if (!workspace || workspace_bytes < ws.total)
+    return fail(ALG_ERR_INVALID, "workspace too small: need %zu bytes", ws.total);
+  alg::PrepParams pp;
+  pp.q = q; pp.k = k; pp.v = v; pp.q_s = q_s;
+  pp.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + ws.prep_part);
+  pp.rows = (size_t)B * H * T;
+  pp.D = D;
+  pp.alpha = (float)(1.0 / (std::sqrt((double)D) * (double)c));
+  pp.want_guard = range_guard ? 1 : 0;
+  // Guard bounds (flash.py:747-748, 840-849), evaluated in double then rounded like the
+  // reference's weakly typed Python-float constants.
+  const double t = root_pow2(1e37 / (T + 1.0), n);
+  const double clamp = 0.5 * (t - 1.0 / t);
+  const double bound = std::fmin(16.0, clamp / 2.0);
+  const int has_sink = sink_logit ? 1 : 0;
+  alg::GuardParams g;
+  g.part = nullptr; g.nblocks = 0;
+  g.sink_logit = sink_logit; g.sink_count = sink_count;
+  g.sink_out = sink_scaled; g.H = H; g.c = c;
+  g.flag = guard_flag;
+  g.q2k2_bound = (float)((bound / 1.01) * (bound / 1.01));
+  g.sink_bound = (float)(bound / 1.01);
+  g.v_bound = (float)std::fmin(1e8, 1e37 / ((T + has_sink) * std::pow(2.0 * bound + 1.0, n)));
+  g.want_guard = range_guard && n <= 32 ? 1 : 0;
+  return hip_status(alg::launch_attn_prep(pp, dtype == ALG_DTYPE_BF16, g, (hipStream_t)stream), "alg_attn_prepare");
+}
+
+int alg_attn_fwd(alg_stream_t stream, int dtype, int B, int H, int T, int D, const void* q_s, const void* k,
+                 const void* v, const float* sink_scaled, int n, int variant, const int* guard_flag, float clamp,
+                 int fast_rho, int inv_stat, void* o, float* o_precise, float* stat) {
+  int rc = check_attn_shape(dtype, B, H, T, D);
+  if (rc) return rc;
+  if ((rc = check_n(n))) return rc;
+  if (!q_s || !k || !v || !o || !stat) return fail(ALG_ERR_INVALID, "q_s, k, v, o and stat are required");
+  if (variant < ALG_ATTN_INRANGE || variant > ALG_ATTN_GUARDED) return fail(ALG_ERR_INVALID, "unknown variant %d", variant);
+  if (variant == ALG_ATTN_GUARDED && !guard_flag) return fail(ALG_ERR_INVALID, "GUARDED needs guard_flag");
+  alg::AttnFwdParams p;
+  p.q = q_s; p.k = k; p.v = v; p.sink = sink_scaled;
+  p.flag = variant == ALG_ATTN_GUARDED ? guard_flag : nullptr;
+  p.o = o; p.o_precise = o_precise; p.stat = stat;
+  p.B = B; p.H = H; p.T = T;
+  p.log2n = log2_pow2(n);
+  p.clamp = clamp; p.fast_rho = fast_rho; p.inv_stat = inv_stat;
+  const bool bf = dtype == ALG_DTYPE_BF16;
+  hipStream_t st = (hipStream_t)stream;
+  if (variant == ALG_ATTN_GUARDED) {
+    alg::AttnFwdParams ps = p;
+    ps.fast_rho = 0;  // the guard's fallback uses stable rho (flash.py:851)
+    rc = hip_status(alg::launch_attn_fwd(p, D, bf, alg::MODE_INRANGE, st), "alg_attn_fwd");
+    if (rc) return rc;
+    return hip_status(alg::launch_attn_fwd(ps, D, bf, alg::MODE_SHIFTED, st), "alg_attn_fwd");
+  }
+  return hip_status(alg::launch_attn_fwd(p, D, bf, variant, st), "alg_attn_fwd");
+}
+
+int alg_attn_bwd(alg_stream_t stream, int dtype, int B, int H, int T, int D, const void* q_s, const void* k,
+                 const void* v, const float* sink_scaled, const void* o, const float* o_precise, const float* stat,
+                 const void* dO, int n, int variant, const int* guard_flag, float clamp, int fast_rho, int inv_stat,
+                 float dq_scale, void* dq, void* dk, void* dv, float* di, float* dsink_scaled, void* workspace,
+                 size_t workspace_bytes) {
+  int rc = check_attn_shape(dtype, B, H, T, D);
+  if (rc) return rc;
+  if ((rc = check_n(n))) return rc;
+  if (!q_s || !k || !v || !o || !stat || !dO || !dq || !dk || !dv || !di)
+    return fail(ALG_ERR_INVALID, "q_s, k, v, o, stat, dO, dq, dk, dv and di are required");
+  if (variant < ALG_ATTN_INRANGE || variant > ALG_ATTN_GUARDED) return fail(ALG_ERR_INVALID, "unknown variant %d", variant);
+  if (variant == ALG_ATTN_GUARDED && !guard_flag) return fail(ALG_ERR_INVALID, "GUARDED needs guard_flag");
+  const AttnWs ws = attn_ws(B, H, T, D);
+  if (!workspace || workspace_bytes < ws.total)
+    return fail(ALG_ERR_INVALID, "workspace too small: need %zu bytes", ws.total);
+  alg::AttnBwdParams p;
+  p.q = q_s; p.k = k; p.v = v; p.o = o; p.o_precise = o_precise; p.dO = dO; p.stat = stat;
+  p.sink = sink_scaled;
+  p.flag = variant == ALG_ATTN_GUARDED ? guard_flag : nullptr;
+  p.di = di;
+  p.dq_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + ws.dq_acc);
+  p.sink_part = reinterpret_cast<float*>(static_cast<char*>(workspace) + ws.sink_part);
+  p.dq = dq; p.dk = dk; p.dv = dv; p.dbeta = dsink_scaled;
+  p.B = B; p.H = H; p.T = T;
+  p.log2n = log2_pow2(n);
+  p.clamp = clamp; p.fast_rho = fast_rho; p.inv_stat = inv_stat;
+  p.mode = variant == ALG_ATTN_GUARDED ? alg::MODE_INRANGE : variant;
+  p.dq_scale = dq_scale;
+  const bool bf = dtype == ALG_DTYPE_BF16;
+  hipStream_t st = (hipStream_t)stream;
+  if (variant == ALG_ATTN_GUARDED) {
+    // Both branches are launched; each exits unless the device flag selects it. The
+    // fallback's fast_rho is forced off in the SHIFTED kernel via the params below.
+    const int modes[2] = {alg::MODE_INRANGE, alg::MODE_SHIFTED};
+    p.fast_rho = 0;
+    return hip_status(alg::launch_attn_bwd(p, D, bf, modes, 2, st), "alg_attn_bwd");
+  }
+  const int modes[1] = {variant};
+  return hip_status(alg::launch_attn_bwd(p, D, bf, modes, 1, st), "alg_attn_bwd");
+}
+
+size_t alg_head_workspace_size(int N, int d, int V, int pass) {
+  if (N <= 0 || d <= 0 || V <= 0) return 0;
+  return head_ws(N, d, V, pass ? 1 : 0).total;
+}
+
+static alg::HeadParams head_params(int N, int d, int V, const void* h, const void* E, const int32_t* targets, int n,
+                                   float c, void* workspace, int pass) {
+  const HeadWs ws = head_ws(N, d, V, pass);
+  alg::HeadParams p;
+  std::memset(&p, 0, sizeof p);
+  p.h = static_cast<const bf16*>(h);
+  p.E = static_cast<const bf16*>(E);
+  p.targets = targets;
+  p.N = N; p.d = d; p.V = V; p.Npad = ws.Npad;
+  p.log2n = log2_pow2(n);
+  p.c = c;
+  p.inv_c = (float)(1.0 / (double)c);
+  p.clamp = (float)(0.25 * root_pow2(1e38 / (double)V, n));  // fused_head.py:273
+  char* w = static_cast<char*>(workspace);
+  p.partial = reinterpret_cast<float*>(w + ws.partial);
+  p.obj_part = reinterpret_cast<float*>(w + ws.obj_part);
+  p.dzt = pass ? reinterpret_cast<bf16*>(w + ws.dzt) : nullptr;
+  return p;
+}
+
+int alg_head_fwd(alg_stream_t stream, int N, int d, int V, const void* h, const void* E, const int32_t* targets,
+                 int n, float c, float* stat, float* zt, float* pt, float* obj, void* workspace,
+                 size_t workspace_bytes) {
+  int rc = check_head(N, d, V, n, c);
+  if (rc) return rc;
+  if (!h || !E || !targets || !stat || !zt || !pt || !obj) return fail(ALG_ERR_INVALID, "null argument");
+  const HeadWs ws = head_ws(N, d, V, 0);
+  if (!workspace || workspace_bytes < ws.total)
+    return fail(ALG_ERR_INVALID, "workspace too small: need %zu bytes", ws.total);
+  alg::HeadParams p = head_params(N, d, V, h, E, targets, n, c, workspace, 0);
+  p.stat = stat; p.zt = zt; p.pt = pt; p.obj = obj;
+  return hip_status(alg::launch_head_fwd(p, (hipStream_t)stream), "alg_head_fwd");
+}
+
+int alg_head_bwd(alg_stream_t stream, int N, int d, int V, const void* h, const void* E, const int32_t* targets,
+                 const float* stat, const float* g, int n, float c, void* dh, void* dE, int dE_dtype,
+                 void* workspace, size_t workspace_bytes) {
+  int rc = check_head(N, d, V, n, c);
+  if (rc) return rc;
+  if (!h || !E || !targets || !stat || !g || !dh || !dE) return fail(ALG_ERR_INVALID, "null argument");
+  if (dE_dtype != ALG_DTYPE_BF16 && dE_dtype != ALG_DTYPE_F32) return fail(ALG_ERR_INVALID, "dE dtype must be bf16 or f32");
+  const HeadWs ws = head_ws(N, d, V, 1);
+  if (!workspace || workspace_bytes < ws.total)
+    return fail(ALG_ERR_INVALID, "workspace too small: need %zu bytes", ws.total);
+  alg::HeadParams p = head_params(N, d, V, h, E, targets, n, c, workspace, 1);
+  p.stat = const_cast<float*>(stat);
+  p.g = g;
+  p.dh = static_cast<bf16*>(dh);
+  p.dE = dE;
+  p.dE_f32 = dE_dtype == ALG_DTYPE_F32;
+  return hip_status(alg::launch_head_bwd(p, (hipStream_t)stream), "alg_head_bwd");
+}
+
+}  // extern "C"

@@ -1,0 +1,23 @@
+// Host launchers of the gfx950 kernels (defined in the *.hip translation units).
+#pragma once
+
+#include "attn_common.h"
+#include "attn_prep.h"
+#include "head_params.h"
+
+namespace alg {
+
+hipError_t launch_attn_fwd(const AttnFwdParams& p, int D, bool bf16_io, int mode, hipStream_t st);
+hipError_t launch_attn_bwd(const AttnBwdParams& p, int D, bool bf16_io, const int* modes, int nmodes,
+                           hipStream_t st);
+int attn_bwd_sink_blocks(int T);
+int attn_prep_blocks(size_t rows);
+hipError_t launch_attn_prep(const PrepParams& p, bool bf16_io, GuardParams g, hipStream_t st);
+
+int head_vocab_tiles(int V);
+int head_token_tiles(int N);
+int head_stat_blocks(int N);
+hipError_t launch_head_fwd(const HeadParams& p, hipStream_t st);
+hipError_t launch_head_bwd(const HeadParams& p, hipStream_t st);
+
+}  // namespace alg

@@ -1,0 +1,113 @@
+/*
+ * algebraic_hip.h -- C ABI of the MI355X (gfx950) algebraic attention and fused
+ * algebraic LM head kernels (libalgebraic_hip.so).
+ *
+ * Every entry point is a pure function over caller-owned device buffers: plain pointers,
+ * sizes, scalars and a HIP stream. No entry point allocates device memory; scratch comes
+ * from a caller workspace sized by the *_workspace_size queries. Calls are asynchronous
+ * on `stream` and reentrant (no global mutable state besides the thread-local error text).
+ * Return value: ALG_OK or an error code; alg_last_error() describes the last failure on
+ * the calling thread.
+ *
+ * Tensor layouts are row-major: attention (B, H, T, D); head h (N, d), E (V, d).
+ * Reference interfaces replaced (paths relative to the reference repository root):
+ *   src/algebraic/kernels/flash.py       flash_attention 763-857, _forward 292-326,
+ *                                        _backward 630-687, _flash_bwd 718-726
+ *   src/algebraic/kernels/head_resident.py forward 125-142, backward 145-163
+ *   src/algebraic/kernels/fused_head.py  _forward 174-191, _backward 194-216,
+ *                                        _telemetry 219-229, fused_head 260-275
+ */
+#ifndef ALGEBRAIC_HIP_H
+#define ALGEBRAIC_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* alg_stream_t; /* a hipStream_t; NULL = the null stream */
+
+enum {
+  ALG_OK = 0,
+  ALG_ERR_INVALID = 1,      /* bad shape, pointer, size or parameter */
+  ALG_ERR_UNSUPPORTED = 2,  /* valid in the reference but not built for gfx950 here */
+  ALG_ERR_HIP = 3           /* a HIP launch error */
+};
+
+enum { ALG_DTYPE_BF16 = 0, ALG_DTYPE_F32 = 1 };
+
+/* Attention variants (flash.py:59-73, 732-760, 850-852).
+ *   INRANGE  unshifted, unclipped weights, stat = 1/Z ("low" branch of range_guard)
+ *   CLIPPED  unshifted with x = min(s, clamp) (range_guard=False, shift=False)
+ *   SHIFTED  running-max accumulation (explicit shift=True, or the guard's fallback)
+ *   GUARDED  INRANGE or SHIFTED chosen on the device by guard_flag (range_guard=True) */
+enum { ALG_ATTN_INRANGE = 0, ALG_ATTN_CLIPPED = 1, ALG_ATTN_SHIFTED = 2, ALG_ATTN_GUARDED = 3 };
+
+const char* alg_last_error(void);
+const char* alg_version(void);
+
+/* Bytes of workspace alg_attn_prepare / alg_attn_bwd need for this shape. */
+size_t alg_attn_workspace_size(int B, int H, int T, int D);
+
+/* Prologue and range guard, flash.py:823-849.
+ * q_s = round(q * 1/(sqrt(D) c)) in the input dtype; sink_scaled[h] = sink_logit[h or 0] / c
+ * (sink_logit may be NULL; sink_count is 1 or H); guard_flag = 1 when
+ *   max||q_s||^2 max||k||^2 <= (bound/1.01)^2, max|sink/c| <= bound/1.01 and
+ *   max|v| <= min(1e8, 1e37/((T+has_sink)(2 bound+1)^n)), bound = min(16, clamp/2),
+ * else 0; with range_guard = 0 the flag is set to 1 and k, v are not read. */
+int alg_attn_prepare(alg_stream_t stream, int dtype, int B, int H, int T, int D,
+                     const void* q, const void* k, const void* v,
+                     const float* sink_logit, int sink_count, float c, int n, int range_guard,
+                     void* q_s, float* sink_scaled, int* guard_flag,
+                     void* workspace, size_t workspace_bytes);
+
+/* Forward, flash.py:189-326 / head_resident.py:25-89 (kernel contract of _forward):
+ * in q_s, k, v (B,H,T,D) and sink_scaled (H) f32 or NULL; out o (B,H,T,D) in the input
+ * dtype and stat (B,H,T) f32 (1/Z, or rho(-m) Z^(-1/n) when shifted, or Z^(-1/n) when
+ * CLIPPED with inv_stat = 0). o_precise (f32, optional) receives the unrounded output of
+ * the SHIFTED branch (precise_output, flash.py:322). guard_flag is read for GUARDED. */
+int alg_attn_fwd(alg_stream_t stream, int dtype, int B, int H, int T, int D,
+                 const void* q_s, const void* k, const void* v, const float* sink_scaled,
+                 int n, int variant, const int* guard_flag, float clamp, int fast_rho, int inv_stat,
+                 void* o, float* o_precise, float* stat);
+
+/* Backward, flash.py:333-361, 515-687, 694-726 / head_resident.py:91-119:
+ * in the forward residuals and dO; out dq = round(round(n * dq_s_acc) * dq_scale)
+ * (dq_scale = 1 gives the kernel's dq_s; = 1/(sqrt(D) c) chains back to q), dk, dv in the
+ * input dtype, di (B,H,T) f32 = sum_d dO*o and dsink_scaled (H) f32 = dL/d(sink/c)
+ * (may be NULL). o_precise is used for di when the SHIFTED branch ran, if given. */
+int alg_attn_bwd(alg_stream_t stream, int dtype, int B, int H, int T, int D,
+                 const void* q_s, const void* k, const void* v, const float* sink_scaled,
+                 const void* o, const float* o_precise, const float* stat, const void* dO,
+                 int n, int variant, const int* guard_flag, float clamp, int fast_rho, int inv_stat,
+                 float dq_scale,
+                 void* dq, void* dk, void* dv, float* di, float* dsink_scaled,
+                 void* workspace, size_t workspace_bytes);
+
+/* Bytes of workspace alg_head_fwd (pass 0) or alg_head_bwd (pass 1) needs. */
+size_t alg_head_workspace_size(int N, int d, int V, int pass);
+
+/* Head forward, fused_head.py:72-117, 174-191, 219-229 (kind="alg_ce"):
+ * in h (N,d) bf16, E (V,d) bf16 (already cast to h's dtype), targets (N) int32;
+ * out stat (N) = l^(-1/n), zt (N) = target logits, pt (N) telemetry, obj (1) = mean(1-pt).
+ * The clamp X = 1/4 (1e38/V)^(1/n) is derived from V and n. d must be a multiple of 128. */
+int alg_head_fwd(alg_stream_t stream, int N, int d, int V,
+                 const void* h, const void* E, const int32_t* targets, int n, float c,
+                 float* stat, float* zt, float* pt, float* obj,
+                 void* workspace, size_t workspace_bytes);
+
+/* Head backward, fused_head.py:120-156, 194-216, 247-254:
+ * in h, E, targets, stat and g (1) f32 on the device (cotangent of obj);
+ * out dh (N,d) bf16 and dE (V,d) in dE_dtype (ALG_DTYPE_BF16 or ALG_DTYPE_F32). */
+int alg_head_bwd(alg_stream_t stream, int N, int d, int V,
+                 const void* h, const void* E, const int32_t* targets, const float* stat,
+                 const float* g, int n, float c, void* dh, void* dE, int dE_dtype,
+                 void* workspace, size_t workspace_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ALGEBRAIC_HIP_H */
