@@ -31,6 +31,8 @@ _SIGNATURES = {
     "alg_head_workspace_size": (_S, [_I, _I, _I, _I]),
     "alg_head_fwd": (_I, [_P, _I, _I, _I, _P, _P, _P, _I, _F, _P, _P, _P, _P, _P, _S]),
     "alg_head_bwd": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _P, _I, _F, _P, _P, _I, _P, _S]),
+    "alg_timer_enable": (None, [_I]),
+    "alg_timer_report": (_S, [ctypes.c_char_p, _S]),
 }
 
 EXPORTS = tuple(_SIGNATURES)
@@ -70,6 +72,21 @@ def check(rc, what):
     if rc == ALG_ERR_UNSUPPORTED:
         raise NotImplementedError(f"{what}: {msg}")
     raise RuntimeError(f"{what}: {msg}")
+
+
+def timer_enable(on=True):
+    """Record a HIP event pair around every kernel launch of the library (measurement)."""
+    load().alg_timer_enable(1 if on else 0)
+
+
+def timer_report():
+    """Per-kernel {name: {"launches", "mean_ms"}} since the last report (synchronises)."""
+    import json
+    buf = ctypes.create_string_buffer(1 << 20)
+    n = load().alg_timer_report(buf, len(buf))
+    if n > len(buf):
+        raise RuntimeError("timer report truncated")
+    return json.loads(buf.value.decode())
 
 
 def ptr(t):

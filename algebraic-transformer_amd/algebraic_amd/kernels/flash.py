@@ -210,8 +210,6 @@ def flash_attention(q, k, v, sink_logit=None, *, kind: str = "softmax",
                                   "algebraic kind='asinh' path is built for MI355X")
     if q.dtype not in _DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
         raise NotImplementedError(f"dtype {q.dtype}: gfx950 kernels take bfloat16 or float32 inputs")
-    if not q.is_cuda:
-        raise RuntimeError("flash_attention needs GPU tensors (no CPU fallback)")
     if range_guard and kind == "asinh" and n <= 32:
         if poly_rho:
             raise ValueError("range_guard is for exact radical evaluation")
@@ -225,4 +223,6 @@ def flash_attention(q, k, v, sink_logit=None, *, kind: str = "softmax",
             if not var.fast_rho:
                 raise NotImplementedError("unshifted accumulation is built with fast rho (the default)")
             plan = _Plan(_lib.ATTN_CLIPPED, var.n, float(c), var.clamp, True, var.inv_stat, False)
+    if not q.is_cuda:
+        raise RuntimeError("flash_attention needs GPU tensors (no CPU fallback)")
     return _FlashFn.apply(q, k, v, sink_logit, plan)

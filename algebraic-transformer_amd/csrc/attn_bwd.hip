@@ -386,9 +386,9 @@ template <typename T, int D>
 static hipError_t launch_bwd_main(const AttnBwdParams& p, int mode, hipStream_t st) {
   dim3 grid(p.B * p.H, ceil_div(p.T, BWD_BK)), block(256);
   switch (mode) {
-    case MODE_INRANGE: hipLaunchKernelGGL((attn_bwd_kernel<T, D, MODE_INRANGE>), grid, block, 0, st, p); break;
-    case MODE_CLIPPED: hipLaunchKernelGGL((attn_bwd_kernel<T, D, MODE_CLIPPED>), grid, block, 0, st, p); break;
-    case MODE_SHIFTED: hipLaunchKernelGGL((attn_bwd_kernel<T, D, MODE_SHIFTED>), grid, block, 0, st, p); break;
+    case MODE_INRANGE: { KTimer t("attn_bwd_inrange", st); hipLaunchKernelGGL((attn_bwd_kernel<T, D, MODE_INRANGE>), grid, block, 0, st, p); } break;
+    case MODE_CLIPPED: { KTimer t("attn_bwd_clipped", st); hipLaunchKernelGGL((attn_bwd_kernel<T, D, MODE_CLIPPED>), grid, block, 0, st, p); } break;
+    case MODE_SHIFTED: { KTimer t("attn_bwd_shifted", st); hipLaunchKernelGGL((attn_bwd_kernel<T, D, MODE_SHIFTED>), grid, block, 0, st, p); } break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -401,8 +401,11 @@ hipError_t launch_attn_bwd(const AttnBwdParams& p, int D, bool bf16_io, const in
                            hipStream_t st) {
   const int nblk = attn_bwd_sink_blocks(p.T);
   dim3 pgrid(p.B * p.H, nblk);
-  if (bf16_io) hipLaunchKernelGGL((attn_bwd_pre_kernel<bf16>), pgrid, dim3(256), 0, st, p, D);
-  else hipLaunchKernelGGL((attn_bwd_pre_kernel<float>), pgrid, dim3(256), 0, st, p, D);
+  {
+    KTimer t("attn_bwd_pre", st);
+    if (bf16_io) hipLaunchKernelGGL((attn_bwd_pre_kernel<bf16>), pgrid, dim3(256), 0, st, p, D);
+    else hipLaunchKernelGGL((attn_bwd_pre_kernel<float>), pgrid, dim3(256), 0, st, p, D);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   for (int m = 0; m < nmodes; ++m) {
@@ -412,8 +415,11 @@ hipError_t launch_attn_bwd(const AttnBwdParams& p, int D, bool bf16_io, const in
   }
   const size_t total = (size_t)p.B * p.H * p.T * D;
   const int blocks = (int)std::min<size_t>((total + 255) / 256, 4096);
-  if (bf16_io) hipLaunchKernelGGL((attn_bwd_post_kernel<bf16>), dim3(blocks), dim3(256), 0, st, p, total, nblk);
-  else hipLaunchKernelGGL((attn_bwd_post_kernel<float>), dim3(blocks), dim3(256), 0, st, p, total, nblk);
+  {
+    KTimer t("attn_bwd_post", st);
+    if (bf16_io) hipLaunchKernelGGL((attn_bwd_post_kernel<bf16>), dim3(blocks), dim3(256), 0, st, p, total, nblk);
+    else hipLaunchKernelGGL((attn_bwd_post_kernel<float>), dim3(blocks), dim3(256), 0, st, p, total, nblk);
+  }
   return hipGetLastError();
 }
 

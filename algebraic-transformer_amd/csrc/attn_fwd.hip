@@ -241,9 +241,9 @@ template <typename T, int D>
 static hipError_t launch_fwd_mode(const AttnFwdParams& p, int mode, hipStream_t st) {
   dim3 grid(p.B * p.H, ceil_div(p.T, FWD_BQ)), block(256);
   switch (mode) {
-    case MODE_INRANGE: hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_INRANGE>), grid, block, 0, st, p); break;
-    case MODE_CLIPPED: hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_CLIPPED>), grid, block, 0, st, p); break;
-    case MODE_SHIFTED: hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_SHIFTED>), grid, block, 0, st, p); break;
+    case MODE_INRANGE: { KTimer t("attn_fwd_inrange", st); hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_INRANGE>), grid, block, 0, st, p); } break;
+    case MODE_CLIPPED: { KTimer t("attn_fwd_clipped", st); hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_CLIPPED>), grid, block, 0, st, p); } break;
+    case MODE_SHIFTED: { KTimer t("attn_fwd_shifted", st); hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_SHIFTED>), grid, block, 0, st, p); } break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

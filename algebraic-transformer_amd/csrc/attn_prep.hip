@@ -117,13 +117,19 @@ int attn_prep_blocks(size_t rows) {
 
 hipError_t launch_attn_prep(const PrepParams& p, bool bf16_io, GuardParams g, hipStream_t st) {
   const int nb = attn_prep_blocks(p.rows);
-  if (bf16_io) hipLaunchKernelGGL((attn_prep_kernel<bf16>), dim3(nb), dim3(256), 0, st, p);
-  else hipLaunchKernelGGL((attn_prep_kernel<float>), dim3(nb), dim3(256), 0, st, p);
+  {
+    KTimer t("attn_prep", st);
+    if (bf16_io) hipLaunchKernelGGL((attn_prep_kernel<bf16>), dim3(nb), dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((attn_prep_kernel<float>), dim3(nb), dim3(256), 0, st, p);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   g.part = p.part;
   g.nblocks = nb;
-  hipLaunchKernelGGL(attn_guard_kernel, dim3(1), dim3(256), 0, st, g);
+  {
+    KTimer t("attn_guard", st);
+    hipLaunchKernelGGL(attn_guard_kernel, dim3(1), dim3(256), 0, st, g);
+  }
   return hipGetLastError();
 }
 

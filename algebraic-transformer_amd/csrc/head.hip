@@ -196,22 +196,22 @@ int head_token_tiles(int N) { return (N + GT_N - 1) / GT_N; }
 int head_stat_blocks(int N) { return (N + 255) / 256; }
 
 hipError_t launch_head_fwd(const HeadParams& p, hipStream_t st) {
-  hipLaunchKernelGGL(head_zero_kernel, dim3((p.N + 255) / 256), dim3(256), 0, st, p.zt, p.N);
+  { KTimer t("head_zero", st); hipLaunchKernelGGL(head_zero_kernel, dim3((p.N + 255) / 256), dim3(256), 0, st, p.zt, p.N); }
   dim3 grid(head_token_tiles(p.N), head_vocab_tiles(p.V));
-  hipLaunchKernelGGL(head_fwd_kernel, grid, dim3(256), 0, st, p);
+  { KTimer t("head_fwd", st); hipLaunchKernelGGL(head_fwd_kernel, grid, dim3(256), 0, st, p); }
   const int nb = head_stat_blocks(p.N);
-  hipLaunchKernelGGL(head_stats_kernel, dim3(nb), dim3(256), 0, st, p, head_vocab_tiles(p.V));
-  hipLaunchKernelGGL(head_obj_kernel, dim3(1), dim3(256), 0, st, p, nb);
+  { KTimer t("head_stats", st); hipLaunchKernelGGL(head_stats_kernel, dim3(nb), dim3(256), 0, st, p, head_vocab_tiles(p.V)); }
+  { KTimer t("head_obj", st); hipLaunchKernelGGL(head_obj_kernel, dim3(1), dim3(256), 0, st, p, nb); }
   return hipGetLastError();
 }
 
 hipError_t launch_head_bwd(const HeadParams& p, hipStream_t st) {
   dim3 g1(p.Npad / GT_N, head_vocab_tiles(p.V));
-  hipLaunchKernelGGL(head_dz_kernel, g1, dim3(256), 0, st, p);
+  { KTimer t("head_dz", st); hipLaunchKernelGGL(head_dz_kernel, g1, dim3(256), 0, st, p); }
   dim3 g2(p.d / GT_N, head_token_tiles(p.N));
-  hipLaunchKernelGGL(head_dh_kernel, g2, dim3(256), 0, st, p);
+  { KTimer t("head_dh", st); hipLaunchKernelGGL(head_dh_kernel, g2, dim3(256), 0, st, p); }
   dim3 g3(p.d / GT_N, head_vocab_tiles(p.V));
-  hipLaunchKernelGGL(head_de_kernel, g3, dim3(256), 0, st, p);
+  { KTimer t("head_de", st); hipLaunchKernelGGL(head_de_kernel, g3, dim3(256), 0, st, p); }
   return hipGetLastError();
 }
 

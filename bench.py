@@ -1,0 +1,257 @@
+#!/usr/bin/env python3
+"""Benchmark of the algebraic hot path on one MI355X (the BASELINE.json metric).
+
+One step = the 1B-shape workload of BASELINE.json config 4, inputs resident in HBM:
+  * causal algebraic attention forward + backward, B=8 H=16 T=2048 D=128 bf16, QK
+    RMS-normalised, learned per-head sink, n=16 c=8, range_guard=True
+    (the model's call, src/algebraic/model.py:145-150);
+  * fused algebraic head forward + backward, N=16384 tokens, d=2048, V=32000 bf16,
+    n=8 c=2 (src/algebraic/model.py:219-224).
+FLOP conventions are the reference's: attention fwd 4 B H T^2 D / 2, fwd+bwd 3.5x
+(scripts/bench_attention.py:50, 65); head 3 matmuls 3*2*N*d*V (scripts/bench_head.py:35).
+
+Prints ONE JSON line. ``value`` is the step's algorithmic TFLOP/s (attention + head);
+the attention TFLOP/s, the head tokens/s and each part's fraction of the bf16 dense MFMA
+peak are reported beside it, with a roofline entry for the kernel that takes the most time
+(per-kernel durations from HIP events recorded on the launch stream) and a CPU baseline
+(the NumPy oracle timed on a bounded sample of the same workload on the host cores).
+"""
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "algebraic-transformer_amd"))
+sys.path.insert(0, str(ROOT))
+
+METRIC = "algebraic attn fwd+bwd TFLOP/s & head tokens/s at 1B shape; % MFMA peak"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA (no sparsity)
+PEAK_HBM_GBS = 8000.0
+
+ATTN = dict(B=8, H=16, T=2048, D=128, n=16, c=8.0)
+HEAD = dict(N=16384, d=2048, V=32000, n=8, c=2.0)
+
+
+def attn_flops(B, H, T, D, **_):
+    return 4.0 * B * H * T * T * D / 2
+
+
+def head_flops(N, d, V, **_):
+    return 3.0 * 2.0 * N * d * V
+
+
+def kernel_algorithmic_flops():
+    """Algorithmic FLOPs per launch of each heavy kernel (units x per-unit figure)."""
+    fa = attn_flops(**ATTN)
+    g = 2.0 * HEAD["N"] * HEAD["d"] * HEAD["V"]   # one N x d x V product
+    return {
+        "attn_fwd_inrange": fa,          # QK^T + PV over the causal half
+        "attn_bwd_inrange": 2.5 * fa,    # 3.5x fwd+bwd convention minus the forward
+        "head_fwd": g,                   # z = h E^T
+        "head_dz": g,                    # z recomputed (executed; the 3-matmul convention omits it)
+        "head_dh": g,                    # dh = dZ E
+        "head_de": g,                    # dE = dZ^T h
+    }
+
+
+def rms_norm(x, eps=1e-5):
+    return x * (x.float().pow(2).mean(-1, keepdim=True) + eps).rsqrt().to(x.dtype)
+
+
+def make_inputs(torch, dev, seed=0):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    B, H, T, D = (ATTN[k] for k in "BHTD")
+    rn = lambda *s: torch.randn(*s, device=dev, generator=g, dtype=torch.float32)
+    q = rms_norm(rn(B, H, T, D)).to(torch.bfloat16).requires_grad_(True)
+    k = rms_norm(rn(B, H, T, D)).to(torch.bfloat16).requires_grad_(True)
+    v = rn(B, H, T, D).to(torch.bfloat16).requires_grad_(True)
+    do = rn(B, H, T, D).to(torch.bfloat16)
+    sink = (rn(1, H, 1, 1) * 0.1).requires_grad_(True)
+    N, d, V = HEAD["N"], HEAD["d"], HEAD["V"]
+    h = rms_norm(rn(N, d)).to(torch.bfloat16).requires_grad_(True)
+    E = (rn(V, d) * 0.02).to(torch.bfloat16).requires_grad_(True)
+    t = torch.randint(0, V, (N,), device=dev, generator=g, dtype=torch.int32)
+    return dict(q=q, k=k, v=v, do=do, sink=sink, h=h, E=E, t=t)
+
+
+def make_steps(torch, x):
+    from algebraic_amd.kernels.flash import flash_attention
+    from algebraic_amd.kernels.fused_head import fused_head
+
+    def attn_step():
+        o = flash_attention(x["q"], x["k"], x["v"], x["sink"], kind="asinh", n=ATTN["n"], c=ATTN["c"],
+                            block=512, range_guard=True)
+        return torch.autograd.grad(o, (x["q"], x["k"], x["v"], x["sink"]), x["do"])
+
+    def head_step():
+        obj, _ = fused_head(x["h"], x["E"], x["t"], kind="alg_ce", n=HEAD["n"], c=HEAD["c"])
+        return torch.autograd.grad(obj, (x["h"], x["E"]))
+
+    def full_step():
+        attn_step()
+        head_step()
+
+    return attn_step, head_step, full_step
+
+
+def timed(torch, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def cpu_baseline(seconds_hint=True):
+    """Time the NumPy oracle on a bounded sample of the step on the host cores."""
+    import numpy as np
+    from oracle import attention as OA
+    from oracle import head as OH
+    from oracle.numerics import round_bf16
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover
+        threads = len(os.sched_getaffinity(0))
+    rng = np.random.default_rng(0)
+    B, H, T, D = (ATTN[k] for k in "BHTD")
+    nh = 2
+    mk = lambda: round_bf16(rng.standard_normal((1, nh, T, D)).astype(np.float32))
+    q, k, v, do = mk(), mk(), mk(), mk()
+    sink = (rng.standard_normal((1, nh, 1, 1)) * 0.1).astype(np.float32)
+    t0 = time.perf_counter()
+    r = OA.flash_attention_oracle(q, k, v, sink, do, n=ATTN["n"], c=ATTN["c"], dtype="bf16")
+    t_attn = (time.perf_counter() - t0) / nh * (B * H)
+    N, d, V = HEAD["N"], HEAD["d"], HEAD["V"]
+    ns = 512
+    h = round_bf16(rng.standard_normal((ns, d)).astype(np.float32))
+    E = round_bf16((rng.standard_normal((V, d)) * 0.02).astype(np.float32))
+    tg = rng.integers(0, V, ns)
+    t0 = time.perf_counter()
+    stat, zt, pt, obj = OH.kernel_forward(h, E, tg, n=HEAD["n"], c=HEAD["c"], chunk=256)
+    OH.kernel_backward(h, E, tg, stat, 1.0, n=HEAD["n"], c=HEAD["c"], chunk=256)
+    t_head = (time.perf_counter() - t0) * (N / ns)
+    total = attn_flops(**ATTN) * 3.5 + head_flops(**HEAD)
+    step_s = t_attn + t_head
+    del r
+    return {
+        "value": round(total / step_s / 1e12, 6), "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
+        "sample": (f"NumPy float32 oracle (oracle/attention.py kernel_forward/backward, oracle/head.py "
+                   f"kernel_forward/backward): attention fwd+bwd on {nh} of {B * H} heads "
+                   f"(T={T}, D={D}) scaled x{B * H // nh}, head fwd+bwd on {ns} of {N} tokens "
+                   f"(d={d}, V={V}) scaled x{N // ns}; est. CPU step {step_s:.1f} s "
+                   f"(attention {t_attn:.1f} s, head {t_head:.1f} s)"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X "
+              "(the path shards over (batch, head) and token blocks without cross-GPU exchange; "
+              "one GPU share is the kernel at its real shape). Run with --gpus 1.", file=sys.stderr)
+        return 2
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    from algebraic_amd import _lib
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    x = make_inputs(torch, dev)
+    attn_step, head_step, full_step = make_steps(torch, x)
+
+    K, W = args.steps, args.warmup
+    log = lambda msg: print(f"bench: {msg}", file=sys.stderr, flush=True)
+    step_s = timed(torch, full_step, K, W)
+    log(f"full step {step_s * 1e3:.3f} ms")
+    attn_s = timed(torch, attn_step, K, 1)
+    log(f"attention fwd+bwd {attn_s * 1e3:.3f} ms")
+    head_s = timed(torch, head_step, K, 1)
+    log(f"head fwd+bwd {head_s * 1e3:.3f} ms")
+
+    # Per-kernel durations from HIP events on the launch stream (separate timed pass).
+    _lib.timer_enable(True)
+    for _ in range(K):
+        full_step()
+    torch.cuda.synchronize()
+    kernels = _lib.timer_report()
+    _lib.timer_enable(False)
+
+    fa = attn_flops(**ATTN) * 3.5
+    fh = head_flops(**HEAD)
+    attn_tf = fa / attn_s / 1e12
+    head_tf = fh / head_s / 1e12
+    algo = kernel_algorithmic_flops()
+    per_step = {name: rec["mean_ms"] * rec["launches"] / K for name, rec in kernels.items()}
+    dom = max(per_step, key=per_step.get)
+    dom_ms = kernels[dom]["mean_ms"]
+    achieved = algo.get(dom, 0.0) / (dom_ms * 1e-3) / 1e12 if dom in algo else None
+    roofline = {
+        "kernel": dom,
+        "bound": "mfma",
+        "achieved": round(achieved, 3) if achieved is not None else None,
+        "peak": PEAK_BF16_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(achieved / PEAK_BF16_TFLOPS, 4) if achieved is not None else None,
+        "traffic": None,
+        "mean_ms": round(dom_ms, 4),
+    }
+    out = {
+        "metric": METRIC,
+        "value": round((fa + fh) / step_s / 1e12, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(step_s * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": ("1B shape (BASELINE config 4): causal algebraic attention fwd+bwd "
+                         "B8 H16 T2048 D128 n16 c8 range_guard + fused alg_ce head fwd+bwd "
+                         "N16384 d2048 V32000 n8 c2"),
+            "tokens_per_step": HEAD["N"],
+            "flops_per_step": fa + fh,
+        },
+        "attn": {
+            "ms": round(attn_s * 1e3, 4), "tflops": round(attn_tf, 3),
+            "tokens_per_s": round(ATTN["B"] * ATTN["T"] / attn_s, 1),
+            "frac_peak": round(attn_tf / PEAK_BF16_TFLOPS, 4),
+        },
+        "head": {
+            "ms": round(head_s * 1e3, 4), "tflops": round(head_tf, 3),
+            "tokens_per_s": round(HEAD["N"] / head_s, 1),
+            "frac_peak": round(head_tf / PEAK_BF16_TFLOPS, 4),
+        },
+        "kernels": {n: {"launches_per_step": r["launches"] / K, "mean_ms": round(r["mean_ms"], 4),
+                        **({"tflops": round(algo[n] / (r["mean_ms"] * 1e-3) / 1e12, 2)} if n in algo else {})}
+                    for n, r in sorted(kernels.items())},
+        "roofline": roofline,
+    }
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline sample")
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -106,6 +106,15 @@ int alg_head_bwd(alg_stream_t stream, int N, int d, int V,
                  const float* g, int n, float c, void* dh, void* dE, int dE_dtype,
                  void* workspace, size_t workspace_bytes);
 
+/* Measurement hook (no counterpart in the reference; for benchmarks and profilers):
+ * while enabled, every kernel launch of this library records a HIP event pair on its
+ * stream. alg_timer_report() waits for those events, writes a JSON object
+ * {"kernel": {"launches": L, "mean_ms": M}, ...} into out (truncated to cap bytes, NUL
+ * terminated), clears the records and returns the full length + 1. Not thread-safe with
+ * concurrent timed launches. */
+void alg_timer_enable(int on);
+size_t alg_timer_report(char* out, size_t cap);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,68 @@
+"""CPU: the host mirror raises the reference's errors before touching a GPU.
+
+Mirrors the ValueErrors of src/algebraic/kernels/flash.py:740-743, 796-797, 802-817, 836 and
+src/algebraic/kernels/fused_head.py:163-164, 269-272, plus NotImplementedError for the
+softmax / cross-entropy control arms that this build does not provide.
+"""
+
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from algebraic_amd.kernels.flash import flash_attention, make_variant  # noqa: E402
+from algebraic_amd.kernels.fused_head import fused_head  # noqa: E402
+
+
+def qkv(T=256, D=64, dtype=torch.bfloat16):
+    return [torch.zeros(1, 2, T, D, dtype=dtype) for _ in range(3)]
+
+
+def test_make_variant_matches_reference_defaults():
+    v = make_variant("asinh", 16, 8.0, 2048)
+    assert not v.shift and v.fast_rho and v.inv_stat and abs(v.clamp - 63.7) < 0.05
+    assert make_variant("asinh", 16, 8.0, 10 ** 30).shift  # clamp < 20 -> shifted
+    with pytest.raises(ValueError):
+        make_variant("asinh", 12, 8.0)
+    with pytest.raises(ValueError):
+        make_variant("asinh", 16, -1.0)
+    with pytest.raises(ValueError):
+        make_variant("asinh", 16, 8.0, inv_stat=True, shift=True)
+    with pytest.raises(ValueError):
+        make_variant("nope")
+
+
+def test_flash_validation():
+    q, k, v = qkv(T=256)
+    with pytest.raises(ValueError):
+        flash_attention(q, k, v, kind="asinh", block=96)          # 256 % 96
+    with pytest.raises(ValueError):
+        flash_attention(q, k, v, kind="asinh", n=6)
+    with pytest.raises(ValueError):
+        flash_attention(q, k, v, kind="asinh", resident_bwd=True)  # needs T in {512,1024,2048}
+    with pytest.raises(ValueError):
+        flash_attention(q, k, v, kind="asinh", poly_rho=True, range_guard=True)
+    with pytest.raises(NotImplementedError):
+        flash_attention(q, k, v, kind="softmax")
+    q16, k16, v16 = qkv(dtype=torch.float16)
+    with pytest.raises(NotImplementedError):
+        flash_attention(q16, k16, v16, kind="asinh", range_guard=True)
+    with pytest.raises(RuntimeError):
+        flash_attention(q, k, v, kind="asinh", range_guard=True)   # CPU tensors: no fallback
+
+
+def test_fused_head_validation():
+    h = torch.zeros(256, 128, dtype=torch.bfloat16)
+    E = torch.zeros(300, 128)
+    t = torch.zeros(256, dtype=torch.int32)
+    with pytest.raises(ValueError):
+        fused_head(h, E, t, kind="xent")
+    with pytest.raises(ValueError):
+        fused_head(h, E, t, kind="alg_ce", n=6)
+    with pytest.raises(ValueError):
+        fused_head(h[:200], E, t[:200], kind="alg_ce", block_n=128)   # 200 % 128
+    with pytest.raises(NotImplementedError):
+        fused_head(h, E, t, kind="ce")
+    with pytest.raises(NotImplementedError):
+        fused_head(h.float(), E, t, kind="alg_ce")
+    with pytest.raises(RuntimeError):
+        fused_head(h, E, t, kind="alg_ce", n=8, c=2.0)               # CPU tensors: no fallback
