@@ -12,9 +12,16 @@ fused_head.py:215). Returns ``(objective, telemetry)``: the mean target-miss pro
 receives no gradient. ``kind="ce"`` (the softmax control arm) raises NotImplementedError.
 """
 
+import os
+
 import torch
 
 from .. import _lib
+
+# Backward schedule: "residual" keeps the vocab-major bf16 block U = w r (and l) from the
+# forward so the backward runs 3 products; "recompute" keeps only (h, E, targets, stat) as
+# the reference does (fused_head.py:244) and recomputes the logits (4 products).
+SCHEDULE = os.environ.get("ALGEBRAIC_HEAD_SCHEDULE", "residual")
 
 
 def _root(value, n):
@@ -43,31 +50,35 @@ class _HeadFn(torch.autograd.Function):
         zt = torch.empty(N, dtype=torch.float32, device=dev)
         pt = torch.empty(N, dtype=torch.float32, device=dev)
         obj = torch.empty((), dtype=torch.float32, device=dev)
+        residual = None
+        if SCHEDULE == "residual" and any(ctx.needs_input_grad[:2]):
+            residual = torch.empty(lib.alg_head_residual_size(N, d, V), dtype=torch.uint8, device=dev)
         _lib.check(lib.alg_head_fwd(st, N, d, V, _lib.ptr(h), _lib.ptr(e), _lib.ptr(t), n, c, _lib.ptr(stat),
-                                    _lib.ptr(zt), _lib.ptr(pt), _lib.ptr(obj), _lib.ptr(ws), ws_bytes),
+                                    _lib.ptr(zt), _lib.ptr(pt), _lib.ptr(obj), _lib.ptr(residual),
+                                    _lib.ptr(ws), ws_bytes),
                    "fused_head forward")
         ctx.n, ctx.c = n, c
         ctx.embed_dtype = embed.dtype
-        ctx.save_for_backward(h, e, t, stat)
+        ctx.save_for_backward(h, e, t, stat, residual)
         ctx.mark_non_differentiable(pt)
         return obj, pt
 
     @staticmethod
     def backward(ctx, g_obj, g_tel):
-        h, e, t, stat = ctx.saved_tensors
+        h, e, t, stat, residual = ctx.saved_tensors
         N, d = h.shape
         V = e.shape[0]
         lib = _lib.load()
         dev = h.device
         st = _lib.stream_of(h)
         g = (g_obj if g_obj is not None else torch.zeros((), device=dev)).to(torch.float32).reshape(1).contiguous()
-        ws_bytes = lib.alg_head_workspace_size(N, d, V, 1)
+        ws_bytes = lib.alg_head_workspace_size(N, d, V, 2 if residual is not None else 1)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         dh = torch.empty_like(h)
         de_f32 = ctx.embed_dtype == torch.float32
         dE = torch.empty((V, d), dtype=torch.float32 if de_f32 else torch.bfloat16, device=dev)
         _lib.check(lib.alg_head_bwd(st, N, d, V, _lib.ptr(h), _lib.ptr(e), _lib.ptr(t), _lib.ptr(stat), _lib.ptr(g),
-                                    ctx.n, ctx.c, _lib.ptr(dh), _lib.ptr(dE),
+                                    ctx.n, ctx.c, _lib.ptr(residual), _lib.ptr(dh), _lib.ptr(dE),
                                     _lib.DTYPE_F32 if de_f32 else _lib.DTYPE_BF16, _lib.ptr(ws), ws_bytes),
                    "fused_head backward")
         return dh, dE.to(ctx.embed_dtype), None, None, None

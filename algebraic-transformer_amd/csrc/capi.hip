@@ -74,26 +74,32 @@ AttnWs attn_ws(int B, int H, int T, int D) {
   return w;
 }
 
-// Workspace layout for the head: [partials f32 nvt*N][obj parts][dZ^T bf16 V*Npad (pass 1)]
+// Head buffers. Workspace: [partials f32 nvt*N][obj parts] (+ bwd: dZ^T bf16 V*Npad for the
+// recompute schedule, or s*h/l bf16 N*d for the residual schedule). Residual (optional,
+// forward -> backward): [U^T bf16 V*Npad][l f32 N].
 struct HeadWs {
-  size_t partial, obj_part, dzt, total;
+  size_t partial, obj_part, bwd, total;
+  size_t res_ut, res_l, res_total;
   int Npad;
 };
-HeadWs head_ws(int N, int d, int V, int pass) {
-  (void)d;
+HeadWs head_ws(int N, int d, int V, int pass, bool residual) {
   HeadWs w;
-  w.Npad = ((N + 127) / 128) * 128;
+  w.Npad = alg::head_token_pad(N);
   w.partial = 0;
   w.obj_part = align256((size_t)alg::head_vocab_tiles(V) * N * sizeof(float));
-  w.dzt = w.obj_part + align256((size_t)alg::head_stat_blocks(N) * sizeof(float));
-  w.total = pass == 0 ? w.dzt : w.dzt + align256((size_t)V * w.Npad * 2);
+  w.bwd = w.obj_part + align256((size_t)alg::head_stat_blocks(N) * sizeof(float));
+  const size_t bwd_bytes = residual ? (size_t)N * d * 2 : (size_t)V * w.Npad * 2;
+  w.total = pass == 0 ? w.bwd : w.bwd + align256(bwd_bytes);
+  w.res_ut = 0;
+  w.res_l = align256((size_t)V * w.Npad * 2);
+  w.res_total = w.res_l + align256((size_t)N * sizeof(float));
   return w;
 }
 
 int check_head(int N, int d, int V, int n, float c) {
   if (N <= 0 || d <= 0 || V <= 0) return fail(ALG_ERR_INVALID, "N, d, V must be positive (got %d, %d, %d)", N, d, V);
   if (d % 128) return fail(ALG_ERR_UNSUPPORTED, "d_model %d: gfx950 head kernels need d %% 128 == 0", d);
-  if ((double)N * d > 2.0e9 || (double)V * d > 2.0e9 || (double)V * ((N + 127) / 128 * 128) > 4.0e9)
+  if ((double)N * d > 2.0e9 || (double)V * d > 2.0e9 || (double)V * alg::head_token_pad(N) > 4.0e9)
     return fail(ALG_ERR_INVALID, "head too large");
   const int k = log2_pow2(n);
   if (k < 0 || k > 6) return fail(ALG_ERR_INVALID, "n must be a power of two in [1, 64] (got %d)", n);
@@ -223,12 +229,17 @@ int alg_attn_bwd(alg_stream_t stream, int dtype, int B, int H, int T, int D, con
 
 size_t alg_head_workspace_size(int N, int d, int V, int pass) {
   if (N <= 0 || d <= 0 || V <= 0) return 0;
-  return head_ws(N, d, V, pass ? 1 : 0).total;
+  // pass 0: forward; 1: backward without a residual; 2: backward with a residual
+  return head_ws(N, d, V, pass ? 1 : 0, pass == 2).total;
+}
+
+size_t alg_head_residual_size(int N, int d, int V) {
+  if (N <= 0 || d <= 0 || V <= 0) return 0;
+  return head_ws(N, d, V, 0, true).res_total;
 }
 
 static alg::HeadParams head_params(int N, int d, int V, const void* h, const void* E, const int32_t* targets, int n,
-                                   float c, void* workspace, int pass) {
-  const HeadWs ws = head_ws(N, d, V, pass);
+                                   float c, void* workspace, const HeadWs& ws) {
   alg::HeadParams p;
   std::memset(&p, 0, sizeof p);
   p.h = static_cast<const bf16*>(h);
@@ -242,37 +253,48 @@ static alg::HeadParams head_params(int N, int d, int V, const void* h, const voi
   char* w = static_cast<char*>(workspace);
   p.partial = reinterpret_cast<float*>(w + ws.partial);
   p.obj_part = reinterpret_cast<float*>(w + ws.obj_part);
-  p.dzt = pass ? reinterpret_cast<bf16*>(w + ws.dzt) : nullptr;
   return p;
 }
 
 int alg_head_fwd(alg_stream_t stream, int N, int d, int V, const void* h, const void* E, const int32_t* targets,
-                 int n, float c, float* stat, float* zt, float* pt, float* obj, void* workspace,
-                 size_t workspace_bytes) {
+                 int n, float c, float* stat, float* zt, float* pt, float* obj, void* residual,
+                 void* workspace, size_t workspace_bytes) {
   int rc = check_head(N, d, V, n, c);
   if (rc) return rc;
   if (!h || !E || !targets || !stat || !zt || !pt || !obj) return fail(ALG_ERR_INVALID, "null argument");
-  const HeadWs ws = head_ws(N, d, V, 0);
+  const HeadWs ws = head_ws(N, d, V, 0, residual != nullptr);
   if (!workspace || workspace_bytes < ws.total)
     return fail(ALG_ERR_INVALID, "workspace too small: need %zu bytes", ws.total);
-  alg::HeadParams p = head_params(N, d, V, h, E, targets, n, c, workspace, 0);
+  alg::HeadParams p = head_params(N, d, V, h, E, targets, n, c, workspace, ws);
   p.stat = stat; p.zt = zt; p.pt = pt; p.obj = obj;
+  if (residual) {
+    p.ut = reinterpret_cast<bf16*>(static_cast<char*>(residual) + ws.res_ut);
+    p.lsum = reinterpret_cast<float*>(static_cast<char*>(residual) + ws.res_l);
+  }
   return hip_status(alg::launch_head_fwd(p, (hipStream_t)stream), "alg_head_fwd");
 }
 
 int alg_head_bwd(alg_stream_t stream, int N, int d, int V, const void* h, const void* E, const int32_t* targets,
-                 const float* stat, const float* g, int n, float c, void* dh, void* dE, int dE_dtype,
-                 void* workspace, size_t workspace_bytes) {
+                 const float* stat, const float* g, int n, float c, const void* residual, void* dh, void* dE,
+                 int dE_dtype, void* workspace, size_t workspace_bytes) {
   int rc = check_head(N, d, V, n, c);
   if (rc) return rc;
   if (!h || !E || !targets || !stat || !g || !dh || !dE) return fail(ALG_ERR_INVALID, "null argument");
   if (dE_dtype != ALG_DTYPE_BF16 && dE_dtype != ALG_DTYPE_F32) return fail(ALG_ERR_INVALID, "dE dtype must be bf16 or f32");
-  const HeadWs ws = head_ws(N, d, V, 1);
+  const HeadWs ws = head_ws(N, d, V, 1, residual != nullptr);
   if (!workspace || workspace_bytes < ws.total)
     return fail(ALG_ERR_INVALID, "workspace too small: need %zu bytes", ws.total);
-  alg::HeadParams p = head_params(N, d, V, h, E, targets, n, c, workspace, 1);
+  alg::HeadParams p = head_params(N, d, V, h, E, targets, n, c, workspace, ws);
   p.stat = const_cast<float*>(stat);
   p.g = g;
+  char* w = static_cast<char*>(workspace);
+  if (residual) {
+    p.ut = reinterpret_cast<bf16*>(static_cast<char*>(const_cast<void*>(residual)) + ws.res_ut);
+    p.lsum = reinterpret_cast<float*>(static_cast<char*>(const_cast<void*>(residual)) + ws.res_l);
+    p.hs = reinterpret_cast<bf16*>(w + ws.bwd);
+  } else {
+    p.dzt = reinterpret_cast<bf16*>(w + ws.bwd);
+  }
   p.dh = static_cast<bf16*>(dh);
   p.dE = dE;
   p.dE_f32 = dE_dtype == ALG_DTYPE_F32;

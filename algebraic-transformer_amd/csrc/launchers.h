@@ -15,7 +15,7 @@ int attn_prep_blocks(size_t rows);
 hipError_t launch_attn_prep(const PrepParams& p, bool bf16_io, GuardParams g, hipStream_t st);
 
 int head_vocab_tiles(int V);
-int head_token_tiles(int N);
+int head_token_pad(int N);
 int head_stat_blocks(int N);
 hipError_t launch_head_fwd(const HeadParams& p, hipStream_t st);
 hipError_t launch_head_bwd(const HeadParams& p, hipStream_t st);

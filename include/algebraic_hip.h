@@ -86,24 +86,33 @@ int alg_attn_bwd(alg_stream_t stream, int dtype, int B, int H, int T, int D,
                  void* dq, void* dk, void* dv, float* di, float* dsink_scaled,
                  void* workspace, size_t workspace_bytes);
 
-/* Bytes of workspace alg_head_fwd (pass 0) or alg_head_bwd (pass 1) needs. */
+/* Bytes of workspace for alg_head_fwd (pass 0), alg_head_bwd without a residual (pass 1)
+ * and alg_head_bwd with a residual (pass 2). */
 size_t alg_head_workspace_size(int N, int d, int V, int pass);
+
+/* Bytes of the optional forward->backward residual: the vocab-major bf16 block
+ * U = w*r (target entries (w_t - l) r_t) and the row sums l. With it the backward needs no
+ * logit recompute (3 products instead of 4); it has no counterpart in the reference, whose
+ * residuals are (h, E, targets, stat) (fused_head.py:244). */
+size_t alg_head_residual_size(int N, int d, int V);
 
 /* Head forward, fused_head.py:72-117, 174-191, 219-229 (kind="alg_ce"):
  * in h (N,d) bf16, E (V,d) bf16 (already cast to h's dtype), targets (N) int32;
- * out stat (N) = l^(-1/n), zt (N) = target logits, pt (N) telemetry, obj (1) = mean(1-pt).
- * The clamp X = 1/4 (1e38/V)^(1/n) is derived from V and n. d must be a multiple of 128. */
+ * out stat (N) = l^(-1/n), zt (N) = target logits, pt (N) telemetry, obj (1) = mean(1-pt),
+ * and, when residual is not NULL, the residual for alg_head_bwd. The clamp
+ * X = 1/4 (1e38/V)^(1/n) is derived from V and n. d must be a multiple of 128. */
 int alg_head_fwd(alg_stream_t stream, int N, int d, int V,
                  const void* h, const void* E, const int32_t* targets, int n, float c,
-                 float* stat, float* zt, float* pt, float* obj,
+                 float* stat, float* zt, float* pt, float* obj, void* residual,
                  void* workspace, size_t workspace_bytes);
 
 /* Head backward, fused_head.py:120-156, 194-216, 247-254:
- * in h, E, targets, stat and g (1) f32 on the device (cotangent of obj);
- * out dh (N,d) bf16 and dE (V,d) in dE_dtype (ALG_DTYPE_BF16 or ALG_DTYPE_F32). */
+ * in h, E, targets, stat, g (1) f32 on the device (cotangent of obj) and optionally the
+ * forward's residual; out dh (N,d) bf16 and dE (V,d) in dE_dtype (ALG_DTYPE_BF16 or
+ * ALG_DTYPE_F32). Without a residual the logits are recomputed (the reference's schedule). */
 int alg_head_bwd(alg_stream_t stream, int N, int d, int V,
                  const void* h, const void* E, const int32_t* targets, const float* stat,
-                 const float* g, int n, float c, void* dh, void* dE, int dE_dtype,
+                 const float* g, int n, float c, const void* residual, void* dh, void* dE, int dE_dtype,
                  void* workspace, size_t workspace_bytes);
 
 /* Measurement hook (no counterpart in the reference; for benchmarks and profilers):

@@ -51,7 +51,10 @@ def test_workspace_sizes():
     assert handle.alg_attn_workspace_size(0, H, T, D) == 0
     fwd = handle.alg_head_workspace_size(16384, 2048, 32000, 0)
     bwd = handle.alg_head_workspace_size(16384, 2048, 32000, 1)
-    assert bwd - fwd >= 32000 * 16384 * 2     # bf16 logit-gradient block
+    assert bwd - fwd >= 32000 * 16384 * 2     # bf16 logit-gradient block (recompute schedule)
+    bwd_res = handle.alg_head_workspace_size(16384, 2048, 32000, 2)
+    assert bwd_res - fwd >= 16384 * 2048 * 2  # bf16 s*h/l (residual schedule)
+    assert handle.alg_head_residual_size(16384, 2048, 32000) >= 32000 * 16384 * 2 + 16384 * 4
 
 
 def test_invalid_arguments_fail_before_launch():
@@ -67,10 +70,10 @@ def test_invalid_arguments_fail_before_launch():
                              P(16), None, P(16))
     assert rc == _lib.ALG_ERR_INVALID and b"power of two" in handle.alg_last_error()
     rc = handle.alg_head_fwd(None, 128, 200, 1000, P(16), P(16), P(16), 8, 2.0, P(16), P(16), P(16), P(16),
-                             P(16), 1 << 30)
+                             None, P(16), 1 << 30)
     assert rc == _lib.ALG_ERR_UNSUPPORTED and b"d_model" in handle.alg_last_error()
-    rc = handle.alg_head_bwd(None, 128, 256, 1000, P(16), P(16), P(16), P(16), P(16), 8, 2.0, P(16), P(16), 0,
-                             P(16), 16)
+    rc = handle.alg_head_bwd(None, 128, 256, 1000, P(16), P(16), P(16), P(16), P(16), 8, 2.0, None, P(16), P(16),
+                             0, P(16), 16)
     assert rc == _lib.ALG_ERR_INVALID and b"workspace" in handle.alg_last_error()
     with pytest.raises(ValueError):
         _lib.check(_lib.ALG_ERR_INVALID, "probe")
