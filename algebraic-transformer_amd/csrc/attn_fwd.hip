@@ -31,14 +31,41 @@ __device__ __forceinline__ void load_rows(T* dst, int pitch, const T* src, int r
   }
 }
 
+// Registers <-> LDS staging of one 64-row K or V tile (16-byte chunks, rows >= T are zero).
+template <typename T, int D>
+struct KVTile {
+  static constexpr int CH = 16 / sizeof(T);
+  static constexpr int CPR = D / CH;
+  static constexpr int PER = FWD_BK * CPR / 256;  // chunks per thread
+  static __device__ __forceinline__ void load(uint4 (&r)[PER], const T* src, int r0, int T_) {
+#pragma unroll
+    for (int c = 0; c < PER; ++c) {
+      const int idx = threadIdx.x + c * 256;
+      const int row = idx / CPR, col = (idx - row * CPR) * CH;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (r0 + row < T_) v = *reinterpret_cast<const uint4*>(src + (size_t)(r0 + row) * D + col);
+      r[c] = v;
+    }
+  }
+  static __device__ __forceinline__ void store(T* dst, int pitch, const uint4 (&r)[PER]) {
+#pragma unroll
+    for (int c = 0; c < PER; ++c) {
+      const int idx = threadIdx.x + c * 256;
+      const int row = idx / CPR, col = (idx - row * CPR) * CH;
+      *reinterpret_cast<uint4*>(dst + row * pitch + col) = r[c];
+    }
+  }
+};
+
 template <typename T, int D, int MODE>
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
   static_assert(D == 64 || D == 128, "head_dim");
   constexpr bool BF = sizeof(T) == 2;
   constexpr int PITCH = D + (BF ? 8 : 4);
   constexpr int NDB = D / 32;  // 32-wide d blocks of the O^T accumulator
-  __shared__ __attribute__((aligned(16))) T Ks[FWD_BK * PITCH];
-  __shared__ __attribute__((aligned(16))) T Vs[FWD_BK * PITCH];
+  typedef KVTile<T, D> KV;
+  __shared__ __attribute__((aligned(16))) T Ks[2][FWD_BK * PITCH];
+  __shared__ __attribute__((aligned(16))) T Vs[2][FWD_BK * PITCH];
 
   if (p.flag) {  // device-side guard dispatch (lax.cond at flash.py:853-856)
     const bool in_range = *p.flag != 0;
@@ -86,109 +113,138 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
   if (MODE == MODE_SHIFTED && has_sink && h == 0) lsum = 1.0f;
   bool first = true;
 
-  const int q_last = min(qb * FWD_BQ + FWD_BQ, T_) - 1;
-  const int ntiles = q_last / FWD_BK + 1;
-  for (int kt = 0; kt < ntiles; ++kt) {
-    __syncthreads();
-    load_rows<T>(Ks, PITCH, K, kt * FWD_BK, FWD_BK, T_, D);
-    load_rows<T>(Vs, PITCH, V, kt * FWD_BK, FWD_BK, T_, D);
-    __syncthreads();
-    if (!wave_live) continue;
+  // One 32-key block of the tile in buffer `buf`: S^T, weights, O^T += V^T P^T.
+  auto block = [&](int buf, int sub, int kb, bool diag) {
+    const T* krow = Ks[buf] + (sub * 32 + l32) * PITCH;
+    floatx16 s = {};
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      const int kb = kt * FWD_BK + sub * 32;
-      if (kb > q0 + 31 || kb >= T_) continue;  // wave-uniform: tile fully masked
-      const T* krow = Ks + (sub * 32 + l32) * PITCH;
-      floatx16 s = {};
-#pragma unroll
-      for (int st = 0; st < NQF; ++st) {
-        if constexpr (BF) {
-          bf16x8 kf = *reinterpret_cast<const bf16x8*>(krow + 16 * st + 8 * h);
-          s = mfma_bf16(kf, qf[st], s);
-        } else {
-          floatx4 kf = *reinterpret_cast<const floatx4*>(krow + 8 * st + 4 * h);
-#pragma unroll
-          for (int u = 0; u < 4; ++u) s = mfma_f32(kf[u], qf[st][u], s);
-        }
-      }
-      const bool diag = kb + 31 > q0;
-      float w[16];
-      if constexpr (MODE != MODE_SHIFTED) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          float x = s[i];
-          if constexpr (MODE == MODE_CLIPPED) x = fminf(x, p.clamp);
-          float t = rho_fast(x);
-          for (int e = 0; e < log2n; ++e) t = t * t;
-          w[i] = t;
-        }
-        if (diag) {
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int key = kb + 8 * (i >> 2) + 4 * h + (i & 3);
-            if (key > myq) w[i] = 0.0f;
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < 16; ++i) lsum += w[i];
-      } else {
-        // Running maximum over this 32-key block (flash.py:235-259).
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = kb + 8 * (i >> 2) + 4 * h + (i & 3);
-          if (!diag || key <= myq) tmax = fmaxf(tmax, s[i]);
-        }
-        tmax = fmaxf(tmax, xor32(tmax));
-        float m_new = fmaxf(m_run, tmax);
-        float m_prev = m_run;
-        if (!has_sink && first) { m_new = tmax; m_prev = tmax; }
-        const float shift = rho_exact(-m_new);
-        const float alpha = ipow_rt(rho_exact(m_prev) * shift, 1 << log2n);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = kb + 8 * (i >> 2) + 4 * h + (i & 3);
-          const bool valid = !diag || key <= myq;
-          const float x = valid ? s[i] : 0.0f;
-          const float r0 = p.fast_rho ? rho_fast(x) : rho_exact(x);
-          float t = r0 * shift;
-          for (int e = 0; e < log2n; ++e) t = t * t;
-          w[i] = valid ? t : 0.0f;
-        }
-        float ts = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) ts += w[i];
-        lsum = alpha * lsum + ts;
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) oacc[db] = oacc[db] * alpha;
-        m_run = m_new;
-      }
-      first = false;
-      // O^T += V^T P^T over the 32 keys of this block.
+    for (int st = 0; st < NQF; ++st) {
       if constexpr (BF) {
-        bf16x8 pf0, pf1;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) { pf0[j] = f2bf(w[j]); pf1[j] = f2bf(w[8 + j]); }
-        const bf16* vt = reinterpret_cast<const bf16*>(Vs);
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          bf16x8 v0 = lds_tr_frag(vt, PITCH, sub * 32 + 4 * h, sub * 32 + 8 + 4 * h, db * 32, lane);
-          oacc[db] = mfma_bf16(v0, pf0, oacc[db]);
-          bf16x8 v1 = lds_tr_frag(vt, PITCH, sub * 32 + 16 + 4 * h, sub * 32 + 24 + 4 * h, db * 32, lane);
-          oacc[db] = mfma_bf16(v1, pf1, oacc[db]);
-        }
+        bf16x8 kf = *reinterpret_cast<const bf16x8*>(krow + 16 * st + 8 * h);
+        s = mfma_bf16(kf, qf[st], s);
       } else {
+        floatx4 kf = *reinterpret_cast<const floatx4*>(krow + 8 * st + 4 * h);
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) {
+        for (int u = 0; u < 4; ++u) s = mfma_f32(kf[u], qf[st][u], s);
+      }
+    }
+    float w[16];
+    if constexpr (MODE != MODE_SHIFTED) {
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int krow_i = sub * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-            const float a = reinterpret_cast<const float*>(Vs)[krow_i * PITCH + db * 32 + l32];
-            oacc[db] = mfma_f32(a, w[i], oacc[db]);
-          }
+      for (int i = 0; i < 16; ++i) {
+        float x = s[i];
+        if constexpr (MODE == MODE_CLIPPED) x = fminf(x, p.clamp);
+        float t = rho_fast(x);
+        if constexpr (MODE == MODE_INRANGE) {
+          t = ipow<16>(t);
+          if (log2n != 4) { t = rho_fast(x); for (int e = 0; e < log2n; ++e) t = t * t; }
+        } else {
+          for (int e = 0; e < log2n; ++e) t = t * t;
+        }
+        w[i] = t;
+      }
+      if (diag) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = kb + 8 * (i >> 2) + 4 * h + (i & 3);
+          if (key > myq) w[i] = 0.0f;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) lsum += w[i];
+    } else {
+      // Running maximum over this 32-key block (flash.py:235-259).
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = kb + 8 * (i >> 2) + 4 * h + (i & 3);
+        if (!diag || key <= myq) tmax = fmaxf(tmax, s[i]);
+      }
+      tmax = fmaxf(tmax, xor32(tmax));
+      float m_new = fmaxf(m_run, tmax);
+      float m_prev = m_run;
+      if (!has_sink && first) { m_new = tmax; m_prev = tmax; }
+      const float shift = rho_exact(-m_new);
+      const float alpha = ipow_rt(rho_exact(m_prev) * shift, 1 << log2n);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = kb + 8 * (i >> 2) + 4 * h + (i & 3);
+        const bool valid = !diag || key <= myq;
+        const float x = valid ? s[i] : 0.0f;
+        const float r0 = p.fast_rho ? rho_fast(x) : rho_exact(x);
+        float t = r0 * shift;
+        for (int e = 0; e < log2n; ++e) t = t * t;
+        w[i] = valid ? t : 0.0f;
+      }
+      float ts = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) ts += w[i];
+      lsum = alpha * lsum + ts;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) oacc[db] = oacc[db] * alpha;
+      m_run = m_new;
+    }
+    first = false;
+    if constexpr (BF) {
+      bf16x8 pf0, pf1;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) { pf0[j] = f2bf(w[j]); pf1[j] = f2bf(w[8 + j]); }
+      const bf16* vt = reinterpret_cast<const bf16*>(Vs[buf]);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        bf16x8 v0 = lds_tr_frag(vt, PITCH, sub * 32 + 4 * h, sub * 32 + 8 + 4 * h, db * 32, lane);
+        oacc[db] = mfma_bf16(v0, pf0, oacc[db]);
+        bf16x8 v1 = lds_tr_frag(vt, PITCH, sub * 32 + 16 + 4 * h, sub * 32 + 24 + 4 * h, db * 32, lane);
+        oacc[db] = mfma_bf16(v1, pf1, oacc[db]);
+      }
+    } else {
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int krow_i = sub * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+          const float a = reinterpret_cast<const float*>(Vs[buf])[krow_i * PITCH + db * 32 + l32];
+          oacc[db] = mfma_f32(a, w[i], oacc[db]);
         }
       }
     }
+  };
+
+  const int q_last = min(qb * FWD_BQ + FWD_BQ, T_) - 1;
+  const int ntiles = q_last / FWD_BK + 1;
+  // K/V tiles are double-buffered: the next tile's global loads are in flight while the
+  // current tile is consumed; one barrier per tile.
+  uint4 kr[KV::PER], vr[KV::PER];
+  KV::load(kr, K, 0, T_);
+  KV::load(vr, V, 0, T_);
+  KV::store(Ks[0], PITCH, kr);
+  KV::store(Vs[0], PITCH, vr);
+  __syncthreads();
+  for (int kt = 0; kt < ntiles; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < ntiles;
+    if (more) {
+      KV::load(kr, K, (kt + 1) * FWD_BK, T_);
+      KV::load(vr, V, (kt + 1) * FWD_BK, T_);
+    }
+    if (wave_live) {
+      const int kb0 = kt * FWD_BK;
+      if (kb0 + FWD_BK - 1 <= q0) {  // every key precedes every query of this wave: no mask
+        block(cur, 0, kb0, false);
+        block(cur, 1, kb0 + 32, false);
+      } else {
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+          const int kb = kb0 + sub * 32;
+          if (kb <= q0 + 31 && kb < T_) block(cur, sub, kb, kb + 31 > q0);
+        }
+      }
+    }
+    if (more) {
+      KV::store(Ks[cur ^ 1], PITCH, kr);
+      KV::store(Vs[cur ^ 1], PITCH, vr);
+    }
+    __syncthreads();
   }
   if (!wave_live) return;
 

@@ -1,12 +1,13 @@
 // bf16 MFMA GEMM main loop for gfx950, shared by the fused-head kernels.
 //
-// C[M][N] = sum_k A[m][k] B[k][n] with f32 accumulation. Workgroup tile TM x TN (128 or 256
-// each), 64-deep k steps, 4 waves as 2x2, each wave (TM/2) x (TN/2) = (TM/64) x (TN/64)
-// blocks of v_mfma_f32_32x32x16_bf16. Operands may be stored k-contiguous (fragments read
-// with ds_read_b128) or m/n-contiguous (fragments read transposed with ds_read_b64_tr_b16),
-// so every head product reads its operands in their natural HBM layout. Global tiles are
-// double-buffered through LDS (the next tile's loads are in flight while the current one is
-// consumed) with one barrier per k step; rows/columns outside the matrix are zero-filled.
+// C[M][N] = sum_k A[m][k] B[k][n] with f32 accumulation. A configuration fixes the
+// workgroup tile TM x TN, 64-deep k steps and a WM x WN grid of waves; each wave owns a
+// (TM/WM) x (TN/WN) sub-tile of 32x32 blocks computed with v_mfma_f32_32x32x16_bf16.
+// Operands may be stored k-contiguous (fragments read with ds_read_b128) or m/n-contiguous
+// (fragments read transposed with ds_read_b64_tr_b16), so every head product reads its
+// operands in their natural HBM layout. Global tiles are double-buffered through LDS (the
+// next tile's loads are in flight while the current one is consumed) with one barrier per
+// k step; rows/columns outside the matrix are zero-filled.
 #pragma once
 
 #include "common.h"
@@ -15,6 +16,14 @@ namespace alg {
 
 constexpr int GT_K = 64;
 enum OperandMode { KMAJOR = 0, MNMAJOR = 1 };
+
+template <int TM_, int TN_, int WM_, int WN_>
+struct GemmCfg {
+  static constexpr int TM = TM_, TN = TN_, WM = WM_, WN = WN_;
+  static constexpr int THREADS = 64 * WM * WN;
+  static constexpr int WTM = TM / WM, WTN = TN / WN;  // wave sub-tile
+  static constexpr int MB = WTM / 32, NB = WTN / 32;  // 32x32 blocks per wave
+};
 
 struct GemmOperand {
   const bf16* ptr;
@@ -35,18 +44,19 @@ struct TileShape<MNMAJOR, TMN> {  // stored [k][mn]
   static constexpr int ROWS = GT_K, COLS = TMN, PITCH = TMN + 8;
 };
 
-template <int MODE, int TMN>
+template <int MODE, int TMN, int NT>
 struct OperandTile {
   typedef TileShape<MODE, TMN> S;
   static constexpr int CPR = S::COLS / 8;               // 16-byte chunks per stored row
-  static constexpr int CHUNKS = S::ROWS * CPR / 256;    // per thread
+  static constexpr int CHUNKS = S::ROWS * CPR / NT;     // per thread
   static constexpr int ELEMS = S::ROWS * S::PITCH;
+  static_assert(S::ROWS * CPR % NT == 0, "tile/threads");
 
   // Global -> registers.
   static __device__ __forceinline__ void load(uint4 (&r)[CHUNKS], const GemmOperand& op, int mn0, int k0) {
 #pragma unroll
     for (int c = 0; c < CHUNKS; ++c) {
-      const int idx = threadIdx.x + c * 256;
+      const int idx = threadIdx.x + c * NT;
       const int row = idx / CPR, col = (idx - row * CPR) * 8;
       const int grow = (MODE == KMAJOR) ? mn0 + row : k0 + row;
       const int gcol = (MODE == KMAJOR) ? k0 + col : mn0 + col;
@@ -60,7 +70,7 @@ struct OperandTile {
   static __device__ __forceinline__ void store(bf16* tile, const uint4 (&r)[CHUNKS]) {
 #pragma unroll
     for (int c = 0; c < CHUNKS; ++c) {
-      const int idx = threadIdx.x + c * 256;
+      const int idx = threadIdx.x + c * NT;
       const int row = idx / CPR, col = (idx - row * CPR) * 8;
       *reinterpret_cast<uint4*>(tile + row * S::PITCH + col) = r[c];
     }
@@ -76,32 +86,34 @@ struct OperandTile {
   }
 };
 
-template <int AM, int BM, int TM, int TN>
+template <int AM, int BM, class C>
 struct GemmSmem {
-  bf16 a[2][OperandTile<AM, TM>::ELEMS];
-  bf16 b[2][OperandTile<BM, TN>::ELEMS];
+  bf16 a[2][OperandTile<AM, C::TM, C::THREADS>::ELEMS];
+  bf16 b[2][OperandTile<BM, C::TN, C::THREADS>::ELEMS];
 };
 
-template <int TM, int TN>
-struct WaveTile {
-  static constexpr int MB = TM / 64, NB = TN / 64;  // 32x32 blocks per wave
-};
+// Wave coordinates inside the workgroup tile.
+template <class C>
+__device__ __forceinline__ void wave_coords(int& wm, int& wn) {
+  const int wave = threadIdx.x >> 6;
+  wm = wave / C::WN;
+  wn = wave % C::WN;
+}
 
 // Accumulate the (m0, n0) tile over k in [0, K). acc[mb][nb] is the wave's 32x32 block at
-// wave rows wm*(TM/2) + mb*32 and columns wn*(TN/2) + nb*32.
-template <int AM, int BM, int TM, int TN>
-__device__ __forceinline__ void gemm_mainloop(GemmSmem<AM, BM, TM, TN>& sm, const GemmOperand& A,
-                                              const GemmOperand& B, int m0, int n0, int K,
-                                              floatx16 (&acc)[TM / 64][TN / 64]) {
-  typedef OperandTile<AM, TM> TA;
-  typedef OperandTile<BM, TN> TB;
-  constexpr int MB = TM / 64, NB = TN / 64;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+// rows wm*WTM + mb*32 and columns wn*WTN + nb*32 of the workgroup tile.
+template <int AM, int BM, class C>
+__device__ __forceinline__ void gemm_mainloop(GemmSmem<AM, BM, C>& sm, const GemmOperand& A, const GemmOperand& B,
+                                              int m0, int n0, int K, floatx16 (&acc)[C::MB][C::NB]) {
+  typedef OperandTile<AM, C::TM, C::THREADS> TA;
+  typedef OperandTile<BM, C::TN, C::THREADS> TB;
+  const int lane = threadIdx.x & 63;
+  int wm, wn;
+  wave_coords<C>(wm, wn);
 #pragma unroll
-  for (int i = 0; i < MB; ++i)
+  for (int i = 0; i < C::MB; ++i)
 #pragma unroll
-    for (int j = 0; j < NB; ++j) acc[i][j] = floatx16{};
+    for (int j = 0; j < C::NB; ++j) acc[i][j] = floatx16{};
   const int nk = (K + GT_K - 1) / GT_K;
   uint4 ra[TA::CHUNKS], rb[TB::CHUNKS];
   TA::load(ra, A, m0, 0);
@@ -118,15 +130,15 @@ __device__ __forceinline__ void gemm_mainloop(GemmSmem<AM, BM, TM, TN>& sm, cons
     }
 #pragma unroll
     for (int ks = 0; ks < GT_K / 16; ++ks) {
-      bf16x8 af[MB], bfr[NB];
+      bf16x8 af[C::MB], bfr[C::NB];
 #pragma unroll
-      for (int i = 0; i < MB; ++i) af[i] = TA::frag(sm.a[cur], wm * (TM / 2) + i * 32, ks, lane);
+      for (int i = 0; i < C::MB; ++i) af[i] = TA::frag(sm.a[cur], wm * C::WTM + i * 32, ks, lane);
 #pragma unroll
-      for (int j = 0; j < NB; ++j) bfr[j] = TB::frag(sm.b[cur], wn * (TN / 2) + j * 32, ks, lane);
+      for (int j = 0; j < C::NB; ++j) bfr[j] = TB::frag(sm.b[cur], wn * C::WTN + j * 32, ks, lane);
 #pragma unroll
-      for (int i = 0; i < MB; ++i)
+      for (int i = 0; i < C::MB; ++i)
 #pragma unroll
-        for (int j = 0; j < NB; ++j) acc[i][j] = mfma_bf16(af[i], bfr[j], acc[i][j]);
+        for (int j = 0; j < C::NB; ++j) acc[i][j] = mfma_bf16(af[i], bfr[j], acc[i][j]);
     }
     if (more) {
       TA::store(sm.a[cur ^ 1], ra);

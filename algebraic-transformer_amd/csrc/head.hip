@@ -26,7 +26,8 @@
 
 namespace alg {
 
-typedef WaveTile<HT_M, HT_N> WT;
+typedef HeadGemm HC;
+constexpr int NT = HC::THREADS;
 
 __device__ __forceinline__ float head_w(float z, const HeadParams& p, float& r) {
   const float x = fminf(z * p.inv_c, p.clamp);  // fused_head.py:98
@@ -41,31 +42,32 @@ __global__ void head_zero_kernel(float* p, int n) {
 }
 
 // z^T = E h^T with the forward epilogue (row sums, target logit, optional U residual).
-__global__ __launch_bounds__(256, 1) void head_fwd_kernel(HeadParams p) {
-  __shared__ __attribute__((aligned(16))) GemmSmem<KMAJOR, KMAJOR, HT_M, HT_N> sm;
-  __shared__ float red[2][HT_N];
+__global__ __launch_bounds__(NT, 1) void head_fwd_kernel(HeadParams p) {
+  __shared__ __attribute__((aligned(16))) GemmSmem<KMAJOR, KMAJOR, HC> sm;
+  __shared__ float red[HC::WM][HT_N];
   const int nbm = (p.V + HT_M - 1) / HT_M, nbn = p.Npad / HT_N;
   int tm, tn;
   xcd_tile(blockIdx.x, nbm, nbn, tm, tn);
   const int m0 = tm * HT_M;  // vocab
   const int n0 = tn * HT_N;  // tokens
   GemmOperand A{p.E, p.d, p.V, p.d}, B{p.h, p.d, p.N, p.d};
-  floatx16 acc[WT::MB][WT::NB];
-  gemm_mainloop<KMAJOR, KMAJOR, HT_M, HT_N>(sm, A, B, m0, n0, p.d, acc);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, wm = wave >> 1, wn = wave & 1;
-  const int h = lane >> 5, l32 = lane & 31;
+  floatx16 acc[HC::MB][HC::NB];
+  gemm_mainloop<KMAJOR, KMAJOR, HC>(sm, A, B, m0, n0, p.d, acc);
+  const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  int wm, wn;
+  wave_coords<HC>(wm, wn);
 #pragma unroll
-  for (int nb = 0; nb < WT::NB; ++nb) {
-    const int col = wn * (HT_N / 2) + nb * 32 + l32;
+  for (int nb = 0; nb < HC::NB; ++nb) {
+    const int col = wn * HC::WTN + nb * 32 + l32;
     const int tok = n0 + col;
     const bool live = tok < p.N;
     const int tgt = live ? p.targets[tok] : -1;
     float part = 0.0f;
 #pragma unroll
-    for (int mb = 0; mb < WT::MB; ++mb) {
+    for (int mb = 0; mb < HC::MB; ++mb) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int v = m0 + wm * (HT_M / 2) + mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+        const int v = m0 + wm * HC::WTM + mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
         const float z = acc[mb][nb][i];
         float r;
         const float w = head_w(z, p, r);
@@ -80,9 +82,12 @@ __global__ __launch_bounds__(256, 1) void head_fwd_kernel(HeadParams p) {
     if (h == 0) red[wm][col] = part;
   }
   __syncthreads();
-  for (int t = threadIdx.x; t < HT_N; t += 256) {
+  for (int t = threadIdx.x; t < HT_N; t += NT) {
     const int tok = n0 + t;
-    if (tok < p.N) p.partial[(size_t)tm * p.N + tok] = red[0][t] + red[1][t];
+    float s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < HC::WM; ++w) s += red[w][t];
+    if (tok < p.N) p.partial[(size_t)tm * p.N + tok] = s;
   }
 }
 
@@ -140,29 +145,30 @@ __device__ __forceinline__ float head_grad_scale(const HeadParams& p) {
 }
 
 // Recompute schedule: z^T again, dZ^T = bf16(s (p - y) r).
-__global__ __launch_bounds__(256, 1) void head_dz_kernel(HeadParams p) {
-  __shared__ __attribute__((aligned(16))) GemmSmem<KMAJOR, KMAJOR, HT_M, HT_N> sm;
+__global__ __launch_bounds__(NT, 1) void head_dz_kernel(HeadParams p) {
+  __shared__ __attribute__((aligned(16))) GemmSmem<KMAJOR, KMAJOR, HC> sm;
   const int nbm = (p.V + HT_M - 1) / HT_M, nbn = p.Npad / HT_N;
   int tm, tn;
   xcd_tile(blockIdx.x, nbm, nbn, tm, tn);
   const int m0 = tm * HT_M, n0 = tn * HT_N;
   GemmOperand A{p.E, p.d, p.V, p.d}, B{p.h, p.d, p.N, p.d};
-  floatx16 acc[WT::MB][WT::NB];
-  gemm_mainloop<KMAJOR, KMAJOR, HT_M, HT_N>(sm, A, B, m0, n0, p.d, acc);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, wm = wave >> 1, wn = wave & 1;
-  const int h = lane >> 5, l32 = lane & 31;
+  floatx16 acc[HC::MB][HC::NB];
+  gemm_mainloop<KMAJOR, KMAJOR, HC>(sm, A, B, m0, n0, p.d, acc);
+  const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  int wm, wn;
+  wave_coords<HC>(wm, wn);
   const float scale = head_grad_scale(p);
 #pragma unroll
-  for (int nb = 0; nb < WT::NB; ++nb) {
-    const int tok = n0 + wn * (HT_N / 2) + nb * 32 + l32;
+  for (int nb = 0; nb < HC::NB; ++nb) {
+    const int tok = n0 + wn * HC::WTN + nb * 32 + l32;
     const bool live = tok < p.N;
     const int tgt = live ? p.targets[tok] : -1;
     const float st = live ? p.stat[tok] : 0.0f;
 #pragma unroll
-    for (int mb = 0; mb < WT::MB; ++mb) {
+    for (int mb = 0; mb < HC::MB; ++mb) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int v = m0 + wm * (HT_M / 2) + mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+        const int v = m0 + wm * HC::WTM + mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
         if (v >= p.V) continue;
         const float x = fminf(acc[mb][nb][i] * p.inv_c, p.clamp);
         float r;
@@ -193,8 +199,8 @@ __global__ __launch_bounds__(256) void head_hscale_kernel(HeadParams p) {
 
 // dh = (U' or dZ) E: A stored [v][n] (m-contiguous), B = E stored [v][d] (n-contiguous).
 // The residual schedule scales token rows by s/l.
-__global__ __launch_bounds__(256, 1) void head_dh_kernel(HeadParams p) {
-  __shared__ __attribute__((aligned(16))) GemmSmem<MNMAJOR, MNMAJOR, HT_M, HT_N> sm;
+__global__ __launch_bounds__(NT, 1) void head_dh_kernel(HeadParams p) {
+  __shared__ __attribute__((aligned(16))) GemmSmem<MNMAJOR, MNMAJOR, HC> sm;
   const int nbm = p.Npad / HT_M, nbn = (p.d + HT_N - 1) / HT_N;
   int tm, tn;
   xcd_tile(blockIdx.x, nbm, nbn, tm, tn);
@@ -202,21 +208,22 @@ __global__ __launch_bounds__(256, 1) void head_dh_kernel(HeadParams p) {
   const int n0 = tn * HT_N;  // d
   const bf16* a = p.ut ? p.ut : p.dzt;
   GemmOperand A{a, p.Npad, p.V, p.Npad}, B{p.E, p.d, p.V, p.d};
-  floatx16 acc[WT::MB][WT::NB];
-  gemm_mainloop<MNMAJOR, MNMAJOR, HT_M, HT_N>(sm, A, B, m0, n0, p.V, acc);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, wm = wave >> 1, wn = wave & 1;
-  const int h = lane >> 5, l32 = lane & 31;
+  floatx16 acc[HC::MB][HC::NB];
+  gemm_mainloop<MNMAJOR, MNMAJOR, HC>(sm, A, B, m0, n0, p.V, acc);
+  const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  int wm, wn;
+  wave_coords<HC>(wm, wn);
   const float s = p.ut ? head_grad_scale(p) : 1.0f;
 #pragma unroll
-  for (int mb = 0; mb < WT::MB; ++mb) {
+  for (int mb = 0; mb < HC::MB; ++mb) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int tok = m0 + wm * (HT_M / 2) + mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+      const int tok = m0 + wm * HC::WTM + mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
       if (tok >= p.N) continue;
       const float f = p.ut ? s / p.lsum[tok] : 1.0f;
 #pragma unroll
-      for (int nb = 0; nb < WT::NB; ++nb) {
-        const int col = n0 + wn * (HT_N / 2) + nb * 32 + l32;
+      for (int nb = 0; nb < HC::NB; ++nb) {
+        const int col = n0 + wn * HC::WTN + nb * 32 + l32;
         if (col < p.d) p.dh[(size_t)tok * p.d + col] = f2bf(acc[mb][nb][i] * f);
       }
     }
@@ -224,8 +231,8 @@ __global__ __launch_bounds__(256, 1) void head_dh_kernel(HeadParams p) {
 }
 
 // dE = (U' or dZ)^T (hs or h): A stored [v][n] (k-contiguous), B stored [n][d] (n-contiguous).
-__global__ __launch_bounds__(256, 1) void head_de_kernel(HeadParams p) {
-  __shared__ __attribute__((aligned(16))) GemmSmem<KMAJOR, MNMAJOR, HT_M, HT_N> sm;
+__global__ __launch_bounds__(NT, 1) void head_de_kernel(HeadParams p) {
+  __shared__ __attribute__((aligned(16))) GemmSmem<KMAJOR, MNMAJOR, HC> sm;
   const int nbm = (p.V + HT_M - 1) / HT_M, nbn = (p.d + HT_N - 1) / HT_N;
   int tm, tn;
   xcd_tile(blockIdx.x, nbm, nbn, tm, tn);
@@ -234,19 +241,20 @@ __global__ __launch_bounds__(256, 1) void head_de_kernel(HeadParams p) {
   const bf16* a = p.ut ? p.ut : p.dzt;
   const bf16* b = p.ut ? p.hs : p.h;
   GemmOperand A{a, p.Npad, p.V, p.Npad}, B{b, p.d, p.N, p.d};
-  floatx16 acc[WT::MB][WT::NB];
-  gemm_mainloop<KMAJOR, MNMAJOR, HT_M, HT_N>(sm, A, B, m0, n0, p.N, acc);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, wm = wave >> 1, wn = wave & 1;
-  const int h = lane >> 5, l32 = lane & 31;
+  floatx16 acc[HC::MB][HC::NB];
+  gemm_mainloop<KMAJOR, MNMAJOR, HC>(sm, A, B, m0, n0, p.N, acc);
+  const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  int wm, wn;
+  wave_coords<HC>(wm, wn);
 #pragma unroll
-  for (int mb = 0; mb < WT::MB; ++mb) {
+  for (int mb = 0; mb < HC::MB; ++mb) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int v = m0 + wm * (HT_M / 2) + mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+      const int v = m0 + wm * HC::WTM + mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
       if (v >= p.V) continue;
 #pragma unroll
-      for (int nb = 0; nb < WT::NB; ++nb) {
-        const int col = n0 + wn * (HT_N / 2) + nb * 32 + l32;
+      for (int nb = 0; nb < HC::NB; ++nb) {
+        const int col = n0 + wn * HC::WTN + nb * 32 + l32;
         if (col >= p.d) continue;
         const size_t o = (size_t)v * p.d + col;
         if (p.dE_f32) reinterpret_cast<float*>(p.dE)[o] = acc[mb][nb][i];
@@ -263,7 +271,7 @@ int head_stat_blocks(int N) { return (N + 255) / 256; }
 hipError_t launch_head_fwd(const HeadParams& p, hipStream_t st) {
   { KTimer t("head_zero", st); hipLaunchKernelGGL(head_zero_kernel, dim3((p.N + 255) / 256), dim3(256), 0, st, p.zt, p.N); }
   const int tiles = head_vocab_tiles(p.V) * (p.Npad / HT_N);
-  { KTimer t("head_fwd", st); hipLaunchKernelGGL(head_fwd_kernel, dim3(tiles), dim3(256), 0, st, p); }
+  { KTimer t("head_fwd", st); hipLaunchKernelGGL(head_fwd_kernel, dim3(tiles), dim3(NT), 0, st, p); }
   const int nb = head_stat_blocks(p.N);
   { KTimer t("head_stats", st); hipLaunchKernelGGL(head_stats_kernel, dim3(nb), dim3(256), 0, st, p, head_vocab_tiles(p.V)); }
   { KTimer t("head_obj", st); hipLaunchKernelGGL(head_obj_kernel, dim3(1), dim3(256), 0, st, p, nb); }
@@ -277,11 +285,11 @@ hipError_t launch_head_bwd(const HeadParams& p, hipStream_t st) {
     { KTimer t("head_hscale", st); hipLaunchKernelGGL(head_hscale_kernel, dim3(blocks), dim3(256), 0, st, p); }
   } else {
     const int tiles = head_vocab_tiles(p.V) * (p.Npad / HT_N);
-    { KTimer t("head_dz", st); hipLaunchKernelGGL(head_dz_kernel, dim3(tiles), dim3(256), 0, st, p); }
+    { KTimer t("head_dz", st); hipLaunchKernelGGL(head_dz_kernel, dim3(tiles), dim3(NT), 0, st, p); }
   }
   const int dtiles = (p.d + HT_N - 1) / HT_N;
-  { KTimer t("head_dh", st); hipLaunchKernelGGL(head_dh_kernel, dim3((p.Npad / HT_M) * dtiles), dim3(256), 0, st, p); }
-  { KTimer t("head_de", st); hipLaunchKernelGGL(head_de_kernel, dim3(head_vocab_tiles(p.V) * dtiles), dim3(256), 0, st, p); }
+  { KTimer t("head_dh", st); hipLaunchKernelGGL(head_dh_kernel, dim3((p.Npad / HT_M) * dtiles), dim3(NT), 0, st, p); }
+  { KTimer t("head_de", st); hipLaunchKernelGGL(head_de_kernel, dim3(head_vocab_tiles(p.V) * dtiles), dim3(NT), 0, st, p); }
   return hipGetLastError();
 }
 

@@ -3,10 +3,14 @@
 
 #include "common.h"
 #include "ktimer.h"
+#include "gemm_core.h"
 
 namespace alg {
 
 constexpr int HT_M = 256, HT_N = 256;  // head GEMM workgroup tile
+#ifndef ALG_HEAD_WN
+#define ALG_HEAD_WN 4                  // waves along the tile's n dimension (x 2 along m)
+#endif
 
 struct HeadParams {
   const bf16* h;        // (N, d)
@@ -30,5 +34,7 @@ struct HeadParams {
   void* dE;             // (V, d) bf16 or f32
   int dE_f32;
 };
+
+typedef GemmCfg<HT_M, HT_N, 2, ALG_HEAD_WN> HeadGemm;
 
 }  // namespace alg
