@@ -47,24 +47,53 @@ __global__ __launch_bounds__(256) void attn_bwd_pre_kernel(AttnBwdParams p, int 
   const bool inv_stat = !shifted && (p.mode != MODE_CLIPPED || p.inv_stat);
   const float rbn = ipow_rt(rb, n);
   float part = 0.0f;
-  for (int r = row0 + wave; r < min(row0 + PRE_ROWS, T_); r += 4) {
-    const size_t off = ((size_t)bh * T_ + r) * D;
-    const T* dO = reinterpret_cast<const T*>(p.dO) + off;
+  // 8 elements per lane, D/8 lanes per row (vector loads of dO, o; vector zero-fill of dq_acc).
+  const int lpr = D / 8, rpw = 64 / lpr;
+  const int sub = lane / lpr, li = lane - sub * lpr;
+  const int rend = min(row0 + PRE_ROWS, T_);
+  for (int r0 = row0 + wave * rpw; r0 < rend; r0 += 4 * rpw) {
+    const int r = r0 + sub;
+    const bool ok = r < rend;
     float s = 0.0f;
-    for (int d = lane; d < D; d += 64) {
-      const float o = precise ? p.o_precise[off + d] : (float)reinterpret_cast<const T*>(p.o)[off + d];
-      s += (float)dO[d] * o;
-      p.dq_acc[off + d] = 0.0f;
-    }
+    if (ok) {
+      const size_t off = ((size_t)bh * T_ + r) * D + li * 8;
+      float dov[8], ov[8];
+      if constexpr (sizeof(T) == 2) {
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p.dO) + off);
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
-    if (lane == 0) {
+        for (int j = 0; j < 8; ++j) dov[j] = (float)a[j];
+      } else {
+        const floatx4 a0 = *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(p.dO) + off);
+        const floatx4 a1 = *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(p.dO) + off + 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { dov[j] = a0[j]; dov[4 + j] = a1[j]; }
+      }
+      if (precise || sizeof(T) == 4) {
+        const float* src = precise ? p.o_precise + off : reinterpret_cast<const float*>(p.o) + off;
+        const floatx4 b0 = *reinterpret_cast<const floatx4*>(src);
+        const floatx4 b1 = *reinterpret_cast<const floatx4*>(src + 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { ov[j] = b0[j]; ov[4 + j] = b1[j]; }
+      } else {
+        const bf16x8 b = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p.o) + off);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ov[j] = (float)b[j];
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s += dov[j] * ov[j];
+      const floatx4 z = {};
+      *reinterpret_cast<floatx4*>(p.dq_acc + off) = z;
+      *reinterpret_cast<floatx4*>(p.dq_acc + off + 4) = z;
+    }
+    for (int m = 1; m < lpr; m <<= 1) s += __shfl_xor(s, m, 64);
+    if (ok && li == 0) {
       p.di[(size_t)bh * T_ + r] = s;
       const float st = p.stat[(size_t)bh * T_ + r];
       const float mass = inv_stat ? rbn * st : ipow_rt(rb * st, n);
       part += mass * s;
     }
   }
+  for (int m = 1; m < 64; m <<= 1) part += __shfl_xor(part, m, 64);
   __shared__ float red[4];
   if (lane == 0) red[wave] = part;
   __syncthreads();
@@ -74,17 +103,32 @@ __global__ __launch_bounds__(256) void attn_bwd_pre_kernel(AttnBwdParams p, int 
 // ---------------------------------------------------------------------------
 // main
 // ---------------------------------------------------------------------------
-template <typename T>
-__device__ __forceinline__ void load_tile(T* dst, int pitch, const T* src, int r0, int nrows, int T_, int D) {
-  constexpr int CH = 16 / sizeof(T);
-  const int cpr = D / CH;
-  for (int c = threadIdx.x; c < nrows * cpr; c += blockDim.x) {
-    const int row = c / cpr, col = (c - row * cpr) * CH;
-    uint4 val = make_uint4(0, 0, 0, 0);
-    if (r0 + row < T_) val = *reinterpret_cast<const uint4*>(src + (size_t)(r0 + row) * D + col);
-    *reinterpret_cast<uint4*>(dst + row * pitch + col) = val;
+// Registers <-> LDS staging of an R-row tile of a (T, D) matrix (16-byte chunks; rows >= T
+// read as zero).
+template <typename T, int D, int R>
+struct RowTile {
+  static constexpr int CH = 16 / sizeof(T);
+  static constexpr int CPR = D / CH;
+  static constexpr int PER = (R * CPR + 255) / 256;  // chunks per thread
+  static __device__ __forceinline__ void load(uint4 (&r)[PER], const T* src, int r0, int T_) {
+#pragma unroll
+    for (int c = 0; c < PER; ++c) {
+      const int idx = threadIdx.x + c * 256;
+      const int row = idx / CPR, col = (idx - row * CPR) * CH;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (row < R && r0 + row < T_) v = *reinterpret_cast<const uint4*>(src + (size_t)(r0 + row) * D + col);
+      r[c] = v;
+    }
   }
-}
+  static __device__ __forceinline__ void store(T* dst, int pitch, const uint4 (&r)[PER]) {
+#pragma unroll
+    for (int c = 0; c < PER; ++c) {
+      const int idx = threadIdx.x + c * 256;
+      const int row = idx / CPR, col = (idx - row * CPR) * CH;
+      if (row < R) *reinterpret_cast<uint4*>(dst + row * pitch + col) = r[c];
+    }
+  }
+};
 
 template <typename T, int D, int MODE>
 __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
@@ -121,7 +165,12 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
   const int mykey = wk0 + l32;
   const int log2n = p.log2n;
 
-  load_tile<T>(Ks, PITCH, K, k0, BWD_BK, T_, D);
+  {
+    typedef RowTile<T, D, BWD_BK> KT;
+    uint4 kr[KT::PER];
+    KT::load(kr, K, k0, T_);
+    KT::store(Ks, PITCH, kr);
+  }
 
   // K and V fragments as B operands of S = Q K^T and dP = dO V^T.
   constexpr int NF = BF ? D / 16 : D / 8;
@@ -147,17 +196,32 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
 
   const int nq = ceil_div(T_, BWD_BQ);
   const int qstart = k0 / BWD_BQ;
-  for (int qt = qstart; qt < nq; ++qt) {
-    const int qbase = qt * BWD_BQ;
-    __syncthreads();
-    load_tile<T>(Qs, PITCH, Q, qbase, BWD_BQ, T_, D);
-    load_tile<T>(dOs, PITCH, dO, qbase, BWD_BQ, T_, D);
+  // Q/dO/stat/di tiles are prefetched into registers one iteration ahead and written to
+  // LDS between the dS barrier and the dQ phase (which reads only dS and K).
+  typedef RowTile<T, D, BWD_BQ> QT;
+  uint4 qr[QT::PER], dr[QT::PER];
+  float str = 0.0f, dir = 0.0f;
+  auto prefetch = [&](int qbase) {
+    QT::load(qr, Q, qbase, T_);
+    QT::load(dr, dO, qbase, T_);
     if (threadIdx.x < BWD_BQ) {
       const int q = qbase + threadIdx.x;
-      st_s[threadIdx.x] = q < T_ ? stat[q] : 0.0f;
-      di_s[threadIdx.x] = q < T_ ? di[q] : 0.0f;
+      str = q < T_ ? stat[q] : 0.0f;
+      dir = q < T_ ? di[q] : 0.0f;
     }
-    __syncthreads();
+  };
+  auto commit = [&]() {
+    QT::store(Qs, PITCH, qr);
+    QT::store(dOs, PITCH, dr);
+    if (threadIdx.x < BWD_BQ) { st_s[threadIdx.x] = str; di_s[threadIdx.x] = dir; }
+  };
+  prefetch(qstart * BWD_BQ);
+  commit();
+  __syncthreads();
+  for (int qt = qstart; qt < nq; ++qt) {
+    const int qbase = qt * BWD_BQ;
+    const bool more = qt + 1 < nq;
+    if (more) prefetch(qbase + BWD_BQ);
 #pragma unroll
     for (int sub = 0; sub < BWD_BQ / 32; ++sub) {
       const int sq0 = qbase + sub * 32;
@@ -285,6 +349,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
       }
     }
     __syncthreads();
+    if (more) commit();
     // dQ tile = dS K over this workgroup's keys; each wave takes 32 queries x DBW blocks.
     {
       constexpr int NQH = BWD_BQ / 32;         // 32-query slices of the tile
@@ -332,6 +397,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
         }
       }
     }
+    __syncthreads();
   }
 
   // dK = n * acc, dV = acc (flash.py:591-597), rounded to the input dtype.
