@@ -130,13 +130,13 @@ struct RowTile {
   }
 };
 
-template <typename T, int D, int MODE>
+template <typename T, int D, int MODE, int L2N>
 __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
   static_assert(D == 64 || D == 128, "head_dim");
   constexpr bool BF = sizeof(T) == 2;
-  constexpr int PITCH = D + (BF ? 8 : 4);
+  constexpr int PITCH = D + (BF ? ALG_BWD_PAD : 4);
   constexpr int BWD_BQ = bwd_bq<T, D>();
-  constexpr int SPITCH = BWD_BQ + (BF ? 8 : 4);
+  constexpr int SPITCH = BWD_BQ + (BF ? ALG_BWD_SPAD : 4);
   constexpr int NDB = D / 32;
   __shared__ __attribute__((aligned(16))) T Ks[BWD_BK * PITCH];
   __shared__ __attribute__((aligned(16))) T Qs[BWD_BQ * PITCH];
@@ -222,129 +222,136 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
     const int qbase = qt * BWD_BQ;
     const bool more = qt + 1 < nq;
     if (more) prefetch(qbase + BWD_BQ);
-#pragma unroll
-    for (int sub = 0; sub < BWD_BQ / 32; ++sub) {
+    // One 32-query block against this wave's 32 keys: S, dP, P, dS, dV += P^T dO,
+    // dK += dS^T Q, dS staged in LDS for the dQ phase.
+    auto sub_block = [&](int sub, bool diag) {
       const int sq0 = qbase + sub * 32;
       T* dsrow = dSs + (wave * 32 + l32) * SPITCH + sub * 32;
-      if (sq0 + 31 < wk0 || wk0 >= T_) {  // all queries precede all keys of this wave
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          if constexpr (BF) { bf16x4 z = {}; *reinterpret_cast<bf16x4*>(dsrow + 8 * g + 4 * h) = z; }
-          else { floatx4 z = {}; *reinterpret_cast<floatx4*>(dsrow + 8 * g + 4 * h) = z; }
-        }
-        continue;
-      }
-      const T* qrow = Qs + (sub * 32 + l32) * PITCH;
-      const T* dorow = dOs + (sub * 32 + l32) * PITCH;
-      floatx16 s = {}, dp = {};
-#pragma unroll
-      for (int st = 0; st < NF; ++st) {
-        if constexpr (BF) {
-          bf16x8 qa = *reinterpret_cast<const bf16x8*>(qrow + 16 * st + 8 * h);
-          s = mfma_bf16(qa, kf[st], s);
-          bf16x8 da = *reinterpret_cast<const bf16x8*>(dorow + 16 * st + 8 * h);
-          dp = mfma_bf16(da, vf[st], dp);
-        } else {
-          floatx4 qa = *reinterpret_cast<const floatx4*>(qrow + 8 * st + 4 * h);
-          floatx4 da = *reinterpret_cast<const floatx4*>(dorow + 8 * st + 4 * h);
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            s = mfma_f32(qa[u], kf[st][u], s);
-            dp = mfma_f32(da[u], vf[st][u], dp);
-          }
-        }
-      }
-      const bool diag = wk0 + 31 > sq0;
-      float pv[16], dsv[16];
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const floatx4 stq = *reinterpret_cast<const floatx4*>(st_s + sub * 32 + 8 * g + 4 * h);
-        const floatx4 diq = *reinterpret_cast<const floatx4*>(di_s + sub * 32 + 8 * g + 4 * h);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int i = 4 * g + e;
-          float x = s[i];
-          float r, pw;
-          if constexpr (MODE == MODE_INRANGE) {
-            float t = rho_fast(x, r);
-            for (int k2 = 0; k2 < log2n; ++k2) t = t * t;
-            pw = t * stq[e];
-          } else if constexpr (MODE == MODE_CLIPPED) {
-            x = fminf(x, p.clamp);
-            float t = rho_fast(x, r);
-            if (p.inv_stat) {
-              for (int k2 = 0; k2 < log2n; ++k2) t = t * t;
-              pw = t * stq[e];
-            } else {
-              t = t * stq[e];
-              for (int k2 = 0; k2 < log2n; ++k2) t = t * t;
-              pw = t;
-            }
+        const T* qrow = Qs + (sub * 32 + l32) * PITCH;
+        const T* dorow = dOs + (sub * 32 + l32) * PITCH;
+        floatx16 s = {}, dp = {};
+  #pragma unroll
+        for (int st = 0; st < NF; ++st) {
+          if constexpr (BF) {
+            bf16x8 qa = *reinterpret_cast<const bf16x8*>(qrow + 16 * st + 8 * h);
+            s = mfma_bf16(qa, kf[st], s);
+            bf16x8 da = *reinterpret_cast<const bf16x8*>(dorow + 16 * st + 8 * h);
+            dp = mfma_bf16(da, vf[st], dp);
           } else {
-            const int q = sq0 + 8 * g + 4 * h + e;
-            if (diag && mykey > q) x = 0.0f;
-            float t = p.fast_rho ? rho_fast(x, r) : rho_exact(x, r);
-            t = t * stq[e];
-            for (int k2 = 0; k2 < log2n; ++k2) t = t * t;
-            pw = t;
+            floatx4 qa = *reinterpret_cast<const floatx4*>(qrow + 8 * st + 4 * h);
+            floatx4 da = *reinterpret_cast<const floatx4*>(dorow + 8 * st + 4 * h);
+  #pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              s = mfma_f32(qa[u], kf[st][u], s);
+              dp = mfma_f32(da[u], vf[st][u], dp);
+            }
           }
-          float dsx = pw * (dp[i] - diq[e]) * r;
-          if constexpr (MODE == MODE_CLIPPED) dsx = s[i] < p.clamp ? dsx : 0.0f;
-          if (diag) {
-            const int q = sq0 + 8 * g + 4 * h + e;
-            if (mykey > q) { pw = 0.0f; dsx = 0.0f; }
-          }
-          pv[i] = pw;
-          dsv[i] = dsx;
         }
-      }
-      if constexpr (BF) {
-        bf16x8 pa0, pa1, da0, da1;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          pa0[j] = f2bf(pv[j]); pa1[j] = f2bf(pv[8 + j]);
-          da0[j] = f2bf(dsv[j]); da1[j] = f2bf(dsv[8 + j]);
-        }
-        const bf16* qt_ = reinterpret_cast<const bf16*>(Qs);
-        const bf16* dot_ = reinterpret_cast<const bf16*>(dOs);
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          const int r0 = sub * 32 + 4 * h;
-          bf16x8 ob0 = lds_tr_frag(dot_, PITCH, r0, r0 + 8, db * 32, lane);
-          bf16x8 ob1 = lds_tr_frag(dot_, PITCH, r0 + 16, r0 + 24, db * 32, lane);
-          dv[db] = mfma_bf16(pa0, ob0, dv[db]);
-          dv[db] = mfma_bf16(pa1, ob1, dv[db]);
-          bf16x8 qb0 = lds_tr_frag(qt_, PITCH, r0, r0 + 8, db * 32, lane);
-          bf16x8 qb1 = lds_tr_frag(qt_, PITCH, r0 + 16, r0 + 24, db * 32, lane);
-          dk[db] = mfma_bf16(da0, qb0, dk[db]);
-          dk[db] = mfma_bf16(da1, qb1, dk[db]);
-        }
-        // Stage dS (rounded, as the dq/dk operands are) in LDS as [key][query].
-#pragma unroll
+        float pv[16], dsv[16];
+  #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          bf16x4 v4;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v4[e] = f2bf(dsv[4 * g + e]);
-          *reinterpret_cast<bf16x4*>(dsrow + 8 * g + 4 * h) = v4;
-        }
-      } else {
-        const float* qt_ = reinterpret_cast<const float*>(Qs);
-        const float* dot_ = reinterpret_cast<const float*>(dOs);
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int qr = sub * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-            dv[db] = mfma_f32(pv[i], dot_[qr * PITCH + db * 32 + l32], dv[db]);
-            dk[db] = mfma_f32(dsv[i], qt_[qr * PITCH + db * 32 + l32], dk[db]);
+          const floatx4 stq = *reinterpret_cast<const floatx4*>(st_s + sub * 32 + 8 * g + 4 * h);
+          const floatx4 diq = *reinterpret_cast<const floatx4*>(di_s + sub * 32 + 8 * g + 4 * h);
+  #pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int i = 4 * g + e;
+            float x = s[i];
+            float r, pw;
+            if constexpr (MODE == MODE_INRANGE) {
+              pw = pow2n<L2N>(rho_fast(x, r), log2n) * stq[e];
+            } else if constexpr (MODE == MODE_CLIPPED) {
+              x = fminf(x, p.clamp);
+              float t = rho_fast(x, r);
+              if (p.inv_stat) {
+                for (int k2 = 0; k2 < log2n; ++k2) t = t * t;
+                pw = t * stq[e];
+              } else {
+                t = t * stq[e];
+                for (int k2 = 0; k2 < log2n; ++k2) t = t * t;
+                pw = t;
+              }
+            } else {
+              const int q = sq0 + 8 * g + 4 * h + e;
+              if (diag && mykey > q) x = 0.0f;
+              const float t = p.fast_rho ? rho_fast(x, r) : rho_exact(x, r);
+              pw = pow2n<L2N>(t * stq[e], log2n);
+            }
+            float dsx = pw * (dp[i] - diq[e]) * r;
+            if constexpr (MODE == MODE_CLIPPED) dsx = s[i] < p.clamp ? dsx : 0.0f;
+            if (diag) {
+              const int q = sq0 + 8 * g + 4 * h + e;
+              if (mykey > q) { pw = 0.0f; dsx = 0.0f; }
+            }
+            pv[i] = pw;
+            dsv[i] = dsx;
           }
         }
+        if constexpr (BF) {
+          bf16x8 pa0, pa1, da0, da1;
+  #pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            pa0[j] = f2bf(pv[j]); pa1[j] = f2bf(pv[8 + j]);
+            da0[j] = f2bf(dsv[j]); da1[j] = f2bf(dsv[8 + j]);
+          }
+          const bf16* qt_ = reinterpret_cast<const bf16*>(Qs);
+          const bf16* dot_ = reinterpret_cast<const bf16*>(dOs);
+  #pragma unroll
+          for (int db = 0; db < NDB; ++db) {
+            const int r0 = sub * 32 + 4 * h;
+            bf16x8 ob0 = lds_tr_frag(dot_, PITCH, r0, r0 + 8, db * 32, lane);
+            bf16x8 ob1 = lds_tr_frag(dot_, PITCH, r0 + 16, r0 + 24, db * 32, lane);
+            dv[db] = mfma_bf16(pa0, ob0, dv[db]);
+            dv[db] = mfma_bf16(pa1, ob1, dv[db]);
+            bf16x8 qb0 = lds_tr_frag(qt_, PITCH, r0, r0 + 8, db * 32, lane);
+            bf16x8 qb1 = lds_tr_frag(qt_, PITCH, r0 + 16, r0 + 24, db * 32, lane);
+            dk[db] = mfma_bf16(da0, qb0, dk[db]);
+            dk[db] = mfma_bf16(da1, qb1, dk[db]);
+          }
+          // Stage dS (rounded, as the dq/dk operands are) in LDS as [key][query].
+  #pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            bf16x4 v4;
+  #pragma unroll
+            for (int e = 0; e < 4; ++e) v4[e] = f2bf(dsv[4 * g + e]);
+            *reinterpret_cast<bf16x4*>(dsrow + 8 * g + 4 * h) = v4;
+          }
+        } else {
+          const float* qt_ = reinterpret_cast<const float*>(Qs);
+          const float* dot_ = reinterpret_cast<const float*>(dOs);
+  #pragma unroll
+          for (int db = 0; db < NDB; ++db) {
+  #pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const int qr = sub * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+              dv[db] = mfma_f32(pv[i], dot_[qr * PITCH + db * 32 + l32], dv[db]);
+              dk[db] = mfma_f32(dsv[i], qt_[qr * PITCH + db * 32 + l32], dk[db]);
+            }
+          }
+  #pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            floatx4 v4;
+  #pragma unroll
+            for (int e = 0; e < 4; ++e) v4[e] = dsv[4 * g + e];
+            *reinterpret_cast<floatx4*>(dsrow + 8 * g + 4 * h) = v4;
+          }
+        }
+    };
+    if (wk0 < T_ && qbase >= wk0 + 31) {  // every query follows every key: no masking
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          floatx4 v4;
+      for (int sub = 0; sub < BWD_BQ / 32; ++sub) sub_block(sub, false);
+    } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v4[e] = dsv[4 * g + e];
-          *reinterpret_cast<floatx4*>(dsrow + 8 * g + 4 * h) = v4;
+      for (int sub = 0; sub < BWD_BQ / 32; ++sub) {
+        const int sq0 = qbase + sub * 32;
+        if (sq0 + 31 < wk0 || wk0 >= T_) {  // all queries precede all keys of this wave
+          T* dsrow = dSs + (wave * 32 + l32) * SPITCH + sub * 32;
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            if constexpr (BF) { bf16x4 z = {}; *reinterpret_cast<bf16x4*>(dsrow + 8 * g + 4 * h) = z; }
+            else { floatx4 z = {}; *reinterpret_cast<floatx4*>(dsrow + 8 * g + 4 * h) = z; }
+          }
+        } else {
+          sub_block(sub, wk0 + 31 > sq0);
         }
       }
     }
@@ -364,16 +371,24 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
       if constexpr (BF) {
         const bf16* ds_ = reinterpret_cast<const bf16*>(dSs);
         const bf16* k_ = reinterpret_cast<const bf16*>(Ks);
+        floatx16 dqb[DBW];  // second accumulator chain (odd k steps)
 #pragma unroll
-        for (int ks = 0; ks < BWD_BK / 16; ++ks) {
+        for (int j = 0; j < DBW; ++j) dqb[j] = floatx16{};
+#pragma unroll
+        for (int ks = 0; ks < BWD_BK / 16; ks += 2) {
           const int klo = ks * 16 + 8 * h;
-          bf16x8 a = lds_tr_frag(ds_, SPITCH, klo, klo + 4, qs * 32, lane);
+          bf16x8 a0 = lds_tr_frag(ds_, SPITCH, klo, klo + 4, qs * 32, lane);
+          bf16x8 a1 = lds_tr_frag(ds_, SPITCH, klo + 16, klo + 20, qs * 32, lane);
 #pragma unroll
           for (int j = 0; j < DBW; ++j) {
-            bf16x8 bk = lds_tr_frag(k_, PITCH, klo, klo + 4, (db0 + j) * 32, lane);
-            dqa[j] = mfma_bf16(a, bk, dqa[j]);
+            bf16x8 b0 = lds_tr_frag(k_, PITCH, klo, klo + 4, (db0 + j) * 32, lane);
+            bf16x8 b1 = lds_tr_frag(k_, PITCH, klo + 16, klo + 20, (db0 + j) * 32, lane);
+            dqa[j] = mfma_bf16(a0, b0, dqa[j]);
+            dqb[j] = mfma_bf16(a1, b1, dqb[j]);
           }
         }
+#pragma unroll
+        for (int j = 0; j < DBW; ++j) dqa[j] += dqb[j];
       } else {
         const float* ds_ = reinterpret_cast<const float*>(dSs);
         const float* k_ = reinterpret_cast<const float*>(Ks);
@@ -452,9 +467,13 @@ template <typename T, int D>
 static hipError_t launch_bwd_main(const AttnBwdParams& p, int mode, hipStream_t st) {
   dim3 grid(p.B * p.H, ceil_div(p.T, BWD_BK)), block(256);
   switch (mode) {
-    case MODE_INRANGE: { KTimer t("attn_bwd_inrange", st); hipLaunchKernelGGL((attn_bwd_kernel<T, D, MODE_INRANGE>), grid, block, 0, st, p); } break;
-    case MODE_CLIPPED: { KTimer t("attn_bwd_clipped", st); hipLaunchKernelGGL((attn_bwd_kernel<T, D, MODE_CLIPPED>), grid, block, 0, st, p); } break;
-    case MODE_SHIFTED: { KTimer t("attn_bwd_shifted", st); hipLaunchKernelGGL((attn_bwd_kernel<T, D, MODE_SHIFTED>), grid, block, 0, st, p); } break;
+    case MODE_INRANGE: {
+      KTimer t("attn_bwd_inrange", st);
+      if (p.log2n == 4) hipLaunchKernelGGL((attn_bwd_kernel<T, D, MODE_INRANGE, 4>), grid, block, 0, st, p);
+      else hipLaunchKernelGGL((attn_bwd_kernel<T, D, MODE_INRANGE, 0>), grid, block, 0, st, p);
+    } break;
+    case MODE_CLIPPED: { KTimer t("attn_bwd_clipped", st); hipLaunchKernelGGL((attn_bwd_kernel<T, D, MODE_CLIPPED, 0>), grid, block, 0, st, p); } break;
+    case MODE_SHIFTED: { KTimer t("attn_bwd_shifted", st); hipLaunchKernelGGL((attn_bwd_kernel<T, D, MODE_SHIFTED, 0>), grid, block, 0, st, p); } break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

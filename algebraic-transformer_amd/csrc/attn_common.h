@@ -56,4 +56,16 @@ struct AttnBwdParams {
 
 __host__ __device__ inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
+// LDS row padding (elements) of the bf16 tiles: row pitch = width + pad, chosen against
+// bank conflicts of the row-fragment and transposed (ds_read_b64_tr_b16) reads.
+#ifndef ALG_FWD_PAD
+#define ALG_FWD_PAD 8
+#endif
+#ifndef ALG_BWD_PAD
+#define ALG_BWD_PAD 8
+#endif
+#ifndef ALG_BWD_SPAD
+#define ALG_BWD_SPAD 8
+#endif
+
 }  // namespace alg

@@ -57,11 +57,11 @@ struct KVTile {
   }
 };
 
-template <typename T, int D, int MODE>
+template <typename T, int D, int MODE, int L2N>
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
   static_assert(D == 64 || D == 128, "head_dim");
   constexpr bool BF = sizeof(T) == 2;
-  constexpr int PITCH = D + (BF ? 8 : 4);
+  constexpr int PITCH = D + (BF ? ALG_FWD_PAD : 4);
   constexpr int NDB = D / 32;  // 32-wide d blocks of the O^T accumulator
   typedef KVTile<T, D> KV;
   __shared__ __attribute__((aligned(16))) T Ks[2][FWD_BK * PITCH];
@@ -134,14 +134,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
       for (int i = 0; i < 16; ++i) {
         float x = s[i];
         if constexpr (MODE == MODE_CLIPPED) x = fminf(x, p.clamp);
-        float t = rho_fast(x);
-        if constexpr (MODE == MODE_INRANGE) {
-          t = ipow<16>(t);
-          if (log2n != 4) { t = rho_fast(x); for (int e = 0; e < log2n; ++e) t = t * t; }
-        } else {
-          for (int e = 0; e < log2n; ++e) t = t * t;
-        }
-        w[i] = t;
+        w[i] = pow2n<L2N>(rho_fast(x), log2n);
       }
       if (diag) {
 #pragma unroll
@@ -172,8 +165,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
         const bool valid = !diag || key <= myq;
         const float x = valid ? s[i] : 0.0f;
         const float r0 = p.fast_rho ? rho_fast(x) : rho_exact(x);
-        float t = r0 * shift;
-        for (int e = 0; e < log2n; ++e) t = t * t;
+        const float t = pow2n<L2N>(r0 * shift, log2n);
         w[i] = valid ? t : 0.0f;
       }
       float ts = 0.0f;
@@ -255,9 +247,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
     if (has_sink) {
       float b = beta;
       if constexpr (MODE == MODE_CLIPPED) b = fminf(b, p.clamp);
-      float t = rho_fast(b);
-      for (int e = 0; e < log2n; ++e) t = t * t;
-      Z += t;
+      Z += pow2n<L2N>(rho_fast(b), log2n);
     }
     const float inv = 1.0f / Z;
     stat = (MODE == MODE_CLIPPED && !p.inv_stat) ? inv_root(Z, 1 << log2n) : inv;
@@ -297,9 +287,13 @@ template <typename T, int D>
 static hipError_t launch_fwd_mode(const AttnFwdParams& p, int mode, hipStream_t st) {
   dim3 grid(p.B * p.H, ceil_div(p.T, FWD_BQ)), block(256);
   switch (mode) {
-    case MODE_INRANGE: { KTimer t("attn_fwd_inrange", st); hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_INRANGE>), grid, block, 0, st, p); } break;
-    case MODE_CLIPPED: { KTimer t("attn_fwd_clipped", st); hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_CLIPPED>), grid, block, 0, st, p); } break;
-    case MODE_SHIFTED: { KTimer t("attn_fwd_shifted", st); hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_SHIFTED>), grid, block, 0, st, p); } break;
+    case MODE_INRANGE: {
+      KTimer t("attn_fwd_inrange", st);
+      if (p.log2n == 4) hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_INRANGE, 4>), grid, block, 0, st, p);
+      else hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_INRANGE, 0>), grid, block, 0, st, p);
+    } break;
+    case MODE_CLIPPED: { KTimer t("attn_fwd_clipped", st); hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_CLIPPED, 0>), grid, block, 0, st, p); } break;
+    case MODE_SHIFTED: { KTimer t("attn_fwd_shifted", st); hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_SHIFTED, 0>), grid, block, 0, st, p); } break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -10,7 +10,7 @@
 #include <cstring>
 #include <string>
 
-#include "../../include/algebraic_hip.h"
+#include "algebraic_hip.h"
 #include "launchers.h"
 
 namespace {

@@ -70,6 +70,18 @@ __device__ __forceinline__ float ipow(float x) {
     return y * y;
   }
 }
+// t^(2^L2N) with the exponent fixed at compile time (L2N > 0) or given at run time (L2N == 0).
+template <int L2N>
+__device__ __forceinline__ float pow2n(float t, int log2n) {
+  if constexpr (L2N > 0) {
+#pragma unroll
+    for (int e = 0; e < L2N; ++e) t = t * t;
+  } else {
+    for (int e = 0; e < log2n; ++e) t = t * t;
+  }
+  return t;
+}
+
 // Runtime power-of-two exponent (cold paths only).
 __device__ __forceinline__ float ipow_rt(float x, int n) {
   float out = x;

@@ -7,7 +7,7 @@
 #include <string>
 #include <vector>
 
-#include "../../include/algebraic_hip.h"
+#include "algebraic_hip.h"
 #include "ktimer.h"
 
 namespace alg {
