@@ -3,11 +3,20 @@
 // C[M][N] = sum_k A[m][k] B[k][n] with f32 accumulation. A configuration fixes the
 // workgroup tile TM x TN, 64-deep k steps and a WM x WN grid of waves; each wave owns a
 // (TM/WM) x (TN/WN) sub-tile of 32x32 blocks computed with v_mfma_f32_32x32x16_bf16.
-// Operands may be stored k-contiguous (fragments read with ds_read_b128) or m/n-contiguous
-// (fragments read transposed with ds_read_b64_tr_b16), so every head product reads its
-// operands in their natural HBM layout. Global tiles are double-buffered through LDS (the
-// next tile's loads are in flight while the current one is consumed) with one barrier per
-// k step; rows/columns outside the matrix are zero-filled.
+//
+// Operands are stored either k-contiguous ([mn][k]; fragments read with ds_read_b128) or
+// m/n-contiguous ([k][mn]; fragments read transposed with ds_read_b64_tr_b16), so every
+// head product reads its operands in their natural HBM layout.
+//
+// Global -> LDS copies use global_load_lds_dwordx4 (each lane of a wave instruction writes
+// 16 bytes at base + 16*lane), so no VGPRs stage the tiles and the next tile's copy is in
+// flight while the current one feeds the MFMAs; tiles are double-buffered with one barrier
+// per k step. Because the copy writes rows without padding, 16-byte chunks are placed with an
+// XOR swizzle that keeps the fragment reads free of bank conflicts:
+//   k-contiguous rows (128 B):      chunk c of row r lives at chunk c ^ ((r >> 1) & 7)
+//   mn-contiguous rows (2*TMN B):   chunk c of row r lives at chunk c ^ (4 * (r & 3))
+// Tiles that reach past the matrix edge in m or n, and a partial last k tile, are copied
+// through registers with zero fill instead.
 #pragma once
 
 #include "common.h"
@@ -15,6 +24,8 @@
 namespace alg {
 
 constexpr int GT_K = 64;
+// s_waitcnt immediate for vmcnt(0) with expcnt/lgkmcnt left at their maxima (gfx9 encoding).
+constexpr int VMCNT0 = 0x0F70;
 enum OperandMode { KMAJOR = 0, MNMAJOR = 1 };
 
 template <int TM_, int TN_, int WM_, int WN_>
@@ -28,68 +39,125 @@ struct GemmCfg {
 struct GemmOperand {
   const bf16* ptr;
   long ld;         // leading dimension (elements) of the stored matrix
-  int rows_valid;  // stored rows at or beyond this are read as zero
-  int cols_valid;  // stored columns at or beyond this are read as zero (multiple of 8)
+  int rows_valid;  // stored rows at or beyond this are not read
+  int cols_valid;  // stored columns at or beyond this are not read (multiple of 8)
 };
 
-// LDS tile of an operand covering TMN (m or n) x 64 (k).
-template <int MODE, int TMN>
-struct TileShape;
-template <int TMN>
-struct TileShape<KMAJOR, TMN> {   // stored [mn][k]
-  static constexpr int ROWS = TMN, COLS = GT_K, PITCH = GT_K + 8;
-};
-template <int TMN>
-struct TileShape<MNMAJOR, TMN> {  // stored [k][mn]
-  static constexpr int ROWS = GT_K, COLS = TMN, PITCH = TMN + 8;
-};
-
+// One operand tile covering TMN (m or n) x 64 (k) in LDS, unpadded and swizzled.
 template <int MODE, int TMN, int NT>
 struct OperandTile {
-  typedef TileShape<MODE, TMN> S;
-  static constexpr int CPR = S::COLS / 8;               // 16-byte chunks per stored row
-  static constexpr int CHUNKS = S::ROWS * CPR / NT;     // per thread
-  static constexpr int ELEMS = S::ROWS * S::PITCH;
-  static_assert(S::ROWS * CPR % NT == 0, "tile/threads");
+  static constexpr int ROWS = MODE == KMAJOR ? TMN : GT_K;   // stored rows in the tile
+  static constexpr int CPR = (MODE == KMAJOR ? GT_K : TMN) / 8;  // 16-byte chunks per row
+  static constexpr int ELEMS = ROWS * CPR * 8;
+  static constexpr int WAVES = NT / 64;
+  static constexpr int INSTR = ROWS * CPR / 64;             // wave copy instructions per tile
+  static_assert(INSTR % WAVES == 0, "tile/waves");
+  static constexpr int PER_WAVE = INSTR / WAVES;
 
-  // Global -> registers.
-  static __device__ __forceinline__ void load(uint4 (&r)[CHUNKS], const GemmOperand& op, int mn0, int k0) {
+  static constexpr int READS_PER_FRAG = MODE == KMAJOR ? 1 : 2;  // LDS instructions per fragment
+
+  static __device__ __forceinline__ int swz(int row) {
+    return MODE == KMAJOR ? ((row >> 1) & 7) : 4 * (row & 3);
+  }
+  // Element offset of logical (row, chunk) inside the tile.
+  static __device__ __forceinline__ int at(int row, int chunk) { return (row * CPR + (chunk ^ swz(row))) * 8; }
+
+  // Rows of the tile one wave instruction covers, and the swizzle period in rows.
+  static constexpr int RPI = 64 / CPR;
+  static_assert(CPR <= 64 && 64 % CPR == 0, "chunks per row");
+  static constexpr int SWZ_PERIOD = MODE == KMAJOR ? 16 : 4;  // swz(row) depends on row mod this
+  static_assert((RPI * PER_WAVE) % SWZ_PERIOD == 0 && (2 * RPI) % SWZ_PERIOD == 0,
+                "the swizzle of instruction J must depend on J's parity only");
+
+  // Per-lane byte offsets (relative to the instruction's first row and the tile's first
+  // column) for even and odd instructions; computed once per kernel.
+  static __device__ __forceinline__ void lane_offsets(long ld, uint32_t (&off)[2]) {
+    const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int c = 0; c < CHUNKS; ++c) {
-      const int idx = threadIdx.x + c * NT;
-      const int row = idx / CPR, col = (idx - row * CPR) * 8;
-      const int grow = (MODE == KMAJOR) ? mn0 + row : k0 + row;
-      const int gcol = (MODE == KMAJOR) ? k0 + col : mn0 + col;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (grow < op.rows_valid && gcol < op.cols_valid)
-        v = *reinterpret_cast<const uint4*>(op.ptr + (long)grow * op.ld + gcol);
-      r[c] = v;
+    for (int par = 0; par < 2; ++par) {
+      const int row = RPI * par + lane / CPR;  // row inside the tile modulo the swizzle period
+      const int c = (lane % CPR) ^ swz(row);   // logical chunk this lane fetches
+      off[par] = (uint32_t)((lane / CPR) * ld * 2 + 16 * c);
     }
   }
-  // Registers -> LDS.
-  static __device__ __forceinline__ void store(bf16* tile, const uint4 (&r)[CHUNKS]) {
+
+  // Asynchronous global -> LDS copy of the tile at (mn0, k0); the tile must lie inside the
+  // stored matrix. Lane `lane` of instruction J writes the physical chunk 64*J + lane.
+  // `wave` must be wave-uniform (from readfirstlane) so the addressing stays scalar.
+  // Instructions [J0, J1) of this wave's share (all of it by default).
+  template <int J0 = 0, int J1 = PER_WAVE>
+  static __device__ __forceinline__ void copy(bf16* tile, const GemmOperand& op, const uint32_t (&off)[2], int wave,
+                                              int mn0, int k0) {
+    const int r0 = (MODE == KMAJOR) ? mn0 : k0;
+    const int c0 = (MODE == KMAJOR) ? k0 : mn0;
 #pragma unroll
-    for (int c = 0; c < CHUNKS; ++c) {
-      const int idx = threadIdx.x + c * NT;
-      const int row = idx / CPR, col = (idx - row * CPR) * 8;
-      *reinterpret_cast<uint4*>(tile + row * S::PITCH + col) = r[c];
+    for (int j = J0; j < J1; ++j) {
+      const int J = wave * PER_WAVE + j;
+      const char* base = reinterpret_cast<const char*>(op.ptr + ((long)(r0 + RPI * J) * op.ld + c0));
+      __builtin_amdgcn_global_load_lds(base + off[j & 1], LDS_PTR(void, tile + J * 512), 16, 0, 0);
+    }
+  }
+  // Synchronous copy with zero fill (partial last k tile).
+  static __device__ __forceinline__ void copy_zero_fill(bf16* tile, const GemmOperand& op, int mn0, int k0, int K) {
+    for (int p = threadIdx.x; p < ROWS * CPR; p += NT) {
+      const int row = p / CPR, c = p - row * CPR;
+      const int grow = (MODE == KMAJOR) ? mn0 + row : k0 + row;
+      const int gcol = (MODE == KMAJOR) ? k0 + 8 * c : mn0 + 8 * c;
+      const bool kin = (MODE == KMAJOR) ? gcol < K : grow < K;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (kin && grow < op.rows_valid && gcol < op.cols_valid)
+        v = *reinterpret_cast<const uint4*>(op.ptr + (long)grow * op.ld + gcol);
+      *reinterpret_cast<uint4*>(tile + at(row, c)) = v;
     }
   }
   // Fragment of the 32-wide block starting at tile-local mn for k step ks (16 k).
   static __device__ __forceinline__ bf16x8 frag(const bf16* tile, int mn, int ks, int lane) {
+    const int h = lane >> 5;
     if constexpr (MODE == KMAJOR) {
-      return *reinterpret_cast<const bf16x8*>(tile + (mn + (lane & 31)) * S::PITCH + ks * 16 + 8 * (lane >> 5));
+      return *reinterpret_cast<const bf16x8*>(tile + at(mn + (lane & 31), 2 * ks + h));
     } else {
-      const int klo = ks * 16 + 8 * (lane >> 5);
-      return lds_tr_frag(tile, S::PITCH, klo, klo + 4, mn, lane);
+      // ds_read_b64_tr_b16: lane i of each 16-lane group addresses row klo + i/4 at column
+      // n0 + 4*(i%4) and receives column n0 + i for rows klo..klo+3 (see common.h).
+      const int i = lane & 15;
+      const int col = mn + ((lane >> 4) & 1) * 16 + 4 * (i & 3);
+      const int r0 = ks * 16 + 8 * h + (i >> 2);
+      const bf16* p0 = tile + at(r0, col >> 3) + (col & 7);
+      const bf16* p1 = tile + at(r0 + 4, col >> 3) + (col & 7);
+      bf16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, p0));
+      bf16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, p1));
+      bf16x8 r;
+      r[0] = a[0]; r[1] = a[1]; r[2] = a[2]; r[3] = a[3];
+      r[4] = b[0]; r[5] = b[1]; r[6] = b[2]; r[7] = b[3];
+      return r;
     }
   }
 };
 
+// Scheduling template for one pipelined phase: NM independent MFMAs, NR LDS reads of the
+// next phase's fragments and NG global->LDS copies. Reads are issued early (ceil(NR/8)
+// after each of the first MFMAs) so they have landed by the time the next phase needs them;
+// copies are spread one per MFMA so the vector memory queue never stalls the wave.
+template <int NM, int NR, int NG = 0>
+__device__ __forceinline__ void interleave_phase() {
+  constexpr int PER = (NR + 7) / 8;
+  constexpr int HEAD = (NR + PER - 1) / PER;  // MFMAs that carry reads
+  static_assert(HEAD <= NM && NG <= NM, "phase shape");
+#pragma unroll
+  for (int i = 0; i < NM; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                  // one MFMA
+    if (i < HEAD) __builtin_amdgcn_sched_group_barrier(0x100, PER, 0);  // PER LDS reads
+    if (i < NG) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);      // one copy
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// One pipeline stage (A and B tiles). The two stages are separate __shared__ objects so
+// the compiler can tell reads of one stage from the DMA writes into the other and does not
+// wait for the next tile's copy before reading the current one.
 template <int AM, int BM, class C>
-struct GemmSmem {
-  bf16 a[2][OperandTile<AM, C::TM, C::THREADS>::ELEMS];
-  bf16 b[2][OperandTile<BM, C::TN, C::THREADS>::ELEMS];
+struct GemmStage {
+  bf16 a[OperandTile<AM, C::TM, C::THREADS>::ELEMS];
+  bf16 b[OperandTile<BM, C::TN, C::THREADS>::ELEMS];
 };
 
 // Wave coordinates inside the workgroup tile.
@@ -103,8 +171,9 @@ __device__ __forceinline__ void wave_coords(int& wm, int& wn) {
 // Accumulate the (m0, n0) tile over k in [0, K). acc[mb][nb] is the wave's 32x32 block at
 // rows wm*WTM + mb*32 and columns wn*WTN + nb*32 of the workgroup tile.
 template <int AM, int BM, class C>
-__device__ __forceinline__ void gemm_mainloop(GemmSmem<AM, BM, C>& sm, const GemmOperand& A, const GemmOperand& B,
-                                              int m0, int n0, int K, floatx16 (&acc)[C::MB][C::NB]) {
+__device__ __forceinline__ void gemm_mainloop(GemmStage<AM, BM, C>& s0, GemmStage<AM, BM, C>& s1,
+                                              const GemmOperand& A, const GemmOperand& B, int m0, int n0, int K,
+                                              floatx16 (&acc)[C::MB][C::NB]) {
   typedef OperandTile<AM, C::TM, C::THREADS> TA;
   typedef OperandTile<BM, C::TN, C::THREADS> TB;
   const int lane = threadIdx.x & 63;
@@ -115,37 +184,111 @@ __device__ __forceinline__ void gemm_mainloop(GemmSmem<AM, BM, C>& sm, const Gem
 #pragma unroll
     for (int j = 0; j < C::NB; ++j) acc[i][j] = floatx16{};
   const int nk = (K + GT_K - 1) / GT_K;
-  uint4 ra[TA::CHUNKS], rb[TB::CHUNKS];
-  TA::load(ra, A, m0, 0);
-  TB::load(rb, B, n0, 0);
-  TA::store(sm.a[0], ra);
-  TB::store(sm.b[0], rb);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < nk;
-    if (more) {
-      TA::load(ra, A, m0, (kt + 1) * GT_K);
-      TB::load(rb, B, n0, (kt + 1) * GT_K);
+  struct Frags {
+    bf16x8 a[C::MB], b[C::NB];
+  };
+  // Fragments are read in the order the MFMAs consume them (all of B, then A row by row).
+  auto load = [&](const GemmStage<AM, BM, C>& st, int ks, Frags& f) {
+#pragma unroll
+    for (int j = 0; j < C::NB; ++j) f.b[j] = TB::frag(st.b, wn * C::WTN + j * 32, ks, lane);
+#pragma unroll
+    for (int i = 0; i < C::MB; ++i) f.a[i] = TA::frag(st.a, wm * C::WTM + i * 32, ks, lane);
+  };
+  auto mma = [&](const Frags& f) {
+#pragma unroll
+    for (int i = 0; i < C::MB; ++i)
+#pragma unroll
+      for (int j = 0; j < C::NB; ++j) acc[i][j] = mfma_bf16(f.a[i], f.b[j], acc[i][j]);
+  };
+  // Tiles that reach past the stored matrix in m or n, or a K that is not a multiple of
+  // two k steps, take a plain single-stage loop with register copies and zero fill.
+  const bool a_full = (AM == KMAJOR ? A.rows_valid : A.cols_valid) >= m0 + C::TM;
+  const bool b_full = (BM == KMAJOR ? B.rows_valid : B.cols_valid) >= n0 + C::TN;
+  if (!a_full || !b_full || (K % (2 * GT_K)) != 0) {
+    for (int kt = 0; kt < nk; ++kt) {
+      __syncthreads();
+      TA::copy_zero_fill(s0.a, A, m0, kt * GT_K, K);
+      TB::copy_zero_fill(s0.b, B, n0, kt * GT_K, K);
+      __syncthreads();
+#pragma unroll
+      for (int ks = 0; ks < GT_K / 16; ++ks) {
+        Frags f;
+        load(s0, ks, f);
+        mma(f);
+      }
     }
-#pragma unroll
-    for (int ks = 0; ks < GT_K / 16; ++ks) {
-      bf16x8 af[C::MB], bfr[C::NB];
-#pragma unroll
-      for (int i = 0; i < C::MB; ++i) af[i] = TA::frag(sm.a[cur], wm * C::WTM + i * 32, ks, lane);
-#pragma unroll
-      for (int j = 0; j < C::NB; ++j) bfr[j] = TB::frag(sm.b[cur], wn * C::WTN + j * 32, ks, lane);
-#pragma unroll
-      for (int i = 0; i < C::MB; ++i)
-#pragma unroll
-        for (int j = 0; j < C::NB; ++j) acc[i][j] = mfma_bf16(af[i], bfr[j], acc[i][j]);
-    }
-    if (more) {
-      TA::store(sm.a[cur ^ 1], ra);
-      TB::store(sm.b[cur ^ 1], rb);
-    }
-    __syncthreads();
+    return;
   }
+  uint32_t aoff[2], boff[2];
+  TA::lane_offsets(A.ld, aoff);
+  TB::lane_offsets(B.ld, boff);
+  const int wave_u = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  auto copy_tile = [&](GemmStage<AM, BM, C>& st, int kt) {
+    TA::copy(st.a, A, aoff, wave_u, m0, kt * GT_K);
+    TB::copy(st.b, B, boff, wave_u, n0, kt * GT_K);
+  };
+  // The copy of a tile in two halves, issued during the first two phases of a step.
+  constexpr int HA = TA::PER_WAVE / 2, HB = TB::PER_WAVE / 2;
+  auto copy_half0 = [&](GemmStage<AM, BM, C>& st, int kt) {
+    TA::template copy<0, HA>(st.a, A, aoff, wave_u, m0, kt * GT_K);
+    TB::template copy<0, HB>(st.b, B, boff, wave_u, n0, kt * GT_K);
+  };
+  auto copy_half1 = [&](GemmStage<AM, BM, C>& st, int kt) {
+    TA::template copy<HA, TA::PER_WAVE>(st.a, A, aoff, wave_u, m0, kt * GT_K);
+    TB::template copy<HB, TB::PER_WAVE>(st.b, B, boff, wave_u, n0, kt * GT_K);
+  };
+  constexpr int NG0 = HA + HB, NG1 = TA::PER_WAVE + TB::PER_WAVE - NG0;
+  // One k step with a next tile, software-pipelined over its four 16-deep sub-steps:
+  // fragments of sub-step ks+1 are read while sub-step ks multiplies. f0 holds sub-step 0
+  // of `cur` on entry and sub-step 0 of `nxt` on exit. The copy of tile kt+1 into `nxt` is
+  // spread over the first two sub-steps; the barrier (after this wave's copies have landed,
+  // vmcnt) comes before the last sub-step so the next tile's first fragments are read
+  // while it multiplies.
+  Frags f0, f1;
+  constexpr int NM = C::MB * C::NB;
+  constexpr int NR = C::MB * TA::READS_PER_FRAG + C::NB * TB::READS_PER_FRAG;
+  auto step = [&](const GemmStage<AM, BM, C>& cur, GemmStage<AM, BM, C>& nxt, int kt) {
+    copy_half0(nxt, kt + 1);
+    load(cur, 1, f1);
+    mma(f0);
+    interleave_phase<NM, NR, NG0>();
+    copy_half1(nxt, kt + 1);
+    load(cur, 2, f0);
+    mma(f1);
+    interleave_phase<NM, NR, NG1>();
+    load(cur, 3, f1);
+    mma(f0);
+    interleave_phase<NM, NR>();
+    __builtin_amdgcn_s_waitcnt(VMCNT0);
+    __syncthreads();
+    load(nxt, 0, f0);
+    mma(f1);
+    interleave_phase<NM, NR>();
+  };
+  // The last k step: no copy.
+  auto last = [&](const GemmStage<AM, BM, C>& cur) {
+    load(cur, 1, f1);
+    mma(f0);
+    interleave_phase<NM, NR>();
+    load(cur, 2, f0);
+    mma(f1);
+    interleave_phase<NM, NR>();
+    load(cur, 3, f1);
+    mma(f0);
+    interleave_phase<NM, NR>();
+    mma(f1);
+  };
+  copy_tile(s0, 0);
+  __builtin_amdgcn_s_waitcnt(VMCNT0);
+  __syncthreads();
+  load(s0, 0, f0);
+  int kt = 0;  // nk is even here
+  for (; kt + 2 < nk; kt += 2) {
+    step(s0, s1, kt);
+    step(s1, s0, kt + 1);
+  }
+  step(s0, s1, kt);
+  last(s1);
 }
 
 // Map a linear workgroup id to (tile_m, tile_n) so that the workgroups one XCD runs

@@ -43,7 +43,7 @@ __global__ void head_zero_kernel(float* p, int n) {
 
 // z^T = E h^T with the forward epilogue (row sums, target logit, optional U residual).
 __global__ __launch_bounds__(NT, 1) void head_fwd_kernel(HeadParams p) {
-  __shared__ __attribute__((aligned(16))) GemmSmem<KMAJOR, KMAJOR, HC> sm;
+  __shared__ __attribute__((aligned(16))) GemmStage<KMAJOR, KMAJOR, HC> s0, s1;
   __shared__ float red[HC::WM][HT_N];
   const int nbm = (p.V + HT_M - 1) / HT_M, nbn = p.Npad / HT_N;
   int tm, tn;
@@ -52,7 +52,7 @@ __global__ __launch_bounds__(NT, 1) void head_fwd_kernel(HeadParams p) {
   const int n0 = tn * HT_N;  // tokens
   GemmOperand A{p.E, p.d, p.V, p.d}, B{p.h, p.d, p.N, p.d};
   floatx16 acc[HC::MB][HC::NB];
-  gemm_mainloop<KMAJOR, KMAJOR, HC>(sm, A, B, m0, n0, p.d, acc);
+  gemm_mainloop<KMAJOR, KMAJOR, HC>(s0, s1, A, B, m0, n0, p.d, acc);
   const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
   int wm, wn;
   wave_coords<HC>(wm, wn);
@@ -146,14 +146,14 @@ __device__ __forceinline__ float head_grad_scale(const HeadParams& p) {
 
 // Recompute schedule: z^T again, dZ^T = bf16(s (p - y) r).
 __global__ __launch_bounds__(NT, 1) void head_dz_kernel(HeadParams p) {
-  __shared__ __attribute__((aligned(16))) GemmSmem<KMAJOR, KMAJOR, HC> sm;
+  __shared__ __attribute__((aligned(16))) GemmStage<KMAJOR, KMAJOR, HC> s0, s1;
   const int nbm = (p.V + HT_M - 1) / HT_M, nbn = p.Npad / HT_N;
   int tm, tn;
   xcd_tile(blockIdx.x, nbm, nbn, tm, tn);
   const int m0 = tm * HT_M, n0 = tn * HT_N;
   GemmOperand A{p.E, p.d, p.V, p.d}, B{p.h, p.d, p.N, p.d};
   floatx16 acc[HC::MB][HC::NB];
-  gemm_mainloop<KMAJOR, KMAJOR, HC>(sm, A, B, m0, n0, p.d, acc);
+  gemm_mainloop<KMAJOR, KMAJOR, HC>(s0, s1, A, B, m0, n0, p.d, acc);
   const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
   int wm, wn;
   wave_coords<HC>(wm, wn);
@@ -200,7 +200,7 @@ __global__ __launch_bounds__(256) void head_hscale_kernel(HeadParams p) {
 // dh = (U' or dZ) E: A stored [v][n] (m-contiguous), B = E stored [v][d] (n-contiguous).
 // The residual schedule scales token rows by s/l.
 __global__ __launch_bounds__(NT, 1) void head_dh_kernel(HeadParams p) {
-  __shared__ __attribute__((aligned(16))) GemmSmem<MNMAJOR, MNMAJOR, HC> sm;
+  __shared__ __attribute__((aligned(16))) GemmStage<MNMAJOR, MNMAJOR, HC> s0, s1;
   const int nbm = p.Npad / HT_M, nbn = (p.d + HT_N - 1) / HT_N;
   int tm, tn;
   xcd_tile(blockIdx.x, nbm, nbn, tm, tn);
@@ -209,7 +209,7 @@ __global__ __launch_bounds__(NT, 1) void head_dh_kernel(HeadParams p) {
   const bf16* a = p.ut ? p.ut : p.dzt;
   GemmOperand A{a, p.Npad, p.V, p.Npad}, B{p.E, p.d, p.V, p.d};
   floatx16 acc[HC::MB][HC::NB];
-  gemm_mainloop<MNMAJOR, MNMAJOR, HC>(sm, A, B, m0, n0, p.V, acc);
+  gemm_mainloop<MNMAJOR, MNMAJOR, HC>(s0, s1, A, B, m0, n0, p.V, acc);
   const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
   int wm, wn;
   wave_coords<HC>(wm, wn);
@@ -232,7 +232,7 @@ __global__ __launch_bounds__(NT, 1) void head_dh_kernel(HeadParams p) {
 
 // dE = (U' or dZ)^T (hs or h): A stored [v][n] (k-contiguous), B stored [n][d] (n-contiguous).
 __global__ __launch_bounds__(NT, 1) void head_de_kernel(HeadParams p) {
-  __shared__ __attribute__((aligned(16))) GemmSmem<KMAJOR, MNMAJOR, HC> sm;
+  __shared__ __attribute__((aligned(16))) GemmStage<KMAJOR, MNMAJOR, HC> s0, s1;
   const int nbm = (p.V + HT_M - 1) / HT_M, nbn = (p.d + HT_N - 1) / HT_N;
   int tm, tn;
   xcd_tile(blockIdx.x, nbm, nbn, tm, tn);
@@ -242,7 +242,7 @@ __global__ __launch_bounds__(NT, 1) void head_de_kernel(HeadParams p) {
   const bf16* b = p.ut ? p.hs : p.h;
   GemmOperand A{a, p.Npad, p.V, p.Npad}, B{b, p.d, p.N, p.d};
   floatx16 acc[HC::MB][HC::NB];
-  gemm_mainloop<KMAJOR, MNMAJOR, HC>(sm, A, B, m0, n0, p.N, acc);
+  gemm_mainloop<KMAJOR, MNMAJOR, HC>(s0, s1, A, B, m0, n0, p.N, acc);
   const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
   int wm, wn;
   wave_coords<HC>(wm, wn);

@@ -8,8 +8,11 @@
 namespace alg {
 
 constexpr int HT_M = 256, HT_N = 256;  // head GEMM workgroup tile
+#ifndef ALG_HEAD_WM
+#define ALG_HEAD_WM 2                  // waves along the tile's m dimension
+#endif
 #ifndef ALG_HEAD_WN
-#define ALG_HEAD_WN 4                  // waves along the tile's n dimension (x 2 along m)
+#define ALG_HEAD_WN 4                  // waves along the tile's n dimension
 #endif
 
 struct HeadParams {
@@ -35,6 +38,6 @@ struct HeadParams {
   int dE_f32;
 };
 
-typedef GemmCfg<HT_M, HT_N, 2, ALG_HEAD_WN> HeadGemm;
+typedef GemmCfg<HT_M, HT_N, ALG_HEAD_WM, ALG_HEAD_WN> HeadGemm;
 
 }  // namespace alg
