@@ -26,6 +26,9 @@ typedef float floatx2 __attribute__((ext_vector_type(2)));
 
 #define LDS_PTR(T, p) ((__attribute__((address_space(3))) T*)(p))
 
+// Word 3 of a raw buffer descriptor on gfx9-class targets: 32-bit data format, no swizzle.
+#define BUF_RSRC_WORD3 0x00020000
+
 namespace alg {
 
 __device__ __forceinline__ floatx16 mfma_bf16(const bf16x8& a, const bf16x8& b, const floatx16& c) {

@@ -163,7 +163,7 @@ struct GemmStage {
 // Wave coordinates inside the workgroup tile.
 template <class C>
 __device__ __forceinline__ void wave_coords(int& wm, int& wn) {
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   wm = wave / C::WN;
   wn = wave % C::WN;
 }

@@ -21,6 +21,8 @@
 //    dE = dZ^T h.
 // Every product reads its operands in their natural layout (k-contiguous fragments via
 // ds_read_b128, transposed ones via ds_read_b64_tr_b16).
+#include <type_traits>
+
 #include "gemm_core.h"
 #include "head_params.h"
 
@@ -42,6 +44,8 @@ __global__ void head_zero_kernel(float* p, int n) {
 }
 
 // z^T = E h^T with the forward epilogue (row sums, target logit, optional U residual).
+// L2N > 0 fixes n = 2^L2N at compile time (0: taken from the parameters).
+template <int L2N>
 __global__ __launch_bounds__(NT, 1) void head_fwd_kernel(HeadParams p) {
   __shared__ __attribute__((aligned(16))) GemmStage<KMAJOR, KMAJOR, HC> s0, s1;
   __shared__ float red[HC::WM][HT_N];
@@ -56,30 +60,76 @@ __global__ __launch_bounds__(NT, 1) void head_fwd_kernel(HeadParams p) {
   const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
   int wm, wn;
   wave_coords<HC>(wm, wn);
+  const float inv_c = p.inv_c, clamp = p.clamp;
+  const int vrow0 = m0 + wm * HC::WTM;  // first vocab row of this wave
+  // Interior tile (every row and column live); WITH_U also stores the residual.
+  auto interior = [&](auto with_u) {
+    constexpr bool WITH_U = decltype(with_u)::value;
+    const size_t rest = (size_t)(p.V - vrow0) * p.Npad * 2;  // bytes of U from this wave's first row
+    const __amdgpu_buffer_rsrc_t urs = __builtin_amdgcn_make_buffer_rsrc(
+        p.ut + (size_t)vrow0 * p.Npad, (short)0, (int)std::min<size_t>(rest, 0x7fffffff), BUF_RSRC_WORD3);
 #pragma unroll
-  for (int nb = 0; nb < HC::NB; ++nb) {
-    const int col = wn * HC::WTN + nb * 32 + l32;
-    const int tok = n0 + col;
-    const bool live = tok < p.N;
-    const int tgt = live ? p.targets[tok] : -1;
-    float part = 0.0f;
+    for (int nb = 0; nb < HC::NB; ++nb) {
+      const int col = wn * HC::WTN + nb * 32 + l32;
+      const int tok = n0 + col;
+      const int dt = p.targets[tok] - vrow0 - 4 * h;  // target row relative to this lane's rows
+      // U rows of this wave through a buffer descriptor: the row offset c * Npad is a scalar
+      // (soffset), the lane offset (4h rows + token) a fixed 32-bit voffset.
+      const int uvoff = (4 * h * p.Npad + tok) * 2;
+      float part = 0.0f, ztv = 0.0f;
+      bool hit = false;
 #pragma unroll
-    for (int mb = 0; mb < HC::MB; ++mb) {
+      for (int mb = 0; mb < HC::MB; ++mb) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int v = m0 + wm * HC::WTM + mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-        const float z = acc[mb][nb][i];
-        float r;
-        const float w = head_w(z, p, r);
-        if (v < p.V) {
+        for (int i = 0; i < 16; ++i) {
+          const int c = mb * 32 + 8 * (i >> 2) + (i & 3);  // lane row offset (without 4h)
+          const float z = acc[mb][nb][i];
+          const float x = fminf(z * inv_c, clamp);  // fused_head.py:98
+          float r;
+          const float w = pow2n<L2N>(rho_fast(x, r), p.log2n);
           part += w;
-          if (p.ut) p.ut[(size_t)v * p.Npad + tok] = f2bf(live ? w * r : 0.0f);
+          if constexpr (WITH_U)
+            __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, f2bf(w * r)), urs, uvoff,
+                                                  c * p.Npad * 2, 0);
+          ztv = dt == c ? z : ztv;
+          hit = hit || dt == c;
         }
-        if (v == tgt) p.zt[tok] = z;
       }
+      if (hit) p.zt[tok] = ztv;
+      part += xor32(part);
+      if (h == 0) red[wm][col] = part;
     }
-    part += xor32(part);
-    if (h == 0) red[wm][col] = part;
+  };
+  if (m0 + HT_M <= p.V && n0 + HT_N <= p.N) {
+    if (p.ut) interior(std::true_type{});
+    else interior(std::false_type{});
+  } else {
+#pragma unroll
+    for (int nb = 0; nb < HC::NB; ++nb) {
+      const int col = wn * HC::WTN + nb * 32 + l32;
+      const int tok = n0 + col;
+      const bool live = tok < p.N;
+      const int tgt = live ? p.targets[tok] : -1;
+      float part = 0.0f;
+#pragma unroll
+      for (int mb = 0; mb < HC::MB; ++mb) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int v = vrow0 + mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+          const float z = acc[mb][nb][i];
+          const float x = fminf(z * inv_c, clamp);
+          float r;
+          const float w = pow2n<L2N>(rho_fast(x, r), p.log2n);
+          if (v < p.V) {
+            part += w;
+            if (p.ut) p.ut[(size_t)v * p.Npad + tok] = f2bf(live ? w * r : 0.0f);
+          }
+          if (v == tgt) p.zt[tok] = z;
+        }
+      }
+      part += xor32(part);
+      if (h == 0) red[wm][col] = part;
+    }
   }
   __syncthreads();
   for (int t = threadIdx.x; t < HT_N; t += NT) {
@@ -271,7 +321,11 @@ int head_stat_blocks(int N) { return (N + 255) / 256; }
 hipError_t launch_head_fwd(const HeadParams& p, hipStream_t st) {
   { KTimer t("head_zero", st); hipLaunchKernelGGL(head_zero_kernel, dim3((p.N + 255) / 256), dim3(256), 0, st, p.zt, p.N); }
   const int tiles = head_vocab_tiles(p.V) * (p.Npad / HT_N);
-  { KTimer t("head_fwd", st); hipLaunchKernelGGL(head_fwd_kernel, dim3(tiles), dim3(NT), 0, st, p); }
+  {
+    KTimer t("head_fwd", st);
+    if (p.log2n == 3) hipLaunchKernelGGL(head_fwd_kernel<3>, dim3(tiles), dim3(NT), 0, st, p);
+    else hipLaunchKernelGGL(head_fwd_kernel<0>, dim3(tiles), dim3(NT), 0, st, p);
+  }
   const int nb = head_stat_blocks(p.N);
   { KTimer t("head_stats", st); hipLaunchKernelGGL(head_stats_kernel, dim3(nb), dim3(256), 0, st, p, head_vocab_tiles(p.V)); }
   { KTimer t("head_obj", st); hipLaunchKernelGGL(head_obj_kernel, dim3(1), dim3(256), 0, st, p, nb); }

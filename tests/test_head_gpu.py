@@ -33,6 +33,7 @@ CASES = [  # (N, d, V)
     (128, 128, 517),     # ragged vocab
     (384, 256, 1000),    # token count not a 256 multiple
     (100, 128, 260),     # N < 128 (single ragged token tile)
+    (512, 512, 2304),    # several k-step pairs in every product
 ]
 
 
