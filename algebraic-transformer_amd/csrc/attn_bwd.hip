@@ -120,12 +120,16 @@ struct RowTile {
       r[c] = v;
     }
   }
+  // bf16 tiles are unpadded and swizzled (swz_at); f32 tiles are row-major with `pitch`.
   static __device__ __forceinline__ void store(T* dst, int pitch, const uint4 (&r)[PER]) {
 #pragma unroll
     for (int c = 0; c < PER; ++c) {
       const int idx = threadIdx.x + c * 256;
       const int row = idx / CPR, col = (idx - row * CPR) * CH;
-      if (row < R) *reinterpret_cast<uint4*>(dst + row * pitch + col) = r[c];
+      if (row < R) {
+        if constexpr (sizeof(T) == 2) *reinterpret_cast<uint4*>(dst + swz_at<CPR>(row, col)) = r[c];
+        else *reinterpret_cast<uint4*>(dst + row * pitch + col) = r[c];
+      }
     }
   }
 };
@@ -134,14 +138,16 @@ template <typename T, int D, int MODE, int L2N>
 __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
   static_assert(D == 64 || D == 128, "head_dim");
   constexpr bool BF = sizeof(T) == 2;
-  constexpr int PITCH = D + (BF ? ALG_BWD_PAD : 4);
   constexpr int BWD_BQ = bwd_bq<T, D>();
-  constexpr int SPITCH = BWD_BQ + (BF ? ALG_BWD_SPAD : 4);
+  // f32 tiles: padded row-major; bf16 tiles: unpadded, swizzled (CPR / SCPR chunks per row).
+  constexpr int PITCH = D + F32_PAD;
+  constexpr int SPITCH = BWD_BQ + F32_PAD;
+  constexpr int CPR = D / 8, SCPR = BWD_BQ / 8;
   constexpr int NDB = D / 32;
-  __shared__ __attribute__((aligned(16))) T Ks[BWD_BK * PITCH];
-  __shared__ __attribute__((aligned(16))) T Qs[BWD_BQ * PITCH];
-  __shared__ __attribute__((aligned(16))) T dOs[BWD_BQ * PITCH];
-  __shared__ __attribute__((aligned(16))) T dSs[BWD_BK * SPITCH];
+  __shared__ __attribute__((aligned(16))) T Ks[BF ? BWD_BK * D : BWD_BK * PITCH];
+  __shared__ __attribute__((aligned(16))) T Qs[BF ? BWD_BQ * D : BWD_BQ * PITCH];
+  __shared__ __attribute__((aligned(16))) T dOs[BF ? BWD_BQ * D : BWD_BQ * PITCH];
+  __shared__ __attribute__((aligned(16))) T dSs[BF ? BWD_BK * BWD_BQ : BWD_BK * SPITCH];
   __shared__ __attribute__((aligned(16))) float st_s[BWD_BQ];
   __shared__ __attribute__((aligned(16))) float di_s[BWD_BQ];
 
@@ -233,9 +239,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
   #pragma unroll
         for (int st = 0; st < NF; ++st) {
           if constexpr (BF) {
-            bf16x8 qa = *reinterpret_cast<const bf16x8*>(qrow + 16 * st + 8 * h);
+            const int at = swz_at<CPR>(sub * 32 + l32, 16 * st + 8 * h);
+            bf16x8 qa = *reinterpret_cast<const bf16x8*>(Qs + at);
             s = mfma_bf16(qa, kf[st], s);
-            bf16x8 da = *reinterpret_cast<const bf16x8*>(dorow + 16 * st + 8 * h);
+            bf16x8 da = *reinterpret_cast<const bf16x8*>(dOs + at);
             dp = mfma_bf16(da, vf[st], dp);
           } else {
             floatx4 qa = *reinterpret_cast<const floatx4*>(qrow + 8 * st + 4 * h);
@@ -298,12 +305,12 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
   #pragma unroll
           for (int db = 0; db < NDB; ++db) {
             const int r0 = sub * 32 + 4 * h;
-            bf16x8 ob0 = lds_tr_frag(dot_, PITCH, r0, r0 + 8, db * 32, lane);
-            bf16x8 ob1 = lds_tr_frag(dot_, PITCH, r0 + 16, r0 + 24, db * 32, lane);
+            bf16x8 ob0 = swz_tr_frag<CPR>(dot_, r0, r0 + 8, db * 32, lane);
+            bf16x8 ob1 = swz_tr_frag<CPR>(dot_, r0 + 16, r0 + 24, db * 32, lane);
             dv[db] = mfma_bf16(pa0, ob0, dv[db]);
             dv[db] = mfma_bf16(pa1, ob1, dv[db]);
-            bf16x8 qb0 = lds_tr_frag(qt_, PITCH, r0, r0 + 8, db * 32, lane);
-            bf16x8 qb1 = lds_tr_frag(qt_, PITCH, r0 + 16, r0 + 24, db * 32, lane);
+            bf16x8 qb0 = swz_tr_frag<CPR>(qt_, r0, r0 + 8, db * 32, lane);
+            bf16x8 qb1 = swz_tr_frag<CPR>(qt_, r0 + 16, r0 + 24, db * 32, lane);
             dk[db] = mfma_bf16(da0, qb0, dk[db]);
             dk[db] = mfma_bf16(da1, qb1, dk[db]);
           }
@@ -313,7 +320,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
             bf16x4 v4;
   #pragma unroll
             for (int e = 0; e < 4; ++e) v4[e] = f2bf(dsv[4 * g + e]);
-            *reinterpret_cast<bf16x4*>(dsrow + 8 * g + 4 * h) = v4;
+            *reinterpret_cast<bf16x4*>(dSs + swz_at<SCPR>(wave * 32 + l32, sub * 32 + 8 * g + 4 * h)) = v4;
           }
         } else {
           const float* qt_ = reinterpret_cast<const float*>(Qs);
@@ -347,7 +354,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
           T* dsrow = dSs + (wave * 32 + l32) * SPITCH + sub * 32;
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
-            if constexpr (BF) { bf16x4 z = {}; *reinterpret_cast<bf16x4*>(dsrow + 8 * g + 4 * h) = z; }
+            if constexpr (BF) {
+              bf16x4 z = {};
+              *reinterpret_cast<bf16x4*>(dSs + swz_at<SCPR>(wave * 32 + l32, sub * 32 + 8 * g + 4 * h)) = z;
+            }
             else { floatx4 z = {}; *reinterpret_cast<floatx4*>(dsrow + 8 * g + 4 * h) = z; }
           }
         } else {
@@ -377,12 +387,12 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
 #pragma unroll
         for (int ks = 0; ks < BWD_BK / 16; ks += 2) {
           const int klo = ks * 16 + 8 * h;
-          bf16x8 a0 = lds_tr_frag(ds_, SPITCH, klo, klo + 4, qs * 32, lane);
-          bf16x8 a1 = lds_tr_frag(ds_, SPITCH, klo + 16, klo + 20, qs * 32, lane);
+          bf16x8 a0 = swz_tr_frag<SCPR>(ds_, klo, klo + 4, qs * 32, lane);
+          bf16x8 a1 = swz_tr_frag<SCPR>(ds_, klo + 16, klo + 20, qs * 32, lane);
 #pragma unroll
           for (int j = 0; j < DBW; ++j) {
-            bf16x8 b0 = lds_tr_frag(k_, PITCH, klo, klo + 4, (db0 + j) * 32, lane);
-            bf16x8 b1 = lds_tr_frag(k_, PITCH, klo + 16, klo + 20, (db0 + j) * 32, lane);
+            bf16x8 b0 = swz_tr_frag<CPR>(k_, klo, klo + 4, (db0 + j) * 32, lane);
+            bf16x8 b1 = swz_tr_frag<CPR>(k_, klo + 16, klo + 20, (db0 + j) * 32, lane);
             dqa[j] = mfma_bf16(a0, b0, dqa[j]);
             dqb[j] = mfma_bf16(a1, b1, dqb[j]);
           }

@@ -56,16 +56,42 @@ struct AttnBwdParams {
 
 __host__ __device__ inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
-// LDS row padding (elements) of the bf16 tiles: row pitch = width + pad, chosen against
-// bank conflicts of the row-fragment and transposed (ds_read_b64_tr_b16) reads.
-#ifndef ALG_FWD_PAD
-#define ALG_FWD_PAD 8
-#endif
-#ifndef ALG_BWD_PAD
-#define ALG_BWD_PAD 8
-#endif
-#ifndef ALG_BWD_SPAD
-#define ALG_BWD_SPAD 8
-#endif
+// Unpadded bf16 LDS tiles with CPR 16-byte chunks per row (CPR = 16 for 256-byte rows, 8 for
+// 128-byte rows). Chunk c of row r is stored at chunk c ^ swz_chunk<CPR>(r); the mask is
+// chosen so that both access patterns of the kernels are free of bank conflicts:
+//   * row fragments (ds_read_b128): 16 consecutive rows at one logical chunk land on 16
+//     distinct 16-byte bank groups;
+//   * transposed fragments (ds_read_b64_tr_b16): 4 consecutive rows (aligned to 4) x 4
+//     consecutive chunks (aligned to 4) land on 16 distinct 16-byte bank groups.
+template <int CPR>
+__device__ __forceinline__ int swz_chunk(int row) {
+  static_assert(CPR == 16 || CPR == 8, "row width");
+  if constexpr (CPR == 16) return 4 * (row & 3) + ((row >> 2) & 3);
+  else return 4 * ((row >> 1) & 1) + ((row >> 2) & 3);
+}
+// Element offset of (row, col) in a swizzled tile.
+template <int CPR>
+__device__ __forceinline__ int swz_at(int row, int col) {
+  return row * (CPR * 8) + (((col >> 3) ^ swz_chunk<CPR>(row)) << 3) + (col & 7);
+}
+// Transposed 32x32x16 operand fragment from a swizzled tile M[k][n]: lane l receives
+// M[k][ncol + l%32] for k = k_lo + (0..3) (slots 0..3) and k_hi + (0..3) (slots 4..7);
+// k_lo and k_hi must be multiples of 4 (the ds_read_b64_tr_b16 lane layout is in common.h).
+template <int CPR>
+__device__ __forceinline__ bf16x8 swz_tr_frag(const bf16* tile, int k_lo, int k_hi, int ncol, int lane) {
+  const int i = lane & 15;
+  const int col = ncol + ((lane >> 4) & 1) * 16 + 4 * (i & 3);
+  const bf16* p0 = tile + swz_at<CPR>(k_lo + (i >> 2), col);
+  const bf16* p1 = tile + swz_at<CPR>(k_hi + (i >> 2), col);
+  bf16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, p0));
+  bf16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, p1));
+  bf16x8 r;
+  r[0] = a[0]; r[1] = a[1]; r[2] = a[2]; r[3] = a[3];
+  r[4] = b[0]; r[5] = b[1]; r[6] = b[2]; r[7] = b[3];
+  return r;
+}
+
+// Row padding (elements) of the f32 tiles, which keep a padded row-major layout.
+constexpr int F32_PAD = 4;
 
 }  // namespace alg

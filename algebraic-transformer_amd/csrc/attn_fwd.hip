@@ -47,12 +47,14 @@ struct KVTile {
       r[c] = v;
     }
   }
+  // bf16 tiles are unpadded and swizzled (swz_at); f32 tiles are row-major with `pitch`.
   static __device__ __forceinline__ void store(T* dst, int pitch, const uint4 (&r)[PER]) {
 #pragma unroll
     for (int c = 0; c < PER; ++c) {
       const int idx = threadIdx.x + c * 256;
       const int row = idx / CPR, col = (idx - row * CPR) * CH;
-      *reinterpret_cast<uint4*>(dst + row * pitch + col) = r[c];
+      if constexpr (sizeof(T) == 2) *reinterpret_cast<uint4*>(dst + swz_at<CPR>(row, col)) = r[c];
+      else *reinterpret_cast<uint4*>(dst + row * pitch + col) = r[c];
     }
   }
 };
@@ -61,11 +63,13 @@ template <typename T, int D, int MODE, int L2N>
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
   static_assert(D == 64 || D == 128, "head_dim");
   constexpr bool BF = sizeof(T) == 2;
-  constexpr int PITCH = D + (BF ? ALG_FWD_PAD : 4);
+  constexpr int PITCH = D + F32_PAD;  // f32 tiles
+  constexpr int CPR = D / 8;          // bf16 tiles: 16-byte chunks per row
+  constexpr int TILE = BF ? FWD_BK * D : FWD_BK * PITCH;
   constexpr int NDB = D / 32;  // 32-wide d blocks of the O^T accumulator
   typedef KVTile<T, D> KV;
-  __shared__ __attribute__((aligned(16))) T Ks[2][FWD_BK * PITCH];
-  __shared__ __attribute__((aligned(16))) T Vs[2][FWD_BK * PITCH];
+  __shared__ __attribute__((aligned(16))) T Ks[2][TILE];
+  __shared__ __attribute__((aligned(16))) T Vs[2][TILE];
 
   if (p.flag) {  // device-side guard dispatch (lax.cond at flash.py:853-856)
     const bool in_range = *p.flag != 0;
@@ -120,7 +124,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
 #pragma unroll
     for (int st = 0; st < NQF; ++st) {
       if constexpr (BF) {
-        bf16x8 kf = *reinterpret_cast<const bf16x8*>(krow + 16 * st + 8 * h);
+        bf16x8 kf = *reinterpret_cast<const bf16x8*>(Ks[buf] + swz_at<CPR>(sub * 32 + l32, 16 * st + 8 * h));
         s = mfma_bf16(kf, qf[st], s);
       } else {
         floatx4 kf = *reinterpret_cast<const floatx4*>(krow + 8 * st + 4 * h);
@@ -184,9 +188,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
       const bf16* vt = reinterpret_cast<const bf16*>(Vs[buf]);
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
-        bf16x8 v0 = lds_tr_frag(vt, PITCH, sub * 32 + 4 * h, sub * 32 + 8 + 4 * h, db * 32, lane);
+        bf16x8 v0 = swz_tr_frag<CPR>(vt, sub * 32 + 4 * h, sub * 32 + 8 + 4 * h, db * 32, lane);
         oacc[db] = mfma_bf16(v0, pf0, oacc[db]);
-        bf16x8 v1 = lds_tr_frag(vt, PITCH, sub * 32 + 16 + 4 * h, sub * 32 + 24 + 4 * h, db * 32, lane);
+        bf16x8 v1 = swz_tr_frag<CPR>(vt, sub * 32 + 16 + 4 * h, sub * 32 + 24 + 4 * h, db * 32, lane);
         oacc[db] = mfma_bf16(v1, pf1, oacc[db]);
       }
     } else {
