@@ -98,7 +98,9 @@ HeadWs head_ws(int N, int d, int V, int pass, bool residual) {
 
 int check_head(int N, int d, int V, int n, float c) {
   if (N <= 0 || d <= 0 || V <= 0) return fail(ALG_ERR_INVALID, "N, d, V must be positive (got %d, %d, %d)", N, d, V);
-  if (d % 128) return fail(ALG_ERR_UNSUPPORTED, "d_model %d: gfx950 head kernels need d %% 128 == 0", d);
+  if (d % 8) return fail(ALG_ERR_UNSUPPORTED, "d_model %d: head rows must be 16-byte aligned (d %% 8 == 0)", d);
+  if (alg::head_token_pad(N) > (1 << 23))  // residual rows are addressed with 32-bit buffer offsets
+    return fail(ALG_ERR_UNSUPPORTED, "N = %d tokens: at most %d per call", N, 1 << 23);
   if ((double)N * d > 2.0e9 || (double)V * d > 2.0e9 || (double)V * alg::head_token_pad(N) > 4.0e9)
     return fail(ALG_ERR_INVALID, "head too large");
   const int k = log2_pow2(n);

@@ -100,6 +100,20 @@ def make_steps(torch, x):
     return attn_step, head_step, full_step
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` recorded from rocprofv3 FETCH_SIZE + WRITE_SIZE runs
+    (each scaled by the same counter's reading for a device copy of known size), as listed
+    in profiles/hbm_traffic_1b.txt; None when the kernel has no recorded figure."""
+    path = ROOT / "profiles" / "hbm_traffic_1b.txt"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        fields = dict(f.split("=", 1) for f in line.split() if "=" in f)
+        if fields.get("kernel") == kernel and "traffic_bytes" in fields:
+            return int(float(fields["traffic_bytes"]))
+    return None
+
+
 def timed(torch, fn, steps, warmup):
     for _ in range(warmup):
         fn()
@@ -159,6 +173,10 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", choices=["attn", "head", "step"],
+                    help="run only W+K launches of one part (for profiler runs) and print its time")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="with --only: also run K device copies of this many MiB (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X "
@@ -177,6 +195,20 @@ def main():
 
     K, W = args.steps, args.warmup
     log = lambda msg: print(f"bench: {msg}", file=sys.stderr, flush=True)
+    if args.only:
+        fn = {"attn": attn_step, "head": head_step, "step": full_step}[args.only]
+        t = timed(torch, fn, K, W)
+        res = {"only": args.only, "steps": K, "warmup": W, "ms": round(t * 1e3, 4)}
+        if args.copy_mib:
+            nbytes = args.copy_mib << 20
+            src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
+            dst = torch.empty_like(src)
+            for _ in range(K):
+                dst.copy_(src)
+            torch.cuda.synchronize()
+            res["copy_bytes"] = nbytes
+        print(json.dumps(res), flush=True)
+        return 0
     step_s = timed(torch, full_step, K, W)
     log(f"full step {step_s * 1e3:.3f} ms")
     attn_s = timed(torch, attn_step, K, 1)
@@ -208,7 +240,7 @@ def main():
         "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(achieved / PEAK_BF16_TFLOPS, 4) if achieved is not None else None,
-        "traffic": None,
+        "traffic": measured_traffic(dom),
         "mean_ms": round(dom_ms, 4),
     }
     out = {

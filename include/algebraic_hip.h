@@ -100,7 +100,7 @@ size_t alg_head_residual_size(int N, int d, int V);
  * in h (N,d) bf16, E (V,d) bf16 (already cast to h's dtype), targets (N) int32;
  * out stat (N) = l^(-1/n), zt (N) = target logits, pt (N) telemetry, obj (1) = mean(1-pt),
  * and, when residual is not NULL, the residual for alg_head_bwd. The clamp
- * X = 1/4 (1e38/V)^(1/n) is derived from V and n. d must be a multiple of 128. */
+ * X = 1/4 (1e38/V)^(1/n) is derived from V and n. d must be a multiple of 8 and N at most 2^23. */
 int alg_head_fwd(alg_stream_t stream, int N, int d, int V,
                  const void* h, const void* E, const int32_t* targets, int n, float c,
                  float* stat, float* zt, float* pt, float* obj, void* residual,

@@ -69,8 +69,8 @@ def test_invalid_arguments_fail_before_launch():
     rc = handle.alg_attn_fwd(None, 0, 1, 1, 64, 64, P(16), P(16), P(16), None, 12, 0, None, 0.0, 1, 1,
                              P(16), None, P(16))
     assert rc == _lib.ALG_ERR_INVALID and b"power of two" in handle.alg_last_error()
-    rc = handle.alg_head_fwd(None, 128, 200, 1000, P(16), P(16), P(16), 8, 2.0, P(16), P(16), P(16), P(16),
-                             None, P(16), 1 << 30)
+    rc = handle.alg_head_fwd(None, 128, 100, 1000, P(16), P(16), P(16), 8, 2.0, P(16), P(16), P(16), P(16),
+                             None, P(16), 1 << 30)  # d = 100: rows not 16-byte aligned
     assert rc == _lib.ALG_ERR_UNSUPPORTED and b"d_model" in handle.alg_last_error()
     rc = handle.alg_head_bwd(None, 128, 256, 1000, P(16), P(16), P(16), P(16), P(16), 8, 2.0, None, P(16), P(16),
                              0, P(16), 16)

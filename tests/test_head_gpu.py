@@ -34,6 +34,7 @@ CASES = [  # (N, d, V)
     (384, 256, 1000),    # token count not a 256 multiple
     (100, 128, 260),     # N < 128 (single ragged token tile)
     (512, 512, 2304),    # several k-step pairs in every product
+    (256, 72, 333),      # d not a multiple of the k step or of a tile
 ]
 
 
