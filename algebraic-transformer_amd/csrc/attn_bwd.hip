@@ -110,14 +110,15 @@ struct RowTile {
   static constexpr int CH = 16 / sizeof(T);
   static constexpr int CPR = D / CH;
   static constexpr int PER = (R * CPR + 255) / 256;  // chunks per thread
+  // Rows past T load the last row instead (clamped, unconditional loads that nothing waits
+  // for until the tile is stored). The query tiles' rows past T carry stat = 0, so their
+  // weights and score gradients are exactly zero and the finite stand-in values add nothing.
   static __device__ __forceinline__ void load(uint4 (&r)[PER], const T* src, int r0, int T_) {
 #pragma unroll
     for (int c = 0; c < PER; ++c) {
       const int idx = threadIdx.x + c * 256;
-      const int row = idx / CPR, col = (idx - row * CPR) * CH;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (row < R && r0 + row < T_) v = *reinterpret_cast<const uint4*>(src + (size_t)(r0 + row) * D + col);
-      r[c] = v;
+      const int row = min(idx / CPR, R - 1), col = (idx - (idx / CPR) * CPR) * CH;
+      r[c] = *reinterpret_cast<const uint4*>(src + (size_t)min(r0 + row, T_ - 1) * D + col);
     }
   }
   // bf16 tiles are unpadded and swizzled (swz_at); f32 tiles are row-major with `pitch`.
@@ -155,7 +156,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
     const bool in_range = *p.flag != 0;
     if ((MODE == MODE_SHIFTED) == in_range) return;
   }
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
+  const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int T_ = p.T;
   const int bh = blockIdx.x;
   const int k0 = blockIdx.y * BWD_BK;  // blockIdx.y = 0 has the most causal work
@@ -210,19 +212,23 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
   auto prefetch = [&](int qbase) {
     QT::load(qr, Q, qbase, T_);
     QT::load(dr, dO, qbase, T_);
-    if (threadIdx.x < BWD_BQ) {
-      const int q = qbase + threadIdx.x;
-      str = q < T_ ? stat[q] : 0.0f;
-      dir = q < T_ ? di[q] : 0.0f;
+    if (threadIdx.x < BWD_BQ) {  // raw loads; rows past T are zeroed when committed
+      const int q = min(qbase + (int)threadIdx.x, T_ - 1);
+      str = stat[q];
+      dir = di[q];
     }
   };
-  auto commit = [&]() {
+  auto commit = [&](int qbase) {
     QT::store(Qs, PITCH, qr);
     QT::store(dOs, PITCH, dr);
-    if (threadIdx.x < BWD_BQ) { st_s[threadIdx.x] = str; di_s[threadIdx.x] = dir; }
+    if (threadIdx.x < BWD_BQ) {
+      const bool live = qbase + (int)threadIdx.x < T_;  // stat = 0 removes rows past T
+      st_s[threadIdx.x] = live ? str : 0.0f;
+      di_s[threadIdx.x] = live ? dir : 0.0f;
+    }
   };
   prefetch(qstart * BWD_BQ);
-  commit();
+  commit(qstart * BWD_BQ);
   __syncthreads();
   for (int qt = qstart; qt < nq; ++qt) {
     const int qbase = qt * BWD_BQ;
@@ -366,7 +372,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
       }
     }
     __syncthreads();
-    if (more) commit();
+    if (more) commit(qbase + BWD_BQ);
     // dQ tile = dS K over this workgroup's keys; each wave takes 32 queries x DBW blocks.
     {
       constexpr int NQH = BWD_BQ / 32;         // 32-query slices of the tile
@@ -381,24 +387,17 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
       if constexpr (BF) {
         const bf16* ds_ = reinterpret_cast<const bf16*>(dSs);
         const bf16* k_ = reinterpret_cast<const bf16*>(Ks);
-        floatx16 dqb[DBW];  // second accumulator chain (odd k steps)
+        // DBW >= 2 independent accumulator chains keep the MFMA pipe busy.
 #pragma unroll
-        for (int j = 0; j < DBW; ++j) dqb[j] = floatx16{};
-#pragma unroll
-        for (int ks = 0; ks < BWD_BK / 16; ks += 2) {
+        for (int ks = 0; ks < BWD_BK / 16; ++ks) {
           const int klo = ks * 16 + 8 * h;
           bf16x8 a0 = swz_tr_frag<SCPR>(ds_, klo, klo + 4, qs * 32, lane);
-          bf16x8 a1 = swz_tr_frag<SCPR>(ds_, klo + 16, klo + 20, qs * 32, lane);
 #pragma unroll
           for (int j = 0; j < DBW; ++j) {
             bf16x8 b0 = swz_tr_frag<CPR>(k_, klo, klo + 4, (db0 + j) * 32, lane);
-            bf16x8 b1 = swz_tr_frag<CPR>(k_, klo + 16, klo + 20, (db0 + j) * 32, lane);
             dqa[j] = mfma_bf16(a0, b0, dqa[j]);
-            dqb[j] = mfma_bf16(a1, b1, dqb[j]);
           }
         }
-#pragma unroll
-        for (int j = 0; j < DBW; ++j) dqa[j] += dqb[j];
       } else {
         const float* ds_ = reinterpret_cast<const float*>(dSs);
         const float* k_ = reinterpret_cast<const float*>(Ks);
@@ -411,14 +410,21 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
         }
       }
       {
+        // Buffer atomics over this slice's rows: the row offset is part of the range-checked
+        // VGPR offset, so rows at or past T (beyond num_records) are dropped by the hardware;
+        // the d-block offset is the scalar offset.
+        const int rowbase = qbase + qs * 32;
+        const int live_rows = max(0, T_ - rowbase);
+        const __amdgpu_buffer_rsrc_t dqr = __builtin_amdgcn_make_buffer_rsrc(
+            dq_acc + (size_t)rowbase * D, (short)0, live_rows * D * 4, BUF_RSRC_WORD3);
+        const int lane_off = (4 * h * D + l32) * 4;
 #pragma unroll
         for (int j = 0; j < DBW; ++j) {
-          const int d = (db0 + j) * 32 + l32;
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int q = qbase + qs * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-            if (q < T_) atomicAdd(dq_acc + (size_t)q * D + d, dqa[j][i]);
-          }
+          for (int i = 0; i < 16; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(dqa[j][i], dqr,
+                                                            lane_off + (8 * (i >> 2) + (i & 3)) * D * 4,
+                                                            (db0 + j) * 128, 0);
         }
       }
     }
@@ -438,6 +444,306 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
         const size_t o = (size_t)key * D + db * 32 + l32;
         DK[o] = (T)(dk[db][i] * slope);
         DV[o] = (T)(dv[db][i]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// main, bf16: query tiles staged by direct global -> LDS copies
+// ---------------------------------------------------------------------------
+// Weight p and score gradient dS for one score (flash.py:333-361); `masked` zeroes both
+// (keys after the query, or query rows at or past T).
+template <int MODE, int L2N>
+__device__ __forceinline__ void bwd_elem(float x, float dp, float stq, float diq, bool masked,
+                                         const AttnBwdParams& p, int log2n, float& pw, float& dsx) {
+  const float s0 = x;
+  float r;
+  if constexpr (MODE == MODE_INRANGE) {
+    pw = pow2n<L2N>(rho_fast(x, r), log2n) * stq;
+  } else if constexpr (MODE == MODE_CLIPPED) {
+    x = fminf(x, p.clamp);
+    float t = rho_fast(x, r);
+    if (p.inv_stat) {
+      pw = pow2n<0>(t, log2n) * stq;
+    } else {
+      pw = pow2n<0>(t * stq, log2n);
+    }
+  } else {
+    if (masked) x = 0.0f;
+    const float t = p.fast_rho ? rho_fast(x, r) : rho_exact(x, r);
+    pw = pow2n<L2N>(t * stq, log2n);
+  }
+  dsx = pw * (dp - diq) * r;
+  if constexpr (MODE == MODE_CLIPPED) dsx = s0 < p.clamp ? dsx : 0.0f;
+  if (masked) {
+    pw = 0.0f;
+    dsx = 0.0f;
+  }
+}
+
+constexpr int BF_BQ = 64;  // queries per streamed tile (bf16 kernel)
+
+// Asynchronous copy of the query tile at qbase (q_s, dO, stat, di) into LDS landing buffers
+// with global_load_lds: lane l of a wave instruction writes 16 (or 4) bytes at base + 16 l
+// (4 l), so each lane fetches the logical chunk the swizzle places there. Rows past T read
+// row T-1 (made inert when the tile is committed).
+template <int D>
+__device__ __forceinline__ void bwd_tile_copy(bf16* pq, bf16* pdo, float* pst, float* pdi, const bf16* Q,
+                                              const bf16* dO, const float* stat, const float* di, int qbase, int T_,
+                                              int wave) {
+  constexpr int CPR = D / 8, RPI = 64 / CPR, PW = BF_BQ * CPR / 64 / 4;  // PW instructions per wave
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < PW; ++j) {
+    const int J = wave * PW + j;
+    const int row = RPI * J + lane / CPR;
+    const int c = (lane % CPR) ^ swz_chunk<CPR>(row);
+    const size_t off = (size_t)min(qbase + row, T_ - 1) * D + 8 * c;
+    __builtin_amdgcn_global_load_lds(Q + off, LDS_PTR(void, pq + J * 512), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(dO + off, LDS_PTR(void, pdo + J * 512), 16, 0, 0);
+  }
+  const int row = min(qbase + lane, T_ - 1);
+  if (wave == 0) __builtin_amdgcn_global_load_lds(stat + row, LDS_PTR(void, pst), 4, 0, 0);
+  if (wave == 1) __builtin_amdgcn_global_load_lds(di + row, LDS_PTR(void, pdi), 4, 0, 0);
+}
+
+// Same decomposition as attn_bwd_kernel (128 keys per workgroup, 32 per wave; dK/dV in
+// registers; dQ via the staged dS and f32 atomics), arranged for one wave per SIMD:
+//  * the tile body has no branches: S and dP of both 32-query blocks, then both blocks'
+//    weights and score gradients (masking by select), then dV and dK, so the scheduler can
+//    overlap the MFMAs of one block with the VALU work of the other;
+//  * the next tile is copied into LDS landing buffers by direct copies issued at the top of
+//    the iteration (no staging registers) and moved into the working tiles after the dS
+//    barrier; the dQ atomics come last, a full tile before the next wait on the counter;
+//  * every LDS access is a per-lane swizzled offset computed once plus an immediate;
+//  * the dQ atomics are buffer atomics whose range check drops rows past T.
+template <int D, int MODE, int L2N>
+__global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) {
+  static_assert(D == 64 || D == 128, "head_dim");
+  constexpr int BQ = BF_BQ, CPR = D / 8, SCPR = BQ / 8, NDB = D / 32, NF = D / 16;
+  __shared__ __attribute__((aligned(16))) bf16 Ks[BWD_BK * D];
+  __shared__ __attribute__((aligned(16))) bf16 Qs[BQ * D];
+  __shared__ __attribute__((aligned(16))) bf16 dOs[BQ * D];
+  __shared__ __attribute__((aligned(16))) bf16 dSs[BWD_BK * BQ];
+  __shared__ __attribute__((aligned(16))) float st_s[BQ];
+  __shared__ __attribute__((aligned(16))) float di_s[BQ];
+  __shared__ __attribute__((aligned(16))) bf16 pre_q[BQ * D];  // landing buffers
+  __shared__ __attribute__((aligned(16))) bf16 pre_do[BQ * D];
+  __shared__ __attribute__((aligned(16))) float pre_st[BQ];
+  __shared__ __attribute__((aligned(16))) float pre_di[BQ];
+
+  if (p.flag) {
+    const bool in_range = *p.flag != 0;
+    if ((MODE == MODE_SHIFTED) == in_range) return;
+  }
+  const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int T_ = p.T;
+  const int bh = blockIdx.x;
+  const int k0 = blockIdx.y * BWD_BK;  // blockIdx.y = 0 has the most causal work
+  const size_t base = (size_t)bh * T_ * D;
+  const bf16* Q = reinterpret_cast<const bf16*>(p.q) + base;
+  const bf16* K = reinterpret_cast<const bf16*>(p.k) + base;
+  const bf16* V = reinterpret_cast<const bf16*>(p.v) + base;
+  const bf16* dO = reinterpret_cast<const bf16*>(p.dO) + base;
+  const float* stat = p.stat + (size_t)bh * T_;
+  const float* di = p.di + (size_t)bh * T_;
+  float* dq_acc = p.dq_acc + base;
+  const int wk0 = k0 + wave * 32;  // this wave's first key
+  const int mykey = wk0 + l32;
+  const int log2n = p.log2n;
+  const int nq = ceil_div(T_, BQ);
+  const int qstart = k0 / BQ;
+
+  bwd_tile_copy<D>(pre_q, pre_do, pre_st, pre_di, Q, dO, stat, di, qstart * BQ, T_, wave);
+  {
+    typedef RowTile<bf16, D, BWD_BK> KT;  // keys past T: finite stand-ins whose dS is zero
+    uint4 kr[KT::PER];
+    KT::load(kr, K, k0, T_);
+    KT::store(Ks, 0, kr);
+  }
+  // K and V fragments of this wave's keys: B operands of S = Q K^T and dP = dO V^T.
+  bf16x8 kf[NF], vf[NF];
+#pragma unroll
+  for (int s = 0; s < NF; ++s) {
+    const bf16x8 z = {};
+    const size_t o = (size_t)mykey * D + 16 * s + 8 * h;
+    kf[s] = mykey < T_ ? ld8(K + o) : z;
+    vf[s] = mykey < T_ ? ld8(V + o) : z;
+  }
+  floatx16 dk[NDB], dv[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+    dk[db] = floatx16{};
+    dv[db] = floatx16{};
+  }
+
+  // Per-lane swizzled offsets: both swizzles repeat every 16 rows, so every access below is
+  // one of these plus a multiple of 16 rows (an immediate offset).
+  constexpr int NQH = BQ / 32;    // 32-query slices of a tile (dQ phase)
+  constexpr int WPH = 4 / NQH;    // waves per slice
+  constexpr int DBW = NDB / WPH;  // 32-wide d blocks per wave
+  static_assert(DBW >= 1, "tile shape");
+  const int qs = wave / WPH;
+  const int db0 = (wave % WPH) * DBW;
+  const int trow = (lane & 15) >> 2;  // row within a transposed read's 4-row group
+  int row_off[NF];                    // row fragments of Q / dO: row l32, k chunk 2 st + h
+#pragma unroll
+  for (int st = 0; st < NF; ++st) row_off[st] = swz_at<CPR>(l32, 16 * st + 8 * h);
+  int tq_lo[NDB], tq_hi[NDB];  // transposed Q / dO fragments: rows 4h + (0..3), 4h + 8 + (0..3)
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+    tq_lo[db] = swz_at<CPR>(4 * h + trow, tr_col(db * 32, lane));
+    tq_hi[db] = swz_at<CPR>(4 * h + 8 + trow, tr_col(db * 32, lane));
+  }
+  const int ts_lo = swz_at<SCPR>(8 * h + trow, tr_col(qs * 32, lane));  // dS, dQ phase
+  const int ts_hi = swz_at<SCPR>(8 * h + 4 + trow, tr_col(qs * 32, lane));
+  int tk_lo[DBW], tk_hi[DBW];  // K, dQ phase
+#pragma unroll
+  for (int j = 0; j < DBW; ++j) {
+    tk_lo[j] = swz_at<CPR>(8 * h + trow, tr_col((db0 + j) * 32, lane));
+    tk_hi[j] = swz_at<CPR>(8 * h + 4 + trow, tr_col((db0 + j) * 32, lane));
+  }
+  // dS writes: row wave*32 + l32, columns 32 sub + 8g + 4h. A column shift is not a constant
+  // offset under the swizzle (only multiples of 16 rows are), so each block has its own.
+  int ds_off[2][4];
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) ds_off[sub][g] = swz_at<SCPR>(wave * 32 + l32, sub * 32 + 8 * g + 4 * h);
+  const int lane_off = (4 * h * D + l32) * 4;  // dQ atomics (bytes)
+
+  // Landing buffers -> working tiles (same swizzled layout: a straight 16-byte copy); rows
+  // past T get stat = 0, which makes their weights and score gradients exactly zero.
+  auto commit = [&](int qbase) {
+    constexpr int CH = BQ * D / 8;
+#pragma unroll
+    for (int c = threadIdx.x; c < CH; c += 256) {
+      reinterpret_cast<uint4*>(Qs)[c] = reinterpret_cast<const uint4*>(pre_q)[c];
+      reinterpret_cast<uint4*>(dOs)[c] = reinterpret_cast<const uint4*>(pre_do)[c];
+    }
+    if (threadIdx.x < BQ) {
+      const bool live = qbase + (int)threadIdx.x < T_;
+      st_s[threadIdx.x] = live ? pre_st[threadIdx.x] : 0.0f;
+      di_s[threadIdx.x] = live ? pre_di[threadIdx.x] : 0.0f;
+    }
+  };
+  __builtin_amdgcn_s_waitcnt(VMCNT0);
+  __syncthreads();
+  commit(qstart * BQ);
+  __syncthreads();
+
+  for (int qt = qstart; qt < nq; ++qt) {
+    const int qbase = qt * BQ;
+    const bool more = qt + 1 < nq;
+    if (more) bwd_tile_copy<D>(pre_q, pre_do, pre_st, pre_di, Q, dO, stat, di, qbase + BQ, T_, wave);
+    // S = Q K^T and dP = dO V^T for both 32-query blocks (lane = key).
+    floatx16 s[2], dp[2];
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      s[sub] = floatx16{};
+      dp[sub] = floatx16{};
+#pragma unroll
+      for (int st = 0; st < NF; ++st) {
+        s[sub] = mfma_bf16(*reinterpret_cast<const bf16x8*>(Qs + sub * 32 * D + row_off[st]), kf[st], s[sub]);
+        dp[sub] = mfma_bf16(*reinterpret_cast<const bf16x8*>(dOs + sub * 32 * D + row_off[st]), vf[st], dp[sub]);
+      }
+    }
+    // Weights P and score gradients dS (rounded to bf16 as the gradient products use them);
+    // blocks that cross the diagonal mask keys after the query (all of them for blocks
+    // wholly before this wave's keys).
+    bf16x8 pa[2][2], da[2][2];
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      const int sq0 = qbase + sub * 32;
+      const bool diag = wk0 + 31 > sq0;
+      float pv[16], dsv[16];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const floatx4 stq = *reinterpret_cast<const floatx4*>(st_s + sub * 32 + 8 * g + 4 * h);
+        const floatx4 diq = *reinterpret_cast<const floatx4*>(di_s + sub * 32 + 8 * g + 4 * h);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 4 * g + e;
+          const bool masked = diag && mykey > sq0 + 8 * g + 4 * h + e;
+          bwd_elem<MODE, L2N>(s[sub][i], dp[sub][i], stq[e], diq[e], masked, p, log2n, pv[i], dsv[i]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        pa[sub][0][j] = f2bf(pv[j]);
+        pa[sub][1][j] = f2bf(pv[8 + j]);
+        da[sub][0][j] = f2bf(dsv[j]);
+        da[sub][1][j] = f2bf(dsv[8 + j]);
+      }
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        bf16x4 v4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v4[e] = f2bf(dsv[4 * g + e]);
+        *reinterpret_cast<bf16x4*>(dSs + ds_off[sub][g]) = v4;  // staged [key][query]
+      }
+    }
+    // dV += P^T dO and dK += dS^T Q (transposed dO / Q fragments from LDS).
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      const bf16* qb = Qs + sub * 32 * D;
+      const bf16* ob = dOs + sub * 32 * D;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        dv[db] = mfma_bf16(pa[sub][0], tr_frag_at(ob, tq_lo[db], tq_hi[db]), dv[db]);
+        dv[db] = mfma_bf16(pa[sub][1], tr_frag_at(ob + 16 * D, tq_lo[db], tq_hi[db]), dv[db]);
+        dk[db] = mfma_bf16(da[sub][0], tr_frag_at(qb, tq_lo[db], tq_hi[db]), dk[db]);
+        dk[db] = mfma_bf16(da[sub][1], tr_frag_at(qb + 16 * D, tq_lo[db], tq_hi[db]), dk[db]);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(VMCNT0);  // this wave's copies of the next tile have landed
+    __syncthreads();                     // dS complete; working tiles no longer read
+    if (more) commit(qbase + BQ);
+    // dQ tile = dS K over this workgroup's keys; each wave takes 32 queries x DBW d blocks.
+    floatx16 dqa[DBW];
+#pragma unroll
+    for (int j = 0; j < DBW; ++j) dqa[j] = floatx16{};
+#pragma unroll
+    for (int ks = 0; ks < BWD_BK / 16; ++ks) {
+      const bf16x8 a0 = tr_frag_at(dSs + ks * 16 * BQ, ts_lo, ts_hi);
+#pragma unroll
+      for (int j = 0; j < DBW; ++j) {
+        const bf16x8 b0 = tr_frag_at(Ks + ks * 16 * D, tk_lo[j], tk_hi[j]);
+        dqa[j] = mfma_bf16(a0, b0, dqa[j]);
+      }
+    }
+    // Buffer atomics over this slice's rows: the row offset is part of the range-checked
+    // VGPR offset, so rows at or past T (beyond num_records) are dropped by the hardware;
+    // the d-block offset is the scalar offset.
+    const int rowbase = qbase + qs * 32;
+    const int live_rows = max(0, T_ - rowbase);
+    const __amdgpu_buffer_rsrc_t dqr = __builtin_amdgcn_make_buffer_rsrc(dq_acc + (size_t)rowbase * D, (short)0,
+                                                                         live_rows * D * 4, BUF_RSRC_WORD3);
+#pragma unroll
+    for (int j = 0; j < DBW; ++j) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(dqa[j][i], dqr, lane_off + (8 * (i >> 2) + (i & 3)) * D * 4,
+                                                        (db0 + j) * 128, 0);
+    }
+    __syncthreads();  // dS consumed; the next tile is in the working tiles
+  }
+
+  // dK = n * acc, dV = acc (flash.py:591-597), rounded to bf16.
+  const float slope = (float)(1 << log2n);
+  bf16* DK = reinterpret_cast<bf16*>(p.dk) + base;
+  bf16* DV = reinterpret_cast<bf16*>(p.dv) + base;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int key = wk0 + 8 * (i >> 2) + 4 * h + (i & 3);
+      if (key < T_) {
+        const size_t o = (size_t)key * D + db * 32 + l32;
+        DK[o] = f2bf(dk[db][i] * slope);
+        DV[o] = f2bf(dv[db][i]);
       }
     }
   }
@@ -473,8 +779,25 @@ __global__ __launch_bounds__(256) void attn_bwd_post_kernel(AttnBwdParams p, siz
   }
 }
 
+template <int D>
+static hipError_t launch_bwd_main_bf16(const AttnBwdParams& p, int mode, hipStream_t st) {
+  dim3 grid(p.B * p.H, ceil_div(p.T, BWD_BK)), block(256);
+  switch (mode) {
+    case MODE_INRANGE: {
+      KTimer t("attn_bwd_inrange", st);
+      if (p.log2n == 4) hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_INRANGE, 4>), grid, block, 0, st, p);
+      else hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_INRANGE, 0>), grid, block, 0, st, p);
+    } break;
+    case MODE_CLIPPED: { KTimer t("attn_bwd_clipped", st); hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_CLIPPED, 0>), grid, block, 0, st, p); } break;
+    case MODE_SHIFTED: { KTimer t("attn_bwd_shifted", st); hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_SHIFTED, 0>), grid, block, 0, st, p); } break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 template <typename T, int D>
 static hipError_t launch_bwd_main(const AttnBwdParams& p, int mode, hipStream_t st) {
+  if constexpr (sizeof(T) == 2) return launch_bwd_main_bf16<D>(p, mode, st);
   dim3 grid(p.B * p.H, ceil_div(p.T, BWD_BK)), block(256);
   switch (mode) {
     case MODE_INRANGE: {

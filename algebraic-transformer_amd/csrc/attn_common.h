@@ -91,6 +91,22 @@ __device__ __forceinline__ bf16x8 swz_tr_frag(const bf16* tile, int k_lo, int k_
   return r;
 }
 
+// Transposed fragment from two precomputed swizzled offsets (ds_read_b64_tr_b16 at
+// tile + lo and tile + hi). Both swizzles above repeat every 16 rows, so fragments 16·m rows
+// apart share the per-lane offsets and differ only by a constant added to `tile`.
+__device__ __forceinline__ bf16x8 tr_frag_at(const bf16* tile, int lo, int hi) {
+  bf16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, tile + lo));
+  bf16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, tile + hi));
+  bf16x8 r;
+  r[0] = a[0]; r[1] = a[1]; r[2] = a[2]; r[3] = a[3];
+  r[4] = b[0]; r[5] = b[1]; r[6] = b[2]; r[7] = b[3];
+  return r;
+}
+// Per-lane column of a transposed fragment read whose block starts at column ncol.
+__device__ __forceinline__ int tr_col(int ncol, int lane) {
+  return ncol + ((lane >> 4) & 1) * 16 + 4 * (lane & 3);
+}
+
 // Row padding (elements) of the f32 tiles, which keep a padded row-major layout.
 constexpr int F32_PAD = 4;
 

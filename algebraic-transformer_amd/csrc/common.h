@@ -30,6 +30,11 @@ typedef float floatx2 __attribute__((ext_vector_type(2)));
 #define BUF_RSRC_WORD3 0x00020000
 
 namespace alg {
+// s_waitcnt immediate for vmcnt(0) with expcnt/lgkmcnt left at their maxima (gfx9 encoding).
+constexpr int VMCNT0 = 0x0F70;
+}  // namespace alg
+
+namespace alg {
 
 __device__ __forceinline__ floatx16 mfma_bf16(const bf16x8& a, const bf16x8& b, const floatx16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);

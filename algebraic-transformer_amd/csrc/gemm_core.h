@@ -24,8 +24,6 @@
 namespace alg {
 
 constexpr int GT_K = 64;
-// s_waitcnt immediate for vmcnt(0) with expcnt/lgkmcnt left at their maxima (gfx9 encoding).
-constexpr int VMCNT0 = 0x0F70;
 enum OperandMode { KMAJOR = 0, MNMAJOR = 1 };
 
 template <int TM_, int TN_, int WM_, int WN_>
