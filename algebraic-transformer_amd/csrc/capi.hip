@@ -74,24 +74,26 @@ AttnWs attn_ws(int B, int H, int T, int D) {
   return w;
 }
 
-// Head buffers. Workspace: [partials f32 nvt*N][obj parts] (+ bwd: dZ^T bf16 V*Npad for the
+// Head buffers. Workspace: [partials f32 nvt*N][obj parts] (+ bwd: dZ bf16 Npad*Vp for the
 // recompute schedule, or s*h/l bf16 N*d for the residual schedule). Residual (optional,
-// forward -> backward): [U^T bf16 V*Npad][l f32 N].
+// forward -> backward): [U bf16 Npad*Vp][l f32 N]. dZ and U are token-major with rows of
+// Vp = V rounded up to 8 (16-byte aligned rows).
 struct HeadWs {
   size_t partial, obj_part, bwd, total;
   size_t res_ut, res_l, res_total;
-  int Npad;
+  int Npad, Vp;
 };
 HeadWs head_ws(int N, int d, int V, int pass, bool residual) {
   HeadWs w;
   w.Npad = alg::head_token_pad(N);
+  w.Vp = alg::head_vocab_pitch(V);
   w.partial = 0;
   w.obj_part = align256((size_t)alg::head_vocab_tiles(V) * N * sizeof(float));
   w.bwd = w.obj_part + align256((size_t)alg::head_stat_blocks(N) * sizeof(float));
-  const size_t bwd_bytes = residual ? (size_t)N * d * 2 : (size_t)V * w.Npad * 2;
+  const size_t bwd_bytes = residual ? (size_t)N * d * 2 : (size_t)w.Npad * w.Vp * 2;
   w.total = pass == 0 ? w.bwd : w.bwd + align256(bwd_bytes);
   w.res_ut = 0;
-  w.res_l = align256((size_t)V * w.Npad * 2);
+  w.res_l = align256((size_t)w.Npad * w.Vp * 2);
   w.res_total = w.res_l + align256((size_t)N * sizeof(float));
   return w;
 }
@@ -101,7 +103,8 @@ int check_head(int N, int d, int V, int n, float c) {
   if (d % 8) return fail(ALG_ERR_UNSUPPORTED, "d_model %d: head rows must be 16-byte aligned (d %% 8 == 0)", d);
   if (alg::head_token_pad(N) > (1 << 23))  // residual rows are addressed with 32-bit buffer offsets
     return fail(ALG_ERR_UNSUPPORTED, "N = %d tokens: at most %d per call", N, 1 << 23);
-  if ((double)N * d > 2.0e9 || (double)V * d > 2.0e9 || (double)V * alg::head_token_pad(N) > 4.0e9)
+  if ((double)N * d > 2.0e9 || (double)V * d > 2.0e9 ||
+      (double)alg::head_vocab_pitch(V) * alg::head_token_pad(N) > 4.0e9)
     return fail(ALG_ERR_INVALID, "head too large");
   const int k = log2_pow2(n);
   if (k < 0 || k > 6) return fail(ALG_ERR_INVALID, "n must be a power of two in [1, 64] (got %d)", n);
@@ -247,7 +250,7 @@ static alg::HeadParams head_params(int N, int d, int V, const void* h, const voi
   p.h = static_cast<const bf16*>(h);
   p.E = static_cast<const bf16*>(E);
   p.targets = targets;
-  p.N = N; p.d = d; p.V = V; p.Npad = ws.Npad;
+  p.N = N; p.d = d; p.V = V; p.Npad = ws.Npad; p.Vp = ws.Vp;
   p.log2n = log2_pow2(n);
   p.c = c;
   p.inv_c = (float)(1.0 / (double)c);

@@ -23,11 +23,15 @@ typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 #define LDS_PTR(T, p) ((__attribute__((address_space(3))) T*)(p))
 
 // Word 3 of a raw buffer descriptor on gfx9-class targets: 32-bit data format, no swizzle.
 #define BUF_RSRC_WORD3 0x00020000
+// Cache-policy bit of buffer instructions (aux operand) marking an access non-temporal.
+#define BUF_NT 2
 
 namespace alg {
 // s_waitcnt immediate for vmcnt(0) with expcnt/lgkmcnt left at their maxima (gfx9 encoding).
@@ -105,6 +109,11 @@ __device__ __forceinline__ float inv_root(float l, int n) {
 
 __device__ __forceinline__ float bf2f(bf16 x) { return (float)x; }
 __device__ __forceinline__ bf16 f2bf(float x) { return (bf16)x; }
+// Two floats rounded to bf16 and packed (a in the low half).
+__device__ __forceinline__ unsigned int pack_bf16x2(float a, float b) {
+  return (unsigned int)__builtin_bit_cast(unsigned short, f2bf(a)) |
+         ((unsigned int)__builtin_bit_cast(unsigned short, f2bf(b)) << 16);
+}
 
 __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
 

@@ -38,7 +38,7 @@ struct GemmOperand {
   const bf16* ptr;
   long ld;         // leading dimension (elements) of the stored matrix
   int rows_valid;  // stored rows at or beyond this are not read
-  int cols_valid;  // stored columns at or beyond this are not read (multiple of 8)
+  int cols_valid;  // stored columns at or beyond this are zero (ld >= cols_valid rounded up to 8)
 };
 
 // One operand tile covering TMN (m or n) x 64 (k) in LDS, unpadded and swizzled.
@@ -95,16 +95,26 @@ struct OperandTile {
       __builtin_amdgcn_global_load_lds(base + off[j & 1], LDS_PTR(void, tile + J * 512), 16, 0, 0);
     }
   }
-  // Synchronous copy with zero fill (partial last k tile).
+  // Synchronous copy with zero fill (edge tiles, partial last k tile): elements outside the
+  // stored matrix, or at k >= K, are zero (per element, so rows may end inside a chunk).
   static __device__ __forceinline__ void copy_zero_fill(bf16* tile, const GemmOperand& op, int mn0, int k0, int K) {
     for (int p = threadIdx.x; p < ROWS * CPR; p += NT) {
       const int row = p / CPR, c = p - row * CPR;
       const int grow = (MODE == KMAJOR) ? mn0 + row : k0 + row;
       const int gcol = (MODE == KMAJOR) ? k0 + 8 * c : mn0 + 8 * c;
-      const bool kin = (MODE == KMAJOR) ? gcol < K : grow < K;
+      const int col_end = (MODE == KMAJOR) ? min(K, op.cols_valid) : op.cols_valid;
+      const bool row_ok = grow < op.rows_valid && ((MODE == KMAJOR) || grow < K);
+      const int nv = row_ok ? min(8, col_end - gcol) : 0;  // live elements of this chunk
       uint4 v = make_uint4(0, 0, 0, 0);
-      if (kin && grow < op.rows_valid && gcol < op.cols_valid)
-        v = *reinterpret_cast<const uint4*>(op.ptr + (long)grow * op.ld + gcol);
+      if (nv > 0) v = *reinterpret_cast<const uint4*>(op.ptr + (long)grow * op.ld + gcol);
+      if (nv < 8) {  // keep elements [0, nv): two bf16 per 32-bit word
+        unsigned int* w = reinterpret_cast<unsigned int*>(&v);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const unsigned int keep = nv >= 2 * q + 2 ? 0xffffffffu : (nv == 2 * q + 1 ? 0x0000ffffu : 0u);
+          w[q] &= keep;
+        }
+      }
       *reinterpret_cast<uint4*>(tile + at(row, c)) = v;
     }
   }

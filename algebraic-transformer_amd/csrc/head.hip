@@ -13,11 +13,11 @@
 // Backward, two schedules over the same GEMM core:
 //  * residual (3 products): with p = w/l the logit gradient is
 //        dz = s (p - y) r = (s/l) U',  U' = w r except U'_t = (w_t - l) r_t,
-//    so the forward epilogue also stores U = bf16(w r) vocab-major and the statistics kernel
+//    so the forward epilogue also stores U = bf16(w r) token-major and the statistics kernel
 //    patches the target entries once l is known. Then dh = (s/l) (U' E) and
 //    dE = U'^T (s h / l): no logit recompute.
 //  * recompute (4 products, the reference's schedule, fused_head.py:120-156, 194-216): the
-//    backward recomputes z, writes bf16(s (p - y) r) vocab-major, then dh = dZ E and
+//    backward recomputes z, writes bf16(s (p - y) r) token-major, then dh = dZ E and
 //    dE = dZ^T h.
 // Every product reads its operands in their natural layout (k-contiguous fragments via
 // ds_read_b128, transposed ones via ds_read_b64_tr_b16).
@@ -62,42 +62,72 @@ __global__ __launch_bounds__(NT, 1) void head_fwd_kernel(HeadParams p) {
   wave_coords<HC>(wm, wn);
   const float inv_c = p.inv_c, clamp = p.clamp;
   const int vrow0 = m0 + wm * HC::WTM;  // first vocab row of this wave
-  // Interior tile (every row and column live); WITH_U also stores the residual.
+  // Interior tile (every row and column live); WITH_U also stores the residual. U is
+  // token-major (element (tok, v) at tok * Vp + v). Each wave stages its 128 (v) x 64 (tok)
+  // block of U in its own 16 KB of the (now idle) pipeline buffers as [tok][v] rows of 256 B,
+  // 16-byte chunks XOR-swizzled by (tok & 15), then writes it back with 16-byte stores that
+  // cover 4 whole token rows (8 full cache lines) per instruction, marked non-temporal so the
+  // 1 GB stream of U does not evict the E / h panels the GEMM is reusing from L2.
+  static_assert(HC::WTM == 128 && HC::WTN == 64 && HC::THREADS == 512, "U staging assumes 128x64 wave tiles");
   auto interior = [&](auto with_u) {
     constexpr bool WITH_U = decltype(with_u)::value;
-    const size_t rest = (size_t)(p.V - vrow0) * p.Npad * 2;  // bytes of U from this wave's first row
-    const __amdgpu_buffer_rsrc_t urs = __builtin_amdgcn_make_buffer_rsrc(
-        p.ut + (size_t)vrow0 * p.Npad, (short)0, (int)std::min<size_t>(rest, 0x7fffffff), BUF_RSRC_WORD3);
+    bf16* ub = nullptr;
+    if constexpr (WITH_U) {
+      __syncthreads();  // every wave is done reading the pipeline buffers
+      const int w8 = wm * HC::WN + wn;
+      ub = reinterpret_cast<bf16*>(w8 < 4 ? static_cast<void*>(&s0) : static_cast<void*>(&s1)) + (w8 & 3) * 8192;
+    }
+    auto ub_at = [](int tl, int vl) { return tl * 128 + (((vl >> 3) ^ (tl & 15)) << 3) + (vl & 7); };
 #pragma unroll
     for (int nb = 0; nb < HC::NB; ++nb) {
       const int col = wn * HC::WTN + nb * 32 + l32;
       const int tok = n0 + col;
       const int dt = p.targets[tok] - vrow0 - 4 * h;  // target row relative to this lane's rows
-      // U rows of this wave through a buffer descriptor: the row offset c * Npad is a scalar
-      // (soffset), the lane offset (4h rows + token) a fixed 32-bit voffset.
-      const int uvoff = (4 * h * p.Npad + tok) * 2;
       float part = 0.0f, ztv = 0.0f;
       bool hit = false;
 #pragma unroll
       for (int mb = 0; mb < HC::MB; ++mb) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int c = mb * 32 + 8 * (i >> 2) + (i & 3);  // lane row offset (without 4h)
-          const float z = acc[mb][nb][i];
-          const float x = fminf(z * inv_c, clamp);  // fused_head.py:98
-          float r;
-          const float w = pow2n<L2N>(rho_fast(x, r), p.log2n);
-          part += w;
-          if constexpr (WITH_U)
-            __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, f2bf(w * r)), urs, uvoff,
-                                                  c * p.Npad * 2, 0);
-          ztv = dt == c ? z : ztv;
-          hit = hit || dt == c;
+        for (int g = 0; g < 4; ++g) {
+          float u[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int c = mb * 32 + 8 * g + e;  // lane row offset (without 4h)
+            const float z = acc[mb][nb][4 * g + e];
+            const float x = fminf(z * inv_c, clamp);  // fused_head.py:98
+            float r;
+            const float w = pow2n<L2N>(rho_fast(x, r), p.log2n);
+            part += w;
+            u[e] = w * r;
+            ztv = dt == c ? z : ztv;
+            hit = hit || dt == c;
+          }
+          if constexpr (WITH_U) {
+            u32x2 pk;
+            pk[0] = pack_bf16x2(u[0], u[1]);
+            pk[1] = pack_bf16x2(u[2], u[3]);
+            *reinterpret_cast<u32x2*>(ub + ub_at(nb * 32 + l32, mb * 32 + 8 * g + 4 * h)) = pk;
+          }
         }
       }
       if (hit) p.zt[tok] = ztv;
       part += xor32(part);
       if (h == 0) red[wm][col] = part;
+    }
+    if constexpr (WITH_U) {
+      // Rows of this wave's block: tokens n0 + wn*64 + (0..63), vocabulary vrow0 + (0..127).
+      const size_t ubase = (size_t)(n0 + wn * HC::WTN) * p.Vp + vrow0;
+      const size_t rest = ((size_t)p.Npad * p.Vp - ubase) * 2;  // bytes of U from the base
+      const __amdgpu_buffer_rsrc_t urs = __builtin_amdgcn_make_buffer_rsrc(
+          p.ut + ubase, (short)0, (int)std::min<size_t>(rest, 0x7fffffff), BUF_RSRC_WORD3);
+      const int ch = lane & 15;
+      const int voff = ((lane >> 4) * p.Vp + ch * 8) * 2;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int tl = 4 * j + (lane >> 4);
+        const u32x4 v = *reinterpret_cast<const u32x4*>(ub + ub_at(tl, ch * 8));
+        __builtin_amdgcn_raw_buffer_store_b128(v, urs, voff, 4 * j * p.Vp * 2, BUF_NT);
+      }
     }
   };
   if (m0 + HT_M <= p.V && n0 + HT_N <= p.N) {
@@ -122,7 +152,7 @@ __global__ __launch_bounds__(NT, 1) void head_fwd_kernel(HeadParams p) {
           const float w = pow2n<L2N>(rho_fast(x, r), p.log2n);
           if (v < p.V) {
             part += w;
-            if (p.ut) p.ut[(size_t)v * p.Npad + tok] = f2bf(live ? w * r : 0.0f);
+            if (p.ut && live) p.ut[(size_t)tok * p.Vp + v] = f2bf(w * r);
           }
           if (v == tgt) p.zt[tok] = z;
         }
@@ -164,7 +194,7 @@ __global__ __launch_bounds__(256) void head_stats_kernel(HeadParams p, int nvt) 
       if (tgt >= 0 && tgt < p.V) {
         float r;
         const float w = head_w(zt, p, r);
-        p.ut[(size_t)tgt * p.Npad + tok] = f2bf((w - l) * r);
+        p.ut[(size_t)tok * p.Vp + tgt] = f2bf((w - l) * r);
       }
     }
   }
@@ -225,8 +255,7 @@ __global__ __launch_bounds__(NT, 1) void head_dz_kernel(HeadParams p) {
         float t = rho_fast(x, r) * st;
         for (int e = 0; e < p.log2n; ++e) t = t * t;
         const float y = (v == tgt) ? 1.0f : 0.0f;
-        const float dz = live ? (t - y) * r * scale : 0.0f;
-        p.dzt[(size_t)v * p.Npad + tok] = f2bf(dz);
+        if (live) p.dzt[(size_t)tok * p.Vp + v] = f2bf((t - y) * r * scale);  // token-major
       }
     }
   }
@@ -247,19 +276,19 @@ __global__ __launch_bounds__(256) void head_hscale_kernel(HeadParams p) {
   }
 }
 
-// dh = (U' or dZ) E: A stored [v][n] (m-contiguous), B = E stored [v][d] (n-contiguous).
-// The residual schedule scales token rows by s/l.
+// dh = (U' or dZ) E: A stored token-major [n][v] (k-contiguous), B = E stored [v][d]
+// (n-contiguous). The residual schedule scales token rows by s/l.
 __global__ __launch_bounds__(NT, 1) void head_dh_kernel(HeadParams p) {
-  __shared__ __attribute__((aligned(16))) GemmStage<MNMAJOR, MNMAJOR, HC> s0, s1;
+  __shared__ __attribute__((aligned(16))) GemmStage<KMAJOR, MNMAJOR, HC> s0, s1;
   const int nbm = p.Npad / HT_M, nbn = (p.d + HT_N - 1) / HT_N;
   int tm, tn;
   xcd_tile(blockIdx.x, nbm, nbn, tm, tn);
   const int m0 = tm * HT_M;  // tokens
   const int n0 = tn * HT_N;  // d
   const bf16* a = p.ut ? p.ut : p.dzt;
-  GemmOperand A{a, p.Npad, p.V, p.Npad}, B{p.E, p.d, p.V, p.d};
+  GemmOperand A{a, p.Vp, p.N, p.V}, B{p.E, p.d, p.V, p.d};
   floatx16 acc[HC::MB][HC::NB];
-  gemm_mainloop<MNMAJOR, MNMAJOR, HC>(s0, s1, A, B, m0, n0, p.V, acc);
+  gemm_mainloop<KMAJOR, MNMAJOR, HC>(s0, s1, A, B, m0, n0, p.V, acc);
   const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
   int wm, wn;
   wave_coords<HC>(wm, wn);
@@ -280,9 +309,10 @@ __global__ __launch_bounds__(NT, 1) void head_dh_kernel(HeadParams p) {
   }
 }
 
-// dE = (U' or dZ)^T (hs or h): A stored [v][n] (k-contiguous), B stored [n][d] (n-contiguous).
+// dE = (U' or dZ)^T (hs or h): A = U' stored token-major [n][v] (m-contiguous), B stored
+// [n][d] (n-contiguous).
 __global__ __launch_bounds__(NT, 1) void head_de_kernel(HeadParams p) {
-  __shared__ __attribute__((aligned(16))) GemmStage<KMAJOR, MNMAJOR, HC> s0, s1;
+  __shared__ __attribute__((aligned(16))) GemmStage<MNMAJOR, MNMAJOR, HC> s0, s1;
   const int nbm = (p.V + HT_M - 1) / HT_M, nbn = (p.d + HT_N - 1) / HT_N;
   int tm, tn;
   xcd_tile(blockIdx.x, nbm, nbn, tm, tn);
@@ -290,9 +320,9 @@ __global__ __launch_bounds__(NT, 1) void head_de_kernel(HeadParams p) {
   const int n0 = tn * HT_N;  // d
   const bf16* a = p.ut ? p.ut : p.dzt;
   const bf16* b = p.ut ? p.hs : p.h;
-  GemmOperand A{a, p.Npad, p.V, p.Npad}, B{b, p.d, p.N, p.d};
+  GemmOperand A{a, p.Vp, p.N, p.V}, B{b, p.d, p.N, p.d};
   floatx16 acc[HC::MB][HC::NB];
-  gemm_mainloop<KMAJOR, MNMAJOR, HC>(s0, s1, A, B, m0, n0, p.N, acc);
+  gemm_mainloop<MNMAJOR, MNMAJOR, HC>(s0, s1, A, B, m0, n0, p.N, acc);
   const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
   int wm, wn;
   wave_coords<HC>(wm, wn);
@@ -316,6 +346,7 @@ __global__ __launch_bounds__(NT, 1) void head_de_kernel(HeadParams p) {
 
 int head_vocab_tiles(int V) { return (V + HT_M - 1) / HT_M; }
 int head_token_pad(int N) { return ((N + HT_N - 1) / HT_N) * HT_N; }
+int head_vocab_pitch(int V) { return (V + 7) / 8 * 8; }
 int head_stat_blocks(int N) { return (N + 255) / 256; }
 
 hipError_t launch_head_fwd(const HeadParams& p, hipStream_t st) {

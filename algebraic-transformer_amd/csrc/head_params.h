@@ -20,6 +20,7 @@ struct HeadParams {
   const bf16* E;        // (V, d), already in h's dtype (fused_head.py:168)
   const int* targets;   // (N,)
   int N, d, V, Npad;    // Npad = N rounded up to the GEMM tile
+  int Vp;               // row pitch of the token-major U / dZ: V rounded up to 8
   int log2n;
   float inv_c, c, clamp;
   float* partial;       // (ceil(V/HT_M), N) per-vocab-tile row sums
@@ -29,9 +30,9 @@ struct HeadParams {
   float* obj_part;      // (nblocks,)
   float* obj;           // (1,)
   const float* g;       // (1,) cotangent of the objective
-  bf16* ut;             // residual (V, Npad): bf16(w r), target entry (w_t - l) r_t; or nullptr
+  bf16* ut;             // residual (Npad, Vp): bf16(w r), target entry (w_t - l) r_t; or nullptr
   float* lsum;          // residual (N,): l = sum_v w; or nullptr
-  bf16* dzt;            // recompute path workspace (V, Npad): bf16(s (p - y) r)
+  bf16* dzt;            // recompute path workspace (Npad, Vp): bf16(s (p - y) r)
   bf16* hs;             // residual path workspace (N, d): bf16(s h / l)
   bf16* dh;             // (N, d)
   void* dE;             // (V, d) bf16 or f32

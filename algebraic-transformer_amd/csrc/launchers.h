@@ -16,6 +16,7 @@ hipError_t launch_attn_prep(const PrepParams& p, bool bf16_io, GuardParams g, hi
 
 int head_vocab_tiles(int V);
 int head_token_pad(int N);
+int head_vocab_pitch(int V);
 int head_stat_blocks(int N);
 hipError_t launch_head_fwd(const HeadParams& p, hipStream_t st);
 hipError_t launch_head_bwd(const HeadParams& p, hipStream_t st);
