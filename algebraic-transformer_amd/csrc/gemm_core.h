@@ -316,4 +316,14 @@ __device__ __forceinline__ void xcd_tile(int bid, int nbm, int nbn, int& tm, int
   tn = r / gm;
 }
 
+// Row-major order inside each XCD's contiguous share of the tiles: the tiles an XCD runs
+// together cover a few A row panels with every B column panel, so each A panel is streamed
+// from memory once (for products whose A operand is large and B small).
+__device__ __forceinline__ void xcd_tile_rowmajor(int bid, int nbm, int nbn, int& tm, int& tn) {
+  const int total = nbm * nbn;
+  const int lin = total % 8 == 0 ? (bid % 8) * (total / 8) + bid / 8 : bid;
+  tm = lin / nbn;
+  tn = lin - tm * nbn;
+}
+
 }  // namespace alg

@@ -63,21 +63,27 @@ __global__ __launch_bounds__(NT, 1) void head_fwd_kernel(HeadParams p) {
   const float inv_c = p.inv_c, clamp = p.clamp;
   const int vrow0 = m0 + wm * HC::WTM;  // first vocab row of this wave
   // Interior tile (every row and column live); WITH_U also stores the residual. U is
-  // token-major (element (tok, v) at tok * Vp + v). Each wave stages its 128 (v) x 64 (tok)
-  // block of U in its own 16 KB of the (now idle) pipeline buffers as [tok][v] rows of 256 B,
-  // 16-byte chunks XOR-swizzled by (tok & 15), then writes it back with 16-byte stores that
-  // cover 4 whole token rows (8 full cache lines) per instruction, marked non-temporal so the
+  // token-major (element (tok, v) at tok * Vp + v). Each wave stages its WTM (v) x WTN (tok)
+  // block of U in its own share of the (now idle) pipeline buffers as [tok][v] rows,
+  // 16-byte chunks XOR-swizzled by the token, then writes it back with 16-byte stores that
+  // cover whole token rows (full cache lines) per instruction, marked non-temporal so the
   // 1 GB stream of U does not evict the E / h panels the GEMM is reusing from L2.
-  static_assert(HC::WTM == 128 && HC::WTN == 64 && HC::THREADS == 512, "U staging assumes 128x64 wave tiles");
+  constexpr int UCH = HC::WTM / 8;          // 16-byte chunks per staged token row
+  constexpr int UWAVE = HC::WTM * HC::WTN;  // staged elements per wave
+  constexpr int NWAVES = HC::THREADS / 64;
+  static_assert(UCH <= 64 && 64 % UCH == 0 && (UCH & (UCH - 1)) == 0, "staged row width");
+  static_assert(NWAVES * UWAVE * 2 <= 2 * (int)sizeof(s0), "staging fits the pipeline buffers");
+  static_assert((NWAVES / 2) * UWAVE * 2 <= (int)sizeof(s0) || NWAVES == 1, "half the waves per stage");
   auto interior = [&](auto with_u) {
     constexpr bool WITH_U = decltype(with_u)::value;
     bf16* ub = nullptr;
     if constexpr (WITH_U) {
       __syncthreads();  // every wave is done reading the pipeline buffers
-      const int w8 = wm * HC::WN + wn;
-      ub = reinterpret_cast<bf16*>(w8 < 4 ? static_cast<void*>(&s0) : static_cast<void*>(&s1)) + (w8 & 3) * 8192;
+      const int wi = wm * HC::WN + wn;
+      ub = reinterpret_cast<bf16*>(wi < NWAVES / 2 ? static_cast<void*>(&s0) : static_cast<void*>(&s1)) +
+           (wi % (NWAVES / 2)) * UWAVE;
     }
-    auto ub_at = [](int tl, int vl) { return tl * 128 + (((vl >> 3) ^ (tl & 15)) << 3) + (vl & 7); };
+    auto ub_at = [](int tl, int vl) { return tl * HC::WTM + (((vl >> 3) ^ (tl & (UCH - 1))) << 3) + (vl & 7); };
 #pragma unroll
     for (int nb = 0; nb < HC::NB; ++nb) {
       const int col = wn * HC::WTN + nb * 32 + l32;
@@ -120,13 +126,14 @@ __global__ __launch_bounds__(NT, 1) void head_fwd_kernel(HeadParams p) {
       const size_t rest = ((size_t)p.Npad * p.Vp - ubase) * 2;  // bytes of U from the base
       const __amdgpu_buffer_rsrc_t urs = __builtin_amdgcn_make_buffer_rsrc(
           p.ut + ubase, (short)0, (int)std::min<size_t>(rest, 0x7fffffff), BUF_RSRC_WORD3);
-      const int ch = lane & 15;
-      const int voff = ((lane >> 4) * p.Vp + ch * 8) * 2;
+      constexpr int RPS = 64 / UCH;  // token rows per store instruction
+      const int ch = lane % UCH;
+      const int voff = ((lane / UCH) * p.Vp + ch * 8) * 2;
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int tl = 4 * j + (lane >> 4);
+      for (int j = 0; j < HC::WTN / RPS; ++j) {
+        const int tl = RPS * j + lane / UCH;
         const u32x4 v = *reinterpret_cast<const u32x4*>(ub + ub_at(tl, ch * 8));
-        __builtin_amdgcn_raw_buffer_store_b128(v, urs, voff, 4 * j * p.Vp * 2, BUF_NT);
+        __builtin_amdgcn_raw_buffer_store_b128(v, urs, voff, RPS * j * p.Vp * 2, BUF_NT);
       }
     }
   };
@@ -282,7 +289,7 @@ __global__ __launch_bounds__(NT, 1) void head_dh_kernel(HeadParams p) {
   __shared__ __attribute__((aligned(16))) GemmStage<KMAJOR, MNMAJOR, HC> s0, s1;
   const int nbm = p.Npad / HT_M, nbn = (p.d + HT_N - 1) / HT_N;
   int tm, tn;
-  xcd_tile(blockIdx.x, nbm, nbn, tm, tn);
+  xcd_tile_rowmajor(blockIdx.x, nbm, nbn, tm, tn);  // U panels streamed once
   const int m0 = tm * HT_M;  // tokens
   const int n0 = tn * HT_N;  // d
   const bf16* a = p.ut ? p.ut : p.dzt;
@@ -315,7 +322,7 @@ __global__ __launch_bounds__(NT, 1) void head_de_kernel(HeadParams p) {
   __shared__ __attribute__((aligned(16))) GemmStage<MNMAJOR, MNMAJOR, HC> s0, s1;
   const int nbm = (p.V + HT_M - 1) / HT_M, nbn = (p.d + HT_N - 1) / HT_N;
   int tm, tn;
-  xcd_tile(blockIdx.x, nbm, nbn, tm, tn);
+  xcd_tile_rowmajor(blockIdx.x, nbm, nbn, tm, tn);  // U panels streamed once
   const int m0 = tm * HT_M;  // vocab
   const int n0 = tn * HT_N;  // d
   const bf16* a = p.ut ? p.ut : p.dzt;
