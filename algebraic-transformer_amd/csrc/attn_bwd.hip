@@ -4,19 +4,24 @@
 // resident backward schedules), 630-645 (di), 694-726 (sink VJP) and
 // src/algebraic/kernels/head_resident.py:91-119.
 //
-// Three launches:
+// Launches:
 //   pre   di = sum_d dO*o per row (from the rounded output in range, the f32 output when
-//         shifted; flash.py:633), zero the f32 dQ accumulator, per-(b,h,block) partial sums
-//         of mass*di for the sink gradient (flash.py:694-705, 721-723).
-//   main  one workgroup = 4 waves = 128 keys of one (b,h); dK/dV accumulate in registers
-//         while the kernel streams 64-query tiles of Q and dO through LDS. Scores are
-//         formed as S = Q K^T so a lane owns one key column; P^T and dS^T feed dV += P^T dO
-//         and dK += dS^T Q directly as MFMA A operands, with dO/Q fragments transposed by
-//         ds_read_b64_tr_b16. dS is staged in LDS ([key][query]) and each wave forms one
-//         quarter of the tile's dQ = dS K over the workgroup's 128 keys, added to the f32
-//         accumulator with one atomic per element per key block (no per-key-block dQ
-//         partials in HBM, unlike flash.py:537-544).
-//   post  dq = round(round(n * acc) * dq_scale) and the per-head sink gradient.
+//         shifted; flash.py:633), per-(b,h,block) partial sums of mass*di for the sink
+//         gradient (flash.py:694-705, 721-723); for f32 inputs also zeroes the dQ accumulator.
+//   main  key-stationary: one workgroup = 4 waves = 128 keys of one (b,h); dK/dV accumulate
+//         in registers while the kernel streams 64-query tiles of Q and dO through LDS.
+//         Scores are formed as S = Q K^T so a lane owns one key column; P^T and dS^T feed
+//         dV += P^T dO and dK += dS^T Q directly as MFMA A operands, with dO/Q fragments
+//         transposed by ds_read_b64_tr_b16.
+//   dq    (bf16) query-stationary: one workgroup = 128 queries; S^T and dP^T are formed
+//         again and dQ^T += K^T dS^T accumulates in registers, written once. No atomics and
+//         no per-key-block dQ partials (unlike flash.py:537-544); f32 atomics run at about
+//         a sixth of the store bandwidth on this GPU, so recomputing two products is cheaper.
+//         f32 inputs keep the single key-stationary kernel with dQ added to an f32
+//         accumulator by atomics (one per element per key block).
+//   post  the per-head sink gradient; for f32, dq = round(round(n * acc) * dq_scale).
+#include <type_traits>
+
 #include "attn_common.h"
 
 namespace alg {
@@ -31,7 +36,7 @@ constexpr int PRE_ROWS = 256;  // rows per pre-kernel workgroup
 // pre: di, dq_acc = 0, sink partials
 // ---------------------------------------------------------------------------
 template <typename T>
-__global__ __launch_bounds__(256) void attn_bwd_pre_kernel(AttnBwdParams p, int D) {
+__global__ __launch_bounds__(256) void attn_bwd_pre_kernel(AttnBwdParams p, int D, bool zero_dq) {
   const int bh = blockIdx.x;
   const int head = bh % p.H;
   const int T_ = p.T;
@@ -47,50 +52,60 @@ __global__ __launch_bounds__(256) void attn_bwd_pre_kernel(AttnBwdParams p, int 
   const bool inv_stat = !shifted && (p.mode != MODE_CLIPPED || p.inv_stat);
   const float rbn = ipow_rt(rb, n);
   float part = 0.0f;
-  // 8 elements per lane, D/8 lanes per row (vector loads of dO, o; vector zero-fill of dq_acc).
+  // 8 elements per lane, D/8 lanes per row (vector loads of dO, o; vector zero-fill of dq_acc);
+  // each lane loads PRE_U rows before reducing any, to keep more bytes in flight.
+  constexpr int PRE_U = 4;
   const int lpr = D / 8, rpw = 64 / lpr;
   const int sub = lane / lpr, li = lane - sub * lpr;
   const int rend = min(row0 + PRE_ROWS, T_);
-  for (int r0 = row0 + wave * rpw; r0 < rend; r0 += 4 * rpw) {
-    const int r = r0 + sub;
-    const bool ok = r < rend;
-    float s = 0.0f;
-    if (ok) {
-      const size_t off = ((size_t)bh * T_ + r) * D + li * 8;
-      float dov[8], ov[8];
+  for (int r0 = row0 + wave * rpw; r0 < rend; r0 += 4 * rpw * PRE_U) {
+    float dov[PRE_U][8], ov[PRE_U][8];
+#pragma unroll
+    for (int u = 0; u < PRE_U; ++u) {
+      const int r = r0 + u * 4 * rpw + sub;
+      const size_t off = ((size_t)bh * T_ + min(r, rend - 1)) * D + li * 8;
       if constexpr (sizeof(T) == 2) {
         const bf16x8 a = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p.dO) + off);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dov[j] = (float)a[j];
+        for (int j = 0; j < 8; ++j) dov[u][j] = (float)a[j];
       } else {
         const floatx4 a0 = *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(p.dO) + off);
         const floatx4 a1 = *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(p.dO) + off + 4);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) { dov[j] = a0[j]; dov[4 + j] = a1[j]; }
+        for (int j = 0; j < 4; ++j) { dov[u][j] = a0[j]; dov[u][4 + j] = a1[j]; }
       }
       if (precise || sizeof(T) == 4) {
         const float* src = precise ? p.o_precise + off : reinterpret_cast<const float*>(p.o) + off;
         const floatx4 b0 = *reinterpret_cast<const floatx4*>(src);
         const floatx4 b1 = *reinterpret_cast<const floatx4*>(src + 4);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) { ov[j] = b0[j]; ov[4 + j] = b1[j]; }
+        for (int j = 0; j < 4; ++j) { ov[u][j] = b0[j]; ov[u][4 + j] = b1[j]; }
       } else {
         const bf16x8 b = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p.o) + off);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) ov[j] = (float)b[j];
+        for (int j = 0; j < 8; ++j) ov[u][j] = (float)b[j];
       }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) s += dov[j] * ov[j];
-      const floatx4 z = {};
-      *reinterpret_cast<floatx4*>(p.dq_acc + off) = z;
-      *reinterpret_cast<floatx4*>(p.dq_acc + off + 4) = z;
     }
-    for (int m = 1; m < lpr; m <<= 1) s += __shfl_xor(s, m, 64);
-    if (ok && li == 0) {
-      p.di[(size_t)bh * T_ + r] = s;
-      const float st = p.stat[(size_t)bh * T_ + r];
-      const float mass = inv_stat ? rbn * st : ipow_rt(rb * st, n);
-      part += mass * s;
+#pragma unroll
+    for (int u = 0; u < PRE_U; ++u) {
+      const int r = r0 + u * 4 * rpw + sub;
+      const bool ok = r < rend;
+      float s = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s += dov[u][j] * ov[u][j];
+      if (ok && zero_dq) {
+        const size_t off = ((size_t)bh * T_ + r) * D + li * 8;
+        const floatx4 z = {};
+        *reinterpret_cast<floatx4*>(p.dq_acc + off) = z;
+        *reinterpret_cast<floatx4*>(p.dq_acc + off + 4) = z;
+      }
+      for (int m = 1; m < lpr; m <<= 1) s += __shfl_xor(s, m, 64);
+      if (ok && li == 0) {
+        p.di[(size_t)bh * T_ + r] = s;
+        const float st = p.stat[(size_t)bh * T_ + r];
+        const float mass = inv_stat ? rbn * st : ipow_rt(rb * st, n);
+        part += mass * s;
+      }
     }
   }
   for (int m = 1; m < 64; m <<= 1) part += __shfl_xor(part, m, 64);
@@ -483,55 +498,103 @@ __device__ __forceinline__ void bwd_elem(float x, float dp, float stq, float diq
 }
 
 constexpr int BF_BQ = 64;  // queries per streamed tile (bf16 kernel)
+constexpr int BWD_XCDS = 8;    // workgroup i runs on XCD i % 8
+constexpr int BWD_GROUP = 4;   // heads whose key blocks one XCD interleaves
 
-// Asynchronous copy of the query tile at qbase (q_s, dO, stat, di) into LDS landing buffers
-// with global_load_lds: lane l of a wave instruction writes 16 (or 4) bytes at base + 16 l
-// (4 l), so each lane fetches the logical chunk the swizzle places there. Rows past T read
-// row T-1 (made inert when the tile is committed).
+// Workgroup -> (head, key block) of the bf16 main kernel (1-D grid). Each XCD works through
+// its own share of the heads in groups of BWD_GROUP, key block by key block within a group
+// (heaviest causal blocks first), so the dQ rows and query tiles of only a few heads are live
+// in that XCD's L2 at a time. Head counts that do not split evenly over the XCDs use the
+// plain key-block-major order.
+__device__ __forceinline__ void bwd_block_coords(int nbh, int nkb, int& bh, int& kblk) {
+  const int L = blockIdx.x;
+  if (nbh % (BWD_XCDS * BWD_GROUP) == 0) {
+    const int xcd = L % BWD_XCDS, idx = L / BWD_XCDS;
+    const int g = idx / (BWD_GROUP * nkb), r = idx - g * BWD_GROUP * nkb;
+    kblk = r / BWD_GROUP;
+    bh = xcd * (nbh / BWD_XCDS) + g * BWD_GROUP + (r - kblk * BWD_GROUP);
+  } else {
+    bh = L % nbh;
+    kblk = L / nbh;
+  }
+}
+
+// Copy of one 64-row tile (rows qbase.., D columns) of two (T, D) bf16 matrices into LDS with
+// range-checked buffer loads that write LDS directly: lane l of a wave instruction writes 16
+// bytes at base + 16 l, so each lane fetches the logical chunk the swizzle places there. Rows
+// at or past T lie beyond the descriptors' ranges and land as zeros. The destinations are
+// passed through an empty asm so the compiler cannot tie these copies to a particular LDS
+// array: it then inserts no wait for them before reads of the other buffer set. Every read
+// of a copied tile is preceded by the explicit vmcnt(0) + barrier of the tile before it.
 template <int D>
-__device__ __forceinline__ void bwd_tile_copy(bf16* pq, bf16* pdo, float* pst, float* pdi, const bf16* Q,
-                                              const bf16* dO, const float* stat, const float* di, int qbase, int T_,
-                                              int wave) {
-  constexpr int CPR = D / 8, RPI = 64 / CPR, PW = BF_BQ * CPR / 64 / 4;  // PW instructions per wave
-  const int lane = threadIdx.x & 63;
+__device__ __forceinline__ void bwd_tile_dma2(bf16* la, bf16* lb, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
+                                              int r0, int wave, int lane) {
+  constexpr int CPR = D / 8, RPI = 64 / CPR, PW = 64 * CPR / 64 / 4;  // PW instructions per wave
+  asm volatile("" : "+s"(la), "+s"(lb));
 #pragma unroll
   for (int j = 0; j < PW; ++j) {
     const int J = wave * PW + j;
     const int row = RPI * J + lane / CPR;
     const int c = (lane % CPR) ^ swz_chunk<CPR>(row);
-    const size_t off = (size_t)min(qbase + row, T_ - 1) * D + 8 * c;
-    __builtin_amdgcn_global_load_lds(Q + off, LDS_PTR(void, pq + J * 512), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(dO + off, LDS_PTR(void, pdo + J * 512), 16, 0, 0);
+    const int voff = ((r0 + row) * D + 8 * c) * 2;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, LDS_PTR(void, la + J * 512), 16, voff, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, LDS_PTR(void, lb + J * 512), 16, voff, 0, 0, 0);
   }
-  const int row = min(qbase + lane, T_ - 1);
-  if (wave == 0) __builtin_amdgcn_global_load_lds(stat + row, LDS_PTR(void, pst), 4, 0, 0);
-  if (wave == 1) __builtin_amdgcn_global_load_lds(di + row, LDS_PTR(void, pdi), 4, 0, 0);
+}
+// Per-row statistics of a 64-query tile (stat by wave 0, di by wave 1); rows at or past T
+// land as zeros.
+__device__ __forceinline__ void bwd_stat_dma(float* lst, float* ldi, __amdgpu_buffer_rsrc_t rst,
+                                             __amdgpu_buffer_rsrc_t rdi, int qbase, int wave, int lane) {
+  if (wave == 0) __builtin_amdgcn_raw_ptr_buffer_load_lds(rst, LDS_PTR(void, lst), 4, (qbase + lane) * 4, 0, 0, 0);
+  if (wave == 1) __builtin_amdgcn_raw_ptr_buffer_load_lds(rdi, LDS_PTR(void, ldi), 4, (qbase + lane) * 4, 0, 0, 0);
 }
 
-// Same decomposition as attn_bwd_kernel (128 keys per workgroup, 32 per wave; dK/dV in
-// registers; dQ via the staged dS and f32 atomics), arranged for one wave per SIMD:
-//  * the tile body has no branches: S and dP of both 32-query blocks, then both blocks'
-//    weights and score gradients (masking by select), then dV and dK, so the scheduler can
-//    overlap the MFMAs of one block with the VALU work of the other;
-//  * the next tile is copied into LDS landing buffers by direct copies issued at the top of
-//    the iteration (no staging registers) and moved into the working tiles after the dS
-//    barrier; the dQ atomics come last, a full tile before the next wait on the counter;
-//  * every LDS access is a per-lane swizzled offset computed once plus an immediate;
-//  * the dQ atomics are buffer atomics whose range check drops rows past T.
+// Instruction order of one pipeline step: NM MFMAs, each followed by a share of the step's
+// V VALU instructions, R LDS reads and W LDS writes; nothing moves across the step's end.
+template <int NM, int V, int R, int W>
+__device__ __forceinline__ void bwd_step_order() {
+  constexpr int VP = (V + NM - 1) / NM, RP = (R + NM - 1) / NM, WP = (W + NM - 1) / NM;
+#pragma unroll
+  for (int i = 0; i < NM; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if (RP > 0 && i * RP < R) __builtin_amdgcn_sched_group_barrier(0x100, RP, 0);
+    if (VP > 0 && i * VP < V) __builtin_amdgcn_sched_group_barrier(0x002, VP, 0);
+    if (WP > 0 && i * WP < W) __builtin_amdgcn_sched_group_barrier(0x200, WP, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// VALU instructions per score element (scheduling hint).
+template <int MODE>
+constexpr int bwd_valu_per_elem() { return MODE == MODE_INRANGE ? 14 : 20; }
+
+// dK/dV kernel for bf16 inputs: 128 keys per workgroup, 32 per wave (lane = key), dK/dV
+// accumulated in registers over the 64-query tiles of the causal range. dQ is formed by
+// attn_bwd_dq_kernel, so this kernel stages nothing for it. Arranged for one wave per SIMD
+// as a software pipeline of fixed steps; each step's MFMAs use LDS fragments read in earlier
+// steps, so no MFMA waits on a just-issued read:
+//   R1  S, dP of query block 0                      (MFMA)
+//   R2  S, dP of block 1  | P, dS of block 0        (MFMA | VALU)
+//   R3  dV, dK of block 0 | P, dS of block 1, 0..7  (MFMA | VALU)
+//   R4  dV, dK of block 1 from elements 0..7 | P, dS of block 1, 8..15
+//   R5  dV, dK of block 1 from elements 8..15       (MFMA)
+//   barrier; copy of tile t+2 into this tile's buffer set
+// Query tiles ping-pong between two LDS buffer sets (distinct __shared__ objects); the copy
+// of tile t+2 is issued right after tile t's barrier, a full tile ahead of its use. The
+// causal mask is evaluated only on the two tiles that cross the diagonal; every LDS access is
+// a per-lane swizzled offset computed once plus an immediate.
 template <int D, int MODE, int L2N>
 __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) {
   static_assert(D == 64 || D == 128, "head_dim");
-  constexpr int BQ = BF_BQ, CPR = D / 8, SCPR = BQ / 8, NDB = D / 32, NF = D / 16;
-  __shared__ __attribute__((aligned(16))) bf16 Ks[BWD_BK * D];
-  __shared__ __attribute__((aligned(16))) bf16 Qs[BQ * D];
-  __shared__ __attribute__((aligned(16))) bf16 dOs[BQ * D];
-  __shared__ __attribute__((aligned(16))) bf16 dSs[BWD_BK * BQ];
-  __shared__ __attribute__((aligned(16))) float st_s[BQ];
-  __shared__ __attribute__((aligned(16))) float di_s[BQ];
-  __shared__ __attribute__((aligned(16))) bf16 pre_q[BQ * D];  // landing buffers
-  __shared__ __attribute__((aligned(16))) bf16 pre_do[BQ * D];
-  __shared__ __attribute__((aligned(16))) float pre_st[BQ];
-  __shared__ __attribute__((aligned(16))) float pre_di[BQ];
+  constexpr int BQ = BF_BQ, CPR = D / 8, NDB = D / 32, NF = D / 16;
+  __shared__ __attribute__((aligned(16))) bf16 Qs0[BQ * D];
+  __shared__ __attribute__((aligned(16))) bf16 Qs1[BQ * D];
+  __shared__ __attribute__((aligned(16))) bf16 dOs0[BQ * D];
+  __shared__ __attribute__((aligned(16))) bf16 dOs1[BQ * D];
+  __shared__ __attribute__((aligned(16))) float st0[BQ];
+  __shared__ __attribute__((aligned(16))) float st1[BQ];
+  __shared__ __attribute__((aligned(16))) float di0[BQ];
+  __shared__ __attribute__((aligned(16))) float di1[BQ];
 
   if (p.flag) {
     const bool in_range = *p.flag != 0;
@@ -540,30 +603,34 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
   const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int T_ = p.T;
-  const int bh = blockIdx.x;
-  const int k0 = blockIdx.y * BWD_BK;  // blockIdx.y = 0 has the most causal work
+  int bh, kblk;
+  bwd_block_coords(p.B * p.H, ceil_div(T_, BWD_BK), bh, kblk);
+  const int k0 = kblk * BWD_BK;
   const size_t base = (size_t)bh * T_ * D;
   const bf16* Q = reinterpret_cast<const bf16*>(p.q) + base;
   const bf16* K = reinterpret_cast<const bf16*>(p.k) + base;
   const bf16* V = reinterpret_cast<const bf16*>(p.v) + base;
   const bf16* dO = reinterpret_cast<const bf16*>(p.dO) + base;
-  const float* stat = p.stat + (size_t)bh * T_;
-  const float* di = p.di + (size_t)bh * T_;
-  float* dq_acc = p.dq_acc + base;
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)Q, (short)0, T_ * D * 2, BUF_RSRC_WORD3);
+  const __amdgpu_buffer_rsrc_t rdo = __builtin_amdgcn_make_buffer_rsrc((void*)dO, (short)0, T_ * D * 2, BUF_RSRC_WORD3);
+  const __amdgpu_buffer_rsrc_t rst =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(p.stat + (size_t)bh * T_), (short)0, T_ * 4, BUF_RSRC_WORD3);
+  const __amdgpu_buffer_rsrc_t rdi =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(p.di + (size_t)bh * T_), (short)0, T_ * 4, BUF_RSRC_WORD3);
   const int wk0 = k0 + wave * 32;  // this wave's first key
   const int mykey = wk0 + l32;
   const int log2n = p.log2n;
   const int nq = ceil_div(T_, BQ);
   const int qstart = k0 / BQ;
 
-  bwd_tile_copy<D>(pre_q, pre_do, pre_st, pre_di, Q, dO, stat, di, qstart * BQ, T_, wave);
-  {
-    typedef RowTile<bf16, D, BWD_BK> KT;  // keys past T: finite stand-ins whose dS is zero
-    uint4 kr[KT::PER];
-    KT::load(kr, K, k0, T_);
-    KT::store(Ks, 0, kr);
+  bwd_tile_dma2<D>(Qs0, dOs0, rq, rdo, qstart * BQ, wave, lane);
+  bwd_stat_dma(st0, di0, rst, rdi, qstart * BQ, wave, lane);
+  if (qstart + 1 < nq) {
+    bwd_tile_dma2<D>(Qs1, dOs1, rq, rdo, (qstart + 1) * BQ, wave, lane);
+    bwd_stat_dma(st1, di1, rst, rdi, (qstart + 1) * BQ, wave, lane);
   }
-  // K and V fragments of this wave's keys: B operands of S = Q K^T and dP = dO V^T.
+  // K and V fragments of this wave's keys: B operands of S = Q K^T and dP = dO V^T. Keys
+  // past T are zero and always masked.
   bf16x8 kf[NF], vf[NF];
 #pragma unroll
   for (int s = 0; s < NF; ++s) {
@@ -579,14 +646,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
     dv[db] = floatx16{};
   }
 
-  // Per-lane swizzled offsets: both swizzles repeat every 16 rows, so every access below is
+  // Per-lane swizzled offsets: the swizzle repeats every 16 rows, so every access below is
   // one of these plus a multiple of 16 rows (an immediate offset).
-  constexpr int NQH = BQ / 32;    // 32-query slices of a tile (dQ phase)
-  constexpr int WPH = 4 / NQH;    // waves per slice
-  constexpr int DBW = NDB / WPH;  // 32-wide d blocks per wave
-  static_assert(DBW >= 1, "tile shape");
-  const int qs = wave / WPH;
-  const int db0 = (wave % WPH) * DBW;
   const int trow = (lane & 15) >> 2;  // row within a transposed read's 4-row group
   int row_off[NF];                    // row fragments of Q / dO: row l32, k chunk 2 st + h
 #pragma unroll
@@ -597,138 +658,176 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
     tq_lo[db] = swz_at<CPR>(4 * h + trow, tr_col(db * 32, lane));
     tq_hi[db] = swz_at<CPR>(4 * h + 8 + trow, tr_col(db * 32, lane));
   }
-  const int ts_lo = swz_at<SCPR>(8 * h + trow, tr_col(qs * 32, lane));  // dS, dQ phase
-  const int ts_hi = swz_at<SCPR>(8 * h + 4 + trow, tr_col(qs * 32, lane));
-  int tk_lo[DBW], tk_hi[DBW];  // K, dQ phase
-#pragma unroll
-  for (int j = 0; j < DBW; ++j) {
-    tk_lo[j] = swz_at<CPR>(8 * h + trow, tr_col((db0 + j) * 32, lane));
-    tk_hi[j] = swz_at<CPR>(8 * h + 4 + trow, tr_col((db0 + j) * 32, lane));
-  }
-  // dS writes: row wave*32 + l32, columns 32 sub + 8g + 4h. A column shift is not a constant
-  // offset under the swizzle (only multiples of 16 rows are), so each block has its own.
-  int ds_off[2][4];
-#pragma unroll
-  for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) ds_off[sub][g] = swz_at<SCPR>(wave * 32 + l32, sub * 32 + 8 * g + 4 * h);
-  const int lane_off = (4 * h * D + l32) * 4;  // dQ atomics (bytes)
 
-  // Landing buffers -> working tiles (same swizzled layout: a straight 16-byte copy); rows
-  // past T get stat = 0, which makes their weights and score gradients exactly zero.
-  auto commit = [&](int qbase) {
-    constexpr int CH = BQ * D / 8;
-#pragma unroll
-    for (int c = threadIdx.x; c < CH; c += 256) {
-      reinterpret_cast<uint4*>(Qs)[c] = reinterpret_cast<const uint4*>(pre_q)[c];
-      reinterpret_cast<uint4*>(dOs)[c] = reinterpret_cast<const uint4*>(pre_do)[c];
-    }
-    if (threadIdx.x < BQ) {
-      const bool live = qbase + (int)threadIdx.x < T_;
-      st_s[threadIdx.x] = live ? pre_st[threadIdx.x] : 0.0f;
-      di_s[threadIdx.x] = live ? pre_di[threadIdx.x] : 0.0f;
-    }
-  };
+  bf16x8 rq3[3], ro3[3];  // row fragments of Q / dO, two steps ahead (R1, R2)
   __builtin_amdgcn_s_waitcnt(VMCNT0);
   __syncthreads();
-  commit(qstart * BQ);
-  __syncthreads();
+  rq3[0] = ld8(Qs0 + row_off[0]);
+  ro3[0] = ld8(dOs0 + row_off[0]);
+  rq3[1] = ld8(Qs0 + row_off[1]);
+  ro3[1] = ld8(dOs0 + row_off[1]);
+  constexpr int VE = bwd_valu_per_elem<MODE>();
 
-  for (int qt = qstart; qt < nq; ++qt) {
+  // One query tile. BUF selects the LDS buffer set, MASKED the tiles that cross the diagonal.
+  auto tile = [&](auto bufc, auto maskc, int qt) {
+    constexpr int BUF = decltype(bufc)::value;
+    constexpr bool MASKED = decltype(maskc)::value;
+    const bf16* Qs = BUF ? Qs1 : Qs0;
+    const bf16* dOs = BUF ? dOs1 : dOs0;
+    const float* sts = BUF ? st1 : st0;
+    const float* dis = BUF ? di1 : di0;
     const int qbase = qt * BQ;
-    const bool more = qt + 1 < nq;
-    if (more) bwd_tile_copy<D>(pre_q, pre_do, pre_st, pre_di, Q, dO, stat, di, qbase + BQ, T_, wave);
-    // S = Q K^T and dP = dO V^T for both 32-query blocks (lane = key).
+
     floatx16 s[2], dp[2];
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      s[sub] = floatx16{};
-      dp[sub] = floatx16{};
-#pragma unroll
-      for (int st = 0; st < NF; ++st) {
-        s[sub] = mfma_bf16(*reinterpret_cast<const bf16x8*>(Qs + sub * 32 * D + row_off[st]), kf[st], s[sub]);
-        dp[sub] = mfma_bf16(*reinterpret_cast<const bf16x8*>(dOs + sub * 32 * D + row_off[st]), vf[st], dp[sub]);
-      }
-    }
-    // Weights P and score gradients dS (rounded to bf16 as the gradient products use them);
-    // blocks that cross the diagonal mask keys after the query (all of them for blocks
-    // wholly before this wave's keys).
     bf16x8 pa[2][2], da[2][2];
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      const int sq0 = qbase + sub * 32;
-      const bool diag = wk0 + 31 > sq0;
-      float pv[16], dsv[16];
+    floatx4 stq[2][4], diq[2][4];
+    float pv[16], dsv[16];
+
+    // R1/R2 step g = NF * sub + st: MFMAs on the fragments of step g, reads for step g + 2.
+    auto sdp_step = [&](int g) {
+      const int sub = g / NF, st = g % NF;
+      const int gn = g + 2;
+      if (gn < 2 * NF) {
+        rq3[gn % 3] = ld8(Qs + (gn / NF) * 32 * D + row_off[gn % NF]);
+        ro3[gn % 3] = ld8(dOs + (gn / NF) * 32 * D + row_off[gn % NF]);
+      }
+      s[sub] = mfma_bf16(rq3[g % 3], kf[st], s[sub]);
+      dp[sub] = mfma_bf16(ro3[g % 3], vf[st], dp[sub]);
+    };
+    auto load_stats = [&](int sub) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const floatx4 stq = *reinterpret_cast<const floatx4*>(st_s + sub * 32 + 8 * g + 4 * h);
-        const floatx4 diq = *reinterpret_cast<const floatx4*>(di_s + sub * 32 + 8 * g + 4 * h);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int i = 4 * g + e;
-          const bool masked = diag && mykey > sq0 + 8 * g + 4 * h + e;
-          bwd_elem<MODE, L2N>(s[sub][i], dp[sub][i], stq[e], diq[e], masked, p, log2n, pv[i], dsv[i]);
-        }
+        stq[sub][g] = *reinterpret_cast<const floatx4*>(sts + sub * 32 + 8 * g + 4 * h);
+        diq[sub][g] = *reinterpret_cast<const floatx4*>(dis + sub * 32 + 8 * g + 4 * h);
       }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        pa[sub][0][j] = f2bf(pv[j]);
-        pa[sub][1][j] = f2bf(pv[8 + j]);
-        da[sub][0][j] = f2bf(dsv[j]);
-        da[sub][1][j] = f2bf(dsv[8 + j]);
+    };
+    // Weight P and score gradient dS of element i of block sub, rounded to bf16 as the
+    // gradient products use them.
+    auto elem = [&](int sub, int i) {
+      const int g = i >> 2, e = i & 3;
+      const bool masked = MASKED && mykey > qbase + sub * 32 + 8 * g + 4 * h + e;
+      bwd_elem<MODE, L2N>(s[sub][i], dp[sub][i], stq[sub][g][e], diq[sub][g][e], masked, p, log2n, pv[i], dsv[i]);
+      if (i & 1) {
+        pa[sub][i >> 3][(i & 7) - 1] = f2bf(pv[i - 1]);
+        pa[sub][i >> 3][i & 7] = f2bf(pv[i]);
+        da[sub][i >> 3][(i & 7) - 1] = f2bf(dsv[i - 1]);
+        da[sub][i >> 3][i & 7] = f2bf(dsv[i]);
       }
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        bf16x4 v4;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v4[e] = f2bf(dsv[4 * g + e]);
-        *reinterpret_cast<bf16x4*>(dSs + ds_off[sub][g]) = v4;  // staged [key][query]
-      }
-    }
-    // dV += P^T dO and dK += dS^T Q (transposed dO / Q fragments from LDS).
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
+    };
+    // dV += P^T dO and dK += dS^T Q, one d block per step; fragments one step ahead.
+    // Half `hf` of block sub: the products over its queries 0..15 (hf = 0) or 16..31.
+    bf16x8 ft[2][4];
+    auto dvdk_load = [&](int sub, int db, bf16x8 (&f)[4]) {
       const bf16* qb = Qs + sub * 32 * D;
       const bf16* ob = dOs + sub * 32 * D;
+      f[0] = tr_frag_at(ob, tq_lo[db], tq_hi[db]);
+      f[1] = tr_frag_at(ob + 16 * D, tq_lo[db], tq_hi[db]);
+      f[2] = tr_frag_at(qb, tq_lo[db], tq_hi[db]);
+      f[3] = tr_frag_at(qb + 16 * D, tq_lo[db], tq_hi[db]);
+    };
+    auto dvdk_half_load = [&](int hf, int db, bf16x8 (&f)[4]) {
+      const bf16* qb = Qs + 32 * D + hf * 16 * D;
+      const bf16* ob = dOs + 32 * D + hf * 16 * D;
+      f[0] = tr_frag_at(ob, tq_lo[db], tq_hi[db]);
+      f[2] = tr_frag_at(qb, tq_lo[db], tq_hi[db]);
+    };
+
+    // R1: S and dP of block 0.
 #pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        dv[db] = mfma_bf16(pa[sub][0], tr_frag_at(ob, tq_lo[db], tq_hi[db]), dv[db]);
-        dv[db] = mfma_bf16(pa[sub][1], tr_frag_at(ob + 16 * D, tq_lo[db], tq_hi[db]), dv[db]);
-        dk[db] = mfma_bf16(da[sub][0], tr_frag_at(qb, tq_lo[db], tq_hi[db]), dk[db]);
-        dk[db] = mfma_bf16(da[sub][1], tr_frag_at(qb + 16 * D, tq_lo[db], tq_hi[db]), dk[db]);
-      }
+    for (int sb = 0; sb < 2; ++sb) {
+      s[sb] = floatx16{};
+      dp[sb] = floatx16{};
     }
+    load_stats(0);
+#pragma unroll
+    for (int g = 0; g < NF; ++g) {
+      sdp_step(g);
+      if (g == 0) bwd_step_order<2, 0, 4 + 8, 0>();
+      else bwd_step_order<2, 0, 4, 0>();
+    }
+    // R2: S and dP of block 1 under P and dS of block 0.
+    constexpr int E2 = 16 / NF;
+#pragma unroll
+    for (int g = NF; g < 2 * NF; ++g) {
+      sdp_step(g);
+      const int st = g - NF;
+#pragma unroll
+      for (int k = 0; k < E2; ++k) elem(0, E2 * st + k);
+      if (g == 2 * NF - 2) load_stats(1);
+      if (g == 2 * NF - 1) dvdk_load(0, 0, ft[0]);
+      bwd_step_order<2, VE * E2, 4 + 8, 0>();
+    }
+    // R3: dV/dK of block 0 under P and dS of block 1, elements 0..7.
+    constexpr int E3 = 8 / NDB;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      if (db + 1 < NDB) dvdk_load(0, db + 1, ft[(db + 1) & 1]);
+      else dvdk_half_load(0, 0, ft[0]);
+      const int c = db & 1;
+      dv[db] = mfma_bf16(pa[0][0], ft[c][0], dv[db]);
+      dv[db] = mfma_bf16(pa[0][1], ft[c][1], dv[db]);
+      dk[db] = mfma_bf16(da[0][0], ft[c][2], dk[db]);
+      dk[db] = mfma_bf16(da[0][1], ft[c][3], dk[db]);
+#pragma unroll
+      for (int k = 0; k < E3; ++k) elem(1, E3 * db + k);
+      bwd_step_order<4, VE * E3, 8, 0>();
+    }
+    // R4: dV/dK of block 1 over its queries 0..15 (elements 0..7) under elements 8..15.
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const int c = db & 1;
+      if (db + 1 < NDB) dvdk_half_load(0, db + 1, ft[c ^ 1]);
+      else dvdk_half_load(1, 0, ft[c ^ 1]);
+      dv[db] = mfma_bf16(pa[1][0], ft[c][0], dv[db]);
+      dk[db] = mfma_bf16(da[1][0], ft[c][2], dk[db]);
+#pragma unroll
+      for (int k = 0; k < E3; ++k) elem(1, 8 + E3 * db + k);
+      bwd_step_order<2, VE * E3, 4, 0>();
+    }
+    // R5: dV/dK of block 1 over its queries 16..31 (elements 8..15).
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const int c = (db + NDB) & 1;
+      if (db + 1 < NDB) dvdk_half_load(1, db + 1, ft[c ^ 1]);
+      dv[db] = mfma_bf16(pa[1][1], ft[c][0], dv[db]);
+      dk[db] = mfma_bf16(da[1][1], ft[c][2], dk[db]);
+      bwd_step_order<2, 0, 4, 0>();
+    }
+
     __builtin_amdgcn_s_waitcnt(VMCNT0);  // this wave's copies of the next tile have landed
-    __syncthreads();                     // dS complete; working tiles no longer read
-    if (more) commit(qbase + BQ);
-    // dQ tile = dS K over this workgroup's keys; each wave takes 32 queries x DBW d blocks.
-    floatx16 dqa[DBW];
-#pragma unroll
-    for (int j = 0; j < DBW; ++j) dqa[j] = floatx16{};
-#pragma unroll
-    for (int ks = 0; ks < BWD_BK / 16; ++ks) {
-      const bf16x8 a0 = tr_frag_at(dSs + ks * 16 * BQ, ts_lo, ts_hi);
-#pragma unroll
-      for (int j = 0; j < DBW; ++j) {
-        const bf16x8 b0 = tr_frag_at(Ks + ks * 16 * D, tk_lo[j], tk_hi[j]);
-        dqa[j] = mfma_bf16(a0, b0, dqa[j]);
+    __syncthreads();                     // this buffer set is no longer read
+    {  // first fragments of the next tile (the other buffer set, complete after the barrier)
+      const bf16* Qn = BUF ? Qs0 : Qs1;
+      const bf16* dOn = BUF ? dOs0 : dOs1;
+      rq3[0] = ld8(Qn + row_off[0]);
+      ro3[0] = ld8(dOn + row_off[0]);
+      rq3[1] = ld8(Qn + row_off[1]);
+      ro3[1] = ld8(dOn + row_off[1]);
+    }
+    if (qt + 2 < nq) {
+      if constexpr (BUF) {
+        bwd_tile_dma2<D>(Qs1, dOs1, rq, rdo, qbase + 2 * BQ, wave, lane);
+        bwd_stat_dma(st1, di1, rst, rdi, qbase + 2 * BQ, wave, lane);
+      } else {
+        bwd_tile_dma2<D>(Qs0, dOs0, rq, rdo, qbase + 2 * BQ, wave, lane);
+        bwd_stat_dma(st0, di0, rst, rdi, qbase + 2 * BQ, wave, lane);
       }
     }
-    // Buffer atomics over this slice's rows: the row offset is part of the range-checked
-    // VGPR offset, so rows at or past T (beyond num_records) are dropped by the hardware;
-    // the d-block offset is the scalar offset.
-    const int rowbase = qbase + qs * 32;
-    const int live_rows = max(0, T_ - rowbase);
-    const __amdgpu_buffer_rsrc_t dqr = __builtin_amdgcn_make_buffer_rsrc(dq_acc + (size_t)rowbase * D, (short)0,
-                                                                         live_rows * D * 4, BUF_RSRC_WORD3);
-#pragma unroll
-    for (int j = 0; j < DBW; ++j) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(dqa[j][i], dqr, lane_off + (8 * (i >> 2) + (i & 3)) * D * 4,
-                                                        (db0 + j) * 128, 0);
+  };
+
+  // Tiles qstart and qstart + 1 cross the diagonal; the loop's back edge follows a buffer-1
+  // tile only.
+  int qt = qstart;
+  tile(std::integral_constant<int, 0>{}, std::true_type{}, qt);
+  if (qt + 1 < nq) {
+    tile(std::integral_constant<int, 1>{}, std::true_type{}, qt + 1);
+    qt += 2;
+    while (qt < nq) {
+      tile(std::integral_constant<int, 0>{}, std::false_type{}, qt);
+      if (qt + 1 >= nq) break;
+      tile(std::integral_constant<int, 1>{}, std::false_type{}, qt + 1);
+      qt += 2;
     }
-    __syncthreads();  // dS consumed; the next tile is in the working tiles
   }
 
   // dK = n * acc, dV = acc (flash.py:591-597), rounded to bf16.
@@ -749,15 +848,241 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
   }
 }
 
+// dQ kernel for bf16 inputs (query-stationary; no atomics): one workgroup = 4 waves = 128
+// queries of one (b, h), 32 per wave. Scores are formed transposed, S^T = K Q^T and
+// dP^T = V dO^T (Q and dO fragments held in registers, so each lane owns one query and its
+// stat / di are per-lane scalars); dS^T feeds dQ^T += K^T dS^T directly as the B operand,
+// with K^T fragments read transposed from the K tile. K/V stream through LDS in 64-key tiles
+// that ping-pong between two buffer sets, copied a full tile ahead. Per tile:
+//   R1  S^T, dP^T of keys 0..31                  (MFMA)
+//   R2  S^T, dP^T of keys 32..63 | dS of 0..31   (MFMA | VALU)
+//   R3  dQ^T over keys 0..31     | dS of 32..63  (MFMA | VALU)
+//   R4  dQ^T over keys 32..63                    (MFMA)
+// The output is dq = round(round(n * acc) * dq_scale) (flash.py:592 and the q_s chain rule).
+template <int D, int MODE, int L2N>
+__global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnBwdParams p) {
+  static_assert(D == 64 || D == 128, "head_dim");
+  constexpr int BK = 64, CPR = D / 8, NDB = D / 32, NF = D / 16;
+  __shared__ __attribute__((aligned(16))) bf16 Ks0[BK * D];
+  __shared__ __attribute__((aligned(16))) bf16 Ks1[BK * D];
+  __shared__ __attribute__((aligned(16))) bf16 Vs0[BK * D];
+  __shared__ __attribute__((aligned(16))) bf16 Vs1[BK * D];
+
+  if (p.flag) {
+    const bool in_range = *p.flag != 0;
+    if ((MODE == MODE_SHIFTED) == in_range) return;
+  }
+  const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int T_ = p.T;
+  const int nqb = ceil_div(T_, 128);
+  const int bh = blockIdx.x;
+  const int qb = nqb - 1 - blockIdx.y;  // heaviest causal rows first
+  const size_t base = (size_t)bh * T_ * D;
+  const bf16* Q = reinterpret_cast<const bf16*>(p.q) + base;
+  const bf16* K = reinterpret_cast<const bf16*>(p.k) + base;
+  const bf16* V = reinterpret_cast<const bf16*>(p.v) + base;
+  const bf16* dO = reinterpret_cast<const bf16*>(p.dO) + base;
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)K, (short)0, T_ * D * 2, BUF_RSRC_WORD3);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)V, (short)0, T_ * D * 2, BUF_RSRC_WORD3);
+  const int q0 = qb * 128 + wave * 32;
+  const int myq = q0 + l32;
+  const int log2n = p.log2n;
+  const int ntiles = (min(qb * 128 + 127, T_ - 1)) / BK + 1;  // key tiles up to the last query
+
+  bwd_tile_dma2<D>(Ks0, Vs0, rk, rv, 0, wave, lane);
+  if (ntiles > 1) bwd_tile_dma2<D>(Ks1, Vs1, rk, rv, BK, wave, lane);
+  // Q and dO fragments of this lane's query (B operands of S^T = K Q^T, dP^T = V dO^T);
+  // queries past T carry stat = 0, so their weights and score gradients are zero.
+  bf16x8 qf[NF], of[NF];
+  const bool live = myq < T_;
+#pragma unroll
+  for (int s = 0; s < NF; ++s) {
+    const bf16x8 z = {};
+    const size_t o = (size_t)myq * D + 16 * s + 8 * h;
+    qf[s] = live ? ld8(Q + o) : z;
+    of[s] = live ? ld8(dO + o) : z;
+  }
+  const float stq = live ? p.stat[(size_t)bh * T_ + myq] : 0.0f;
+  const float diq = live ? p.di[(size_t)bh * T_ + myq] : 0.0f;
+  floatx16 dqa[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) dqa[db] = floatx16{};
+
+  // Per-lane swizzled offsets (the swizzle repeats every 16 rows).
+  const int trow = (lane & 15) >> 2;
+  int row_off[NF];  // row fragments of K / V: row l32, k chunk 2 st + h
+#pragma unroll
+  for (int st = 0; st < NF; ++st) row_off[st] = swz_at<CPR>(l32, 16 * st + 8 * h);
+  int tk_lo[NDB], tk_hi[NDB];  // transposed K fragments: rows 4h + (0..3), 4h + 8 + (0..3)
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+    tk_lo[db] = swz_at<CPR>(4 * h + trow, tr_col(db * 32, lane));
+    tk_hi[db] = swz_at<CPR>(4 * h + 8 + trow, tr_col(db * 32, lane));
+  }
+
+  bf16x8 rk3[3], rv3[3];  // row fragments of K / V, two steps ahead (R1, R2)
+  __builtin_amdgcn_s_waitcnt(VMCNT0);
+  __syncthreads();
+  rk3[0] = ld8(Ks0 + row_off[0]);
+  rv3[0] = ld8(Vs0 + row_off[0]);
+  rk3[1] = ld8(Ks0 + row_off[1]);
+  rv3[1] = ld8(Vs0 + row_off[1]);
+  constexpr int VE = bwd_valu_per_elem<MODE>();
+
+  auto tile = [&](auto bufc, auto maskc, int kt) {
+    constexpr int BUF = decltype(bufc)::value;
+    constexpr bool MASKED = decltype(maskc)::value;
+    const bf16* Ks = BUF ? Ks1 : Ks0;
+    const bf16* Vs = BUF ? Vs1 : Vs0;
+    const int kb0 = kt * BK;
+
+    floatx16 s[2], dp[2];
+    bf16x8 da[2][2];
+    float pv[16], dsv[16];
+    auto sdp_step = [&](int g) {
+      const int blk = g / NF, st = g % NF;
+      const int gn = g + 2;
+      if (gn < 2 * NF) {
+        rk3[gn % 3] = ld8(Ks + (gn / NF) * 32 * D + row_off[gn % NF]);
+        rv3[gn % 3] = ld8(Vs + (gn / NF) * 32 * D + row_off[gn % NF]);
+      }
+      s[blk] = mfma_bf16(rk3[g % 3], qf[st], s[blk]);
+      dp[blk] = mfma_bf16(rv3[g % 3], of[st], dp[blk]);
+    };
+    // Score gradient of key element i of block blk (this lane's query), rounded to bf16.
+    auto elem = [&](int blk, int i) {
+      const bool masked = MASKED && kb0 + blk * 32 + 8 * (i >> 2) + 4 * h + (i & 3) > myq;
+      bwd_elem<MODE, L2N>(s[blk][i], dp[blk][i], stq, diq, masked, p, log2n, pv[i], dsv[i]);
+      if (i & 1) {
+        da[blk][i >> 3][(i & 7) - 1] = f2bf(dsv[i - 1]);
+        da[blk][i >> 3][i & 7] = f2bf(dsv[i]);
+      }
+    };
+    // dQ^T += K^T dS^T over one 32-key block, one d block per step (two 16-key halves);
+    // fragments one step ahead.
+    bf16x8 ft[2][2];
+    auto dq_load = [&](int blk, int db, bf16x8 (&f)[2]) {
+      const bf16* kb = Ks + blk * 32 * D;
+      f[0] = tr_frag_at(kb, tk_lo[db], tk_hi[db]);
+      f[1] = tr_frag_at(kb + 16 * D, tk_lo[db], tk_hi[db]);
+    };
+
+    // R1: S^T and dP^T of keys 0..31.
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      s[b] = floatx16{};
+      dp[b] = floatx16{};
+    }
+#pragma unroll
+    for (int g = 0; g < NF; ++g) {
+      sdp_step(g);
+      bwd_step_order<2, 0, 4, 0>();
+    }
+    // R2: S^T and dP^T of keys 32..63 under dS of keys 0..31.
+    constexpr int E2 = 16 / NF;
+#pragma unroll
+    for (int g = NF; g < 2 * NF; ++g) {
+      sdp_step(g);
+#pragma unroll
+      for (int k = 0; k < E2; ++k) elem(0, E2 * (g - NF) + k);
+      if (g == 2 * NF - 1) dq_load(0, 0, ft[0]);
+      bwd_step_order<2, VE * E2, 4 + 4, 0>();
+    }
+    // R3: dQ^T over keys 0..31 under dS of keys 32..63.
+    constexpr int E3 = 16 / NDB;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const int c = db & 1;
+      if (db + 1 < NDB) dq_load(0, db + 1, ft[c ^ 1]);
+      else dq_load(1, 0, ft[c ^ 1]);
+      dqa[db] = mfma_bf16(ft[c][0], da[0][0], dqa[db]);
+      dqa[db] = mfma_bf16(ft[c][1], da[0][1], dqa[db]);
+#pragma unroll
+      for (int k = 0; k < E3; ++k) elem(1, E3 * db + k);
+      bwd_step_order<2, VE * E3, 4, 0>();
+    }
+    // R4: dQ^T over keys 32..63.
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const int c = (db + NDB) & 1;
+      if (db + 1 < NDB) dq_load(1, db + 1, ft[c ^ 1]);
+      dqa[db] = mfma_bf16(ft[c][0], da[1][0], dqa[db]);
+      dqa[db] = mfma_bf16(ft[c][1], da[1][1], dqa[db]);
+      bwd_step_order<2, 0, 4, 0>();
+    }
+
+    __builtin_amdgcn_s_waitcnt(VMCNT0);  // this wave's copies of the next tile have landed
+    __syncthreads();                     // this buffer set is no longer read
+    {
+      const bf16* Kn = BUF ? Ks0 : Ks1;
+      const bf16* Vn = BUF ? Vs0 : Vs1;
+      rk3[0] = ld8(Kn + row_off[0]);
+      rv3[0] = ld8(Vn + row_off[0]);
+      rk3[1] = ld8(Kn + row_off[1]);
+      rv3[1] = ld8(Vn + row_off[1]);
+    }
+    if (kt + 2 < ntiles) {
+      if constexpr (BUF) bwd_tile_dma2<D>(Ks1, Vs1, rk, rv, kb0 + 2 * BK, wave, lane);
+      else bwd_tile_dma2<D>(Ks0, Vs0, rk, rv, kb0 + 2 * BK, wave, lane);
+    }
+  };
+
+  // Key tiles 0 .. 2 qb - 1 lie wholly before this workgroup's queries; tiles 2 qb and
+  // 2 qb + 1 cross the diagonal.
+  const int nfull = min(2 * qb, ntiles);
+  int kt = 0;
+  for (; kt < nfull; kt += 2) {
+    tile(std::integral_constant<int, 0>{}, std::false_type{}, kt);
+    tile(std::integral_constant<int, 1>{}, std::false_type{}, kt + 1);
+  }
+  if (kt < ntiles) {
+    tile(std::integral_constant<int, 0>{}, std::true_type{}, kt);
+    if (kt + 1 < ntiles) tile(std::integral_constant<int, 1>{}, std::true_type{}, kt + 1);
+  }
+
+  if (live) {
+    const float slope = (float)(1 << log2n);
+    bf16* DQ = reinterpret_cast<bf16*>(p.dq) + base + (size_t)myq * D;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        bf16x4 ob;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bf16 dqs = f2bf(dqa[db][4 * g + e] * slope);
+          ob[e] = f2bf((float)dqs * p.dq_scale);
+        }
+        *reinterpret_cast<bf16x4*>(DQ + db * 32 + 8 * g + 4 * h) = ob;
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // post: dq and the per-head sink gradient
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(256) void attn_bwd_post_kernel(AttnBwdParams p, size_t total, int nblk) {
   const float slope = (float)(1 << p.log2n);
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
-    const T dqs = (T)(p.dq_acc[i] * slope);       // kernel output dq_s (flash.py:592)
-    reinterpret_cast<T*>(p.dq)[i] = (T)((float)dqs * p.dq_scale);  // chain rule through q_s
+  // 8 consecutive elements per thread (total is a multiple of D, itself a multiple of 8).
+  const size_t n8 = total / 8;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += (size_t)gridDim.x * blockDim.x) {
+    const floatx4 a0 = *reinterpret_cast<const floatx4*>(p.dq_acc + 8 * i);
+    const floatx4 a1 = *reinterpret_cast<const floatx4*>(p.dq_acc + 8 * i + 4);
+    T out[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const T dqs = (T)((j < 4 ? a0[j] : a1[j - 4]) * slope);  // kernel output dq_s (flash.py:592)
+      out[j] = (T)((float)dqs * p.dq_scale);                   // chain rule through q_s
+    }
+    if constexpr (sizeof(T) == 2) {
+      *reinterpret_cast<uint4*>(reinterpret_cast<T*>(p.dq) + 8 * i) = *reinterpret_cast<const uint4*>(out);
+    } else {
+      *reinterpret_cast<uint4*>(reinterpret_cast<T*>(p.dq) + 8 * i) = *reinterpret_cast<const uint4*>(out);
+      *reinterpret_cast<uint4*>(reinterpret_cast<T*>(p.dq) + 8 * i + 4) = *reinterpret_cast<const uint4*>(out + 4);
+    }
   }
   if (blockIdx.x == 0 && p.dbeta) {
     bool shifted = p.mode == MODE_SHIFTED;
@@ -779,17 +1104,38 @@ __global__ __launch_bounds__(256) void attn_bwd_post_kernel(AttnBwdParams p, siz
   }
 }
 
+// bf16: the dK/dV kernel, then the dQ kernel (which writes dq itself).
 template <int D>
 static hipError_t launch_bwd_main_bf16(const AttnBwdParams& p, int mode, hipStream_t st) {
-  dim3 grid(p.B * p.H, ceil_div(p.T, BWD_BK)), block(256);
+  dim3 grid(p.B * p.H * ceil_div(p.T, BWD_BK)), block(256);
+  dim3 qgrid(p.B * p.H, ceil_div(p.T, 128));
   switch (mode) {
     case MODE_INRANGE: {
-      KTimer t("attn_bwd_inrange", st);
-      if (p.log2n == 4) hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_INRANGE, 4>), grid, block, 0, st, p);
-      else hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_INRANGE, 0>), grid, block, 0, st, p);
+      {
+        KTimer t("attn_bwd_inrange", st);
+        if (p.log2n == 4) hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_INRANGE, 4>), grid, block, 0, st, p);
+        else hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_INRANGE, 0>), grid, block, 0, st, p);
+      }
+      KTimer t("attn_bwd_dq_inrange", st);
+      if (p.log2n == 4) hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE_INRANGE, 4>), qgrid, block, 0, st, p);
+      else hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE_INRANGE, 0>), qgrid, block, 0, st, p);
     } break;
-    case MODE_CLIPPED: { KTimer t("attn_bwd_clipped", st); hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_CLIPPED, 0>), grid, block, 0, st, p); } break;
-    case MODE_SHIFTED: { KTimer t("attn_bwd_shifted", st); hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_SHIFTED, 0>), grid, block, 0, st, p); } break;
+    case MODE_CLIPPED: {
+      {
+        KTimer t("attn_bwd_clipped", st);
+        hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_CLIPPED, 0>), grid, block, 0, st, p);
+      }
+      KTimer t("attn_bwd_dq_clipped", st);
+      hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE_CLIPPED, 0>), qgrid, block, 0, st, p);
+    } break;
+    case MODE_SHIFTED: {
+      {
+        KTimer t("attn_bwd_shifted", st);
+        hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_SHIFTED, 0>), grid, block, 0, st, p);
+      }
+      KTimer t("attn_bwd_dq_shifted", st);
+      hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE_SHIFTED, 0>), qgrid, block, 0, st, p);
+    } break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -821,8 +1167,9 @@ hipError_t launch_attn_bwd(const AttnBwdParams& p, int D, bool bf16_io, const in
   dim3 pgrid(p.B * p.H, nblk);
   {
     KTimer t("attn_bwd_pre", st);
-    if (bf16_io) hipLaunchKernelGGL((attn_bwd_pre_kernel<bf16>), pgrid, dim3(256), 0, st, p, D);
-    else hipLaunchKernelGGL((attn_bwd_pre_kernel<float>), pgrid, dim3(256), 0, st, p, D);
+    // bf16: dq comes from the dQ kernel, the f32 accumulator is not used.
+    if (bf16_io) hipLaunchKernelGGL((attn_bwd_pre_kernel<bf16>), pgrid, dim3(256), 0, st, p, D, false);
+    else hipLaunchKernelGGL((attn_bwd_pre_kernel<float>), pgrid, dim3(256), 0, st, p, D, true);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -831,8 +1178,9 @@ hipError_t launch_attn_bwd(const AttnBwdParams& p, int D, bool bf16_io, const in
     else e = D == 64 ? launch_bwd_main<float, 64>(p, modes[m], st) : launch_bwd_main<float, 128>(p, modes[m], st);
     if (e != hipSuccess) return e;
   }
-  const size_t total = (size_t)p.B * p.H * p.T * D;
-  const int blocks = (int)std::min<size_t>((total + 255) / 256, 4096);
+  // f32: dq from the accumulator; bf16: only the sink gradient is left to do.
+  const size_t total = bf16_io ? 0 : (size_t)p.B * p.H * p.T * D;
+  const int blocks = (int)std::max<size_t>(std::min<size_t>((total / 8 + 255) / 256, 16384), 1);
   {
     KTimer t("attn_bwd_post", st);
     if (bf16_io) hipLaunchKernelGGL((attn_bwd_post_kernel<bf16>), dim3(blocks), dim3(256), 0, st, p, total, nblk);

@@ -22,42 +22,54 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(PrepParams p) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane / lpr, li = lane - sub * lpr;
   float mq = 0.0f, mk = 0.0f, mv = 0.0f;
+  // Each lane loads PREP_U rows before reducing any (more bytes in flight per lane).
+  constexpr int PREP_U = 2;
   const size_t step = (size_t)gridDim.x * 4 * rpw;
-  for (size_t r0 = ((size_t)blockIdx.x * 4 + wave) * rpw; r0 < p.rows; r0 += step) {
-    const size_t r = r0 + sub;
-    const bool ok = r < p.rows;
-    const size_t off = r * p.D + li * CH;
-    float sq = 0.0f, sk = 0.0f, av = 0.0f;
-    if (ok) {
-      T qv[CH], kv[CH], vv[CH];
-      *reinterpret_cast<uint4*>(qv) = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.q) + off);
-      T out[CH];
+  for (size_t r0 = ((size_t)blockIdx.x * 4 + wave) * rpw; r0 < p.rows; r0 += step * PREP_U) {
+    T qv[PREP_U][CH], kv[PREP_U][CH], vv[PREP_U][CH];
 #pragma unroll
-      for (int j = 0; j < CH; ++j) {
-        out[j] = (T)((float)qv[j] * p.alpha);
-        const float f = (float)out[j];
-        sq += f * f;
-      }
-      *reinterpret_cast<uint4*>(reinterpret_cast<T*>(p.q_s) + off) = *reinterpret_cast<uint4*>(out);
+    for (int u = 0; u < PREP_U; ++u) {
+      const size_t r = r0 + u * step + sub;
+      const size_t off = (r < p.rows ? r : p.rows - 1) * p.D + li * CH;
+      *reinterpret_cast<uint4*>(qv[u]) = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.q) + off);
       if (p.want_guard) {
-        *reinterpret_cast<uint4*>(kv) = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.k) + off);
-        *reinterpret_cast<uint4*>(vv) = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.v) + off);
+        *reinterpret_cast<uint4*>(kv[u]) = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.k) + off);
+        *reinterpret_cast<uint4*>(vv[u]) = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.v) + off);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < PREP_U; ++u) {
+      const size_t r = r0 + u * step + sub;
+      const bool ok = r < p.rows;
+      const size_t off = r * p.D + li * CH;
+      float sq = 0.0f, sk = 0.0f, av = 0.0f;
+      if (ok) {
+        T out[CH];
 #pragma unroll
         for (int j = 0; j < CH; ++j) {
-          const float kf = (float)kv[j];
-          sk += kf * kf;
-          av = nanmax(av, __builtin_fabsf((float)vv[j]));
+          out[j] = (T)((float)qv[u][j] * p.alpha);
+          const float f = (float)out[j];
+          sq += f * f;
+        }
+        *reinterpret_cast<uint4*>(reinterpret_cast<T*>(p.q_s) + off) = *reinterpret_cast<uint4*>(out);
+        if (p.want_guard) {
+#pragma unroll
+          for (int j = 0; j < CH; ++j) {
+            const float kf = (float)kv[u][j];
+            sk += kf * kf;
+            av = nanmax(av, __builtin_fabsf((float)vv[u][j]));
+          }
         }
       }
+      // Row sums across the lanes of one row.
+      for (int m = 1; m < lpr; m <<= 1) {
+        sq += __shfl_xor(sq, m, 64);
+        sk += __shfl_xor(sk, m, 64);
+      }
+      mq = nanmax(mq, sq);
+      mk = nanmax(mk, sk);
+      mv = nanmax(mv, av);
     }
-    // Row sums across the lanes of one row.
-    for (int m = 1; m < lpr; m <<= 1) {
-      sq += __shfl_xor(sq, m, 64);
-      sk += __shfl_xor(sk, m, 64);
-    }
-    mq = nanmax(mq, sq);
-    mk = nanmax(mk, sk);
-    mv = nanmax(mv, av);
   }
   for (int m = 32; m >= 1; m >>= 1) {
     mq = nanmax(mq, __shfl_xor(mq, m, 64));
@@ -76,9 +88,15 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(PrepParams p) {
 
 
 
+__device__ __forceinline__ float wave_nanmax(float m) {
+  for (int k = 32; k >= 1; k >>= 1) m = nanmax(m, __shfl_xor(m, k, 64));
+  return m;
+}
+
 __global__ __launch_bounds__(256) void attn_guard_kernel(GuardParams g) {
-  __shared__ float red[256][3];
-  float mq = 0.0f, mk = 0.0f, mv = 0.0f;
+  __shared__ float red[4][4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float mq = 0.0f, mk = 0.0f, mv = 0.0f, ms = 0.0f;
   if (g.want_guard) {
     for (int i = threadIdx.x; i < g.nblocks; i += 256) {
       mq = nanmax(mq, g.part[3 * i]);
@@ -86,26 +104,28 @@ __global__ __launch_bounds__(256) void attn_guard_kernel(GuardParams g) {
       mv = nanmax(mv, g.part[3 * i + 2]);
     }
   }
-  red[threadIdx.x][0] = mq; red[threadIdx.x][1] = mk; red[threadIdx.x][2] = mv;
   for (int hh = threadIdx.x; hh < g.H; hh += 256) {
-    if (g.sink_logit && g.sink_out) {
-      const float s = g.sink_logit[g.sink_count == 1 ? 0 : hh];
-      g.sink_out[hh] = s / g.c;
+    if (g.sink_logit) {
+      const float s = g.sink_logit[g.sink_count == 1 ? 0 : hh] / g.c;
+      if (g.sink_out) g.sink_out[hh] = s;
+      ms = nanmax(ms, __builtin_fabsf(s));
     }
   }
+  mq = wave_nanmax(mq);
+  mk = wave_nanmax(mk);
+  mv = wave_nanmax(mv);
+  ms = wave_nanmax(ms);
+  if (lane == 0) { red[wave][0] = mq; red[wave][1] = mk; red[wave][2] = mv; red[wave][3] = ms; }
   __syncthreads();
   if (threadIdx.x == 0 && g.flag) {
-    for (int i = 1; i < 256; ++i) {
-      mq = nanmax(mq, red[i][0]);
-      mk = nanmax(mk, red[i][1]);
-      mv = nanmax(mv, red[i][2]);
+    for (int w = 1; w < 4; ++w) {
+      mq = nanmax(mq, red[w][0]);
+      mk = nanmax(mk, red[w][1]);
+      mv = nanmax(mv, red[w][2]);
+      ms = nanmax(ms, red[w][3]);
     }
     bool ok = (mq * mk <= g.q2k2_bound) && (mv <= g.v_bound);
-    if (g.sink_logit) {
-      float ms = 0.0f;
-      for (int hh = 0; hh < g.H; ++hh) ms = nanmax(ms, __builtin_fabsf(g.sink_logit[g.sink_count == 1 ? 0 : hh] / g.c));
-      ok = ok && (ms <= g.sink_bound);
-    }
+    if (g.sink_logit) ok = ok && (ms <= g.sink_bound);
     *g.flag = g.want_guard ? (ok ? 1 : 0) : 1;
   }
 }

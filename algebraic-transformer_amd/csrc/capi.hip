@@ -52,6 +52,9 @@ int check_attn_shape(int dtype, int B, int H, int T, int D) {
   if (B <= 0 || H <= 0 || T <= 0) return fail(ALG_ERR_INVALID, "B, H, T must be positive (got %d, %d, %d)", B, H, T);
   if (D != 64 && D != 128) return fail(ALG_ERR_UNSUPPORTED, "head_dim %d: gfx950 kernels are built for D in {64, 128}", D);
   if ((double)B * H * T * D > 4.0e9) return fail(ALG_ERR_INVALID, "tensor too large");
+  // One (b, h) slice of q/k/v/dO is addressed with 32-bit byte offsets (buffer descriptors).
+  if ((double)(T + 64) * D * 4 >= 2147483648.0)
+    return fail(ALG_ERR_UNSUPPORTED, "T = %d: at most %d positions per head", T, (int)(2147483648.0 / (D * 4)) - 64);
   return ALG_OK;
 }
 
