@@ -51,7 +51,8 @@ def kernel_algorithmic_flops():
     g = 2.0 * HEAD["N"] * HEAD["d"] * HEAD["V"]   # one N x d x V product
     return {
         "attn_fwd_inrange": fa,          # QK^T + PV over the causal half
-        "attn_bwd_inrange": 2.5 * fa,    # 3.5x fwd+bwd convention minus the forward
+        "attn_bwd_inrange": 2.0 * fa,    # dK/dV kernel: S, dP, dV, dK
+        "attn_bwd_dq_inrange": 1.5 * fa,  # dQ kernel: S and dP again, dQ
         "head_fwd": g,                   # z = h E^T
         "head_dz": g,                    # z recomputed (executed; the 3-matmul convention omits it)
         "head_dh": g,                    # dh = dZ E
