@@ -519,49 +519,12 @@ __device__ __forceinline__ void bwd_block_coords(int nbh, int nkb, int& bh, int&
   }
 }
 
-// Copy of one 64-row tile (rows qbase.., D columns) of two (T, D) bf16 matrices into LDS with
-// range-checked buffer loads that write LDS directly: lane l of a wave instruction writes 16
-// bytes at base + 16 l, so each lane fetches the logical chunk the swizzle places there. Rows
-// at or past T lie beyond the descriptors' ranges and land as zeros. The destinations are
-// passed through an empty asm so the compiler cannot tie these copies to a particular LDS
-// array: it then inserts no wait for them before reads of the other buffer set. Every read
-// of a copied tile is preceded by the explicit vmcnt(0) + barrier of the tile before it.
-template <int D>
-__device__ __forceinline__ void bwd_tile_dma2(bf16* la, bf16* lb, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
-                                              int r0, int wave, int lane) {
-  constexpr int CPR = D / 8, RPI = 64 / CPR, PW = 64 * CPR / 64 / 4;  // PW instructions per wave
-  asm volatile("" : "+s"(la), "+s"(lb));
-#pragma unroll
-  for (int j = 0; j < PW; ++j) {
-    const int J = wave * PW + j;
-    const int row = RPI * J + lane / CPR;
-    const int c = (lane % CPR) ^ swz_chunk<CPR>(row);
-    const int voff = ((r0 + row) * D + 8 * c) * 2;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, LDS_PTR(void, la + J * 512), 16, voff, 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, LDS_PTR(void, lb + J * 512), 16, voff, 0, 0, 0);
-  }
-}
 // Per-row statistics of a 64-query tile (stat by wave 0, di by wave 1); rows at or past T
 // land as zeros.
 __device__ __forceinline__ void bwd_stat_dma(float* lst, float* ldi, __amdgpu_buffer_rsrc_t rst,
                                              __amdgpu_buffer_rsrc_t rdi, int qbase, int wave, int lane) {
   if (wave == 0) __builtin_amdgcn_raw_ptr_buffer_load_lds(rst, LDS_PTR(void, lst), 4, (qbase + lane) * 4, 0, 0, 0);
   if (wave == 1) __builtin_amdgcn_raw_ptr_buffer_load_lds(rdi, LDS_PTR(void, ldi), 4, (qbase + lane) * 4, 0, 0, 0);
-}
-
-// Instruction order of one pipeline step: NM MFMAs, each followed by a share of the step's
-// V VALU instructions, R LDS reads and W LDS writes; nothing moves across the step's end.
-template <int NM, int V, int R, int W>
-__device__ __forceinline__ void bwd_step_order() {
-  constexpr int VP = (V + NM - 1) / NM, RP = (R + NM - 1) / NM, WP = (W + NM - 1) / NM;
-#pragma unroll
-  for (int i = 0; i < NM; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    if (RP > 0 && i * RP < R) __builtin_amdgcn_sched_group_barrier(0x100, RP, 0);
-    if (VP > 0 && i * VP < V) __builtin_amdgcn_sched_group_barrier(0x002, VP, 0);
-    if (WP > 0 && i * WP < W) __builtin_amdgcn_sched_group_barrier(0x200, WP, 0);
-  }
-  __builtin_amdgcn_sched_barrier(0);
 }
 
 // VALU instructions per score element (scheduling hint).
@@ -623,10 +586,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
   const int nq = ceil_div(T_, BQ);
   const int qstart = k0 / BQ;
 
-  bwd_tile_dma2<D>(Qs0, dOs0, rq, rdo, qstart * BQ, wave, lane);
+  tile_dma2<D>(Qs0, dOs0, rq, rdo, qstart * BQ, wave, lane);
   bwd_stat_dma(st0, di0, rst, rdi, qstart * BQ, wave, lane);
   if (qstart + 1 < nq) {
-    bwd_tile_dma2<D>(Qs1, dOs1, rq, rdo, (qstart + 1) * BQ, wave, lane);
+    tile_dma2<D>(Qs1, dOs1, rq, rdo, (qstart + 1) * BQ, wave, lane);
     bwd_stat_dma(st1, di1, rst, rdi, (qstart + 1) * BQ, wave, lane);
   }
   // K and V fragments of this wave's keys: B operands of S = Q K^T and dP = dO V^T. Keys
@@ -742,8 +705,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
 #pragma unroll
     for (int g = 0; g < NF; ++g) {
       sdp_step(g);
-      if (g == 0) bwd_step_order<2, 0, 4 + 8, 0>();
-      else bwd_step_order<2, 0, 4, 0>();
+      if (g == 0) step_order<2, 0, 4 + 8, 0>();
+      else step_order<2, 0, 4, 0>();
     }
     // R2: S and dP of block 1 under P and dS of block 0.
     constexpr int E2 = 16 / NF;
@@ -755,7 +718,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
       for (int k = 0; k < E2; ++k) elem(0, E2 * st + k);
       if (g == 2 * NF - 2) load_stats(1);
       if (g == 2 * NF - 1) dvdk_load(0, 0, ft[0]);
-      bwd_step_order<2, VE * E2, 4 + 8, 0>();
+      step_order<2, VE * E2, 4 + 8, 0>();
     }
     // R3: dV/dK of block 0 under P and dS of block 1, elements 0..7.
     constexpr int E3 = 8 / NDB;
@@ -770,7 +733,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
       dk[db] = mfma_bf16(da[0][1], ft[c][3], dk[db]);
 #pragma unroll
       for (int k = 0; k < E3; ++k) elem(1, E3 * db + k);
-      bwd_step_order<4, VE * E3, 8, 0>();
+      step_order<4, VE * E3, 8, 0>();
     }
     // R4: dV/dK of block 1 over its queries 0..15 (elements 0..7) under elements 8..15.
 #pragma unroll
@@ -782,7 +745,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
       dk[db] = mfma_bf16(da[1][0], ft[c][2], dk[db]);
 #pragma unroll
       for (int k = 0; k < E3; ++k) elem(1, 8 + E3 * db + k);
-      bwd_step_order<2, VE * E3, 4, 0>();
+      step_order<2, VE * E3, 4, 0>();
     }
     // R5: dV/dK of block 1 over its queries 16..31 (elements 8..15).
 #pragma unroll
@@ -791,7 +754,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
       if (db + 1 < NDB) dvdk_half_load(1, db + 1, ft[c ^ 1]);
       dv[db] = mfma_bf16(pa[1][1], ft[c][0], dv[db]);
       dk[db] = mfma_bf16(da[1][1], ft[c][2], dk[db]);
-      bwd_step_order<2, 0, 4, 0>();
+      step_order<2, 0, 4, 0>();
     }
 
     __builtin_amdgcn_s_waitcnt(VMCNT0);  // this wave's copies of the next tile have landed
@@ -806,10 +769,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
     }
     if (qt + 2 < nq) {
       if constexpr (BUF) {
-        bwd_tile_dma2<D>(Qs1, dOs1, rq, rdo, qbase + 2 * BQ, wave, lane);
+        tile_dma2<D>(Qs1, dOs1, rq, rdo, qbase + 2 * BQ, wave, lane);
         bwd_stat_dma(st1, di1, rst, rdi, qbase + 2 * BQ, wave, lane);
       } else {
-        bwd_tile_dma2<D>(Qs0, dOs0, rq, rdo, qbase + 2 * BQ, wave, lane);
+        tile_dma2<D>(Qs0, dOs0, rq, rdo, qbase + 2 * BQ, wave, lane);
         bwd_stat_dma(st0, di0, rst, rdi, qbase + 2 * BQ, wave, lane);
       }
     }
@@ -890,8 +853,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnBwdParams p) {
   const int log2n = p.log2n;
   const int ntiles = (min(qb * 128 + 127, T_ - 1)) / BK + 1;  // key tiles up to the last query
 
-  bwd_tile_dma2<D>(Ks0, Vs0, rk, rv, 0, wave, lane);
-  if (ntiles > 1) bwd_tile_dma2<D>(Ks1, Vs1, rk, rv, BK, wave, lane);
+  tile_dma2<D>(Ks0, Vs0, rk, rv, 0, wave, lane);
+  if (ntiles > 1) tile_dma2<D>(Ks1, Vs1, rk, rv, BK, wave, lane);
   // Q and dO fragments of this lane's query (B operands of S^T = K Q^T, dP^T = V dO^T);
   // queries past T carry stat = 0, so their weights and score gradients are zero.
   bf16x8 qf[NF], of[NF];
@@ -977,7 +940,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnBwdParams p) {
 #pragma unroll
     for (int g = 0; g < NF; ++g) {
       sdp_step(g);
-      bwd_step_order<2, 0, 4, 0>();
+      step_order<2, 0, 4, 0>();
     }
     // R2: S^T and dP^T of keys 32..63 under dS of keys 0..31.
     constexpr int E2 = 16 / NF;
@@ -987,7 +950,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnBwdParams p) {
 #pragma unroll
       for (int k = 0; k < E2; ++k) elem(0, E2 * (g - NF) + k);
       if (g == 2 * NF - 1) dq_load(0, 0, ft[0]);
-      bwd_step_order<2, VE * E2, 4 + 4, 0>();
+      step_order<2, VE * E2, 4 + 4, 0>();
     }
     // R3: dQ^T over keys 0..31 under dS of keys 32..63.
     constexpr int E3 = 16 / NDB;
@@ -1000,7 +963,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnBwdParams p) {
       dqa[db] = mfma_bf16(ft[c][1], da[0][1], dqa[db]);
 #pragma unroll
       for (int k = 0; k < E3; ++k) elem(1, E3 * db + k);
-      bwd_step_order<2, VE * E3, 4, 0>();
+      step_order<2, VE * E3, 4, 0>();
     }
     // R4: dQ^T over keys 32..63.
 #pragma unroll
@@ -1009,7 +972,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnBwdParams p) {
       if (db + 1 < NDB) dq_load(1, db + 1, ft[c ^ 1]);
       dqa[db] = mfma_bf16(ft[c][0], da[1][0], dqa[db]);
       dqa[db] = mfma_bf16(ft[c][1], da[1][1], dqa[db]);
-      bwd_step_order<2, 0, 4, 0>();
+      step_order<2, 0, 4, 0>();
     }
 
     __builtin_amdgcn_s_waitcnt(VMCNT0);  // this wave's copies of the next tile have landed
@@ -1023,8 +986,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnBwdParams p) {
       rv3[1] = ld8(Vn + row_off[1]);
     }
     if (kt + 2 < ntiles) {
-      if constexpr (BUF) bwd_tile_dma2<D>(Ks1, Vs1, rk, rv, kb0 + 2 * BK, wave, lane);
-      else bwd_tile_dma2<D>(Ks0, Vs0, rk, rv, kb0 + 2 * BK, wave, lane);
+      if constexpr (BUF) tile_dma2<D>(Ks1, Vs1, rk, rv, kb0 + 2 * BK, wave, lane);
+      else tile_dma2<D>(Ks0, Vs0, rk, rv, kb0 + 2 * BK, wave, lane);
     }
   };
 

@@ -110,4 +110,42 @@ __device__ __forceinline__ int tr_col(int ncol, int lane) {
 // Row padding (elements) of the f32 tiles, which keep a padded row-major layout.
 constexpr int F32_PAD = 4;
 
+// Copy of one 64-row tile (rows r0.., D columns) of two (T, D) bf16 matrices into LDS with
+// range-checked buffer loads that write LDS directly: lane l of a wave instruction writes 16
+// bytes at base + 16 l, so each lane fetches the logical chunk the swizzle places there. Rows
+// at or past T lie beyond the descriptors' ranges and land as zeros. The destinations are
+// passed through an empty asm so the compiler cannot tie these copies to a particular LDS
+// array: it then inserts no wait for them before reads of the other buffer set. Every read
+// of a copied tile is preceded by the explicit vmcnt(0) + barrier of the tile before it.
+template <int D>
+__device__ __forceinline__ void tile_dma2(bf16* la, bf16* lb, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
+                                          int r0, int wave, int lane) {
+  constexpr int CPR = D / 8, RPI = 64 / CPR, PW = 64 * CPR / 64 / 4;  // PW instructions per wave
+  asm volatile("" : "+s"(la), "+s"(lb));
+#pragma unroll
+  for (int j = 0; j < PW; ++j) {
+    const int J = wave * PW + j;
+    const int row = RPI * J + lane / CPR;
+    const int c = (lane % CPR) ^ swz_chunk<CPR>(row);
+    const int voff = ((r0 + row) * D + 8 * c) * 2;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, LDS_PTR(void, la + J * 512), 16, voff, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, LDS_PTR(void, lb + J * 512), 16, voff, 0, 0, 0);
+  }
+}
+
+// Instruction order of one pipeline step: NM MFMAs, each followed by a share of the step's
+// V VALU instructions, R LDS reads and W LDS writes; nothing moves across the step's end.
+template <int NM, int V, int R, int W>
+__device__ __forceinline__ void step_order() {
+  constexpr int VP = (V + NM - 1) / NM, RP = (R + NM - 1) / NM, WP = (W + NM - 1) / NM;
+#pragma unroll
+  for (int i = 0; i < NM; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if (RP > 0 && i * RP < R) __builtin_amdgcn_sched_group_barrier(0x100, RP, 0);
+    if (VP > 0 && i * VP < V) __builtin_amdgcn_sched_group_barrier(0x002, VP, 0);
+    if (WP > 0 && i * WP < W) __builtin_amdgcn_sched_group_barrier(0x200, WP, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 }  // namespace alg

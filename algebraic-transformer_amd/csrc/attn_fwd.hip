@@ -12,6 +12,8 @@
 // as the B operand of O^T = V^T P^T; V^T fragments come from the row-major LDS tile with
 // ds_read_b64_tr_b16. Causal tiles above the diagonal are skipped per wave; only tiles
 // crossing it evaluate the mask.
+#include <type_traits>
+
 #include "attn_common.h"
 
 namespace alg {
@@ -287,14 +289,215 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
   }
 }
 
+// In-range forward for bf16 inputs (the guarded "low" variant): same decomposition as
+// attn_fwd_kernel (4 waves x 32 queries, lane = query, S^T = K Q^T, O^T += V^T P^T), with K/V
+// tiles copied into LDS a full tile ahead by range-checked buffer copies (two ping-pong buffer
+// sets) and each 64-key tile software-pipelined over its two 32-key blocks:
+//   R1  S^T of keys 0..31                       (MFMA)
+//   R2  S^T of keys 32..63 | weights of 0..31   (MFMA | VALU)
+//   R3  O^T over keys 0..31 | weights of 32..63 (MFMA | VALU)
+//   R4  O^T over keys 32..63                    (MFMA)
+// The two tiles that cross this workgroup's diagonal evaluate the causal mask per element.
+template <int D, int L2N>
+__global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) {
+  static_assert(D == 64 || D == 128, "head_dim");
+  constexpr int BK = FWD_BK, CPR = D / 8, NDB = D / 32, NF = D / 16;
+  __shared__ __attribute__((aligned(16))) bf16 Ks0[BK * D];
+  __shared__ __attribute__((aligned(16))) bf16 Ks1[BK * D];
+  __shared__ __attribute__((aligned(16))) bf16 Vs0[BK * D];
+  __shared__ __attribute__((aligned(16))) bf16 Vs1[BK * D];
+
+  if (p.flag && *p.flag == 0) return;  // device-side guard dispatch (flash.py:853-856)
+  const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int T_ = p.T;
+  const int nqb = ceil_div(T_, FWD_BQ);
+  const int bh = blockIdx.x;
+  const int qb = nqb - 1 - blockIdx.y;  // heaviest causal rows first
+  const int head = bh % p.H;
+  const size_t base = (size_t)bh * T_ * D;
+  const bf16* Q = reinterpret_cast<const bf16*>(p.q) + base;
+  const bf16* K = reinterpret_cast<const bf16*>(p.k) + base;
+  const bf16* V = reinterpret_cast<const bf16*>(p.v) + base;
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)K, (short)0, T_ * D * 2, BUF_RSRC_WORD3);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)V, (short)0, T_ * D * 2, BUF_RSRC_WORD3);
+  const int myq = qb * FWD_BQ + wave * 32 + l32;
+  const int log2n = p.log2n;
+  const int ntiles = min(qb * FWD_BQ + FWD_BQ - 1, T_ - 1) / BK + 1;  // key tiles up to the last query
+
+  tile_dma2<D>(Ks0, Vs0, rk, rv, 0, wave, lane);
+  if (ntiles > 1) tile_dma2<D>(Ks1, Vs1, rk, rv, BK, wave, lane);
+  // Query fragments (B operand of S^T = K Q^T), held for the whole kernel.
+  bf16x8 qf[NF];
+  const bool live = myq < T_;
+#pragma unroll
+  for (int s = 0; s < NF; ++s) {
+    const bf16x8 z = {};
+    qf[s] = live ? ld8(Q + (size_t)myq * D + 16 * s + 8 * h) : z;
+  }
+  floatx16 oacc[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) oacc[db] = floatx16{};
+  float lsum = 0.0f;
+
+  const int trow = (lane & 15) >> 2;
+  int row_off[NF];  // row fragments of K: row l32, k chunk 2 st + h
+#pragma unroll
+  for (int st = 0; st < NF; ++st) row_off[st] = swz_at<CPR>(l32, 16 * st + 8 * h);
+  int tv_lo[NDB], tv_hi[NDB];  // transposed V fragments: rows 4h + (0..3), 4h + 8 + (0..3)
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+    tv_lo[db] = swz_at<CPR>(4 * h + trow, tr_col(db * 32, lane));
+    tv_hi[db] = swz_at<CPR>(4 * h + 8 + trow, tr_col(db * 32, lane));
+  }
+
+  bf16x8 rk3[3];  // row fragments of K, two steps ahead
+  __builtin_amdgcn_s_waitcnt(VMCNT0);
+  __syncthreads();
+  rk3[0] = ld8(Ks0 + row_off[0]);
+  rk3[1] = ld8(Ks0 + row_off[1]);
+  constexpr int VE = 10;  // VALU instructions per weight (scheduling hint)
+
+  auto tile = [&](auto bufc, auto maskc, int kt) {
+    constexpr int BUF = decltype(bufc)::value;
+    constexpr bool MASKED = decltype(maskc)::value;
+    const bf16* Ks = BUF ? Ks1 : Ks0;
+    const bf16* Vs = BUF ? Vs1 : Vs0;
+    const int kb0 = kt * BK;
+    floatx16 s[2];
+    bf16x8 pf[2][2];
+    float w[16];
+    auto s_step = [&](int g) {
+      const int blk = g / NF, st = g % NF;
+      const int gn = g + 2;
+      if (gn < 2 * NF) rk3[gn % 3] = ld8(Ks + (gn / NF) * 32 * D + row_off[gn % NF]);
+      s[blk] = mfma_bf16(rk3[g % 3], qf[st], s[blk]);
+    };
+    // Weight of key element i of block blk for this lane's query (flash.py:215-233).
+    auto elem = [&](int blk, int i) {
+      float x = s[blk][i];
+      float wi = pow2n<L2N>(rho_fast(x), log2n);
+      if (MASKED && kb0 + blk * 32 + 8 * (i >> 2) + 4 * h + (i & 3) > myq) wi = 0.0f;
+      lsum += wi;
+      w[i] = wi;
+      if (i & 1) {
+        pf[blk][i >> 3][(i & 7) - 1] = f2bf(w[i - 1]);
+        pf[blk][i >> 3][i & 7] = f2bf(w[i]);
+      }
+    };
+    bf16x8 ft[2][2];
+    auto pv_load = [&](int blk, int db, bf16x8 (&f)[2]) {
+      const bf16* vb = Vs + blk * 32 * D;
+      f[0] = tr_frag_at(vb, tv_lo[db], tv_hi[db]);
+      f[1] = tr_frag_at(vb + 16 * D, tv_lo[db], tv_hi[db]);
+    };
+
+    // R1: S^T of keys 0..31.
+    s[0] = floatx16{};
+    s[1] = floatx16{};
+#pragma unroll
+    for (int g = 0; g < NF; ++g) {
+      s_step(g);
+      step_order<1, 0, 2, 0>();
+    }
+    // R2: S^T of keys 32..63 under the weights of keys 0..31.
+    constexpr int E2 = 16 / NF;
+#pragma unroll
+    for (int g = NF; g < 2 * NF; ++g) {
+      s_step(g);
+#pragma unroll
+      for (int k = 0; k < E2; ++k) elem(0, E2 * (g - NF) + k);
+      if (g == 2 * NF - 1) pv_load(0, 0, ft[0]);
+      step_order<1, VE * E2, 2, 0>();
+    }
+    // R3: O^T over keys 0..31 under the weights of keys 32..63.
+    constexpr int E3 = 16 / NDB;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const int c = db & 1;
+      if (db + 1 < NDB) pv_load(0, db + 1, ft[c ^ 1]);
+      else pv_load(1, 0, ft[c ^ 1]);
+      oacc[db] = mfma_bf16(ft[c][0], pf[0][0], oacc[db]);
+      oacc[db] = mfma_bf16(ft[c][1], pf[0][1], oacc[db]);
+#pragma unroll
+      for (int k = 0; k < E3; ++k) elem(1, E3 * db + k);
+      step_order<2, VE * E3, 4, 0>();
+    }
+    // R4: O^T over keys 32..63.
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const int c = (db + NDB) & 1;
+      if (db + 1 < NDB) pv_load(1, db + 1, ft[c ^ 1]);
+      oacc[db] = mfma_bf16(ft[c][0], pf[1][0], oacc[db]);
+      oacc[db] = mfma_bf16(ft[c][1], pf[1][1], oacc[db]);
+      step_order<2, 0, 4, 0>();
+    }
+
+    __builtin_amdgcn_s_waitcnt(VMCNT0);  // this wave's copies of the next tile have landed
+    __syncthreads();                     // this buffer set is no longer read
+    {
+      const bf16* Kn = BUF ? Ks0 : Ks1;
+      rk3[0] = ld8(Kn + row_off[0]);
+      rk3[1] = ld8(Kn + row_off[1]);
+    }
+    if (kt + 2 < ntiles) {
+      if constexpr (BUF) tile_dma2<D>(Ks1, Vs1, rk, rv, kb0 + 2 * BK, wave, lane);
+      else tile_dma2<D>(Ks0, Vs0, rk, rv, kb0 + 2 * BK, wave, lane);
+    }
+  };
+
+  // Key tiles 0 .. 2 qb - 1 lie wholly before this workgroup's queries; tiles 2 qb and
+  // 2 qb + 1 cross the diagonal (keys past T, zero-filled, are masked there too).
+  const int nfull = min(2 * qb, ntiles);
+  int kt = 0;
+  for (; kt < nfull; kt += 2) {
+    tile(std::integral_constant<int, 0>{}, std::false_type{}, kt);
+    tile(std::integral_constant<int, 1>{}, std::false_type{}, kt + 1);
+  }
+  if (kt < ntiles) {
+    tile(std::integral_constant<int, 0>{}, std::true_type{}, kt);
+    if (kt + 1 < ntiles) tile(std::integral_constant<int, 1>{}, std::true_type{}, kt + 1);
+  }
+  if (!live) return;
+
+  // Finalize (flash.py:271-284): Z over both lane halves (+ the sink's weight), stat = 1/Z.
+  float Z = lsum + xor32(lsum);
+  if (p.sink) Z += pow2n<L2N>(rho_fast(p.sink[head]), log2n);
+  const float inv = 1.0f / Z;
+  bf16* O = reinterpret_cast<bf16*>(p.o) + base + (size_t)myq * D;
+  float* OP = p.o_precise ? p.o_precise + base + (size_t)myq * D : nullptr;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = db * 32 + 8 * g + 4 * h;
+      floatx4 val;
+      bf16x4 ob;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        val[e] = oacc[db][4 * g + e] * inv;
+        ob[e] = f2bf(val[e]);
+      }
+      *reinterpret_cast<bf16x4*>(O + d0) = ob;
+      if (OP) *reinterpret_cast<floatx4*>(OP + d0) = val;
+    }
+  }
+  if (h == 0) p.stat[(size_t)bh * T_ + myq] = inv;
+}
+
 template <typename T, int D>
 static hipError_t launch_fwd_mode(const AttnFwdParams& p, int mode, hipStream_t st) {
   dim3 grid(p.B * p.H, ceil_div(p.T, FWD_BQ)), block(256);
   switch (mode) {
     case MODE_INRANGE: {
       KTimer t("attn_fwd_inrange", st);
-      if (p.log2n == 4) hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_INRANGE, 4>), grid, block, 0, st, p);
-      else hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_INRANGE, 0>), grid, block, 0, st, p);
+      if constexpr (sizeof(T) == 2) {
+        if (p.log2n == 4) hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, 4>), grid, block, 0, st, p);
+        else hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, 0>), grid, block, 0, st, p);
+      } else {
+        if (p.log2n == 4) hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_INRANGE, 4>), grid, block, 0, st, p);
+        else hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_INRANGE, 0>), grid, block, 0, st, p);
+      }
     } break;
     case MODE_CLIPPED: { KTimer t("attn_fwd_clipped", st); hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_CLIPPED, 0>), grid, block, 0, st, p); } break;
     case MODE_SHIFTED: { KTimer t("attn_fwd_shifted", st); hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_SHIFTED, 0>), grid, block, 0, st, p); } break;
