@@ -823,7 +823,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
 //   R4  dQ^T over keys 32..63                    (MFMA)
 // The output is dq = round(round(n * acc) * dq_scale) (flash.py:592 and the q_s chain rule).
 template <int D, int MODE, int L2N>
-__global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnBwdParams p) {
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
   static_assert(D == 64 || D == 128, "head_dim");
   constexpr int BK = 64, CPR = D / 8, NDB = D / 32, NF = D / 16;
   __shared__ __attribute__((aligned(16))) bf16 Ks0[BK * D];
@@ -884,13 +884,11 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnBwdParams p) {
     tk_hi[db] = swz_at<CPR>(4 * h + 8 + trow, tr_col(db * 32, lane));
   }
 
-  bf16x8 rk3[3], rv3[3];  // row fragments of K / V, two steps ahead (R1, R2)
+  bf16x8 rk2[2], rv2[2];  // row fragments of K / V, one step ahead (R1, R2)
   __builtin_amdgcn_s_waitcnt(VMCNT0);
   __syncthreads();
-  rk3[0] = ld8(Ks0 + row_off[0]);
-  rv3[0] = ld8(Vs0 + row_off[0]);
-  rk3[1] = ld8(Ks0 + row_off[1]);
-  rv3[1] = ld8(Vs0 + row_off[1]);
+  rk2[0] = ld8(Ks0 + row_off[0]);
+  rv2[0] = ld8(Vs0 + row_off[0]);
   constexpr int VE = bwd_valu_per_elem<MODE>();
 
   auto tile = [&](auto bufc, auto maskc, int kt) {
@@ -905,13 +903,13 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnBwdParams p) {
     float pv[16], dsv[16];
     auto sdp_step = [&](int g) {
       const int blk = g / NF, st = g % NF;
-      const int gn = g + 2;
+      const int gn = g + 1;
       if (gn < 2 * NF) {
-        rk3[gn % 3] = ld8(Ks + (gn / NF) * 32 * D + row_off[gn % NF]);
-        rv3[gn % 3] = ld8(Vs + (gn / NF) * 32 * D + row_off[gn % NF]);
+        rk2[gn % 2] = ld8(Ks + (gn / NF) * 32 * D + row_off[gn % NF]);
+        rv2[gn % 2] = ld8(Vs + (gn / NF) * 32 * D + row_off[gn % NF]);
       }
-      s[blk] = mfma_bf16(rk3[g % 3], qf[st], s[blk]);
-      dp[blk] = mfma_bf16(rv3[g % 3], of[st], dp[blk]);
+      s[blk] = mfma_bf16(rk2[g % 2], qf[st], s[blk]);
+      dp[blk] = mfma_bf16(rv2[g % 2], of[st], dp[blk]);
     };
     // Score gradient of key element i of block blk (this lane's query), rounded to bf16.
     auto elem = [&](int blk, int i) {
@@ -980,10 +978,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(AttnBwdParams p) {
     {
       const bf16* Kn = BUF ? Ks0 : Ks1;
       const bf16* Vn = BUF ? Vs0 : Vs1;
-      rk3[0] = ld8(Kn + row_off[0]);
-      rv3[0] = ld8(Vn + row_off[0]);
-      rk3[1] = ld8(Kn + row_off[1]);
-      rv3[1] = ld8(Vn + row_off[1]);
+      rk2[0] = ld8(Kn + row_off[0]);
+      rv2[0] = ld8(Vn + row_off[0]);
     }
     if (kt + 2 < ntiles) {
       if constexpr (BUF) tile_dma2<D>(Ks1, Vs1, rk, rv, kb0 + 2 * BK, wave, lane);
