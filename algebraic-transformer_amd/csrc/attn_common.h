@@ -117,17 +117,22 @@ constexpr int F32_PAD = 4;
 // passed through an empty asm so the compiler cannot tie these copies to a particular LDS
 // array: it then inserts no wait for them before reads of the other buffer set. Every read
 // of a copied tile is preceded by the explicit vmcnt(0) + barrier of the tile before it.
+// Instruction J covers rows RPI J + r (r = lane / CPR); its swizzle is swz(r) ^ swz(RPI J), so
+// every instruction's lane offset is one XOR of a per-lane chunk term with a wave-uniform
+// value: two per-lane registers serve all of them.
 template <int D>
 __device__ __forceinline__ void tile_dma2(bf16* la, bf16* lb, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
                                           int r0, int wave, int lane) {
   constexpr int CPR = D / 8, RPI = 64 / CPR, PW = 64 * CPR / 64 / 4;  // PW instructions per wave
   asm volatile("" : "+s"(la), "+s"(lb));
+  const int r = lane / CPR;
+  int rowb = r * D * 2;                                         // per-lane row bytes
+  int chunkb = 16 * ((lane % CPR) ^ swz_chunk<CPR>(r));         // per-lane chunk bytes
+  asm volatile("" : "+v"(rowb), "+v"(chunkb));                  // computed here, not kept live
 #pragma unroll
   for (int j = 0; j < PW; ++j) {
     const int J = wave * PW + j;
-    const int row = RPI * J + lane / CPR;
-    const int c = (lane % CPR) ^ swz_chunk<CPR>(row);
-    const int voff = ((r0 + row) * D + 8 * c) * 2;
+    const int voff = (r0 + RPI * J) * D * 2 + rowb + (chunkb ^ (16 * swz_chunk<CPR>(RPI * J)));
     __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, LDS_PTR(void, la + J * 512), 16, voff, 0, 0, 0);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, LDS_PTR(void, lb + J * 512), 16, voff, 0, 0, 0);
   }
