@@ -534,22 +534,22 @@ constexpr int bwd_valu_per_elem() { return MODE == MODE_INRANGE ? 14 : 20; }
 // dK/dV kernel for bf16 inputs: 128 keys per workgroup, 32 per wave (lane = key), dK/dV
 // accumulated in registers over the 64-query tiles of the causal range. dQ is formed by
 // attn_bwd_dq_kernel, so this kernel stages nothing for it. Arranged for one wave per SIMD
-// as a software pipeline of fixed steps; each step's MFMAs use LDS fragments read in earlier
-// steps, so no MFMA waits on a just-issued read:
-//   R1  S, dP of query block 0                      (MFMA)
-//   R2  S, dP of block 1  | P, dS of block 0        (MFMA | VALU)
-//   R3  dV, dK of block 0 | P, dS of block 1, 0..7  (MFMA | VALU)
-//   R4  dV, dK of block 1 from elements 0..7 | P, dS of block 1, 8..15
-//   R5  dV, dK of block 1 from elements 8..15       (MFMA)
-//   barrier; copy of tile t+2 into this tile's buffer set
-// Query tiles ping-pong between two LDS buffer sets (distinct __shared__ objects); the copy
-// of tile t+2 is issued right after tile t's barrier, a full tile ahead of its use. The
-// causal mask is evaluated only on the two tiles that cross the diagonal; every LDS access is
-// a per-lane swizzled offset computed once plus an immediate.
+// as a software pipeline of fixed steps; each step's MFMAs use LDS fragments read two steps
+// earlier, so no MFMA waits on a just-issued read:
+//   R1  S, dP of query block 0 (MFMA), the copy of the next tile spread over its steps
+//   R2  S, dP of block 1 (MFMA) | P, dS of block 0, elements 0..7 (VALU)
+//   C   16 steps of dV += P^T dO, dK += dS^T Q, one 16-query quarter and one d block each:
+//       quarter 0 under elements 8..15 of block 0, quarter 1 under 0..7 of block 1, quarter
+//       2 under 8..15 of block 1, quarter 3 alone (every quarter's weights are ready by then)
+//   barrier (the next tile's copy has landed)
+// Query tiles ping-pong between two LDS buffer sets (distinct __shared__ objects). The causal
+// mask is evaluated only on the two tiles that cross the diagonal; every LDS access is a
+// per-lane swizzled offset computed once plus an immediate.
 template <int D, int MODE, int L2N>
 __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) {
   static_assert(D == 64 || D == 128, "head_dim");
   constexpr int BQ = BF_BQ, CPR = D / 8, NDB = D / 32, NF = D / 16;
+  constexpr int PW = 64 * CPR / 64 / 4;  // copy instruction pairs per wave and tile
   __shared__ __attribute__((aligned(16))) bf16 Qs0[BQ * D];
   __shared__ __attribute__((aligned(16))) bf16 Qs1[BQ * D];
   __shared__ __attribute__((aligned(16))) bf16 dOs0[BQ * D];
@@ -588,10 +588,6 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
 
   tile_dma2<D>(Qs0, dOs0, rq, rdo, qstart * BQ, wave, lane);
   bwd_stat_dma(st0, di0, rst, rdi, qstart * BQ, wave, lane);
-  if (qstart + 1 < nq) {
-    tile_dma2<D>(Qs1, dOs1, rq, rdo, (qstart + 1) * BQ, wave, lane);
-    bwd_stat_dma(st1, di1, rst, rdi, (qstart + 1) * BQ, wave, lane);
-  }
   // K and V fragments of this wave's keys: B operands of S = Q K^T and dP = dO V^T. Keys
   // past T are zero and always masked.
   bf16x8 kf[NF], vf[NF];
@@ -622,13 +618,14 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
     tq_hi[db] = swz_at<CPR>(4 * h + 8 + trow, tr_col(db * 32, lane));
   }
 
-  bf16x8 rq3[3], ro3[3];  // row fragments of Q / dO, two steps ahead (R1, R2)
+  bf16x8 rq4[4], ro4[4];  // row fragments of Q / dO, three steps ahead (R1, R2)
   __builtin_amdgcn_s_waitcnt(VMCNT0);
   __syncthreads();
-  rq3[0] = ld8(Qs0 + row_off[0]);
-  ro3[0] = ld8(dOs0 + row_off[0]);
-  rq3[1] = ld8(Qs0 + row_off[1]);
-  ro3[1] = ld8(dOs0 + row_off[1]);
+#pragma unroll
+  for (int g = 0; g < 3; ++g) {
+    rq4[g] = ld8(Qs0 + row_off[g]);
+    ro4[g] = ld8(dOs0 + row_off[g]);
+  }
   constexpr int VE = bwd_valu_per_elem<MODE>();
 
   // One query tile. BUF selects the LDS buffer set, MASKED the tiles that cross the diagonal.
@@ -646,16 +643,16 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
     floatx4 stq[2][4], diq[2][4];
     float pv[16], dsv[16];
 
-    // R1/R2 step g = NF * sub + st: MFMAs on the fragments of step g, reads for step g + 2.
+    // R1/R2 step g = NF * sub + st: MFMAs on the fragments of step g, reads for step g + 3.
     auto sdp_step = [&](int g) {
       const int sub = g / NF, st = g % NF;
-      const int gn = g + 2;
+      const int gn = g + 3;
       if (gn < 2 * NF) {
-        rq3[gn % 3] = ld8(Qs + (gn / NF) * 32 * D + row_off[gn % NF]);
-        ro3[gn % 3] = ld8(dOs + (gn / NF) * 32 * D + row_off[gn % NF]);
+        rq4[gn % 4] = ld8(Qs + (gn / NF) * 32 * D + row_off[gn % NF]);
+        ro4[gn % 4] = ld8(dOs + (gn / NF) * 32 * D + row_off[gn % NF]);
       }
-      s[sub] = mfma_bf16(rq3[g % 3], kf[st], s[sub]);
-      dp[sub] = mfma_bf16(ro3[g % 3], vf[st], dp[sub]);
+      s[sub] = mfma_bf16(rq4[g % 4], kf[st], s[sub]);
+      dp[sub] = mfma_bf16(ro4[g % 4], vf[st], dp[sub]);
     };
     auto load_stats = [&](int sub) {
 #pragma unroll
@@ -677,25 +674,25 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
         da[sub][i >> 3][i & 7] = f2bf(dsv[i]);
       }
     };
-    // dV += P^T dO and dK += dS^T Q, one d block per step; fragments one step ahead.
-    // Half `hf` of block sub: the products over its queries 0..15 (hf = 0) or 16..31.
-    bf16x8 ft[2][4];
-    auto dvdk_load = [&](int sub, int db, bf16x8 (&f)[4]) {
-      const bf16* qb = Qs + sub * 32 * D;
-      const bf16* ob = dOs + sub * 32 * D;
-      f[0] = tr_frag_at(ob, tq_lo[db], tq_hi[db]);
-      f[1] = tr_frag_at(ob + 16 * D, tq_lo[db], tq_hi[db]);
-      f[2] = tr_frag_at(qb, tq_lo[db], tq_hi[db]);
-      f[3] = tr_frag_at(qb + 16 * D, tq_lo[db], tq_hi[db]);
+    // C step c = NDB * qq + db: dV += P^T dO and dK += dS^T Q over the tile's queries
+    // 16 qq .. 16 qq + 15 and d block db; its fragments sit in ring slot c % 4.
+    constexpr int NC = 4 * NDB;
+    bf16x8 fc[4][2];
+    auto c_load = [&](int c) {
+      const int qq = c / NDB, db = c % NDB;
+      fc[c % 4][0] = tr_frag_at(dOs + qq * 16 * D, tq_lo[db], tq_hi[db]);
+      fc[c % 4][1] = tr_frag_at(Qs + qq * 16 * D, tq_lo[db], tq_hi[db]);
     };
-    auto dvdk_half_load = [&](int hf, int db, bf16x8 (&f)[4]) {
-      const bf16* qb = Qs + 32 * D + hf * 16 * D;
-      const bf16* ob = dOs + 32 * D + hf * 16 * D;
-      f[0] = tr_frag_at(ob, tq_lo[db], tq_hi[db]);
-      f[2] = tr_frag_at(qb, tq_lo[db], tq_hi[db]);
+    auto c_mma = [&](int c) {
+      const int qq = c / NDB, db = c % NDB;
+      dv[db] = mfma_bf16(pa[qq >> 1][qq & 1], fc[c % 4][0], dv[db]);
+      dk[db] = mfma_bf16(da[qq >> 1][qq & 1], fc[c % 4][1], dk[db]);
     };
 
-    // R1: S and dP of block 0.
+    // R1: S and dP of block 0; the copy of the next tile, one instruction pair per step. It
+    // is issued unconditionally: past the last tile every row lies beyond the descriptors'
+    // ranges (no memory is read, zeros land in the unused buffer set), and it has completed
+    // by this tile's vmcnt(0).
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
       s[sb] = floatx16{};
@@ -705,75 +702,61 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
 #pragma unroll
     for (int g = 0; g < NF; ++g) {
       sdp_step(g);
+      if (g < PW) {
+        if constexpr (BUF) tile_dma2_part<D>(Qs0, dOs0, rq, rdo, qbase + BQ, wave, lane, g);
+        else tile_dma2_part<D>(Qs1, dOs1, rq, rdo, qbase + BQ, wave, lane, g);
+      }
+      if (g == PW) {
+        if constexpr (BUF) bwd_stat_dma(st0, di0, rst, rdi, qbase + BQ, wave, lane);
+        else bwd_stat_dma(st1, di1, rst, rdi, qbase + BQ, wave, lane);
+      }
       if (g == 0) step_order<2, 0, 4 + 8, 0>();
       else step_order<2, 0, 4, 0>();
     }
-    // R2: S and dP of block 1 under P and dS of block 0.
-    constexpr int E2 = 16 / NF;
+    // R2: S and dP of block 1 under elements 0..7 of block 0.
+    constexpr int E2 = 8 / NF > 0 ? 8 / NF : 1;
 #pragma unroll
     for (int g = NF; g < 2 * NF; ++g) {
       sdp_step(g);
       const int st = g - NF;
 #pragma unroll
-      for (int k = 0; k < E2; ++k) elem(0, E2 * st + k);
-      if (g == 2 * NF - 2) load_stats(1);
-      if (g == 2 * NF - 1) dvdk_load(0, 0, ft[0]);
-      step_order<2, VE * E2, 4 + 8, 0>();
+      for (int k = 0; k < E2; ++k)
+        if (E2 * st + k < 8) elem(0, E2 * st + k);
+      if (g == 2 * NF - 3) c_load(0);
+      if (g == 2 * NF - 2) c_load(1);
+      if (g == 2 * NF - 1) c_load(2);
+      step_order<2, VE * E2, 4 + 4, 0>();
     }
-    // R3: dV/dK of block 0 under P and dS of block 1, elements 0..7.
-    constexpr int E3 = 8 / NDB;
+    // C steps: quarter 0 under elements 8..15 of block 0, quarter 1 under 0..7 of block 1,
+    // quarter 2 under 8..15 of block 1, quarter 3 alone.
+    load_stats(1);
+    constexpr int EC = 8 / NDB;
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-      if (db + 1 < NDB) dvdk_load(0, db + 1, ft[(db + 1) & 1]);
-      else dvdk_half_load(0, 0, ft[0]);
-      const int c = db & 1;
-      dv[db] = mfma_bf16(pa[0][0], ft[c][0], dv[db]);
-      dv[db] = mfma_bf16(pa[0][1], ft[c][1], dv[db]);
-      dk[db] = mfma_bf16(da[0][0], ft[c][2], dk[db]);
-      dk[db] = mfma_bf16(da[0][1], ft[c][3], dk[db]);
+    for (int c = 0; c < NC; ++c) {
+      if (c + 3 < NC) c_load(c + 3);
+      c_mma(c);
+      const int qq = c / NDB, db = c % NDB;
+      if (qq < 3) {
 #pragma unroll
-      for (int k = 0; k < E3; ++k) elem(1, E3 * db + k);
-      step_order<4, VE * E3, 8, 0>();
-    }
-    // R4: dV/dK of block 1 over its queries 0..15 (elements 0..7) under elements 8..15.
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-      const int c = db & 1;
-      if (db + 1 < NDB) dvdk_half_load(0, db + 1, ft[c ^ 1]);
-      else dvdk_half_load(1, 0, ft[c ^ 1]);
-      dv[db] = mfma_bf16(pa[1][0], ft[c][0], dv[db]);
-      dk[db] = mfma_bf16(da[1][0], ft[c][2], dk[db]);
-#pragma unroll
-      for (int k = 0; k < E3; ++k) elem(1, 8 + E3 * db + k);
-      step_order<2, VE * E3, 4, 0>();
-    }
-    // R5: dV/dK of block 1 over its queries 16..31 (elements 8..15).
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-      const int c = (db + NDB) & 1;
-      if (db + 1 < NDB) dvdk_half_load(1, db + 1, ft[c ^ 1]);
-      dv[db] = mfma_bf16(pa[1][1], ft[c][0], dv[db]);
-      dk[db] = mfma_bf16(da[1][1], ft[c][2], dk[db]);
-      step_order<2, 0, 4, 0>();
+        for (int k = 0; k < EC; ++k) {
+          const int idx = EC * db + k;  // quarter 0: 8..15 of block 0; 1: 0..7 of block 1; 2: 8..15
+          elem(qq == 0 ? 0 : 1, qq == 1 ? idx : 8 + idx);
+        }
+        step_order<2, VE * EC, 4, 0>();
+      } else {
+        step_order<2, 0, 4, 0>();
+      }
     }
 
     __builtin_amdgcn_s_waitcnt(VMCNT0);  // this wave's copies of the next tile have landed
-    __syncthreads();                     // this buffer set is no longer read
-    {  // first fragments of the next tile (the other buffer set, complete after the barrier)
+    __syncthreads();                     // the next buffer set is complete; this one is free
+    {  // first fragments of the next tile
       const bf16* Qn = BUF ? Qs0 : Qs1;
       const bf16* dOn = BUF ? dOs0 : dOs1;
-      rq3[0] = ld8(Qn + row_off[0]);
-      ro3[0] = ld8(dOn + row_off[0]);
-      rq3[1] = ld8(Qn + row_off[1]);
-      ro3[1] = ld8(dOn + row_off[1]);
-    }
-    if (qt + 2 < nq) {
-      if constexpr (BUF) {
-        tile_dma2<D>(Qs1, dOs1, rq, rdo, qbase + 2 * BQ, wave, lane);
-        bwd_stat_dma(st1, di1, rst, rdi, qbase + 2 * BQ, wave, lane);
-      } else {
-        tile_dma2<D>(Qs0, dOs0, rq, rdo, qbase + 2 * BQ, wave, lane);
-        bwd_stat_dma(st0, di0, rst, rdi, qbase + 2 * BQ, wave, lane);
+#pragma unroll
+      for (int g = 0; g < 3; ++g) {
+        rq4[g] = ld8(Qn + row_off[g]);
+        ro4[g] = ld8(dOn + row_off[g]);
       }
     }
   };

@@ -124,7 +124,9 @@ template <int D>
 __device__ __forceinline__ void tile_dma2(bf16* la, bf16* lb, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
                                           int r0, int wave, int lane) {
   constexpr int CPR = D / 8, RPI = 64 / CPR, PW = 64 * CPR / 64 / 4;  // PW instructions per wave
-  asm volatile("" : "+s"(la), "+s"(lb));
+  auto lla = LDS_PTR(bf16, la);
+  auto llb = LDS_PTR(bf16, lb);
+  asm volatile("" : "+s"(lla), "+s"(llb));
   const int r = lane / CPR;
   int rowb = r * D * 2;                                         // per-lane row bytes
   int chunkb = 16 * ((lane % CPR) ^ swz_chunk<CPR>(r));         // per-lane chunk bytes
@@ -133,9 +135,27 @@ __device__ __forceinline__ void tile_dma2(bf16* la, bf16* lb, __amdgpu_buffer_rs
   for (int j = 0; j < PW; ++j) {
     const int J = wave * PW + j;
     const int voff = (r0 + RPI * J) * D * 2 + rowb + (chunkb ^ (16 * swz_chunk<CPR>(RPI * J)));
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, LDS_PTR(void, la + J * 512), 16, voff, 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, LDS_PTR(void, lb + J * 512), 16, voff, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, lla + J * 512, 16, voff, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, llb + J * 512, 16, voff, 0, 0, 0);
   }
+}
+// Instruction pair j of tile_dma2 alone (lets a kernel spread a tile copy over several
+// pipeline steps).
+template <int D>
+__device__ __forceinline__ void tile_dma2_part(bf16* la, bf16* lb, __amdgpu_buffer_rsrc_t ra,
+                                               __amdgpu_buffer_rsrc_t rb, int r0, int wave, int lane, int j) {
+  constexpr int CPR = D / 8, RPI = 64 / CPR, PW = 64 * CPR / 64 / 4;
+  auto lla = LDS_PTR(bf16, la);
+  auto llb = LDS_PTR(bf16, lb);
+  asm volatile("" : "+s"(lla), "+s"(llb));
+  const int r = lane / CPR;
+  int rowb = r * D * 2;
+  int chunkb = 16 * ((lane % CPR) ^ swz_chunk<CPR>(r));
+  asm volatile("" : "+v"(rowb), "+v"(chunkb));
+  const int J = wave * PW + j;
+  const int voff = (r0 + RPI * J) * D * 2 + rowb + (chunkb ^ (16 * swz_chunk<CPR>(RPI * J)));
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, lla + J * 512, 16, voff, 0, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, llb + J * 512, 16, voff, 0, 0, 0);
 }
 
 // Instruction order of one pipeline step: NM MFMAs, each followed by a share of the step's
