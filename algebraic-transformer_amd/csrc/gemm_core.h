@@ -19,6 +19,8 @@
 // through registers with zero fill instead.
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace alg {
@@ -235,43 +237,33 @@ __device__ __forceinline__ void gemm_mainloop(GemmStage<AM, BM, C>& s0, GemmStag
     TA::copy(st.a, A, aoff, wave_u, m0, kt * GT_K);
     TB::copy(st.b, B, boff, wave_u, n0, kt * GT_K);
   };
-  // The copy of a tile in two halves, issued during the first two phases of a step.
-  constexpr int HA = TA::PER_WAVE / 2, HB = TB::PER_WAVE / 2;
-  auto copy_half0 = [&](GemmStage<AM, BM, C>& st, int kt) {
-    TA::template copy<0, HA>(st.a, A, aoff, wave_u, m0, kt * GT_K);
-    TB::template copy<0, HB>(st.b, B, boff, wave_u, n0, kt * GT_K);
-  };
-  auto copy_half1 = [&](GemmStage<AM, BM, C>& st, int kt) {
-    TA::template copy<HA, TA::PER_WAVE>(st.a, A, aoff, wave_u, m0, kt * GT_K);
-    TB::template copy<HB, TB::PER_WAVE>(st.b, B, boff, wave_u, n0, kt * GT_K);
-  };
-  constexpr int NG0 = HA + HB, NG1 = TA::PER_WAVE + TB::PER_WAVE - NG0;
-  // One k step with a next tile, software-pipelined over its four 16-deep sub-steps:
-  // fragments of sub-step ks+1 are read while sub-step ks multiplies. f0 holds sub-step 0
-  // of `cur` on entry and sub-step 0 of `nxt` on exit. The copy of tile kt+1 into `nxt` is
-  // spread over the first two sub-steps; the barrier (after this wave's copies have landed,
-  // vmcnt) comes before the last sub-step so the next tile's first fragments are read
-  // while it multiplies.
+  constexpr int NG = TA::PER_WAVE + TB::PER_WAVE;  // copy instructions per wave and tile
+  // One k step, software-pipelined over its four 16-deep sub-steps: fragments of sub-step
+  // ks+1 are read while ks multiplies. f0 holds sub-step 0 of `cur` on entry and sub-step 0
+  // of `nxt` on exit. The barrier (after this wave's copies into `nxt` have landed, vmcnt)
+  // comes before the last sub-step; after it no wave reads `cur` again, so the copy of tile
+  // kt+2 into `cur` is issued right there, under the last sub-step's MFMAs: each copy has a
+  // whole k step to land before the next barrier waits for it.
   Frags f0, f1;
   constexpr int NM = C::MB * C::NB;
   constexpr int NR = C::MB * TA::READS_PER_FRAG + C::NB * TB::READS_PER_FRAG;
-  auto step = [&](const GemmStage<AM, BM, C>& cur, GemmStage<AM, BM, C>& nxt, int kt) {
-    copy_half0(nxt, kt + 1);
+  static_assert(NG <= NM, "one copy per MFMA at most");
+  auto step = [&](GemmStage<AM, BM, C>& cur, GemmStage<AM, BM, C>& nxt, int kt, auto copyc) {
     load(cur, 1, f1);
     mma(f0);
-    interleave_phase<NM, NR, NG0>();
-    copy_half1(nxt, kt + 1);
+    interleave_phase<NM, NR>();
     load(cur, 2, f0);
     mma(f1);
-    interleave_phase<NM, NR, NG1>();
+    interleave_phase<NM, NR>();
     load(cur, 3, f1);
     mma(f0);
     interleave_phase<NM, NR>();
     __builtin_amdgcn_s_waitcnt(VMCNT0);
     __syncthreads();
+    if constexpr (decltype(copyc)::value) copy_tile(cur, kt + 2);
     load(nxt, 0, f0);
     mma(f1);
-    interleave_phase<NM, NR>();
+    interleave_phase<NM, NR, decltype(copyc)::value ? NG : 0>();
   };
   // The last k step: no copy.
   auto last = [&](const GemmStage<AM, BM, C>& cur) {
@@ -287,15 +279,16 @@ __device__ __forceinline__ void gemm_mainloop(GemmStage<AM, BM, C>& s0, GemmStag
     mma(f1);
   };
   copy_tile(s0, 0);
+  copy_tile(s1, 1);  // nk is even here, so there are at least two k steps
   __builtin_amdgcn_s_waitcnt(VMCNT0);
   __syncthreads();
   load(s0, 0, f0);
-  int kt = 0;  // nk is even here
+  int kt = 0;
   for (; kt + 2 < nk; kt += 2) {
-    step(s0, s1, kt);
-    step(s1, s0, kt + 1);
+    step(s0, s1, kt, std::true_type{});
+    step(s1, s0, kt + 1, std::true_type{});
   }
-  step(s0, s1, kt);
+  step(s0, s1, kt, std::false_type{});
   last(s1);
 }
 
