@@ -265,7 +265,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
   const float scale = Z;
   if (myq < T_) {
     T* O = reinterpret_cast<T*>(p.o) + base + (size_t)myq * D;
-    float* OP = p.o_precise ? p.o_precise + base + (size_t)myq * D : nullptr;
+    // o_precise carries the shifted branch's unrounded output only (flash.py:322).
+    float* OP = (MODE == MODE_SHIFTED && p.o_precise) ? p.o_precise + base + (size_t)myq * D : nullptr;
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
 #pragma unroll
@@ -464,22 +465,16 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) 
   float Z = lsum + xor32(lsum);
   if (p.sink) Z += pow2n<L2N>(rho_fast(p.sink[head]), log2n);
   const float inv = 1.0f / Z;
-  bf16* O = reinterpret_cast<bf16*>(p.o) + base + (size_t)myq * D;
-  float* OP = p.o_precise ? p.o_precise + base + (size_t)myq * D : nullptr;
+  bf16* O = reinterpret_cast<bf16*>(p.o) + base + (size_t)myq * D;  // (o_precise: shifted only)
 #pragma unroll
   for (int db = 0; db < NDB; ++db) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int d0 = db * 32 + 8 * g + 4 * h;
-      floatx4 val;
       bf16x4 ob;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        val[e] = oacc[db][4 * g + e] * inv;
-        ob[e] = f2bf(val[e]);
-      }
+      for (int e = 0; e < 4; ++e) ob[e] = f2bf(oacc[db][4 * g + e] * inv);
       *reinterpret_cast<bf16x4*>(O + d0) = ob;
-      if (OP) *reinterpret_cast<floatx4*>(OP + d0) = val;
     }
   }
   if (h == 0) p.stat[(size_t)bh * T_ + myq] = inv;

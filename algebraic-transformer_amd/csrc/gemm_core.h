@@ -85,16 +85,21 @@ struct OperandTile {
   // stored matrix. Lane `lane` of instruction J writes the physical chunk 64*J + lane.
   // `wave` must be wave-uniform (from readfirstlane) so the addressing stays scalar.
   // Instructions [J0, J1) of this wave's share (all of it by default).
+  // The copies are buffer loads that write LDS: the descriptor's base is the tile's first
+  // element (scalar), the instruction's row offset is the scalar offset, and the per-lane part
+  // is one of the two lane offsets, so no per-instruction vector address is formed.
   template <int J0 = 0, int J1 = PER_WAVE>
   static __device__ __forceinline__ void copy(bf16* tile, const GemmOperand& op, const uint32_t (&off)[2], int wave,
                                               int mn0, int k0) {
     const int r0 = (MODE == KMAJOR) ? mn0 : k0;
     const int c0 = (MODE == KMAJOR) ? k0 : mn0;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(op.ptr + ((long)r0 * op.ld + c0)), (short)0, 0x7FFFFFFF, BUF_RSRC_WORD3);
 #pragma unroll
     for (int j = J0; j < J1; ++j) {
       const int J = wave * PER_WAVE + j;
-      const char* base = reinterpret_cast<const char*>(op.ptr + ((long)(r0 + RPI * J) * op.ld + c0));
-      __builtin_amdgcn_global_load_lds(base + off[j & 1], LDS_PTR(void, tile + J * 512), 16, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, LDS_PTR(void, tile + J * 512), 16, off[j & 1],
+                                               (int)(RPI * J * op.ld * 2), 0, 0);
     }
   }
   // Synchronous copy with zero fill (edge tiles, partial last k tile): elements outside the
