@@ -254,6 +254,7 @@ __device__ __forceinline__ void gemm_mainloop(GemmStage<AM, BM, C>& s0, GemmStag
   constexpr int NR = C::MB * TA::READS_PER_FRAG + C::NB * TB::READS_PER_FRAG;
   static_assert(NG <= NM, "one copy per MFMA at most");
   auto step = [&](GemmStage<AM, BM, C>& cur, GemmStage<AM, BM, C>& nxt, int kt, auto copyc) {
+    __builtin_amdgcn_s_setprio(0);
     load(cur, 1, f1);
     mma(f0);
     interleave_phase<NM, NR>();
@@ -265,6 +266,10 @@ __device__ __forceinline__ void gemm_mainloop(GemmStage<AM, BM, C>& s0, GemmStag
     interleave_phase<NM, NR>();
     __builtin_amdgcn_s_waitcnt(VMCNT0);
     __syncthreads();
+    // Raised wave priority from the barrier to the end of the step: the waves that leave the
+    // barrier first issue their copies and the next stage's first fragments ahead of the
+    // other wave's sub-step MFMAs (measured: about 1 % on the head products).
+    __builtin_amdgcn_s_setprio(1);
     if constexpr (decltype(copyc)::value) copy_tile(cur, kt + 2);
     load(nxt, 0, f0);
     mma(f1);
