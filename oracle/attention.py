@@ -155,23 +155,26 @@ def prologue(q, sink_logit, *, c=8.0, dtype="bf16"):
     return q_s, sink, alpha
 
 
-def kernel_forward(q_s, k, v, sink, *, n=16, dtype="bf16", shifted=False, heads=None):
+def kernel_forward(q_s, k, v, sink, *, n=16, dtype="bf16", shifted=False, heads=None, rows=None):
     """Forward of the kernel on pre-scaled queries; returns (o, stat, o_precise).
 
     Unshifted (in range): w = rho_fast(x)^n, Z = rho_fast(beta)^n + sum_j w,
     o = round(sum_j round(w) v * (1/Z)), stat = 1/Z (flash.py:197-234, 271-284).
     Shifted fallback: m = max(beta, max_j x); w = (rho(x) rho(-m))^n with stable rho;
     stat = rho(-m) Z^(-1/n); o kept in f32 as well (precise_output).
-    ``heads`` restricts the computation to a list of (b, h) pairs (bounded CPU samples).
+    ``heads`` restricts the computation to a list of (b, h) pairs and ``rows`` to a list of
+    query rows (each row still sees every causal key j <= i); entries outside them stay 0.
+    Both bound the CPU work at long sequence lengths.
     """
     B, H, T, D = q_s.shape
     o = np.zeros((B, H, T, D), F32)
     o_precise = np.zeros((B, H, T, D), F32)
     stat = np.zeros((B, H, T), F32)
-    mask = np.tril(np.ones((T, T), bool))
+    ri = np.arange(T) if rows is None else np.asarray(rows)
+    mask = ri[:, None] >= np.arange(T)[None, :]
     pairs = heads if heads is not None else [(b, h) for b in range(B) for h in range(H)]
     for b, h in pairs:
-        qb = q_s[b, h].astype(F32)
+        qb = q_s[b, h][ri].astype(F32)
         kb = k[b, h].astype(F32)
         vb = v[b, h].astype(F32)
         x = qb @ kb.T
@@ -182,9 +185,9 @@ def kernel_forward(q_s, k, v, sink, *, n=16, dtype="bf16", shifted=False, heads=
                 Z = Z + int_pow(rho_fast(F32(sink[h]))[0], n)
             acc = round_to(w, dtype) @ vb
             inv = (F32(1) / Z).astype(F32)
-            o[b, h] = round_to(acc * inv[:, None], dtype)
-            o_precise[b, h] = acc * inv[:, None]
-            stat[b, h] = inv
+            o[b, h, ri] = round_to(acc * inv[:, None], dtype)
+            o_precise[b, h, ri] = acc * inv[:, None]
+            stat[b, h, ri] = inv
         else:
             xm = np.where(mask, x, -np.inf)
             m = np.max(xm, axis=1)
@@ -197,9 +200,9 @@ def kernel_forward(q_s, k, v, sink, *, n=16, dtype="bf16", shifted=False, heads=
                 Z = Z + int_pow(rho_exact(F32(sink[h]))[0] * shift, n)
             acc = round_to(w, dtype) @ vb
             inv = (F32(1) / Z).astype(F32)
-            o_precise[b, h] = acc * inv[:, None]
-            o[b, h] = round_to(o_precise[b, h], dtype)
-            stat[b, h] = shift * inv_root(Z, n)
+            o_precise[b, h, ri] = acc * inv[:, None]
+            o[b, h, ri] = round_to(o_precise[b, h, ri], dtype)
+            stat[b, h, ri] = shift * inv_root(Z, n)
     return o, stat, o_precise
 
 

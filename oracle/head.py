@@ -86,8 +86,13 @@ def kernel_forward(h, E, targets, *, n=8, c=2.0, dtype="bf16", rows=None, chunk=
 
 
 def kernel_backward(h, E, targets, stat, g=1.0, *, n=8, c=2.0, dtype="bf16", e_dtype="bf16",
-                    chunk=2048):
-    """(dh, dE) of the fused head backward with the kernel's rounding points."""
+                    chunk=2048, rows=None):
+    """(dh, dE) of the fused head backward with the kernel's rounding points.
+
+    ``rows`` restricts the work to a token subset (bounded CPU samples): dh is exact on those
+    rows (0 elsewhere) and dE then sums only their contributions. The scale keeps the full
+    token count N of ``h``.
+    """
     Eb = round_to(E, dtype).astype(F32)
     hh = h.astype(F32)
     N = h.shape[0]
@@ -97,8 +102,9 @@ def kernel_backward(h, E, targets, stat, g=1.0, *, n=8, c=2.0, dtype="bf16", e_d
     scale = F32(g * (n / c) / N)
     dh = np.zeros(h.shape, F32)
     dE = np.zeros(E.shape, F32)
-    for s in range(0, N, chunk):
-        ids = np.arange(s, min(N, s + chunk))
+    idx = np.arange(N) if rows is None else np.asarray(rows)
+    for s in range(0, len(idx), chunk):
+        ids = idx[s:s + chunk]
         z = hh[ids] @ Eb.T
         x = np.minimum(z * inv_c, X)
         rad = F32(1) + x * x
