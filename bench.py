@@ -15,6 +15,9 @@ the attention TFLOP/s, the head tokens/s and each part's fraction of the bf16 de
 peak are reported beside it, with a roofline entry for the kernel that takes the most time
 (per-kernel durations from HIP events recorded on the launch stream) and a CPU baseline
 (the NumPy oracle timed on a bounded sample of the same workload on the host cores).
+The other BASELINE configs (C1 attention fwd fp32, C2 head, C3 attention fwd+bwd D64, C5
+long-context attention fwd) are timed as well (median of 20 wrapper calls) and reported under
+``other_configs``; they are not part of ``value``.
 """
 
 import argparse
@@ -101,6 +104,83 @@ def make_steps(torch, x):
     return attn_step, head_step, full_step
 
 
+PEAK_FP32_TFLOPS = 157.3   # MI355X dense fp32 MFMA
+
+# The other BASELINE.json configs, reported beside the headline (timed unit: the wrapper call).
+OTHER_CONFIGS = {
+    "C1": dict(part="attn", dtype="f32", backward=False, B=2, H=12, T=1024, D=64,
+               workload="attention fwd fp32 B2 H12 T1024 D64 (125M shape)"),
+    "C2": dict(part="head", N=8192, d=768, V=50257,
+               workload="fused alg_ce head fwd+bwd N8192 d768 V50257 bf16 (125M shape)"),
+    "C3": dict(part="attn", dtype="bf16", backward=True, B=8, H=16, T=2048, D=64,
+               workload="attention fwd+bwd bf16 B8 H16 T2048 D64 (350M shape)"),
+    "C5": dict(part="attn", dtype="bf16", backward=False, B=1, H=16, T=16384, D=128,
+               workload="attention fwd bf16 B1 H16 T16384 D128 (long context)"),
+}
+
+
+def time_other_configs(torch, dev, iters=20, warmup=3, seed=1):
+    """Median wrapper-call time over ``iters`` calls (CUDA events on the launch stream) of
+    each other BASELINE config, with the same input distributions as the headline."""
+    from algebraic_amd.kernels.flash import flash_attention
+    from algebraic_amd.kernels.fused_head import fused_head
+    res = {}
+    for name, cfg in OTHER_CONFIGS.items():
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        rn = lambda *s: torch.randn(*s, device=dev, generator=g, dtype=torch.float32)
+        if cfg["part"] == "attn":
+            B, H, T, D = cfg["B"], cfg["H"], cfg["T"], cfg["D"]
+            dt = torch.bfloat16 if cfg["dtype"] == "bf16" else torch.float32
+            bwd = cfg["backward"]
+            q = rms_norm(rn(B, H, T, D)).to(dt).requires_grad_(bwd)
+            k = rms_norm(rn(B, H, T, D)).to(dt).requires_grad_(bwd)
+            v = rn(B, H, T, D).to(dt).requires_grad_(bwd)
+            sink = (rn(1, H, 1, 1) * 0.1).requires_grad_(bwd)
+            do = rn(B, H, T, D).to(dt)
+
+            def call():
+                if not bwd:
+                    with torch.no_grad():
+                        flash_attention(q, k, v, sink, kind="asinh", n=16, c=8.0, block=512, range_guard=True)
+                    return
+                o = flash_attention(q, k, v, sink, kind="asinh", n=16, c=8.0, block=512, range_guard=True)
+                torch.autograd.grad(o, (q, k, v, sink), do)
+            flops = attn_flops(B, H, T, D) * (3.5 if bwd else 1.0)
+            tokens = B * T
+            peak = PEAK_BF16_TFLOPS if dt == torch.bfloat16 else PEAK_FP32_TFLOPS
+        else:
+            N, d, V = cfg["N"], cfg["d"], cfg["V"]
+            h = rms_norm(rn(N, d)).to(torch.bfloat16).requires_grad_(True)
+            E = (rn(V, d) * 0.02).to(torch.bfloat16).requires_grad_(True)
+            t = torch.randint(0, V, (N,), device=dev, generator=g, dtype=torch.int32)
+
+            def call():
+                obj, _ = fused_head(h, E, t, kind="alg_ce", n=8, c=2.0)
+                torch.autograd.grad(obj, (h, E))
+            flops = head_flops(N, d, V)
+            tokens = N
+            peak = PEAK_BF16_TFLOPS
+        for _ in range(warmup):
+            call()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(iters):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            call()
+            e1.record()
+            e1.synchronize()
+            times.append(e0.elapsed_time(e1))
+        ms = sorted(times)[len(times) // 2]
+        tf = flops / (ms * 1e-3) / 1e12
+        res[name] = {"workload": cfg["workload"], "ms": round(ms, 4), "tflops": round(tf, 3),
+                     "tokens_per_s": round(tokens / (ms * 1e-3), 1), "peak": peak,
+                     "frac_peak": round(tf / peak, 4), "flops": flops}
+    torch.cuda.synchronize()
+    return res
+
+
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` recorded from rocprofv3 FETCH_SIZE + WRITE_SIZE runs
     (each scaled by the same counter's reading for a device copy of known size), as listed
@@ -174,6 +254,8 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip timing BASELINE configs 1, 2, 3 and 5 beside the headline")
     ap.add_argument("--only", choices=["attn", "head", "step"],
                     help="run only W+K launches of one part (for profiler runs) and print its time")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -279,6 +361,9 @@ def main():
                     for n, r in sorted(kernels.items())},
         "roofline": roofline,
     }
+    if not args.no_other_configs:
+        log("timing the other BASELINE configs (C1, C2, C3, C5)")
+        out["other_configs"] = time_other_configs(torch, dev)
     if not args.no_cpu_baseline:
         log("timing the CPU baseline sample")
         out["cpu_baseline"] = cpu_baseline()
