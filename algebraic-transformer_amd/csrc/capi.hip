@@ -78,13 +78,14 @@ AttnWs attn_ws(int B, int H, int T, int D) {
 }
 
 // Head buffers. Workspace: [partials f32 nvt*N][obj parts] (+ bwd: dZ bf16 Npad*Vp for the
-// recompute schedule, or s*h/l bf16 N*d for the residual schedule). Residual (optional,
+// recompute schedule, or s*h/l bf16 N*d for the residual schedule; then, when the dh product
+// is split over the vocabulary, its f32 partials split*N*d). Residual (optional,
 // forward -> backward): [U bf16 Npad*Vp][l f32 N]. dZ and U are token-major with rows of
 // Vp = V rounded up to 8 (16-byte aligned rows).
 struct HeadWs {
-  size_t partial, obj_part, bwd, total;
+  size_t partial, obj_part, bwd, dh_part, total;
   size_t res_ut, res_l, res_total;
-  int Npad, Vp;
+  int Npad, Vp, dh_split;
 };
 HeadWs head_ws(int N, int d, int V, int pass, bool residual) {
   HeadWs w;
@@ -94,7 +95,10 @@ HeadWs head_ws(int N, int d, int V, int pass, bool residual) {
   w.obj_part = align256((size_t)alg::head_vocab_tiles(V) * N * sizeof(float));
   w.bwd = w.obj_part + align256((size_t)alg::head_stat_blocks(N) * sizeof(float));
   const size_t bwd_bytes = residual ? (size_t)N * d * 2 : (size_t)w.Npad * w.Vp * 2;
-  w.total = pass == 0 ? w.bwd : w.bwd + align256(bwd_bytes);
+  w.dh_split = alg::head_dh_split(N, d, V);
+  w.dh_part = w.bwd + align256(bwd_bytes);
+  const size_t part_bytes = w.dh_split > 1 ? (size_t)w.dh_split * N * d * sizeof(float) : 0;
+  w.total = pass == 0 ? w.bwd : w.dh_part + align256(part_bytes);
   w.res_ut = 0;
   w.res_l = align256((size_t)w.Npad * w.Vp * 2);
   w.res_total = w.res_l + align256((size_t)N * sizeof(float));
@@ -304,6 +308,9 @@ int alg_head_bwd(alg_stream_t stream, int N, int d, int V, const void* h, const 
     p.dzt = reinterpret_cast<bf16*>(w + ws.bwd);
   }
   p.dh = static_cast<bf16*>(dh);
+  p.dh_split = ws.dh_split;
+  p.dh_kchunk = alg::head_dh_kchunk(V, ws.dh_split);
+  p.dh_part = ws.dh_split > 1 ? reinterpret_cast<float*>(w + ws.dh_part) : nullptr;
   p.dE = dE;
   p.dE_f32 = dE_dtype == ALG_DTYPE_F32;
   return hip_status(alg::launch_head_bwd(p, (hipStream_t)stream), "alg_head_bwd");

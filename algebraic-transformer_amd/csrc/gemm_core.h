@@ -8,15 +8,19 @@
 // m/n-contiguous ([k][mn]; fragments read transposed with ds_read_b64_tr_b16), so every
 // head product reads its operands in their natural HBM layout.
 //
-// Global -> LDS copies use global_load_lds_dwordx4 (each lane of a wave instruction writes
-// 16 bytes at base + 16*lane), so no VGPRs stage the tiles and the next tile's copy is in
-// flight while the current one feeds the MFMAs; tiles are double-buffered with one barrier
+// Global -> LDS copies are buffer loads that write LDS (each lane of a wave instruction
+// writes 16 bytes at base + 16*lane), so no VGPRs stage the tiles and the next tile's copy is
+// in flight while the current one feeds the MFMAs; tiles are double-buffered with one barrier
 // per k step. Because the copy writes rows without padding, 16-byte chunks are placed with an
 // XOR swizzle that keeps the fragment reads free of bank conflicts:
 //   k-contiguous rows (128 B):      chunk c of row r lives at chunk c ^ ((r >> 1) & 7)
 //   mn-contiguous rows (2*TMN B):   chunk c of row r lives at chunk c ^ (4 * (r & 3))
-// Tiles that reach past the matrix edge in m or n, and a partial last k tile, are copied
-// through registers with zero fill instead.
+// The pipelined loop covers the largest multiple of 128 in the k range; a remaining partial
+// k tile is copied through registers with zero fill. Tiles that reach past the matrix edge in
+// m or n stay on the pipelined loop with range-checked copies: every copy instruction gets a
+// descriptor whose range ends at the operand's allocation, so reads past it return zeros, and
+// the values read past a row's logical end (the next row's data) only reach output rows or
+// columns outside the matrix, which the epilogues do not store.
 #pragma once
 
 #include <type_traits>
@@ -39,8 +43,9 @@ struct GemmCfg {
 struct GemmOperand {
   const bf16* ptr;
   long ld;         // leading dimension (elements) of the stored matrix
-  int rows_valid;  // stored rows at or beyond this are not read
-  int cols_valid;  // stored columns at or beyond this are zero (ld >= cols_valid rounded up to 8)
+  int rows_valid;  // rows of the logical matrix
+  int cols_valid;  // columns of the logical matrix (ld >= cols_valid rounded up to 8)
+  long extent;     // elements readable from ptr (the allocation); a multiple of 8
 };
 
 // One operand tile covering TMN (m or n) x 64 (k) in LDS, unpadded and swizzled.
@@ -88,18 +93,34 @@ struct OperandTile {
   // The copies are buffer loads that write LDS: the descriptor's base is the tile's first
   // element (scalar), the instruction's row offset is the scalar offset, and the per-lane part
   // is one of the two lane offsets, so no per-instruction vector address is formed.
-  template <int J0 = 0, int J1 = PER_WAVE>
+  // CHECKED (edge tiles): one descriptor per instruction, based at the instruction's first
+  // row, whose range ends at the operand's allocation (the buffer range check covers the
+  // per-lane offset only, not the scalar one), so chunks past the allocation read as zeros.
+  template <bool CHECKED = false, int J0 = 0, int J1 = PER_WAVE>
   static __device__ __forceinline__ void copy(bf16* tile, const GemmOperand& op, const uint32_t (&off)[2], int wave,
                                               int mn0, int k0) {
     const int r0 = (MODE == KMAJOR) ? mn0 : k0;
     const int c0 = (MODE == KMAJOR) ? k0 : mn0;
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(op.ptr + ((long)r0 * op.ld + c0)), (short)0, 0x7FFFFFFF, BUF_RSRC_WORD3);
+    if constexpr (!CHECKED) {
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(op.ptr + ((long)r0 * op.ld + c0)), (short)0, 0x7FFFFFFF, BUF_RSRC_WORD3);
 #pragma unroll
-    for (int j = J0; j < J1; ++j) {
-      const int J = wave * PER_WAVE + j;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, LDS_PTR(void, tile + J * 512), 16, off[j & 1],
-                                               (int)(RPI * J * op.ld * 2), 0, 0);
+      for (int j = J0; j < J1; ++j) {
+        const int J = wave * PER_WAVE + j;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, LDS_PTR(void, tile + J * 512), 16, off[j & 1],
+                                                 (int)(RPI * J * op.ld * 2), 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int j = J0; j < J1; ++j) {
+        const int J = wave * PER_WAVE + j;
+        const long first = (long)(r0 + RPI * J) * op.ld + c0;  // element offset of the instruction's base
+        const long rest = op.extent - first;
+        const int nrec = rest <= 0 ? 0 : (int)(rest >= 0x3FFFFFFF ? 0x7FFFFFFE : 2 * rest);
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(op.ptr + (rest <= 0 ? 0 : first)), (short)0, nrec, BUF_RSRC_WORD3);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, LDS_PTR(void, tile + J * 512), 16, off[j & 1], 0, 0, 0);
+      }
     }
   }
   // Synchronous copy with zero fill (edge tiles, partial last k tile): elements outside the
@@ -183,12 +204,12 @@ __device__ __forceinline__ void wave_coords(int& wm, int& wn) {
   wn = wave % C::WN;
 }
 
-// Accumulate the (m0, n0) tile over k in [0, K). acc[mb][nb] is the wave's 32x32 block at
+// Accumulate the (m0, n0) tile over k in [kbeg, K). acc[mb][nb] is the wave's 32x32 block at
 // rows wm*WTM + mb*32 and columns wn*WTN + nb*32 of the workgroup tile.
 template <int AM, int BM, class C>
 __device__ __forceinline__ void gemm_mainloop(GemmStage<AM, BM, C>& s0, GemmStage<AM, BM, C>& s1,
-                                              const GemmOperand& A, const GemmOperand& B, int m0, int n0, int K,
-                                              floatx16 (&acc)[C::MB][C::NB]) {
+                                              const GemmOperand& A, const GemmOperand& B, int m0, int n0, int kbeg,
+                                              int K, floatx16 (&acc)[C::MB][C::NB]) {
   typedef OperandTile<AM, C::TM, C::THREADS> TA;
   typedef OperandTile<BM, C::TN, C::THREADS> TB;
   const int lane = threadIdx.x & 63;
@@ -198,7 +219,6 @@ __device__ __forceinline__ void gemm_mainloop(GemmStage<AM, BM, C>& s0, GemmStag
   for (int i = 0; i < C::MB; ++i)
 #pragma unroll
     for (int j = 0; j < C::NB; ++j) acc[i][j] = floatx16{};
-  const int nk = (K + GT_K - 1) / GT_K;
   struct Frags {
     bf16x8 a[C::MB], b[C::NB];
   };
@@ -215,91 +235,97 @@ __device__ __forceinline__ void gemm_mainloop(GemmStage<AM, BM, C>& s0, GemmStag
 #pragma unroll
       for (int j = 0; j < C::NB; ++j) acc[i][j] = mfma_bf16(f.a[i], f.b[j], acc[i][j]);
   };
-  // Tiles that reach past the stored matrix in m or n, or a K that is not a multiple of
-  // two k steps, take a plain single-stage loop with register copies and zero fill.
+  const int klen = K - kbeg;
+  const int kmain = klen >= 2 * GT_K ? klen - klen % (2 * GT_K) : 0;  // pipelined part
   const bool a_full = (AM == KMAJOR ? A.rows_valid : A.cols_valid) >= m0 + C::TM;
   const bool b_full = (BM == KMAJOR ? B.rows_valid : B.cols_valid) >= n0 + C::TN;
-  if (!a_full || !b_full || (K % (2 * GT_K)) != 0) {
-    for (int kt = 0; kt < nk; ++kt) {
+  if (kmain > 0) {
+    uint32_t aoff[2], boff[2];
+    TA::lane_offsets(A.ld, aoff);
+    TB::lane_offsets(B.ld, boff);
+    const int wave_u = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nk = kmain / GT_K;  // even, >= 2
+    // One k step, software-pipelined over its four 16-deep sub-steps: fragments of sub-step
+    // ks+1 are read while ks multiplies. f0 holds sub-step 0 of `cur` on entry and sub-step 0
+    // of `nxt` on exit. The barrier (after this wave's copies into `nxt` have landed, vmcnt)
+    // comes before the last sub-step; after it no wave reads `cur` again, so the copy of tile
+    // kt+2 into `cur` is issued right there, under the last sub-step's MFMAs: each copy has a
+    // whole k step to land before the next barrier waits for it.
+    auto pipelined = [&](auto checked) {
+      constexpr bool CHK = decltype(checked)::value;
+      auto copy_tile = [&](GemmStage<AM, BM, C>& st, int kt) {
+        TA::template copy<CHK>(st.a, A, aoff, wave_u, m0, kbeg + kt * GT_K);
+        TB::template copy<CHK>(st.b, B, boff, wave_u, n0, kbeg + kt * GT_K);
+      };
+      constexpr int NG = TA::PER_WAVE + TB::PER_WAVE;  // copy instructions per wave and tile
+      Frags f0, f1;
+      constexpr int NM = C::MB * C::NB;
+      constexpr int NR = C::MB * TA::READS_PER_FRAG + C::NB * TB::READS_PER_FRAG;
+      static_assert(NG <= NM, "one copy per MFMA at most");
+      auto step = [&](GemmStage<AM, BM, C>& cur, GemmStage<AM, BM, C>& nxt, int kt, auto copyc) {
+        __builtin_amdgcn_s_setprio(0);
+        load(cur, 1, f1);
+        mma(f0);
+        interleave_phase<NM, NR>();
+        load(cur, 2, f0);
+        mma(f1);
+        interleave_phase<NM, NR>();
+        load(cur, 3, f1);
+        mma(f0);
+        interleave_phase<NM, NR>();
+        __builtin_amdgcn_s_waitcnt(VMCNT0);
+        __syncthreads();
+        // Raised wave priority from the barrier to the end of the step: the waves that leave
+        // the barrier first issue their copies and the next stage's first fragments ahead of
+        // the other wave's sub-step MFMAs (measured: about 1 % on the head products).
+        __builtin_amdgcn_s_setprio(1);
+        if constexpr (decltype(copyc)::value) copy_tile(cur, kt + 2);
+        load(nxt, 0, f0);
+        mma(f1);
+        interleave_phase<NM, NR, decltype(copyc)::value ? NG : 0>();
+      };
+      // The last k step: no copy.
+      auto last = [&](const GemmStage<AM, BM, C>& cur) {
+        load(cur, 1, f1);
+        mma(f0);
+        interleave_phase<NM, NR>();
+        load(cur, 2, f0);
+        mma(f1);
+        interleave_phase<NM, NR>();
+        load(cur, 3, f1);
+        mma(f0);
+        interleave_phase<NM, NR>();
+        mma(f1);
+      };
+      copy_tile(s0, 0);
+      copy_tile(s1, 1);
+      __builtin_amdgcn_s_waitcnt(VMCNT0);
       __syncthreads();
-      TA::copy_zero_fill(s0.a, A, m0, kt * GT_K, K);
-      TB::copy_zero_fill(s0.b, B, n0, kt * GT_K, K);
-      __syncthreads();
-#pragma unroll
-      for (int ks = 0; ks < GT_K / 16; ++ks) {
-        Frags f;
-        load(s0, ks, f);
-        mma(f);
+      load(s0, 0, f0);
+      int kt = 0;
+      for (; kt + 2 < nk; kt += 2) {
+        step(s0, s1, kt, std::true_type{});
+        step(s1, s0, kt + 1, std::true_type{});
       }
-    }
-    return;
+      step(s0, s1, kt, std::false_type{});
+      last(s1);
+    };
+    if (a_full && b_full) pipelined(std::false_type{});
+    else pipelined(std::true_type{});
   }
-  uint32_t aoff[2], boff[2];
-  TA::lane_offsets(A.ld, aoff);
-  TB::lane_offsets(B.ld, boff);
-  const int wave_u = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  auto copy_tile = [&](GemmStage<AM, BM, C>& st, int kt) {
-    TA::copy(st.a, A, aoff, wave_u, m0, kt * GT_K);
-    TB::copy(st.b, B, boff, wave_u, n0, kt * GT_K);
-  };
-  constexpr int NG = TA::PER_WAVE + TB::PER_WAVE;  // copy instructions per wave and tile
-  // One k step, software-pipelined over its four 16-deep sub-steps: fragments of sub-step
-  // ks+1 are read while ks multiplies. f0 holds sub-step 0 of `cur` on entry and sub-step 0
-  // of `nxt` on exit. The barrier (after this wave's copies into `nxt` have landed, vmcnt)
-  // comes before the last sub-step; after it no wave reads `cur` again, so the copy of tile
-  // kt+2 into `cur` is issued right there, under the last sub-step's MFMAs: each copy has a
-  // whole k step to land before the next barrier waits for it.
-  Frags f0, f1;
-  constexpr int NM = C::MB * C::NB;
-  constexpr int NR = C::MB * TA::READS_PER_FRAG + C::NB * TB::READS_PER_FRAG;
-  static_assert(NG <= NM, "one copy per MFMA at most");
-  auto step = [&](GemmStage<AM, BM, C>& cur, GemmStage<AM, BM, C>& nxt, int kt, auto copyc) {
-    __builtin_amdgcn_s_setprio(0);
-    load(cur, 1, f1);
-    mma(f0);
-    interleave_phase<NM, NR>();
-    load(cur, 2, f0);
-    mma(f1);
-    interleave_phase<NM, NR>();
-    load(cur, 3, f1);
-    mma(f0);
-    interleave_phase<NM, NR>();
-    __builtin_amdgcn_s_waitcnt(VMCNT0);
+  // Remaining partial k tiles (and short k ranges): register copies with zero fill.
+  for (int k0 = kbeg + kmain; k0 < K; k0 += GT_K) {
     __syncthreads();
-    // Raised wave priority from the barrier to the end of the step: the waves that leave the
-    // barrier first issue their copies and the next stage's first fragments ahead of the
-    // other wave's sub-step MFMAs (measured: about 1 % on the head products).
-    __builtin_amdgcn_s_setprio(1);
-    if constexpr (decltype(copyc)::value) copy_tile(cur, kt + 2);
-    load(nxt, 0, f0);
-    mma(f1);
-    interleave_phase<NM, NR, decltype(copyc)::value ? NG : 0>();
-  };
-  // The last k step: no copy.
-  auto last = [&](const GemmStage<AM, BM, C>& cur) {
-    load(cur, 1, f1);
-    mma(f0);
-    interleave_phase<NM, NR>();
-    load(cur, 2, f0);
-    mma(f1);
-    interleave_phase<NM, NR>();
-    load(cur, 3, f1);
-    mma(f0);
-    interleave_phase<NM, NR>();
-    mma(f1);
-  };
-  copy_tile(s0, 0);
-  copy_tile(s1, 1);  // nk is even here, so there are at least two k steps
-  __builtin_amdgcn_s_waitcnt(VMCNT0);
-  __syncthreads();
-  load(s0, 0, f0);
-  int kt = 0;
-  for (; kt + 2 < nk; kt += 2) {
-    step(s0, s1, kt, std::true_type{});
-    step(s1, s0, kt + 1, std::true_type{});
+    TA::copy_zero_fill(s0.a, A, m0, k0, K);
+    TB::copy_zero_fill(s0.b, B, n0, k0, K);
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < GT_K / 16; ++ks) {
+      Frags f;
+      load(s0, ks, f);
+      mma(f);
+    }
   }
-  step(s0, s1, kt, std::false_type{});
-  last(s1);
 }
 
 // Map a linear workgroup id to (tile_m, tile_n) so that the workgroups one XCD runs

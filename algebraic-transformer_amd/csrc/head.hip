@@ -21,6 +21,7 @@
 //    dE = dZ^T h.
 // Every product reads its operands in their natural layout (k-contiguous fragments via
 // ds_read_b128, transposed ones via ds_read_b64_tr_b16).
+#include <cmath>
 #include <type_traits>
 
 #include "gemm_core.h"
@@ -54,9 +55,9 @@ __global__ __launch_bounds__(NT, 1) void head_fwd_kernel(HeadParams p) {
   xcd_tile(blockIdx.x, nbm, nbn, tm, tn);
   const int m0 = tm * HT_M;  // vocab
   const int n0 = tn * HT_N;  // tokens
-  GemmOperand A{p.E, p.d, p.V, p.d}, B{p.h, p.d, p.N, p.d};
+  GemmOperand A{p.E, p.d, p.V, p.d, (long)p.V * p.d}, B{p.h, p.d, p.N, p.d, (long)p.N * p.d};
   floatx16 acc[HC::MB][HC::NB];
-  gemm_mainloop<KMAJOR, KMAJOR, HC>(s0, s1, A, B, m0, n0, p.d, acc);
+  gemm_mainloop<KMAJOR, KMAJOR, HC>(s0, s1, A, B, m0, n0, 0, p.d, acc);
   const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
   int wm, wn;
   wave_coords<HC>(wm, wn);
@@ -238,9 +239,9 @@ __global__ __launch_bounds__(NT, 1) void head_dz_kernel(HeadParams p) {
   int tm, tn;
   xcd_tile(blockIdx.x, nbm, nbn, tm, tn);
   const int m0 = tm * HT_M, n0 = tn * HT_N;
-  GemmOperand A{p.E, p.d, p.V, p.d}, B{p.h, p.d, p.N, p.d};
+  GemmOperand A{p.E, p.d, p.V, p.d, (long)p.V * p.d}, B{p.h, p.d, p.N, p.d, (long)p.N * p.d};
   floatx16 acc[HC::MB][HC::NB];
-  gemm_mainloop<KMAJOR, KMAJOR, HC>(s0, s1, A, B, m0, n0, p.d, acc);
+  gemm_mainloop<KMAJOR, KMAJOR, HC>(s0, s1, A, B, m0, n0, 0, p.d, acc);
   const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
   int wm, wn;
   wave_coords<HC>(wm, wn);
@@ -284,22 +285,28 @@ __global__ __launch_bounds__(256) void head_hscale_kernel(HeadParams p) {
 }
 
 // dh = (U' or dZ) E: A stored token-major [n][v] (k-contiguous), B = E stored [v][d]
-// (n-contiguous). The residual schedule scales token rows by s/l.
+// (n-contiguous). The residual schedule scales token rows by s/l. When the product has too
+// few output tiles to fill the chip (small N*d, long V) the vocabulary is split into
+// dh_split ranges: each workgroup writes its f32 partial and head_dh_reduce_kernel sums them
+// in a fixed order before the scale and the rounding.
 __global__ __launch_bounds__(NT, 1) void head_dh_kernel(HeadParams p) {
   __shared__ __attribute__((aligned(16))) GemmStage<KMAJOR, MNMAJOR, HC> s0, s1;
   const int nbm = p.Npad / HT_M, nbn = (p.d + HT_N - 1) / HT_N;
-  int tm, tn;
-  xcd_tile_rowmajor(blockIdx.x, nbm, nbn, tm, tn);  // U panels streamed once
+  int tr, tn;
+  xcd_tile_rowmajor(blockIdx.x, nbm * p.dh_split, nbn, tr, tn);  // U panels streamed once
+  const int tm = tr / p.dh_split, split = tr - tm * p.dh_split;
   const int m0 = tm * HT_M;  // tokens
   const int n0 = tn * HT_N;  // d
+  const int kbeg = min(p.V, split * p.dh_kchunk), kend = min(p.V, kbeg + p.dh_kchunk);
   const bf16* a = p.ut ? p.ut : p.dzt;
-  GemmOperand A{a, p.Vp, p.N, p.V}, B{p.E, p.d, p.V, p.d};
+  GemmOperand A{a, p.Vp, p.N, p.V, (long)p.Npad * p.Vp}, B{p.E, p.d, p.V, p.d, (long)p.V * p.d};
   floatx16 acc[HC::MB][HC::NB];
-  gemm_mainloop<KMAJOR, MNMAJOR, HC>(s0, s1, A, B, m0, n0, p.V, acc);
+  gemm_mainloop<KMAJOR, MNMAJOR, HC>(s0, s1, A, B, m0, n0, kbeg, kend, acc);
   const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
   int wm, wn;
   wave_coords<HC>(wm, wn);
   const float s = p.ut ? head_grad_scale(p) : 1.0f;
+  float* part = p.dh_part ? p.dh_part + (size_t)split * p.N * p.d : nullptr;
 #pragma unroll
   for (int mb = 0; mb < HC::MB; ++mb) {
 #pragma unroll
@@ -310,9 +317,34 @@ __global__ __launch_bounds__(NT, 1) void head_dh_kernel(HeadParams p) {
 #pragma unroll
       for (int nb = 0; nb < HC::NB; ++nb) {
         const int col = n0 + wn * HC::WTN + nb * 32 + l32;
-        if (col < p.d) p.dh[(size_t)tok * p.d + col] = f2bf(acc[mb][nb][i] * f);
+        if (col >= p.d) continue;
+        if (part) part[(size_t)tok * p.d + col] = acc[mb][nb][i];
+        else p.dh[(size_t)tok * p.d + col] = f2bf(acc[mb][nb][i] * f);
       }
     }
+  }
+}
+
+// dh = bf16(f * sum_s partial_s) over the vocabulary splits, summed in split order.
+__global__ __launch_bounds__(256) void head_dh_reduce_kernel(HeadParams p) {
+  const float s = p.ut ? head_grad_scale(p) : 1.0f;
+  const size_t plane = (size_t)p.N * p.d;
+  const size_t total8 = plane / 8;
+  for (size_t c = (size_t)blockIdx.x * 256 + threadIdx.x; c < total8; c += (size_t)gridDim.x * 256) {
+    const int row = (int)((c * 8) / p.d);
+    const float4* src = reinterpret_cast<const float4*>(p.dh_part + c * 8);
+    float4 a = src[0], b = src[1];
+    for (int k = 1; k < p.dh_split; ++k) {
+      const float4* q = reinterpret_cast<const float4*>(p.dh_part + k * plane + c * 8);
+      const float4 x = q[0], y = q[1];
+      a.x += x.x; a.y += x.y; a.z += x.z; a.w += x.w;
+      b.x += y.x; b.y += y.y; b.z += y.z; b.w += y.w;
+    }
+    const float f = p.ut ? s / p.lsum[row] : 1.0f;
+    bf16x8 out;
+    out[0] = f2bf(a.x * f); out[1] = f2bf(a.y * f); out[2] = f2bf(a.z * f); out[3] = f2bf(a.w * f);
+    out[4] = f2bf(b.x * f); out[5] = f2bf(b.y * f); out[6] = f2bf(b.z * f); out[7] = f2bf(b.w * f);
+    *reinterpret_cast<bf16x8*>(p.dh + c * 8) = out;
   }
 }
 
@@ -327,9 +359,9 @@ __global__ __launch_bounds__(NT, 1) void head_de_kernel(HeadParams p) {
   const int n0 = tn * HT_N;  // d
   const bf16* a = p.ut ? p.ut : p.dzt;
   const bf16* b = p.ut ? p.hs : p.h;
-  GemmOperand A{a, p.Vp, p.N, p.V}, B{b, p.d, p.N, p.d};
+  GemmOperand A{a, p.Vp, p.N, p.V, (long)p.Npad * p.Vp}, B{b, p.d, p.N, p.d, (long)p.N * p.d};
   floatx16 acc[HC::MB][HC::NB];
-  gemm_mainloop<MNMAJOR, MNMAJOR, HC>(s0, s1, A, B, m0, n0, p.N, acc);
+  gemm_mainloop<MNMAJOR, MNMAJOR, HC>(s0, s1, A, B, m0, n0, 0, p.N, acc);
   const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
   int wm, wn;
   wave_coords<HC>(wm, wn);
@@ -356,6 +388,22 @@ int head_token_pad(int N) { return ((N + HT_N - 1) / HT_N) * HT_N; }
 int head_vocab_pitch(int V) { return (V + 7) / 8 * 8; }
 int head_stat_blocks(int N) { return (N + 255) / 256; }
 
+// Vocabulary splits of the dh product: minimise the rounds of 256 workgroups per unit of
+// k work (ceil(tiles*S/256)/S) for products with fewer than two rounds of tiles, keeping at
+// least 512 vocabulary entries per split; ties keep the smaller split count.
+int head_dh_split(int N, int d, int V) {
+  const int tiles = (head_token_pad(N) / HT_M) * ((d + HT_N - 1) / HT_N);
+  if (tiles >= 512) return 1;
+  int best = 1;
+  double best_cost = std::ceil(tiles / 256.0);
+  for (int s = 2; s <= 16 && V / s >= 512; ++s) {
+    const double cost = std::ceil(tiles * (double)s / 256.0) / s;
+    if (cost < best_cost - 1e-9) { best = s; best_cost = cost; }
+  }
+  return best;
+}
+int head_dh_kchunk(int V, int split) { return ((V + split - 1) / split + 127) / 128 * 128; }
+
 hipError_t launch_head_fwd(const HeadParams& p, hipStream_t st) {
   { KTimer t("head_zero", st); hipLaunchKernelGGL(head_zero_kernel, dim3((p.N + 255) / 256), dim3(256), 0, st, p.zt, p.N); }
   const int tiles = head_vocab_tiles(p.V) * (p.Npad / HT_N);
@@ -380,7 +428,16 @@ hipError_t launch_head_bwd(const HeadParams& p, hipStream_t st) {
     { KTimer t("head_dz", st); hipLaunchKernelGGL(head_dz_kernel, dim3(tiles), dim3(NT), 0, st, p); }
   }
   const int dtiles = (p.d + HT_N - 1) / HT_N;
-  { KTimer t("head_dh", st); hipLaunchKernelGGL(head_dh_kernel, dim3((p.Npad / HT_M) * dtiles), dim3(NT), 0, st, p); }
+  {
+    KTimer t("head_dh", st);
+    hipLaunchKernelGGL(head_dh_kernel, dim3((p.Npad / HT_M) * dtiles * p.dh_split), dim3(NT), 0, st, p);
+  }
+  if (p.dh_part) {
+    const size_t chunks = (size_t)p.N * p.d / 8;
+    const int blocks = (int)std::min<size_t>((chunks + 255) / 256, 4096);
+    KTimer t("head_dh_reduce", st);
+    hipLaunchKernelGGL(head_dh_reduce_kernel, dim3(blocks), dim3(256), 0, st, p);
+  }
   { KTimer t("head_de", st); hipLaunchKernelGGL(head_de_kernel, dim3(head_vocab_tiles(p.V) * dtiles), dim3(NT), 0, st, p); }
   return hipGetLastError();
 }

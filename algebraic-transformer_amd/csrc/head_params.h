@@ -35,6 +35,9 @@ struct HeadParams {
   bf16* dzt;            // recompute path workspace (Npad, Vp): bf16(s (p - y) r)
   bf16* hs;             // residual path workspace (N, d): bf16(s h / l)
   bf16* dh;             // (N, d)
+  float* dh_part;       // split-K partials of dh (dh_split, N, d) f32, or nullptr (one split)
+  int dh_split;         // k splits of the dh product (1: none)
+  int dh_kchunk;        // vocabulary entries per split (a multiple of 128)
   void* dE;             // (V, d) bf16 or f32
   int dE_f32;
 };

@@ -18,6 +18,8 @@ int head_vocab_tiles(int V);
 int head_token_pad(int N);
 int head_vocab_pitch(int V);
 int head_stat_blocks(int N);
+int head_dh_split(int N, int d, int V);
+int head_dh_kchunk(int V, int split);
 hipError_t launch_head_fwd(const HeadParams& p, hipStream_t st);
 hipError_t launch_head_bwd(const HeadParams& p, hipStream_t st);
 
