@@ -14,6 +14,7 @@ LIB_PATH = Path(os.environ.get("ALGEBRAIC_HIP_LIB", _HERE / "libalgebraic_hip.so
 ALG_OK, ALG_ERR_INVALID, ALG_ERR_UNSUPPORTED, ALG_ERR_HIP = 0, 1, 2, 3
 DTYPE_BF16, DTYPE_F32 = 0, 1
 ATTN_INRANGE, ATTN_CLIPPED, ATTN_SHIFTED, ATTN_GUARDED = 0, 1, 2, 3
+LAYOUT_BHTD, LAYOUT_BTHD = 0, 1
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -28,6 +29,12 @@ _SIGNATURES = {
     "alg_attn_fwd": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _P, _F, _I, _I, _P, _P, _P]),
     "alg_attn_bwd": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P, _F, _I, _I, _F,
                           _P, _P, _P, _P, _P, _P, _S]),
+    "alg_attn_prologue_workspace_size": (_S, [_I, _I, _I, _I]),
+    "alg_cayley_tables": (_I, [_P, _P, _I, _I, _P, _P]),
+    "alg_attn_qk_prologue": (_I, [_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _F, _P, _I, _F, _I, _I,
+                                  _P, _P, _P, _P, _P, _P, _P, _S]),
+    "alg_attn_qk_prologue_bwd": (_I, [_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                      _P, _P, _P, _S]),
     "alg_head_workspace_size": (_S, [_I, _I, _I, _I]),
     "alg_head_residual_size": (_S, [_I, _I, _I]),
     "alg_head_fwd": (_I, [_P, _I, _I, _I, _P, _P, _P, _I, _F, _P, _P, _P, _P, _P, _P, _S]),

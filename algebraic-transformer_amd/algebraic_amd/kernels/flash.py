@@ -182,6 +182,14 @@ def flash_attention(q, k, v, sink_logit=None, *, kind: str = "softmax",
     Same arguments, validation and maths as flash.py:763-857 for ``kind="asinh"``.
     Differentiable in q, k, v and sink_logit through torch autograd.
     """
+    plan = _make_plan(q, k, v, kind, n, c, block, block_q, block_k, shift, fast_rho, inv_stat, compact_stat,
+                      poly_rho, range_guard, resident_bwd, diagonal_bwd, diagonal_fwd, head_resident)
+    return _FlashFn.apply(q, k, v, sink_logit, plan)
+
+
+def _make_plan(q, k, v, kind, n, c, block, block_q, block_k, shift, fast_rho, inv_stat, compact_stat, poly_rho,
+               range_guard, resident_bwd, diagonal_bwd, diagonal_fwd, head_resident) -> _Plan:
+    """Argument validation of flash.py:793-822 and the kernel variant it selects."""
     if q.dim() != 4 or k.shape != q.shape or v.shape != q.shape:
         raise ValueError("q, k, v must share the shape (B, H, T, D)")
     B, H, T, D = q.shape
@@ -225,4 +233,4 @@ def flash_attention(q, k, v, sink_logit=None, *, kind: str = "softmax",
             plan = _Plan(_lib.ATTN_CLIPPED, var.n, float(c), var.clamp, True, var.inv_stat, False)
     if not q.is_cuda:
         raise RuntimeError("flash_attention needs GPU tensors (no CPU fallback)")
-    return _FlashFn.apply(q, k, v, sink_logit, plan)
+    return plan

@@ -28,4 +28,30 @@ struct GuardParams {
   int want_guard;
 };
 
+// Fused prologue (QK RMS norm + gain, Cayley rotation, q pre-scale, guard maxima).
+struct QkPrologueParams {
+  const void* q; const void* k; const void* v;  // raw projections in `layout`
+  const float* q_gain; const float* k_gain;     // (D,) or nullptr (no gain)
+  const float* cos; const float* sin;           // (T, D/2) or nullptr (no rotation)
+  void* q_s; void* k_r;                         // (B, H, T, D) outputs
+  float* tau_q; float* tau_k;                   // (B, H, T) 1/rms per row
+  float* part;                                  // (nblocks, 3) guard maxima
+  int B, H, T, D;
+  int layout;                                   // 0: (B, H, T, D), 1: (B, T, H, D)
+  float eps, alpha;
+  int want_guard;
+};
+
+struct QkPrologueBwdParams {
+  const void* q; const void* k;                 // raw projections in `layout`
+  const float* q_gain; const float* k_gain;
+  const float* cos; const float* sin;
+  const float* tau_q; const float* tau_k;
+  const void* dq_r; const void* dk_r;           // (B, H, T, D) cotangents of the rotated rows
+  void* dq; void* dk;                           // outputs in `layout`
+  float* gpart;                                 // (nblocks, 2, D) gain-gradient partials
+  int B, H, T, D;
+  int layout;
+};
+
 }  // namespace alg

@@ -6,7 +6,7 @@
 //   finalize  one workgroup reduces the maxima, writes sink/c broadcast to (H,)
 //             (flash.py:826-828) and the guard flag (1 = in range) that the forward and
 //             backward kernels read on the device (the lax.cond of flash.py:853-856).
-#include "attn_prep.h"
+#include "launchers.h"
 
 namespace alg {
 
@@ -146,6 +146,10 @@ hipError_t launch_attn_prep(const PrepParams& p, bool bf16_io, GuardParams g, hi
   if (e != hipSuccess) return e;
   g.part = p.part;
   g.nblocks = nb;
+  return launch_attn_guard(g, st);
+}
+
+hipError_t launch_attn_guard(const GuardParams& g, hipStream_t st) {
   {
     KTimer t("attn_guard", st);
     hipLaunchKernelGGL(attn_guard_kernel, dim3(1), dim3(256), 0, st, g);

@@ -1,0 +1,401 @@
+// Fused attention prologue for gfx950: QK RMS normalisation with a learned gain, the Cayley
+// rotation, the query pre-scale and the range guard's maxima in one pass over q, k and v,
+// and its VJP in one pass back.
+//
+// Replaces the model's path into the attention kernel, src/algebraic/model.py:170-174
+// (qk_norm: algebraic.py:76-83; apply_rotary: algebraic.py:172-179), plus
+// flash.py:823-849 (q_s = round(q alpha), guard maxima), and the Cayley tables of
+// algebraic.py:124-169.
+//
+// Rows are (b, h, t) in (B, H, T, D) order on output. The raw projections may be stored
+// (B, H, T, D) or (B, T, H, D) (the projection layout before the head transpose,
+// model.py:167-169). A row of D elements is split between D/(2 CH) lanes; lane li holds the
+// 16-byte chunk li of both halves, so the rotate-half pairs (x_j, x_{j+D/2}) sit in one lane
+// and only the row's sum of squares crosses lanes.
+//
+// Rounding follows the reference: tau = 1/sqrt(mean(x^2) + eps) in f32; y = round((x tau) g);
+// the tables are rounded to the input dtype and every rotated product and sum is rounded
+// (XLA's bf16 elementwise semantics); q_s = round(y alpha). Floating-point contraction is
+// off in this file: a product of two bf16 values rounded to bf16 and then added is otherwise
+// rewritten as a bf16 multiply fused into the add, which drops the product's rounding.
+#include "launchers.h"
+
+#pragma clang fp contract(off)
+
+namespace alg {
+
+namespace {
+
+__device__ __forceinline__ float nanmax_p(float a, float b) { return (a > b || a != a) ? a : b; }
+
+template <typename T>
+__device__ __forceinline__ float rnd(float x) { return (float)(T)x; }
+
+__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
+
+// Element offset of row r (in (B, H, T) order) of a tensor stored in `layout`.
+__device__ __forceinline__ size_t row_offset(size_t r, int H, int T, int D, int layout) {
+  if (layout == 0) return r * D;
+  const size_t bh = r / T;
+  const int t = (int)(r - bh * T);
+  const size_t b = bh / H;
+  const int h = (int)(bh - b * H);
+  return ((b * T + t) * H + h) * (size_t)D;
+}
+
+template <typename T, int CH>
+__device__ __forceinline__ void load_chunk(const void* base, size_t off, float (&x)[CH]) {
+  T v[CH];
+  *reinterpret_cast<uint4*>(v) = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(base) + off);
+#pragma unroll
+  for (int e = 0; e < CH; ++e) x[e] = (float)v[e];
+}
+
+template <typename T, int CH>
+__device__ __forceinline__ void store_chunk(void* base, size_t off, const float (&x)[CH]) {
+  T v[CH];
+#pragma unroll
+  for (int e = 0; e < CH; ++e) v[e] = (T)x[e];
+  *reinterpret_cast<uint4*>(reinterpret_cast<T*>(base) + off) = *reinterpret_cast<uint4*>(v);
+}
+
+template <int CH>
+__device__ __forceinline__ void load_f32(const float* p, float (&x)[CH]) {
+#pragma unroll
+  for (int e = 0; e < CH; e += 4) *reinterpret_cast<float4*>(&x[e]) = *reinterpret_cast<const float4*>(p + e);
+}
+
+template <int LPR>
+__device__ __forceinline__ float row_sum(float s) {
+#pragma unroll
+  for (int m = 1; m < LPR; m <<= 1) s += __shfl_xor(s, m, 64);
+  return s;
+}
+
+// One tensor's row: y = rot(round((x tau) g)) in the I/O dtype (as f32 values), tau out.
+template <typename T, int CH, int LPR>
+__device__ __forceinline__ float norm_rotate(float (&a)[CH], float (&b)[CH], const float (&ga)[CH],
+                                             const float (&gb)[CH], bool has_gain, const float (&ca)[CH],
+                                             const float (&sa)[CH], bool rotate, float inv_d, float eps) {
+  float ss = 0.0f;
+#pragma unroll
+  for (int e = 0; e < CH; ++e) ss += a[e] * a[e] + b[e] * b[e];
+  ss = row_sum<LPR>(ss);
+  const float tau = 1.0f / sqrtf(ss * inv_d + eps);
+#pragma unroll
+  for (int e = 0; e < CH; ++e) {
+    float ya = mul_rn(a[e], tau), yb = mul_rn(b[e], tau);
+    if (has_gain) { ya = mul_rn(ya, ga[e]); yb = mul_rn(yb, gb[e]); }
+    ya = rnd<T>(ya);
+    yb = rnd<T>(yb);
+    if (rotate) {
+      const float c = rnd<T>(ca[e]), s = rnd<T>(sa[e]);
+      a[e] = rnd<T>(rnd<T>(mul_rn(ya, c)) - rnd<T>(mul_rn(yb, s)));
+      b[e] = rnd<T>(rnd<T>(mul_rn(ya, s)) + rnd<T>(mul_rn(yb, c)));
+    } else {
+      a[e] = ya;
+      b[e] = yb;
+    }
+  }
+  return tau;
+}
+
+}  // namespace
+
+__global__ __launch_bounds__(256) void cayley_tables_kernel(const float* w, int half, int T, float* cos_out,
+                                                            float* sin_out) {
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (long)T * half) return;
+  const int m = (int)(idx / half), kk = (int)(idx - (long)m * half);
+  const float wk = w[kk];
+  const float w2 = mul_rn(wk, wk);
+  float c = (1.0f - w2) / (1.0f + w2);
+  float s = mul_rn(2.0f, wk) / (1.0f + w2);
+  float oc = 1.0f, os = 0.0f;
+  for (int bit = 0; (1 << bit) < T; ++bit) {
+    if ((m >> bit) & 1) {
+      const float nc = __fsub_rn(mul_rn(oc, c), mul_rn(os, s));
+      const float ns = __fadd_rn(mul_rn(oc, s), mul_rn(os, c));
+      oc = nc;
+      os = ns;
+    }
+    const float c2 = __fsub_rn(mul_rn(c, c), mul_rn(s, s));
+    const float s2 = mul_rn(mul_rn(2.0f, c), s);
+    const float inv = 1.0f / sqrtf(__fadd_rn(mul_rn(c2, c2), mul_rn(s2, s2)));
+    c = mul_rn(c2, inv);
+    s = mul_rn(s2, inv);
+  }
+  const float inv = 1.0f / sqrtf(__fadd_rn(mul_rn(oc, oc), mul_rn(os, os)));
+  cos_out[idx] = mul_rn(oc, inv);
+  sin_out[idx] = mul_rn(os, inv);
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void attn_qk_prologue_kernel(QkPrologueParams p) {
+  constexpr int CH = 16 / sizeof(T), HALF = D / 2, LPR = HALF / CH, RPW = 64 / LPR;
+  static_assert(HALF % CH == 0 && 64 % LPR == 0, "row split");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane / LPR, li = lane - sub * LPR;
+  const int c0 = li * CH;
+  float gqa[CH], gqb[CH], gka[CH], gkb[CH];
+#pragma unroll
+  for (int e = 0; e < CH; ++e) {
+    gqa[e] = p.q_gain ? p.q_gain[c0 + e] : 1.0f;
+    gqb[e] = p.q_gain ? p.q_gain[HALF + c0 + e] : 1.0f;
+    gka[e] = p.k_gain ? p.k_gain[c0 + e] : 1.0f;
+    gkb[e] = p.k_gain ? p.k_gain[HALF + c0 + e] : 1.0f;
+  }
+  const bool rotate = p.cos != nullptr;
+  const float inv_d = 1.0f / (float)D;
+  float mq = 0.0f, mk = 0.0f, mv = 0.0f;
+  const size_t rows = (size_t)p.B * p.H * p.T;
+  const size_t step = (size_t)gridDim.x * 4 * RPW;
+  for (size_t r = ((size_t)blockIdx.x * 4 + wave) * RPW + sub; r - sub < rows; r += step) {
+    const bool ok = r < rows;
+    const size_t rr = ok ? r : rows - 1;
+    const size_t in = row_offset(rr, p.H, p.T, D, p.layout) + c0;
+    const size_t out = rr * D + c0;
+    const int t = (int)(rr % p.T);
+    float qa[CH], qb[CH], ka[CH], kb[CH], ca[CH], sa[CH];
+    load_chunk<T, CH>(p.q, in, qa);
+    load_chunk<T, CH>(p.q, in + HALF, qb);
+    load_chunk<T, CH>(p.k, in, ka);
+    load_chunk<T, CH>(p.k, in + HALF, kb);
+    if (rotate) {
+      load_f32<CH>(p.cos + (size_t)t * HALF + c0, ca);
+      load_f32<CH>(p.sin + (size_t)t * HALF + c0, sa);
+    }
+    float av = 0.0f;
+    if (p.want_guard) {
+      float va[CH], vb[CH];
+      load_chunk<T, CH>(p.v, in, va);
+      load_chunk<T, CH>(p.v, in + HALF, vb);
+#pragma unroll
+      for (int e = 0; e < CH; ++e) av = nanmax_p(av, nanmax_p(__builtin_fabsf(va[e]), __builtin_fabsf(vb[e])));
+    }
+    const float tq = norm_rotate<T, CH, LPR>(qa, qb, gqa, gqb, p.q_gain != nullptr, ca, sa, rotate, inv_d, p.eps);
+    const float tk = norm_rotate<T, CH, LPR>(ka, kb, gka, gkb, p.k_gain != nullptr, ca, sa, rotate, inv_d, p.eps);
+    float sq = 0.0f, sk = 0.0f;
+#pragma unroll
+    for (int e = 0; e < CH; ++e) {
+      qa[e] = rnd<T>(mul_rn(qa[e], p.alpha));
+      qb[e] = rnd<T>(mul_rn(qb[e], p.alpha));
+      sq += qa[e] * qa[e] + qb[e] * qb[e];
+      sk += ka[e] * ka[e] + kb[e] * kb[e];
+    }
+    sq = row_sum<LPR>(sq);
+    sk = row_sum<LPR>(sk);
+    if (ok) {
+      store_chunk<T, CH>(p.q_s, out, qa);
+      store_chunk<T, CH>(p.q_s, out + HALF, qb);
+      store_chunk<T, CH>(p.k_r, out, ka);
+      store_chunk<T, CH>(p.k_r, out + HALF, kb);
+      if (li == 0) {
+        p.tau_q[r] = tq;
+        p.tau_k[r] = tk;
+      }
+      mq = nanmax_p(mq, sq);
+      mk = nanmax_p(mk, sk);
+      mv = nanmax_p(mv, av);
+    }
+  }
+  for (int m = 32; m >= 1; m >>= 1) {
+    mq = nanmax_p(mq, __shfl_xor(mq, m, 64));
+    mk = nanmax_p(mk, __shfl_xor(mk, m, 64));
+    mv = nanmax_p(mv, __shfl_xor(mv, m, 64));
+  }
+  __shared__ float red[4][3];
+  if (lane == 0) { red[wave][0] = mq; red[wave][1] = mk; red[wave][2] = mv; }
+  __syncthreads();
+  if (threadIdx.x < 3) {
+    float m = red[0][threadIdx.x];
+    for (int w = 1; w < 4; ++w) m = nanmax_p(m, red[w][threadIdx.x]);
+    p.part[blockIdx.x * 3 + threadIdx.x] = m;
+  }
+}
+
+// VJP of one row of one tensor. dy (the rotated output's cotangent) arrives in a/b; on exit
+// a/b hold dx. Accumulates the gain-gradient terms dy_n * (x tau) into ga_acc/gb_acc.
+template <typename T, int CH, int LPR>
+__device__ __forceinline__ void norm_rotate_vjp(float (&a)[CH], float (&b)[CH], const float (&xa)[CH],
+                                                const float (&xb)[CH], const float (&ga)[CH], const float (&gb)[CH],
+                                                const float (&ca)[CH], const float (&sa)[CH], bool rotate, float tau,
+                                                float inv_d, float (&ga_acc)[CH], float (&gb_acc)[CH]) {
+  if (rotate) {
+#pragma unroll
+    for (int e = 0; e < CH; ++e) {
+      const float c = rnd<T>(ca[e]), s = rnd<T>(sa[e]);
+      const float d1 = a[e], d2 = b[e];
+      a[e] = rnd<T>(rnd<T>(mul_rn(d1, c)) + rnd<T>(mul_rn(d2, s)));
+      b[e] = rnd<T>(rnd<T>(mul_rn(d2, c)) - rnd<T>(mul_rn(d1, s)));
+    }
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int e = 0; e < CH; ++e) {
+    ga_acc[e] += mul_rn(a[e], mul_rn(xa[e], tau));
+    gb_acc[e] += mul_rn(b[e], mul_rn(xb[e], tau));
+    a[e] = mul_rn(ga[e], a[e]);
+    b[e] = mul_rn(gb[e], b[e]);
+    s += mul_rn(a[e], xa[e]) + mul_rn(b[e], xb[e]);
+  }
+  s = row_sum<LPR>(s);
+  const float coef = mul_rn(mul_rn(mul_rn(tau, tau), tau), s) * inv_d;
+#pragma unroll
+  for (int e = 0; e < CH; ++e) {
+    a[e] = rnd<T>(__fsub_rn(mul_rn(a[e], tau), mul_rn(xa[e], coef)));
+    b[e] = rnd<T>(__fsub_rn(mul_rn(b[e], tau), mul_rn(xb[e], coef)));
+  }
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void attn_qk_prologue_bwd_kernel(QkPrologueBwdParams p) {
+  constexpr int CH = 16 / sizeof(T), HALF = D / 2, LPR = HALF / CH, RPW = 64 / LPR;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane / LPR, li = lane - sub * LPR;
+  const int c0 = li * CH;
+  float gqa[CH], gqb[CH], gka[CH], gkb[CH];
+  float aq_a[CH], aq_b[CH], ak_a[CH], ak_b[CH];  // gain-gradient accumulators
+#pragma unroll
+  for (int e = 0; e < CH; ++e) {
+    gqa[e] = p.q_gain ? p.q_gain[c0 + e] : 1.0f;
+    gqb[e] = p.q_gain ? p.q_gain[HALF + c0 + e] : 1.0f;
+    gka[e] = p.k_gain ? p.k_gain[c0 + e] : 1.0f;
+    gkb[e] = p.k_gain ? p.k_gain[HALF + c0 + e] : 1.0f;
+    aq_a[e] = aq_b[e] = ak_a[e] = ak_b[e] = 0.0f;
+  }
+  const bool rotate = p.cos != nullptr;
+  const float inv_d = 1.0f / (float)D;
+  const size_t rows = (size_t)p.B * p.H * p.T;
+  const size_t step = (size_t)gridDim.x * 4 * RPW;
+  for (size_t r = ((size_t)blockIdx.x * 4 + wave) * RPW + sub; r - sub < rows; r += step) {
+    const bool ok = r < rows;
+    const size_t rr = ok ? r : rows - 1;
+    const size_t in = row_offset(rr, p.H, p.T, D, p.layout) + c0;
+    const size_t gr = rr * D + c0;
+    const int t = (int)(rr % p.T);
+    float ca[CH], sa[CH];
+    if (rotate) {
+      load_f32<CH>(p.cos + (size_t)t * HALF + c0, ca);
+      load_f32<CH>(p.sin + (size_t)t * HALF + c0, sa);
+    }
+    float xqa[CH], xqb[CH], xka[CH], xkb[CH], dqa[CH], dqb[CH], dka[CH], dkb[CH];
+    load_chunk<T, CH>(p.q, in, xqa);
+    load_chunk<T, CH>(p.q, in + HALF, xqb);
+    load_chunk<T, CH>(p.k, in, xka);
+    load_chunk<T, CH>(p.k, in + HALF, xkb);
+    load_chunk<T, CH>(p.dq_r, gr, dqa);
+    load_chunk<T, CH>(p.dq_r, gr + HALF, dqb);
+    load_chunk<T, CH>(p.dk_r, gr, dka);
+    load_chunk<T, CH>(p.dk_r, gr + HALF, dkb);
+    const float tq = p.tau_q[rr], tk = p.tau_k[rr];
+    float zq_a[CH], zq_b[CH], zk_a[CH], zk_b[CH];
+#pragma unroll
+    for (int e = 0; e < CH; ++e) zq_a[e] = zq_b[e] = zk_a[e] = zk_b[e] = 0.0f;
+    norm_rotate_vjp<T, CH, LPR>(dqa, dqb, xqa, xqb, gqa, gqb, ca, sa, rotate, tq, inv_d, zq_a, zq_b);
+    norm_rotate_vjp<T, CH, LPR>(dka, dkb, xka, xkb, gka, gkb, ca, sa, rotate, tk, inv_d, zk_a, zk_b);
+    if (ok) {
+      store_chunk<T, CH>(p.dq, in, dqa);
+      store_chunk<T, CH>(p.dq, in + HALF, dqb);
+      store_chunk<T, CH>(p.dk, in, dka);
+      store_chunk<T, CH>(p.dk, in + HALF, dkb);
+#pragma unroll
+      for (int e = 0; e < CH; ++e) {
+        aq_a[e] += zq_a[e]; aq_b[e] += zq_b[e];
+        ak_a[e] += zk_a[e]; ak_b[e] += zk_b[e];
+      }
+    }
+  }
+  // Gain-gradient partials: lanes with the same li (same columns) are LPR apart.
+#pragma unroll
+  for (int e = 0; e < CH; ++e) {
+    for (int m = LPR; m < 64; m <<= 1) {
+      aq_a[e] += __shfl_xor(aq_a[e], m, 64);
+      aq_b[e] += __shfl_xor(aq_b[e], m, 64);
+      ak_a[e] += __shfl_xor(ak_a[e], m, 64);
+      ak_b[e] += __shfl_xor(ak_b[e], m, 64);
+    }
+  }
+  __shared__ float red[4][2][D];
+  if (sub == 0) {
+#pragma unroll
+    for (int e = 0; e < CH; ++e) {
+      red[wave][0][c0 + e] = aq_a[e];
+      red[wave][0][HALF + c0 + e] = aq_b[e];
+      red[wave][1][c0 + e] = ak_a[e];
+      red[wave][1][HALF + c0 + e] = ak_b[e];
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < 2 * D; i += 256) {
+    const int x = i / D, d = i - x * D;
+    p.gpart[(size_t)blockIdx.x * 2 * D + i] = red[0][x][d] + red[1][x][d] + red[2][x][d] + red[3][x][d];
+  }
+}
+
+// Gain gradients: sum of the per-block partials in block order.
+__global__ __launch_bounds__(256) void attn_qk_gain_reduce_kernel(const float* gpart, int nblocks, int D,
+                                                                  float* dq_gain, float* dk_gain) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= 2 * D) return;
+  float s = 0.0f;
+  for (int b = 0; b < nblocks; ++b) s += gpart[(size_t)b * 2 * D + i];
+  float* dst = i < D ? dq_gain : dk_gain;
+  if (dst) dst[i < D ? i : i - D] = s;
+}
+
+int attn_qk_prologue_blocks(size_t rows) {
+  const size_t b = (rows + 31) / 32;
+  return (int)(b < 1024 ? (b ? b : 1) : 1024);
+}
+
+hipError_t launch_cayley_tables(const float* w, int half, int T, float* cos_out, float* sin_out, hipStream_t st) {
+  const long n = (long)T * half;
+  hipLaunchKernelGGL(cayley_tables_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, w, half, T, cos_out,
+                     sin_out);
+  return hipGetLastError();
+}
+
+hipError_t launch_attn_qk_prologue(const QkPrologueParams& p, bool bf16_io, GuardParams g, hipStream_t st) {
+  const int nb = attn_qk_prologue_blocks((size_t)p.B * p.H * p.T);
+  {
+    KTimer t("attn_qk_prologue", st);
+    if (bf16_io) {
+      if (p.D == 128) hipLaunchKernelGGL((attn_qk_prologue_kernel<bf16, 128>), dim3(nb), dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((attn_qk_prologue_kernel<bf16, 64>), dim3(nb), dim3(256), 0, st, p);
+    } else {
+      if (p.D == 128) hipLaunchKernelGGL((attn_qk_prologue_kernel<float, 128>), dim3(nb), dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((attn_qk_prologue_kernel<float, 64>), dim3(nb), dim3(256), 0, st, p);
+    }
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  g.part = p.part;
+  g.nblocks = nb;
+  return launch_attn_guard(g, st);
+}
+
+hipError_t launch_attn_qk_prologue_bwd(const QkPrologueBwdParams& p, bool bf16_io, float* dq_gain, float* dk_gain,
+                                       hipStream_t st) {
+  const int nb = attn_qk_prologue_blocks((size_t)p.B * p.H * p.T);
+  {
+    KTimer t("attn_qk_prologue_bwd", st);
+    if (bf16_io) {
+      if (p.D == 128) hipLaunchKernelGGL((attn_qk_prologue_bwd_kernel<bf16, 128>), dim3(nb), dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((attn_qk_prologue_bwd_kernel<bf16, 64>), dim3(nb), dim3(256), 0, st, p);
+    } else {
+      if (p.D == 128) hipLaunchKernelGGL((attn_qk_prologue_bwd_kernel<float, 128>), dim3(nb), dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((attn_qk_prologue_bwd_kernel<float, 64>), dim3(nb), dim3(256), 0, st, p);
+    }
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (dq_gain || dk_gain) {
+    KTimer t("attn_qk_gain_reduce", st);
+    hipLaunchKernelGGL(attn_qk_gain_reduce_kernel, dim3((2 * p.D + 255) / 256), dim3(256), 0, st, p.gpart, nb, p.D,
+                       dq_gain, dk_gain);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace alg

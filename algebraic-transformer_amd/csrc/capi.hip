@@ -119,6 +119,48 @@ int check_head(int N, int d, int V, int n, float c) {
   return ALG_OK;
 }
 
+// Guard bounds (flash.py:747-748, 840-849), evaluated in double then rounded like the
+// reference's weakly typed Python-float constants.
+alg::GuardParams guard_params(int H, int T, int n, float c, const float* sink_logit, int sink_count, float* sink_scaled,
+                              int* guard_flag, int range_guard) {
+  const double t = root_pow2(1e37 / (T + 1.0), n);
+  const double clamp = 0.5 * (t - 1.0 / t);
+  const double bound = std::fmin(16.0, clamp / 2.0);
+  const int has_sink = sink_logit ? 1 : 0;
+  alg::GuardParams g;
+  g.part = nullptr; g.nblocks = 0;
+  g.sink_logit = sink_logit; g.sink_count = sink_count;
+  g.sink_out = sink_scaled; g.H = H; g.c = c;
+  g.flag = guard_flag;
+  g.q2k2_bound = (float)((bound / 1.01) * (bound / 1.01));
+  g.sink_bound = (float)(bound / 1.01);
+  g.v_bound = (float)std::fmin(1e8, 1e37 / ((T + has_sink) * std::pow(2.0 * bound + 1.0, n)));
+  g.want_guard = range_guard && n <= 32 ? 1 : 0;
+  return g;
+}
+
+// Prologue workspace: [guard maxima f32 3*1024][gain-gradient partials f32 1024*2*D].
+struct PrologueWs {
+  size_t guard_part, gain_part, total;
+};
+PrologueWs prologue_ws(int D) {
+  PrologueWs w;
+  w.guard_part = 0;
+  w.gain_part = align256(3 * 1024 * sizeof(float));
+  w.total = w.gain_part + align256((size_t)1024 * 2 * D * sizeof(float));
+  return w;
+}
+
+int check_prologue(int dtype, int layout, int B, int H, int T, int D, const float* cos_t, const float* sin_t,
+                   float eps) {
+  int rc = check_attn_shape(dtype, B, H, T, D);
+  if (rc) return rc;
+  if (layout != ALG_LAYOUT_BHTD && layout != ALG_LAYOUT_BTHD) return fail(ALG_ERR_INVALID, "unknown layout %d", layout);
+  if ((cos_t == nullptr) != (sin_t == nullptr)) return fail(ALG_ERR_INVALID, "cos and sin are given together");
+  if (!(eps > 0.0f) || !std::isfinite(eps)) return fail(ALG_ERR_INVALID, "eps must be positive and finite");
+  return ALG_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -152,22 +194,75 @@ int alg_attn_prepare(alg_stream_t stream, int dtype, int B, int H, int T, int D,
   pp.D = D;
   pp.alpha = (float)(1.0 / (std::sqrt((double)D) * (double)c));
   pp.want_guard = range_guard ? 1 : 0;
-  // Guard bounds (flash.py:747-748, 840-849), evaluated in double then rounded like the
-  // reference's weakly typed Python-float constants.
-  const double t = root_pow2(1e37 / (T + 1.0), n);
-  const double clamp = 0.5 * (t - 1.0 / t);
-  const double bound = std::fmin(16.0, clamp / 2.0);
-  const int has_sink = sink_logit ? 1 : 0;
-  alg::GuardParams g;
-  g.part = nullptr; g.nblocks = 0;
-  g.sink_logit = sink_logit; g.sink_count = sink_count;
-  g.sink_out = sink_scaled; g.H = H; g.c = c;
-  g.flag = guard_flag;
-  g.q2k2_bound = (float)((bound / 1.01) * (bound / 1.01));
-  g.sink_bound = (float)(bound / 1.01);
-  g.v_bound = (float)std::fmin(1e8, 1e37 / ((T + has_sink) * std::pow(2.0 * bound + 1.0, n)));
-  g.want_guard = range_guard && n <= 32 ? 1 : 0;
+  const alg::GuardParams g = guard_params(H, T, n, c, sink_logit, sink_count, sink_scaled, guard_flag, range_guard);
   return hip_status(alg::launch_attn_prep(pp, dtype == ALG_DTYPE_BF16, g, (hipStream_t)stream), "alg_attn_prepare");
+}
+
+size_t alg_attn_prologue_workspace_size(int B, int H, int T, int D) {
+  if (B <= 0 || H <= 0 || T <= 0 || D <= 0) return 0;
+  return prologue_ws(D).total;
+}
+
+int alg_cayley_tables(alg_stream_t stream, const float* w, int half, int seq_len, float* cos_out, float* sin_out) {
+  if (!w || !cos_out || !sin_out) return fail(ALG_ERR_INVALID, "w, cos and sin are required");
+  if (half <= 0 || seq_len <= 0) return fail(ALG_ERR_INVALID, "half and seq_len must be positive");
+  if ((double)half * seq_len > 2.0e9) return fail(ALG_ERR_INVALID, "table too large");
+  return hip_status(alg::launch_cayley_tables(w, half, seq_len, cos_out, sin_out, (hipStream_t)stream),
+                    "alg_cayley_tables");
+}
+
+int alg_attn_qk_prologue(alg_stream_t stream, int dtype, int layout, int B, int H, int T, int D, const void* q,
+                         const void* k, const void* v, const float* q_gain, const float* k_gain, const float* cos_t,
+                         const float* sin_t, float eps, const float* sink_logit, int sink_count, float c, int n,
+                         int range_guard, void* q_s, void* k_r, float* tau_q, float* tau_k, float* sink_scaled,
+                         int* guard_flag, void* workspace, size_t workspace_bytes) {
+  int rc = check_prologue(dtype, layout, B, H, T, D, cos_t, sin_t, eps);
+  if (rc) return rc;
+  if ((rc = check_n(n))) return rc;
+  if (!(c > 0.0f) || !std::isfinite(c)) return fail(ALG_ERR_INVALID, "asinh scale c must be positive and finite");
+  if (!q || !k || !q_s || !k_r || !tau_q || !tau_k || !guard_flag)
+    return fail(ALG_ERR_INVALID, "q, k, q_s, k_r, tau_q, tau_k and guard_flag are required");
+  if (range_guard && !v) return fail(ALG_ERR_INVALID, "range_guard needs v");
+  if (sink_logit && sink_count != 1 && sink_count != H) return fail(ALG_ERR_INVALID, "sink_count must be 1 or H");
+  if (sink_logit && !sink_scaled) return fail(ALG_ERR_INVALID, "sink_scaled output required with a sink");
+  const PrologueWs ws = prologue_ws(D);
+  if (!workspace || workspace_bytes < ws.total)
+    return fail(ALG_ERR_INVALID, "workspace too small: need %zu bytes", ws.total);
+  alg::QkPrologueParams p;
+  p.q = q; p.k = k; p.v = v;
+  p.q_gain = q_gain; p.k_gain = k_gain; p.cos = cos_t; p.sin = sin_t;
+  p.q_s = q_s; p.k_r = k_r; p.tau_q = tau_q; p.tau_k = tau_k;
+  p.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + ws.guard_part);
+  p.B = B; p.H = H; p.T = T; p.D = D; p.layout = layout;
+  p.eps = eps;
+  p.alpha = (float)(1.0 / (std::sqrt((double)D) * (double)c));
+  p.want_guard = range_guard ? 1 : 0;
+  const alg::GuardParams g = guard_params(H, T, n, c, sink_logit, sink_count, sink_scaled, guard_flag, range_guard);
+  return hip_status(alg::launch_attn_qk_prologue(p, dtype == ALG_DTYPE_BF16, g, (hipStream_t)stream),
+                    "alg_attn_qk_prologue");
+}
+
+int alg_attn_qk_prologue_bwd(alg_stream_t stream, int dtype, int layout, int B, int H, int T, int D, const void* q,
+                             const void* k, const float* q_gain, const float* k_gain, const float* cos_t,
+                             const float* sin_t, const float* tau_q, const float* tau_k, const void* dq_r,
+                             const void* dk_r, void* dq, void* dk, float* dq_gain, float* dk_gain, void* workspace,
+                             size_t workspace_bytes) {
+  int rc = check_prologue(dtype, layout, B, H, T, D, cos_t, sin_t, 1.0f);
+  if (rc) return rc;
+  if (!q || !k || !tau_q || !tau_k || !dq_r || !dk_r || !dq || !dk)
+    return fail(ALG_ERR_INVALID, "q, k, tau_q, tau_k, dq_r, dk_r, dq and dk are required");
+  if ((dq_gain && !q_gain) || (dk_gain && !k_gain))
+    return fail(ALG_ERR_INVALID, "a gain gradient needs the gain it differentiates");
+  const PrologueWs ws = prologue_ws(D);
+  if (!workspace || workspace_bytes < ws.total)
+    return fail(ALG_ERR_INVALID, "workspace too small: need %zu bytes", ws.total);
+  alg::QkPrologueBwdParams p;
+  p.q = q; p.k = k; p.q_gain = q_gain; p.k_gain = k_gain; p.cos = cos_t; p.sin = sin_t;
+  p.tau_q = tau_q; p.tau_k = tau_k; p.dq_r = dq_r; p.dk_r = dk_r; p.dq = dq; p.dk = dk;
+  p.gpart = reinterpret_cast<float*>(static_cast<char*>(workspace) + ws.gain_part);
+  p.B = B; p.H = H; p.T = T; p.D = D; p.layout = layout;
+  return hip_status(alg::launch_attn_qk_prologue_bwd(p, dtype == ALG_DTYPE_BF16, dq_gain, dk_gain, (hipStream_t)stream),
+                    "alg_attn_qk_prologue_bwd");
 }
 
 int alg_attn_fwd(alg_stream_t stream, int dtype, int B, int H, int T, int D, const void* q_s, const void* k,

@@ -16,6 +16,9 @@
  *   src/algebraic/kernels/head_resident.py forward 125-142, backward 145-163
  *   src/algebraic/kernels/fused_head.py  _forward 174-191, _backward 194-216,
  *                                        _telemetry 219-229, fused_head 260-275
+ *   src/algebraic/model.py 170-174, src/algebraic/algebraic.py 76-83, 124-179
+ *                                        (QK norm, Cayley tables and rotation: the
+ *                                        attention prologue)
  */
 #ifndef ALGEBRAIC_HIP_H
 #define ALGEBRAIC_HIP_H
@@ -37,6 +40,10 @@ enum {
 };
 
 enum { ALG_DTYPE_BF16 = 0, ALG_DTYPE_F32 = 1 };
+
+/* Storage of the raw attention projections for the fused prologue: (B, H, T, D), or the
+ * projection layout (B, T, H, D) before the head transpose of model.py:167-169. */
+enum { ALG_LAYOUT_BHTD = 0, ALG_LAYOUT_BTHD = 1 };
 
 /* Attention variants (flash.py:59-73, 732-760, 850-852).
  *   INRANGE  unshifted, unclipped weights, stat = 1/Z ("low" branch of range_guard)
@@ -85,6 +92,42 @@ int alg_attn_bwd(alg_stream_t stream, int dtype, int B, int H, int T, int D,
                  float dq_scale,
                  void* dq, void* dk, void* dv, float* di, float* dsink_scaled,
                  void* workspace, size_t workspace_bytes);
+
+/* Cayley rotation tables, src/algebraic/algebraic.py:124-149 (cayley_powers): for the
+ * frequencies w (half) f32, cos/sin (seq_len, half) f32 hold the rows
+ * ((1 + i w)^2 / (1 + w^2))^m, m < seq_len, by binary exponentiation with a renormalisation
+ * after every squaring, as the reference builds them. */
+int alg_cayley_tables(alg_stream_t stream, const float* w, int half, int seq_len, float* cos, float* sin);
+
+/* Bytes of workspace alg_attn_qk_prologue / alg_attn_qk_prologue_bwd need. */
+size_t alg_attn_prologue_workspace_size(int B, int H, int T, int D);
+
+/* Fused attention prologue, replacing model.py:170-174 (qk_norm = rms_norm with a learned
+ * gain, algebraic.py:76-83; apply_rotary, algebraic.py:172-179) followed by
+ * flash_attention's prologue and guard (flash.py:823-849), in one pass:
+ *   k_r = rot(round((k tau_k) k_gain)),  q_s = round(rot(round((q tau_q) q_gain)) alpha),
+ *   tau = 1/sqrt(mean(x^2) + eps) per row (written to tau_q / tau_k for the backward),
+ *   alpha = 1/(sqrt(D) c); the guard flag and sink_scaled exactly as alg_attn_prepare
+ *   (the guard's ||q_s||^2 and ||k||^2 maxima are taken over q_s and k_r).
+ * q, k, v are read in `layout`; q_s and k_r are written (B, H, T, D) for alg_attn_fwd /
+ * alg_attn_bwd. Gains (D) f32 may be NULL (no gain); cos/sin (T, D/2) f32 may both be NULL
+ * (no rotation); the tables are rounded to the input dtype before use, like the reference. */
+int alg_attn_qk_prologue(alg_stream_t stream, int dtype, int layout, int B, int H, int T, int D,
+                         const void* q, const void* k, const void* v,
+                         const float* q_gain, const float* k_gain, const float* cos, const float* sin,
+                         float eps, const float* sink_logit, int sink_count, float c, int n, int range_guard,
+                         void* q_s, void* k_r, float* tau_q, float* tau_k, float* sink_scaled, int* guard_flag,
+                         void* workspace, size_t workspace_bytes);
+
+/* VJP of the fused prologue's normalisation and rotation (JAX autodiff of
+ * algebraic.py:76-83 and 172-179): dq_r, dk_r (B, H, T, D) are the cotangents of the rotated
+ * rows (alg_attn_bwd's dq with dq_scale = alpha, and its dk); out dq, dk in `layout` and the
+ * gain gradients dq_gain, dk_gain (D) f32 (summed over all rows; NULL to skip). */
+int alg_attn_qk_prologue_bwd(alg_stream_t stream, int dtype, int layout, int B, int H, int T, int D,
+                             const void* q, const void* k, const float* q_gain, const float* k_gain,
+                             const float* cos, const float* sin, const float* tau_q, const float* tau_k,
+                             const void* dq_r, const void* dk_r, void* dq, void* dk,
+                             float* dq_gain, float* dk_gain, void* workspace, size_t workspace_bytes);
 
 /* Bytes of workspace for alg_head_fwd (pass 0), alg_head_bwd without a residual (pass 1)
  * and alg_head_bwd with a residual (pass 2). */
