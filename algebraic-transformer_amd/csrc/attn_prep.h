@@ -49,7 +49,7 @@ struct QkPrologueBwdParams {
   const float* tau_q; const float* tau_k;
   const void* dq_r; const void* dk_r;           // (B, H, T, D) cotangents of the rotated rows
   void* dq; void* dk;                           // outputs in `layout`
-  float* gpart;                                 // (nblocks, 2, D) gain-gradient partials
+  float* gpart;                                 // (2, D, nblocks) gain-gradient partials
   int B, H, T, D;
   int layout;
 };

@@ -22,6 +22,10 @@
 
 #pragma clang fp contract(off)
 
+#ifndef PRO_U
+#define PRO_U 1
+#endif
+
 namespace alg {
 
 namespace {
@@ -33,20 +37,43 @@ __device__ __forceinline__ float rnd(float x) { return (float)(T)x; }
 
 __device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
 
-// Element offset of row r (in (B, H, T) order) of a tensor stored in `layout`.
-__device__ __forceinline__ size_t row_offset(size_t r, int H, int T, int D, int layout) {
-  if (layout == 0) return r * D;
-  const size_t bh = r / T;
-  const int t = (int)(r - bh * T);
-  const size_t b = bh / H;
-  const int h = (int)(bh - b * H);
-  return ((b * T + t) * H + h) * (size_t)D;
+// Grid: one workgroup per (b*H + h, block of 4*RPW*PRO_ITER consecutive positions t); wave w
+// handles positions t0 + RPW*(w + 4 j) + sub, j < PRO_ITER. Row addresses are a per-head base
+// plus t times the row stride of the layout (D for (B, H, T, D), H*D for (B, T, H, D)).
+#ifndef PRO_ITER_N
+#define PRO_ITER_N 8
+#endif
+constexpr int PRO_ITER = PRO_ITER_N;
+
+struct RowAddr {
+  size_t in_base, out_base;  // element offsets of position 0 of this head
+  size_t in_stride;          // elements between consecutive positions in the input layout
+};
+
+__device__ __forceinline__ RowAddr head_rows(int H, int T, int D, int layout) {
+  const int bh = blockIdx.x;
+  const int b = bh / H, h = bh - b * H;
+  RowAddr a;
+  a.out_base = (size_t)bh * T * D;
+  if (layout == 0) {
+    a.in_base = a.out_base;
+    a.in_stride = D;
+  } else {
+    a.in_base = ((size_t)b * T * H + h) * D;
+    a.in_stride = (size_t)H * D;
+  }
+  return a;
+}
+
+template <typename T>
+__device__ __forceinline__ uint4 ld16(const void* base, size_t off) {
+  return *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(base) + off);
 }
 
 template <typename T, int CH>
-__device__ __forceinline__ void load_chunk(const void* base, size_t off, float (&x)[CH]) {
+__device__ __forceinline__ void cvt_chunk(const uint4& raw, float (&x)[CH]) {
   T v[CH];
-  *reinterpret_cast<uint4*>(v) = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(base) + off);
+  *reinterpret_cast<uint4*>(v) = raw;
 #pragma unroll
   for (int e = 0; e < CH; ++e) x[e] = (float)v[e];
 }
@@ -148,55 +175,86 @@ __global__ __launch_bounds__(256) void attn_qk_prologue_kernel(QkPrologueParams 
   const bool rotate = p.cos != nullptr;
   const float inv_d = 1.0f / (float)D;
   float mq = 0.0f, mk = 0.0f, mv = 0.0f;
-  const size_t rows = (size_t)p.B * p.H * p.T;
-  const size_t step = (size_t)gridDim.x * 4 * RPW;
-  for (size_t r = ((size_t)blockIdx.x * 4 + wave) * RPW + sub; r - sub < rows; r += step) {
-    const bool ok = r < rows;
-    const size_t rr = ok ? r : rows - 1;
-    const size_t in = row_offset(rr, p.H, p.T, D, p.layout) + c0;
-    const size_t out = rr * D + c0;
-    const int t = (int)(rr % p.T);
-    float qa[CH], qb[CH], ka[CH], kb[CH], ca[CH], sa[CH];
-    load_chunk<T, CH>(p.q, in, qa);
-    load_chunk<T, CH>(p.q, in + HALF, qb);
-    load_chunk<T, CH>(p.k, in, ka);
-    load_chunk<T, CH>(p.k, in + HALF, kb);
-    if (rotate) {
-      load_f32<CH>(p.cos + (size_t)t * HALF + c0, ca);
-      load_f32<CH>(p.sin + (size_t)t * HALF + c0, sa);
-    }
-    float av = 0.0f;
-    if (p.want_guard) {
-      float va[CH], vb[CH];
-      load_chunk<T, CH>(p.v, in, va);
-      load_chunk<T, CH>(p.v, in + HALF, vb);
+  const RowAddr ra = head_rows(p.H, p.T, D, p.layout);
+  const int t0 = blockIdx.y * (4 * RPW * PRO_ITER) + wave * RPW + sub;
+  // U rows per lane and iteration: every load of the U rows is issued before any compute.
+  constexpr int U = PRO_U;
+#pragma unroll 1
+  for (int j = 0; j < PRO_ITER; j += U) {
+    uint4 rq[U][2], rk[U][2], rv[U][2];
+    float ca[U][CH], sa[U][CH];
+    int tt[U];
+    bool ok[U];
 #pragma unroll
-      for (int e = 0; e < CH; ++e) av = nanmax_p(av, nanmax_p(__builtin_fabsf(va[e]), __builtin_fabsf(vb[e])));
-    }
-    const float tq = norm_rotate<T, CH, LPR>(qa, qb, gqa, gqb, p.q_gain != nullptr, ca, sa, rotate, inv_d, p.eps);
-    const float tk = norm_rotate<T, CH, LPR>(ka, kb, gka, gkb, p.k_gain != nullptr, ca, sa, rotate, inv_d, p.eps);
-    float sq = 0.0f, sk = 0.0f;
-#pragma unroll
-    for (int e = 0; e < CH; ++e) {
-      qa[e] = rnd<T>(mul_rn(qa[e], p.alpha));
-      qb[e] = rnd<T>(mul_rn(qb[e], p.alpha));
-      sq += qa[e] * qa[e] + qb[e] * qb[e];
-      sk += ka[e] * ka[e] + kb[e] * kb[e];
-    }
-    sq = row_sum<LPR>(sq);
-    sk = row_sum<LPR>(sk);
-    if (ok) {
-      store_chunk<T, CH>(p.q_s, out, qa);
-      store_chunk<T, CH>(p.q_s, out + HALF, qb);
-      store_chunk<T, CH>(p.k_r, out, ka);
-      store_chunk<T, CH>(p.k_r, out + HALF, kb);
-      if (li == 0) {
-        p.tau_q[r] = tq;
-        p.tau_k[r] = tk;
+    for (int u = 0; u < U; ++u) {
+      const int t = t0 + 4 * RPW * (j + u);
+      ok[u] = t < p.T;
+      tt[u] = ok[u] ? t : p.T - 1;
+      const size_t in = ra.in_base + (size_t)tt[u] * ra.in_stride + c0;
+      rq[u][0] = ld16<T>(p.q, in);
+      rq[u][1] = ld16<T>(p.q, in + HALF);
+      rk[u][0] = ld16<T>(p.k, in);
+      rk[u][1] = ld16<T>(p.k, in + HALF);
+      if (p.want_guard) {
+        rv[u][0] = ld16<T>(p.v, in);
+        rv[u][1] = ld16<T>(p.v, in + HALF);
       }
-      mq = nanmax_p(mq, sq);
-      mk = nanmax_p(mk, sk);
-      mv = nanmax_p(mv, av);
+      if (rotate) {
+        load_f32<CH>(p.cos + (size_t)tt[u] * HALF + c0, ca[u]);
+        load_f32<CH>(p.sin + (size_t)tt[u] * HALF + c0, sa[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float qa[CH], qb[CH], ka[CH], kb[CH];
+      cvt_chunk<T, CH>(rq[u][0], qa);
+      cvt_chunk<T, CH>(rq[u][1], qb);
+      cvt_chunk<T, CH>(rk[u][0], ka);
+      cvt_chunk<T, CH>(rk[u][1], kb);
+      // max |v| with NaN propagation at two VALU ops per element: a NaN-ignoring maximum plus
+      // a sum of v*0, which is NaN exactly when some v is NaN or infinite (either fails the
+      // guard's |v| bound, as the reference's comparison with a NaN maximum does).
+      float av = 0.0f;
+      if (p.want_guard) {
+        float va[CH], vb[CH], nan_acc = 0.0f;
+        cvt_chunk<T, CH>(rv[u][0], va);
+        cvt_chunk<T, CH>(rv[u][1], vb);
+#pragma unroll
+        for (int e = 0; e < CH; ++e) {
+          av = fmaxf(av, fmaxf(__builtin_fabsf(va[e]), __builtin_fabsf(vb[e])));
+          nan_acc = __builtin_fmaf(va[e], 0.0f, __builtin_fmaf(vb[e], 0.0f, nan_acc));
+        }
+        if (nan_acc != nan_acc) av = nan_acc;
+      }
+      const float tq =
+          norm_rotate<T, CH, LPR>(qa, qb, gqa, gqb, p.q_gain != nullptr, ca[u], sa[u], rotate, inv_d, p.eps);
+      const float tk =
+          norm_rotate<T, CH, LPR>(ka, kb, gka, gkb, p.k_gain != nullptr, ca[u], sa[u], rotate, inv_d, p.eps);
+      float sq = 0.0f, sk = 0.0f;
+#pragma unroll
+      for (int e = 0; e < CH; ++e) {
+        qa[e] = rnd<T>(mul_rn(qa[e], p.alpha));
+        qb[e] = rnd<T>(mul_rn(qb[e], p.alpha));
+        sq += qa[e] * qa[e] + qb[e] * qb[e];
+        sk += ka[e] * ka[e] + kb[e] * kb[e];
+      }
+      sq = row_sum<LPR>(sq);
+      sk = row_sum<LPR>(sk);
+      if (ok[u]) {
+        const size_t out = ra.out_base + (size_t)tt[u] * D + c0;
+        store_chunk<T, CH>(p.q_s, out, qa);
+        store_chunk<T, CH>(p.q_s, out + HALF, qb);
+        store_chunk<T, CH>(p.k_r, out, ka);
+        store_chunk<T, CH>(p.k_r, out + HALF, kb);
+        if (li == 0) {
+          const size_t row = (size_t)blockIdx.x * p.T + tt[u];
+          p.tau_q[row] = tq;
+          p.tau_k[row] = tk;
+        }
+        mq = nanmax_p(mq, sq);
+        mk = nanmax_p(mk, sk);
+        mv = nanmax_p(mv, av);
+      }
     }
   }
   for (int m = 32; m >= 1; m >>= 1) {
@@ -210,7 +268,7 @@ __global__ __launch_bounds__(256) void attn_qk_prologue_kernel(QkPrologueParams 
   if (threadIdx.x < 3) {
     float m = red[0][threadIdx.x];
     for (int w = 1; w < 4; ++w) m = nanmax_p(m, red[w][threadIdx.x]);
-    p.part[blockIdx.x * 3 + threadIdx.x] = m;
+    p.part[((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 3 + threadIdx.x] = m;
   }
 }
 
@@ -266,43 +324,64 @@ __global__ __launch_bounds__(256) void attn_qk_prologue_bwd_kernel(QkPrologueBwd
   }
   const bool rotate = p.cos != nullptr;
   const float inv_d = 1.0f / (float)D;
-  const size_t rows = (size_t)p.B * p.H * p.T;
-  const size_t step = (size_t)gridDim.x * 4 * RPW;
-  for (size_t r = ((size_t)blockIdx.x * 4 + wave) * RPW + sub; r - sub < rows; r += step) {
-    const bool ok = r < rows;
-    const size_t rr = ok ? r : rows - 1;
-    const size_t in = row_offset(rr, p.H, p.T, D, p.layout) + c0;
-    const size_t gr = rr * D + c0;
-    const int t = (int)(rr % p.T);
-    float ca[CH], sa[CH];
-    if (rotate) {
-      load_f32<CH>(p.cos + (size_t)t * HALF + c0, ca);
-      load_f32<CH>(p.sin + (size_t)t * HALF + c0, sa);
+  const RowAddr ra = head_rows(p.H, p.T, D, p.layout);
+  const int t0 = blockIdx.y * (4 * RPW * PRO_ITER) + wave * RPW + sub;
+  constexpr int U = PRO_U;
+#pragma unroll 1
+  for (int j = 0; j < PRO_ITER; j += U) {
+    uint4 rxq[U][2], rxk[U][2], rdq[U][2], rdk[U][2];
+    float ca[U][CH], sa[U][CH], tq[U], tk[U];
+    size_t in[U];
+    bool ok[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int t = t0 + 4 * RPW * (j + u);
+      ok[u] = t < p.T;
+      const int tc = ok[u] ? t : p.T - 1;
+      in[u] = ra.in_base + (size_t)tc * ra.in_stride + c0;
+      const size_t gr = ra.out_base + (size_t)tc * D + c0;
+      rxq[u][0] = ld16<T>(p.q, in[u]);
+      rxq[u][1] = ld16<T>(p.q, in[u] + HALF);
+      rxk[u][0] = ld16<T>(p.k, in[u]);
+      rxk[u][1] = ld16<T>(p.k, in[u] + HALF);
+      rdq[u][0] = ld16<T>(p.dq_r, gr);
+      rdq[u][1] = ld16<T>(p.dq_r, gr + HALF);
+      rdk[u][0] = ld16<T>(p.dk_r, gr);
+      rdk[u][1] = ld16<T>(p.dk_r, gr + HALF);
+      const size_t row = (size_t)blockIdx.x * p.T + tc;
+      tq[u] = p.tau_q[row];
+      tk[u] = p.tau_k[row];
+      if (rotate) {
+        load_f32<CH>(p.cos + (size_t)tc * HALF + c0, ca[u]);
+        load_f32<CH>(p.sin + (size_t)tc * HALF + c0, sa[u]);
+      }
     }
-    float xqa[CH], xqb[CH], xka[CH], xkb[CH], dqa[CH], dqb[CH], dka[CH], dkb[CH];
-    load_chunk<T, CH>(p.q, in, xqa);
-    load_chunk<T, CH>(p.q, in + HALF, xqb);
-    load_chunk<T, CH>(p.k, in, xka);
-    load_chunk<T, CH>(p.k, in + HALF, xkb);
-    load_chunk<T, CH>(p.dq_r, gr, dqa);
-    load_chunk<T, CH>(p.dq_r, gr + HALF, dqb);
-    load_chunk<T, CH>(p.dk_r, gr, dka);
-    load_chunk<T, CH>(p.dk_r, gr + HALF, dkb);
-    const float tq = p.tau_q[rr], tk = p.tau_k[rr];
-    float zq_a[CH], zq_b[CH], zk_a[CH], zk_b[CH];
 #pragma unroll
-    for (int e = 0; e < CH; ++e) zq_a[e] = zq_b[e] = zk_a[e] = zk_b[e] = 0.0f;
-    norm_rotate_vjp<T, CH, LPR>(dqa, dqb, xqa, xqb, gqa, gqb, ca, sa, rotate, tq, inv_d, zq_a, zq_b);
-    norm_rotate_vjp<T, CH, LPR>(dka, dkb, xka, xkb, gka, gkb, ca, sa, rotate, tk, inv_d, zk_a, zk_b);
-    if (ok) {
-      store_chunk<T, CH>(p.dq, in, dqa);
-      store_chunk<T, CH>(p.dq, in + HALF, dqb);
-      store_chunk<T, CH>(p.dk, in, dka);
-      store_chunk<T, CH>(p.dk, in + HALF, dkb);
+    for (int u = 0; u < U; ++u) {
+      float xqa[CH], xqb[CH], xka[CH], xkb[CH], dqa[CH], dqb[CH], dka[CH], dkb[CH];
+      cvt_chunk<T, CH>(rxq[u][0], xqa);
+      cvt_chunk<T, CH>(rxq[u][1], xqb);
+      cvt_chunk<T, CH>(rxk[u][0], xka);
+      cvt_chunk<T, CH>(rxk[u][1], xkb);
+      cvt_chunk<T, CH>(rdq[u][0], dqa);
+      cvt_chunk<T, CH>(rdq[u][1], dqb);
+      cvt_chunk<T, CH>(rdk[u][0], dka);
+      cvt_chunk<T, CH>(rdk[u][1], dkb);
+      float zq_a[CH], zq_b[CH], zk_a[CH], zk_b[CH];
 #pragma unroll
-      for (int e = 0; e < CH; ++e) {
-        aq_a[e] += zq_a[e]; aq_b[e] += zq_b[e];
-        ak_a[e] += zk_a[e]; ak_b[e] += zk_b[e];
+      for (int e = 0; e < CH; ++e) zq_a[e] = zq_b[e] = zk_a[e] = zk_b[e] = 0.0f;
+      norm_rotate_vjp<T, CH, LPR>(dqa, dqb, xqa, xqb, gqa, gqb, ca[u], sa[u], rotate, tq[u], inv_d, zq_a, zq_b);
+      norm_rotate_vjp<T, CH, LPR>(dka, dkb, xka, xkb, gka, gkb, ca[u], sa[u], rotate, tk[u], inv_d, zk_a, zk_b);
+      if (ok[u]) {
+        store_chunk<T, CH>(p.dq, in[u], dqa);
+        store_chunk<T, CH>(p.dq, in[u] + HALF, dqb);
+        store_chunk<T, CH>(p.dk, in[u], dka);
+        store_chunk<T, CH>(p.dk, in[u] + HALF, dkb);
+#pragma unroll
+        for (int e = 0; e < CH; ++e) {
+          aq_a[e] += zq_a[e]; aq_b[e] += zq_b[e];
+          ak_a[e] += zk_a[e]; ak_b[e] += zk_b[e];
+        }
       }
     }
   }
@@ -329,24 +408,42 @@ __global__ __launch_bounds__(256) void attn_qk_prologue_bwd_kernel(QkPrologueBwd
   __syncthreads();
   for (int i = threadIdx.x; i < 2 * D; i += 256) {
     const int x = i / D, d = i - x * D;
-    p.gpart[(size_t)blockIdx.x * 2 * D + i] = red[0][x][d] + red[1][x][d] + red[2][x][d] + red[3][x][d];
+    const size_t nb = (size_t)gridDim.x * gridDim.y, blk = (size_t)blockIdx.y * gridDim.x + blockIdx.x;
+    p.gpart[(size_t)i * nb + blk] = red[0][x][d] + red[1][x][d] + red[2][x][d] + red[3][x][d];
   }
 }
 
-// Gain gradients: sum of the per-block partials in block order.
+// Gain gradients: one workgroup per column sums that column's per-block partials (stored
+// column by column) with a fixed-order tree.
 __global__ __launch_bounds__(256) void attn_qk_gain_reduce_kernel(const float* gpart, int nblocks, int D,
                                                                   float* dq_gain, float* dk_gain) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= 2 * D) return;
+  __shared__ float red[256];
+  const int i = blockIdx.x;
   float s = 0.0f;
-  for (int b = 0; b < nblocks; ++b) s += gpart[(size_t)b * 2 * D + i];
-  float* dst = i < D ? dq_gain : dk_gain;
-  if (dst) dst[i < D ? i : i - D] = s;
+  for (int b = threadIdx.x; b < nblocks; b += 256) s += gpart[(size_t)i * nblocks + b];
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    float* dst = i < D ? dq_gain : dk_gain;
+    if (dst) dst[i < D ? i : i - D] = red[0];
+  }
 }
 
-int attn_qk_prologue_blocks(size_t rows) {
-  const size_t b = (rows + 31) / 32;
-  return (int)(b < 1024 ? (b ? b : 1) : 1024);
+// Positions per workgroup: 4 waves x rows per wave x PRO_ITER.
+int attn_qk_rows_per_wg(int D, bool bf16_io) {
+  const int ch = bf16_io ? 8 : 4;
+  const int lpr = D / 2 / ch;
+  return 4 * (64 / lpr) * PRO_ITER;
+}
+// Workgroups of the prologue grids; sizes the guard and gain partials (an upper bound over
+// both dtypes when bf16_io is unknown: the f32 rows per workgroup are the fewer).
+int attn_qk_prologue_blocks(int B, int H, int T, int D, bool bf16_io) {
+  const int rpw = attn_qk_rows_per_wg(D, bf16_io);
+  return B * H * ((T + rpw - 1) / rpw);
 }
 
 hipError_t launch_cayley_tables(const float* w, int half, int T, float* cos_out, float* sin_out, hipStream_t st) {
@@ -357,15 +454,16 @@ hipError_t launch_cayley_tables(const float* w, int half, int T, float* cos_out,
 }
 
 hipError_t launch_attn_qk_prologue(const QkPrologueParams& p, bool bf16_io, GuardParams g, hipStream_t st) {
-  const int nb = attn_qk_prologue_blocks((size_t)p.B * p.H * p.T);
+  const int nb = attn_qk_prologue_blocks(p.B, p.H, p.T, p.D, bf16_io);
+  const dim3 grid(p.B * p.H, (p.T + attn_qk_rows_per_wg(p.D, bf16_io) - 1) / attn_qk_rows_per_wg(p.D, bf16_io));
   {
     KTimer t("attn_qk_prologue", st);
     if (bf16_io) {
-      if (p.D == 128) hipLaunchKernelGGL((attn_qk_prologue_kernel<bf16, 128>), dim3(nb), dim3(256), 0, st, p);
-      else hipLaunchKernelGGL((attn_qk_prologue_kernel<bf16, 64>), dim3(nb), dim3(256), 0, st, p);
+      if (p.D == 128) hipLaunchKernelGGL((attn_qk_prologue_kernel<bf16, 128>), grid, dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((attn_qk_prologue_kernel<bf16, 64>), grid, dim3(256), 0, st, p);
     } else {
-      if (p.D == 128) hipLaunchKernelGGL((attn_qk_prologue_kernel<float, 128>), dim3(nb), dim3(256), 0, st, p);
-      else hipLaunchKernelGGL((attn_qk_prologue_kernel<float, 64>), dim3(nb), dim3(256), 0, st, p);
+      if (p.D == 128) hipLaunchKernelGGL((attn_qk_prologue_kernel<float, 128>), grid, dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((attn_qk_prologue_kernel<float, 64>), grid, dim3(256), 0, st, p);
     }
   }
   hipError_t e = hipGetLastError();
@@ -377,23 +475,24 @@ hipError_t launch_attn_qk_prologue(const QkPrologueParams& p, bool bf16_io, Guar
 
 hipError_t launch_attn_qk_prologue_bwd(const QkPrologueBwdParams& p, bool bf16_io, float* dq_gain, float* dk_gain,
                                        hipStream_t st) {
-  const int nb = attn_qk_prologue_blocks((size_t)p.B * p.H * p.T);
+  const int nb = attn_qk_prologue_blocks(p.B, p.H, p.T, p.D, bf16_io);
+  const dim3 grid(p.B * p.H, (p.T + attn_qk_rows_per_wg(p.D, bf16_io) - 1) / attn_qk_rows_per_wg(p.D, bf16_io));
   {
     KTimer t("attn_qk_prologue_bwd", st);
     if (bf16_io) {
-      if (p.D == 128) hipLaunchKernelGGL((attn_qk_prologue_bwd_kernel<bf16, 128>), dim3(nb), dim3(256), 0, st, p);
-      else hipLaunchKernelGGL((attn_qk_prologue_bwd_kernel<bf16, 64>), dim3(nb), dim3(256), 0, st, p);
+      if (p.D == 128) hipLaunchKernelGGL((attn_qk_prologue_bwd_kernel<bf16, 128>), grid, dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((attn_qk_prologue_bwd_kernel<bf16, 64>), grid, dim3(256), 0, st, p);
     } else {
-      if (p.D == 128) hipLaunchKernelGGL((attn_qk_prologue_bwd_kernel<float, 128>), dim3(nb), dim3(256), 0, st, p);
-      else hipLaunchKernelGGL((attn_qk_prologue_bwd_kernel<float, 64>), dim3(nb), dim3(256), 0, st, p);
+      if (p.D == 128) hipLaunchKernelGGL((attn_qk_prologue_bwd_kernel<float, 128>), grid, dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((attn_qk_prologue_bwd_kernel<float, 64>), grid, dim3(256), 0, st, p);
     }
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (dq_gain || dk_gain) {
     KTimer t("attn_qk_gain_reduce", st);
-    hipLaunchKernelGGL(attn_qk_gain_reduce_kernel, dim3((2 * p.D + 255) / 256), dim3(256), 0, st, p.gpart, nb, p.D,
-                       dq_gain, dk_gain);
+    hipLaunchKernelGGL(attn_qk_gain_reduce_kernel, dim3(2 * p.D), dim3(256), 0, st, p.gpart, nb, p.D, dq_gain,
+                       dk_gain);
   }
   return hipGetLastError();
 }

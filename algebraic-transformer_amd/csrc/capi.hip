@@ -139,15 +139,17 @@ alg::GuardParams guard_params(int H, int T, int n, float c, const float* sink_lo
   return g;
 }
 
-// Prologue workspace: [guard maxima f32 3*1024][gain-gradient partials f32 1024*2*D].
+// Prologue workspace: [guard maxima f32 3*nb][gain-gradient partials f32 2*D*nb], nb the
+// prologue's workgroup count (the f32 count, the larger of the two dtypes).
 struct PrologueWs {
   size_t guard_part, gain_part, total;
 };
-PrologueWs prologue_ws(int D) {
+PrologueWs prologue_ws(int B, int H, int T, int D) {
+  const size_t nb = (size_t)alg::attn_qk_prologue_blocks(B, H, T, D, false);
   PrologueWs w;
   w.guard_part = 0;
-  w.gain_part = align256(3 * 1024 * sizeof(float));
-  w.total = w.gain_part + align256((size_t)1024 * 2 * D * sizeof(float));
+  w.gain_part = align256(3 * nb * sizeof(float));
+  w.total = w.gain_part + align256(nb * 2 * D * sizeof(float));
   return w;
 }
 
@@ -200,7 +202,7 @@ int alg_attn_prepare(alg_stream_t stream, int dtype, int B, int H, int T, int D,
 
 size_t alg_attn_prologue_workspace_size(int B, int H, int T, int D) {
   if (B <= 0 || H <= 0 || T <= 0 || D <= 0) return 0;
-  return prologue_ws(D).total;
+  return prologue_ws(B, H, T, D).total;
 }
 
 int alg_cayley_tables(alg_stream_t stream, const float* w, int half, int seq_len, float* cos_out, float* sin_out) {
@@ -225,7 +227,7 @@ int alg_attn_qk_prologue(alg_stream_t stream, int dtype, int layout, int B, int 
   if (range_guard && !v) return fail(ALG_ERR_INVALID, "range_guard needs v");
   if (sink_logit && sink_count != 1 && sink_count != H) return fail(ALG_ERR_INVALID, "sink_count must be 1 or H");
   if (sink_logit && !sink_scaled) return fail(ALG_ERR_INVALID, "sink_scaled output required with a sink");
-  const PrologueWs ws = prologue_ws(D);
+  const PrologueWs ws = prologue_ws(B, H, T, D);
   if (!workspace || workspace_bytes < ws.total)
     return fail(ALG_ERR_INVALID, "workspace too small: need %zu bytes", ws.total);
   alg::QkPrologueParams p;
@@ -253,7 +255,7 @@ int alg_attn_qk_prologue_bwd(alg_stream_t stream, int dtype, int layout, int B, 
     return fail(ALG_ERR_INVALID, "q, k, tau_q, tau_k, dq_r, dk_r, dq and dk are required");
   if ((dq_gain && !q_gain) || (dk_gain && !k_gain))
     return fail(ALG_ERR_INVALID, "a gain gradient needs the gain it differentiates");
-  const PrologueWs ws = prologue_ws(D);
+  const PrologueWs ws = prologue_ws(B, H, T, D);
   if (!workspace || workspace_bytes < ws.total)
     return fail(ALG_ERR_INVALID, "workspace too small: need %zu bytes", ws.total);
   alg::QkPrologueBwdParams p;

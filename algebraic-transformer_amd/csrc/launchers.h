@@ -14,7 +14,7 @@ int attn_bwd_sink_blocks(int T);
 int attn_prep_blocks(size_t rows);
 hipError_t launch_attn_prep(const PrepParams& p, bool bf16_io, GuardParams g, hipStream_t st);
 hipError_t launch_attn_guard(const GuardParams& g, hipStream_t st);
-int attn_qk_prologue_blocks(size_t rows);
+int attn_qk_prologue_blocks(int B, int H, int T, int D, bool bf16_io);
 hipError_t launch_cayley_tables(const float* w, int half, int T, float* cos_out, float* sin_out, hipStream_t st);
 hipError_t launch_attn_qk_prologue(const QkPrologueParams& p, bool bf16_io, GuardParams g, hipStream_t st);
 hipError_t launch_attn_qk_prologue_bwd(const QkPrologueBwdParams& p, bool bf16_io, float* dq_gain, float* dk_gain,

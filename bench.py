@@ -181,6 +181,69 @@ def time_other_configs(torch, dev, iters=20, warmup=3, seed=1):
     return res
 
 
+def time_prologue(torch, dev, iters=20, warmup=3, seed=2):
+    """Fused attention prologue at the C4a shape, raw projections in the (B, T, H, D) layout:
+    forward (norm + gain, rotation, q pre-scale, guard) and VJP, each timed with CUDA events
+    over ``iters`` calls (median). Algorithmic bytes: forward reads q, k, v and writes q_s,
+    k_r and the two 1/rms rows; the VJP reads q, k, the two cotangents and 1/rms and writes
+    dq, dk. Both are HBM-bound streams."""
+    from algebraic_amd import _lib as L
+    lib = L.load()
+    B, H, T, D = (ATTN[k] for k in "BHTD")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    rn = lambda *s: torch.randn(*s, device=dev, generator=g, dtype=torch.float32)
+    q, k, v = (rn(B, T, H, D).to(torch.bfloat16) for _ in range(3))
+    dq_r, dk_r = (rn(B, H, T, D).to(torch.bfloat16) for _ in range(2))
+    gq, gk = 1 + 0.1 * rn(D), 1 + 0.1 * rn(D)
+    from algebraic_amd.kernels.prologue import cayley_table_geometric
+    cs, sn = cayley_table_geometric(D, T, device=dev)
+    sink = 0.1 * rn(H)
+    q_s, k_r = torch.empty((B, H, T, D), dtype=torch.bfloat16, device=dev), torch.empty((B, H, T, D), dtype=torch.bfloat16, device=dev)
+    tau_q, tau_k = torch.empty((B, H, T), device=dev), torch.empty((B, H, T), device=dev)
+    sink_out, flag = torch.empty(H, device=dev), torch.empty(1, dtype=torch.int32, device=dev)
+    dq, dk = torch.empty_like(q), torch.empty_like(k)
+    dgq, dgk = torch.empty(D, device=dev), torch.empty(D, device=dev)
+    nbytes = lib.alg_attn_prologue_workspace_size(B, H, T, D)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    st = L.stream_of(q)
+    P = L.ptr
+
+    def fwd():
+        L.check(lib.alg_attn_qk_prologue(st, L.DTYPE_BF16, L.LAYOUT_BTHD, B, H, T, D, P(q), P(k), P(v), P(gq), P(gk),
+                                          P(cs), P(sn), 1e-5, P(sink), H, ATTN["c"], ATTN["n"], 1, P(q_s), P(k_r),
+                                          P(tau_q), P(tau_k), P(sink_out), P(flag), P(ws), nbytes), "prologue")
+
+    def bwd():
+        L.check(lib.alg_attn_qk_prologue_bwd(st, L.DTYPE_BF16, L.LAYOUT_BTHD, B, H, T, D, P(q), P(k), P(gq), P(gk),
+                                              P(cs), P(sn), P(tau_q), P(tau_k), P(dq_r), P(dk_r), P(dq), P(dk),
+                                              P(dgq), P(dgk), P(ws), nbytes), "prologue bwd")
+
+    def median_ms(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(iters):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            e1.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        return sorted(ts)[len(ts) // 2]
+
+    elems = B * H * T * D
+    fwd_bytes = 5 * elems * 2 + 2 * B * H * T * 4
+    bwd_bytes = 6 * elems * 2 + 2 * B * H * T * 4
+    f_ms, b_ms = median_ms(fwd), median_ms(bwd)
+    fg, bg = fwd_bytes / (f_ms * 1e-3) / 1e9, bwd_bytes / (b_ms * 1e-3) / 1e9
+    return {"workload": "fused QK norm + gain + Cayley rotation + q*alpha + guard, C4a shape, (B,T,H,D) input",
+            "fwd_ms": round(f_ms, 4), "fwd_bytes": fwd_bytes, "fwd_gbs": round(fg, 1),
+            "bwd_ms": round(b_ms, 4), "bwd_bytes": bwd_bytes, "bwd_gbs": round(bg, 1),
+            "peak_gbs": PEAK_HBM_GBS, "fwd_frac": round(fg / PEAK_HBM_GBS, 4), "bwd_frac": round(bg / PEAK_HBM_GBS, 4)}
+
+
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` recorded from rocprofv3 FETCH_SIZE + WRITE_SIZE runs
     (each scaled by the same counter's reading for a device copy of known size), as listed
@@ -364,6 +427,7 @@ def main():
     if not args.no_other_configs:
         log("timing the other BASELINE configs (C1, C2, C3, C5)")
         out["other_configs"] = time_other_configs(torch, dev)
+        out["prologue"] = time_prologue(torch, dev)
     if not args.no_cpu_baseline:
         log("timing the CPU baseline sample")
         out["cpu_baseline"] = cpu_baseline()
