@@ -92,6 +92,7 @@ class _Plan(NamedTuple):
     fast_rho: bool
     inv_stat: bool
     range_guard: bool
+    layout: int = 0     # _lib.LAYOUT_BHTD or _lib.LAYOUT_BTHD
 
 
 class _FlashFn(torch.autograd.Function):
@@ -99,7 +100,7 @@ class _FlashFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, sink_logit, plan: _Plan):
-        B, H, T, D = q.shape
+        B, H, T, D = _bhtd(q.shape, plan.layout)
         lib = _lib.load()
         dt = _DTYPES[q.dtype]
         dev = q.device
@@ -125,7 +126,7 @@ class _FlashFn(torch.autograd.Function):
         o_precise = torch.empty(q.shape, dtype=torch.float32, device=dev) if need_precise else None
         stat = torch.empty((B, H, T), dtype=torch.float32, device=dev)
         _lib.check(lib.alg_attn_fwd(
-            st, dt, B, H, T, D, _lib.ptr(q_s), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink), plan.n, plan.variant,
+            st, dt, plan.layout, B, H, T, D, _lib.ptr(q_s), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink), plan.n, plan.variant,
             _lib.ptr(flag), plan.clamp, int(plan.fast_rho), int(plan.inv_stat),
             _lib.ptr(o), _lib.ptr(o_precise), _lib.ptr(stat)), "flash_attention forward")
         ctx.plan = plan
@@ -138,7 +139,7 @@ class _FlashFn(torch.autograd.Function):
     def backward(ctx, do):
         q_s, k, v, sink, o, o_precise, stat, flag = ctx.saved_tensors
         plan = ctx.plan
-        B, H, T, D = q_s.shape
+        B, H, T, D = _bhtd(q_s.shape, plan.layout)
         lib = _lib.load()
         dt = _DTYPES[q_s.dtype]
         dev = q_s.device
@@ -153,7 +154,7 @@ class _FlashFn(torch.autograd.Function):
         dbeta = torch.empty(H, dtype=torch.float32, device=dev) if sink is not None else None
         alpha = 1.0 / (math.sqrt(D) * plan.c)
         _lib.check(lib.alg_attn_bwd(
-            st, dt, B, H, T, D, _lib.ptr(q_s), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink), _lib.ptr(o),
+            st, dt, plan.layout, B, H, T, D, _lib.ptr(q_s), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink), _lib.ptr(o),
             _lib.ptr(o_precise), _lib.ptr(stat), _lib.ptr(do), plan.n, plan.variant, _lib.ptr(flag), plan.clamp,
             int(plan.fast_rho), int(plan.inv_stat), alpha, _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(di),
             _lib.ptr(dbeta), _lib.ptr(ws), ws_bytes), "flash_attention backward")
@@ -176,23 +177,41 @@ def flash_attention(q, k, v, sink_logit=None, *, kind: str = "softmax",
                     resident_bwd: Optional[bool] = None,
                     diagonal_bwd: Optional[bool] = None,
                     diagonal_fwd: Optional[bool] = None,
-                    head_resident: Optional[bool] = None):
+                    head_resident: Optional[bool] = None, layout: str = "bhtd"):
     """Causal attention on (B, H, T, D) GPU tensors; ``sink_logit`` broadcastable to (H,).
 
     Same arguments, validation and maths as flash.py:763-857 for ``kind="asinh"``.
     Differentiable in q, k, v and sink_logit through torch autograd.
+    ``layout="bthd"`` (an addition to the reference's signature) takes q, k, v in the
+    projection layout (B, T, H, D) of model.py:167-169 and returns o in it, so the model's
+    head transposes (model.py:167-169, 182) and their copies drop out: ``o.reshape(B, T, H*D)``
+    is a view.
     """
     plan = _make_plan(q, k, v, kind, n, c, block, block_q, block_k, shift, fast_rho, inv_stat, compact_stat,
-                      poly_rho, range_guard, resident_bwd, diagonal_bwd, diagonal_fwd, head_resident)
+                      poly_rho, range_guard, resident_bwd, diagonal_bwd, diagonal_fwd, head_resident, layout)
     return _FlashFn.apply(q, k, v, sink_logit, plan)
 
 
+_LAYOUTS = {"bhtd": 0, "bthd": 1}
+
+
+def _bhtd(shape, layout: int):
+    """(B, H, T, D) of a tensor stored in `layout`."""
+    if layout == _lib.LAYOUT_BTHD:
+        B, T, H, D = shape
+        return B, H, T, D
+    return tuple(shape)
+
+
 def _make_plan(q, k, v, kind, n, c, block, block_q, block_k, shift, fast_rho, inv_stat, compact_stat, poly_rho,
-               range_guard, resident_bwd, diagonal_bwd, diagonal_fwd, head_resident) -> _Plan:
+               range_guard, resident_bwd, diagonal_bwd, diagonal_fwd, head_resident, layout="bhtd") -> _Plan:
     """Argument validation of flash.py:793-822 and the kernel variant it selects."""
+    if layout not in _LAYOUTS:
+        raise ValueError(f"layout must be one of {sorted(_LAYOUTS)}")
+    lay = _LAYOUTS[layout]
     if q.dim() != 4 or k.shape != q.shape or v.shape != q.shape:
-        raise ValueError("q, k, v must share the shape (B, H, T, D)")
-    B, H, T, D = q.shape
+        raise ValueError("q, k, v must share the shape " + ("(B, T, H, D)" if lay else "(B, H, T, D)"))
+    B, H, T, D = _bhtd(q.shape, lay)
     bq = min(block_q or block, T)
     bk = min(block_k or block, T)
     if T % bq or T % bk:
@@ -221,16 +240,16 @@ def _make_plan(q, k, v, kind, n, c, block, block_q, block_k, shift, fast_rho, in
     if range_guard and kind == "asinh" and n <= 32:
         if poly_rho:
             raise ValueError("range_guard is for exact radical evaluation")
-        plan = _Plan(_lib.ATTN_GUARDED, var.n, float(c), var.clamp, True, True, True)
+        plan = _Plan(_lib.ATTN_GUARDED, var.n, float(c), var.clamp, True, True, True, lay)
     else:
         if var.poly_rho:
             raise NotImplementedError("poly_rho is an opt-in TPU experiment; use exact rho")
         if var.shift:
-            plan = _Plan(_lib.ATTN_SHIFTED, var.n, float(c), var.clamp, var.fast_rho, False, False)
+            plan = _Plan(_lib.ATTN_SHIFTED, var.n, float(c), var.clamp, var.fast_rho, False, False, lay)
         else:
             if not var.fast_rho:
                 raise NotImplementedError("unshifted accumulation is built with fast rho (the default)")
-            plan = _Plan(_lib.ATTN_CLIPPED, var.n, float(c), var.clamp, True, var.inv_stat, False)
+            plan = _Plan(_lib.ATTN_CLIPPED, var.n, float(c), var.clamp, True, var.inv_stat, False, lay)
     if not q.is_cuda:
         raise RuntimeError("flash_attention needs GPU tensors (no CPU fallback)")
     return plan

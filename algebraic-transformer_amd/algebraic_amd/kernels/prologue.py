@@ -21,7 +21,7 @@ from typing import Optional
 import torch
 
 from .. import _lib
-from .flash import _DTYPES, _make_plan
+from .flash import _DTYPES, _bhtd, _make_plan
 
 
 def cayley_powers(w: torch.Tensor, seq_len: int):
@@ -66,7 +66,7 @@ class _PrologueFlashFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, sink_logit, q_gain, k_gain, cos, sin, eps, plan):
-        B, H, T, D = q.shape
+        B, H, T, D = _bhtd(q.shape, plan.layout)
         lib = _lib.load()
         dt = _DTYPES[q.dtype]
         dev = q.device
@@ -95,7 +95,7 @@ class _PrologueFlashFn(torch.autograd.Function):
         sink = torch.empty(H, dtype=torch.float32, device=dev) if has_sink else None
         flag = torch.empty(1, dtype=torch.int32, device=dev)
         _lib.check(lib.alg_attn_qk_prologue(
-            st, dt, _lib.LAYOUT_BHTD, B, H, T, D, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(gq), _lib.ptr(gk),
+            st, dt, plan.layout, B, H, T, D, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(gq), _lib.ptr(gk),
             _lib.ptr(cs), _lib.ptr(sn), float(eps), _lib.ptr(sink_in), sink_in.numel() if has_sink else 0, plan.c,
             plan.n, int(plan.range_guard), _lib.ptr(q_s), _lib.ptr(k_r), _lib.ptr(tau_q), _lib.ptr(tau_k),
             _lib.ptr(sink), _lib.ptr(flag), _lib.ptr(ws), ws_bytes), "attention prologue")
@@ -103,7 +103,7 @@ class _PrologueFlashFn(torch.autograd.Function):
         o_precise = torch.empty(q.shape, dtype=torch.float32, device=dev) if plan.variant == _lib.ATTN_GUARDED else None
         stat = torch.empty((B, H, T), dtype=torch.float32, device=dev)
         _lib.check(lib.alg_attn_fwd(
-            st, dt, B, H, T, D, _lib.ptr(q_s), _lib.ptr(k_r), _lib.ptr(v), _lib.ptr(sink), plan.n, plan.variant,
+            st, dt, plan.layout, B, H, T, D, _lib.ptr(q_s), _lib.ptr(k_r), _lib.ptr(v), _lib.ptr(sink), plan.n, plan.variant,
             _lib.ptr(flag), plan.clamp, int(plan.fast_rho), int(plan.inv_stat),
             _lib.ptr(o), _lib.ptr(o_precise), _lib.ptr(stat)), "attention forward")
         ctx.plan = plan
@@ -117,7 +117,7 @@ class _PrologueFlashFn(torch.autograd.Function):
     def backward(ctx, do):
         q, k, v, gq, gk, cs, sn, q_s, k_r, tau_q, tau_k, sink, o, o_precise, stat, flag = ctx.saved_tensors
         plan = ctx.plan
-        B, H, T, D = q.shape
+        B, H, T, D = _bhtd(q.shape, plan.layout)
         lib = _lib.load()
         dt = _DTYPES[q.dtype]
         dev = q.device
@@ -130,7 +130,7 @@ class _PrologueFlashFn(torch.autograd.Function):
         dbeta = torch.empty(H, dtype=torch.float32, device=dev) if sink is not None else None
         alpha = 1.0 / (math.sqrt(D) * plan.c)
         _lib.check(lib.alg_attn_bwd(
-            st, dt, B, H, T, D, _lib.ptr(q_s), _lib.ptr(k_r), _lib.ptr(v), _lib.ptr(sink), _lib.ptr(o),
+            st, dt, plan.layout, B, H, T, D, _lib.ptr(q_s), _lib.ptr(k_r), _lib.ptr(v), _lib.ptr(sink), _lib.ptr(o),
             _lib.ptr(o_precise), _lib.ptr(stat), _lib.ptr(do), plan.n, plan.variant, _lib.ptr(flag), plan.clamp,
             int(plan.fast_rho), int(plan.inv_stat), alpha, _lib.ptr(dq_r), _lib.ptr(dk_r), _lib.ptr(dv),
             _lib.ptr(di), _lib.ptr(dbeta), _lib.ptr(ws), ws_bytes), "attention backward")
@@ -140,7 +140,7 @@ class _PrologueFlashFn(torch.autograd.Function):
         dgq = torch.empty(D, dtype=torch.float32, device=dev) if gq is not None else None
         dgk = torch.empty(D, dtype=torch.float32, device=dev) if gk is not None else None
         _lib.check(lib.alg_attn_qk_prologue_bwd(
-            st, dt, _lib.LAYOUT_BHTD, B, H, T, D, _lib.ptr(q), _lib.ptr(k), _lib.ptr(gq), _lib.ptr(gk), _lib.ptr(cs),
+            st, dt, plan.layout, B, H, T, D, _lib.ptr(q), _lib.ptr(k), _lib.ptr(gq), _lib.ptr(gk), _lib.ptr(cs),
             _lib.ptr(sn), _lib.ptr(tau_q), _lib.ptr(tau_k), _lib.ptr(dq_r), _lib.ptr(dk_r), _lib.ptr(dq),
             _lib.ptr(dk), _lib.ptr(dgq), _lib.ptr(dgk), _lib.ptr(pws), pws_bytes), "attention prologue backward")
         dsink = None
@@ -162,18 +162,20 @@ def qk_norm_rotary_flash_attention(q, k, v, sink_logit=None, q_gain=None, k_gain
                                    inv_stat: Optional[bool] = None, compact_stat: bool = True,
                                    poly_rho: bool = False, range_guard: bool = False,
                                    resident_bwd: Optional[bool] = None, diagonal_bwd: Optional[bool] = None,
-                                   diagonal_fwd: Optional[bool] = None, head_resident: Optional[bool] = None):
+                                   diagonal_fwd: Optional[bool] = None, head_resident: Optional[bool] = None,
+                                   layout: str = "bhtd"):
     """``flash_attention(rot(rms_norm(q, q_gain)), rot(rms_norm(k, k_gain)), v, sink, ...)``.
 
-    q, k, v: (B, H, T, D) raw projections (bf16 or f32) on the GPU; gains (D,) or None;
-    cos/sin: (>= T, D/2) float32 tables or None (no rotation). Attention arguments and
-    their validation are flash_attention's (flash.py:763-857). Differentiable in q, k, v,
-    sink_logit and the gains.
+    q, k, v: raw projections (bf16 or f32) on the GPU, (B, H, T, D) or, with
+    ``layout="bthd"``, the projection layout (B, T, H, D) (the output then has it too);
+    gains (D,) or None; cos/sin: (>= T, D/2) float32 tables or None (no rotation).
+    Attention arguments and their validation are flash_attention's (flash.py:763-857).
+    Differentiable in q, k, v, sink_logit and the gains.
     """
     if (cos is None) != (sin is None):
         raise ValueError("cos and sin are given together")
     if not (eps > 0) or not math.isfinite(eps):
         raise ValueError("eps must be positive and finite")
     plan = _make_plan(q, k, v, kind, n, c, block, block_q, block_k, shift, fast_rho, inv_stat, compact_stat,
-                      poly_rho, range_guard, resident_bwd, diagonal_bwd, diagonal_fwd, head_resident)
+                      poly_rho, range_guard, resident_bwd, diagonal_bwd, diagonal_fwd, head_resident, layout)
     return _PrologueFlashFn.apply(q, k, v, sink_logit, q_gain, k_gain, cos, sin, float(eps), plan)

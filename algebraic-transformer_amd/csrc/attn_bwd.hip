@@ -45,6 +45,8 @@ __global__ __launch_bounds__(256) void attn_bwd_pre_kernel(AttnBwdParams p, int 
   const bool precise = shifted && p.o_precise != nullptr;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row0 = blockIdx.y * PRE_ROWS;
+  const size_t hb = head_base(bh, p.H, T_, D, p.layout);
+  const int ld = row_stride(p.H, D, p.layout);
   const int n = 1 << p.log2n;
   float b = p.sink ? p.sink[head] : 0.0f;
   if (p.mode == MODE_CLIPPED && !p.flag) b = fminf(b, p.clamp);
@@ -63,25 +65,27 @@ __global__ __launch_bounds__(256) void attn_bwd_pre_kernel(AttnBwdParams p, int 
 #pragma unroll
     for (int u = 0; u < PRE_U; ++u) {
       const int r = r0 + u * 4 * rpw + sub;
-      const size_t off = ((size_t)bh * T_ + min(r, rend - 1)) * D + li * 8;
+      const int rc = min(r, rend - 1);
+      const size_t off = ((size_t)bh * T_ + rc) * D + li * 8;  // internal (B, H, T, D) buffers
+      const size_t xoff = hb + (size_t)rc * ld + li * 8;        // dO and o in the call's layout
       if constexpr (sizeof(T) == 2) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p.dO) + off);
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p.dO) + xoff);
 #pragma unroll
         for (int j = 0; j < 8; ++j) dov[u][j] = (float)a[j];
       } else {
-        const floatx4 a0 = *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(p.dO) + off);
-        const floatx4 a1 = *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(p.dO) + off + 4);
+        const floatx4 a0 = *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(p.dO) + xoff);
+        const floatx4 a1 = *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(p.dO) + xoff + 4);
 #pragma unroll
         for (int j = 0; j < 4; ++j) { dov[u][j] = a0[j]; dov[u][4 + j] = a1[j]; }
       }
       if (precise || sizeof(T) == 4) {
-        const float* src = precise ? p.o_precise + off : reinterpret_cast<const float*>(p.o) + off;
+        const float* src = precise ? p.o_precise + off : reinterpret_cast<const float*>(p.o) + xoff;
         const floatx4 b0 = *reinterpret_cast<const floatx4*>(src);
         const floatx4 b1 = *reinterpret_cast<const floatx4*>(src + 4);
 #pragma unroll
         for (int j = 0; j < 4; ++j) { ov[u][j] = b0[j]; ov[u][4 + j] = b1[j]; }
       } else {
-        const bf16x8 b = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p.o) + off);
+        const bf16x8 b = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p.o) + xoff);
 #pragma unroll
         for (int j = 0; j < 8; ++j) ov[u][j] = (float)b[j];
       }
@@ -128,12 +132,12 @@ struct RowTile {
   // Rows past T load the last row instead (clamped, unconditional loads that nothing waits
   // for until the tile is stored). The query tiles' rows past T carry stat = 0, so their
   // weights and score gradients are exactly zero and the finite stand-in values add nothing.
-  static __device__ __forceinline__ void load(uint4 (&r)[PER], const T* src, int r0, int T_) {
+  static __device__ __forceinline__ void load(uint4 (&r)[PER], const T* src, int r0, int T_, int ld) {
 #pragma unroll
     for (int c = 0; c < PER; ++c) {
       const int idx = threadIdx.x + c * 256;
       const int row = min(idx / CPR, R - 1), col = (idx - (idx / CPR) * CPR) * CH;
-      r[c] = *reinterpret_cast<const uint4*>(src + (size_t)min(r0 + row, T_ - 1) * D + col);
+      r[c] = *reinterpret_cast<const uint4*>(src + (size_t)min(r0 + row, T_ - 1) * ld + col);
     }
   }
   // bf16 tiles are unpadded and swizzled (swz_at); f32 tiles are row-major with `pitch`.
@@ -176,11 +180,13 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
   const int T_ = p.T;
   const int bh = blockIdx.x;
   const int k0 = blockIdx.y * BWD_BK;  // blockIdx.y = 0 has the most causal work
-  const size_t base = (size_t)bh * T_ * D;
-  const T* Q = reinterpret_cast<const T*>(p.q) + base;
-  const T* K = reinterpret_cast<const T*>(p.k) + base;
-  const T* V = reinterpret_cast<const T*>(p.v) + base;
-  const T* dO = reinterpret_cast<const T*>(p.dO) + base;
+  const size_t base = (size_t)bh * T_ * D;  // internal (B, H, T, D) buffers (dq_acc)
+  const size_t hb = head_base(bh, p.H, T_, D, p.layout);
+  const int ld = row_stride(p.H, D, p.layout);
+  const T* Q = reinterpret_cast<const T*>(p.q) + hb;
+  const T* K = reinterpret_cast<const T*>(p.k) + hb;
+  const T* V = reinterpret_cast<const T*>(p.v) + hb;
+  const T* dO = reinterpret_cast<const T*>(p.dO) + hb;
   const float* stat = p.stat + (size_t)bh * T_;
   const float* di = p.di + (size_t)bh * T_;
   float* dq_acc = p.dq_acc + base;
@@ -191,7 +197,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
   {
     typedef RowTile<T, D, BWD_BK> KT;
     uint4 kr[KT::PER];
-    KT::load(kr, K, k0, T_);
+    KT::load(kr, K, k0, T_, ld);
     KT::store(Ks, PITCH, kr);
   }
 
@@ -203,12 +209,12 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
   for (int s = 0; s < NF; ++s) {
     if constexpr (BF) {
       bf16x8 z = {};
-      const size_t o = (size_t)mykey * D + 16 * s + 8 * h;
+      const size_t o = (size_t)mykey * ld + 16 * s + 8 * h;
       kf[s] = mykey < T_ ? ld8(reinterpret_cast<const bf16*>(K) + o) : z;
       vf[s] = mykey < T_ ? ld8(reinterpret_cast<const bf16*>(V) + o) : z;
     } else {
       floatx4 z = {};
-      const size_t o = (size_t)mykey * D + 8 * s + 4 * h;
+      const size_t o = (size_t)mykey * ld + 8 * s + 4 * h;
       kf[s] = mykey < T_ ? *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(K) + o) : z;
       vf[s] = mykey < T_ ? *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(V) + o) : z;
     }
@@ -225,8 +231,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
   uint4 qr[QT::PER], dr[QT::PER];
   float str = 0.0f, dir = 0.0f;
   auto prefetch = [&](int qbase) {
-    QT::load(qr, Q, qbase, T_);
-    QT::load(dr, dO, qbase, T_);
+    QT::load(qr, Q, qbase, T_, ld);
+    QT::load(dr, dO, qbase, T_, ld);
     if (threadIdx.x < BWD_BQ) {  // raw loads; rows past T are zeroed when committed
       const int q = min(qbase + (int)threadIdx.x, T_ - 1);
       str = stat[q];
@@ -448,15 +454,15 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
 
   // dK = n * acc, dV = acc (flash.py:591-597), rounded to the input dtype.
   const float slope = (float)(1 << log2n);
-  T* DK = reinterpret_cast<T*>(p.dk) + base;
-  T* DV = reinterpret_cast<T*>(p.dv) + base;
+  T* DK = reinterpret_cast<T*>(p.dk) + hb;
+  T* DV = reinterpret_cast<T*>(p.dv) + hb;
 #pragma unroll
   for (int db = 0; db < NDB; ++db) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int key = wk0 + 8 * (i >> 2) + 4 * h + (i & 3);
       if (key < T_) {
-        const size_t o = (size_t)key * D + db * 32 + l32;
+        const size_t o = (size_t)key * ld + db * 32 + l32;
         DK[o] = (T)(dk[db][i] * slope);
         DV[o] = (T)(dv[db][i]);
       }
@@ -545,7 +551,7 @@ constexpr int bwd_valu_per_elem() { return MODE == MODE_INRANGE ? 14 : 20; }
 // Query tiles ping-pong between two LDS buffer sets (distinct __shared__ objects). The causal
 // mask is evaluated only on the two tiles that cross the diagonal; every LDS access is a
 // per-lane swizzled offset computed once plus an immediate.
-template <int D, int MODE, int L2N>
+template <int D, int MODE, int L2N, int LAYOUT>
 __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) {
   static_assert(D == 64 || D == 128, "head_dim");
   constexpr int BQ = BF_BQ, CPR = D / 8, NDB = D / 32, NF = D / 16;
@@ -569,13 +575,15 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
   int bh, kblk;
   bwd_block_coords(p.B * p.H, ceil_div(T_, BWD_BK), bh, kblk);
   const int k0 = kblk * BWD_BK;
-  const size_t base = (size_t)bh * T_ * D;
+  const size_t base = head_base(bh, p.H, T_, D, LAYOUT);
+  const int ld = LAYOUT ? p.H * D : D;  // elements between positions
   const bf16* Q = reinterpret_cast<const bf16*>(p.q) + base;
   const bf16* K = reinterpret_cast<const bf16*>(p.k) + base;
   const bf16* V = reinterpret_cast<const bf16*>(p.v) + base;
   const bf16* dO = reinterpret_cast<const bf16*>(p.dO) + base;
-  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)Q, (short)0, T_ * D * 2, BUF_RSRC_WORD3);
-  const __amdgpu_buffer_rsrc_t rdo = __builtin_amdgcn_make_buffer_rsrc((void*)dO, (short)0, T_ * D * 2, BUF_RSRC_WORD3);
+  const int nbytes = head_bytes(T_, ld, D, 2);
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)Q, (short)0, nbytes, BUF_RSRC_WORD3);
+  const __amdgpu_buffer_rsrc_t rdo = __builtin_amdgcn_make_buffer_rsrc((void*)dO, (short)0, nbytes, BUF_RSRC_WORD3);
   const __amdgpu_buffer_rsrc_t rst =
       __builtin_amdgcn_make_buffer_rsrc((void*)(p.stat + (size_t)bh * T_), (short)0, T_ * 4, BUF_RSRC_WORD3);
   const __amdgpu_buffer_rsrc_t rdi =
@@ -586,7 +594,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
   const int nq = ceil_div(T_, BQ);
   const int qstart = k0 / BQ;
 
-  tile_dma2<D>(Qs0, dOs0, rq, rdo, qstart * BQ, wave, lane);
+  tile_dma2<D>(Qs0, dOs0, rq, rdo, qstart * BQ, wave, lane, ld);
   bwd_stat_dma(st0, di0, rst, rdi, qstart * BQ, wave, lane);
   // K and V fragments of this wave's keys: B operands of S = Q K^T and dP = dO V^T. Keys
   // past T are zero and always masked.
@@ -594,7 +602,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
 #pragma unroll
   for (int s = 0; s < NF; ++s) {
     const bf16x8 z = {};
-    const size_t o = (size_t)mykey * D + 16 * s + 8 * h;
+    const size_t o = (size_t)mykey * ld + 16 * s + 8 * h;
     kf[s] = mykey < T_ ? ld8(K + o) : z;
     vf[s] = mykey < T_ ? ld8(V + o) : z;
   }
@@ -703,8 +711,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
     for (int g = 0; g < NF; ++g) {
       sdp_step(g);
       if (g < PW) {
-        if constexpr (BUF) tile_dma2_part<D>(Qs0, dOs0, rq, rdo, qbase + BQ, wave, lane, g);
-        else tile_dma2_part<D>(Qs1, dOs1, rq, rdo, qbase + BQ, wave, lane, g);
+        if constexpr (BUF) tile_dma2_part<D>(Qs0, dOs0, rq, rdo, qbase + BQ, wave, lane, g, ld);
+        else tile_dma2_part<D>(Qs1, dOs1, rq, rdo, qbase + BQ, wave, lane, g, ld);
       }
       if (g == PW) {
         if constexpr (BUF) bwd_stat_dma(st0, di0, rst, rdi, qbase + BQ, wave, lane);
@@ -786,7 +794,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
     for (int i = 0; i < 16; ++i) {
       const int key = wk0 + 8 * (i >> 2) + 4 * h + (i & 3);
       if (key < T_) {
-        const size_t o = (size_t)key * D + db * 32 + l32;
+        const size_t o = (size_t)key * ld + db * 32 + l32;
         DK[o] = f2bf(dk[db][i] * slope);
         DV[o] = f2bf(dv[db][i]);
       }
@@ -805,7 +813,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
 //   R3  dQ^T over keys 0..31     | dS of 32..63  (MFMA | VALU)
 //   R4  dQ^T over keys 32..63                    (MFMA)
 // The output is dq = round(round(n * acc) * dq_scale) (flash.py:592 and the q_s chain rule).
-template <int D, int MODE, int L2N>
+template <int D, int MODE, int L2N, int LAYOUT>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
   static_assert(D == 64 || D == 128, "head_dim");
   constexpr int BK = 64, CPR = D / 8, NDB = D / 32, NF = D / 16;
@@ -824,20 +832,22 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
   const int nqb = ceil_div(T_, 128);
   const int bh = blockIdx.x;
   const int qb = nqb - 1 - blockIdx.y;  // heaviest causal rows first
-  const size_t base = (size_t)bh * T_ * D;
+  const size_t base = head_base(bh, p.H, T_, D, LAYOUT);
+  const int ld = LAYOUT ? p.H * D : D;  // elements between positions
   const bf16* Q = reinterpret_cast<const bf16*>(p.q) + base;
   const bf16* K = reinterpret_cast<const bf16*>(p.k) + base;
   const bf16* V = reinterpret_cast<const bf16*>(p.v) + base;
   const bf16* dO = reinterpret_cast<const bf16*>(p.dO) + base;
-  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)K, (short)0, T_ * D * 2, BUF_RSRC_WORD3);
-  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)V, (short)0, T_ * D * 2, BUF_RSRC_WORD3);
+  const int nbytes = head_bytes(T_, ld, D, 2);
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)K, (short)0, nbytes, BUF_RSRC_WORD3);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)V, (short)0, nbytes, BUF_RSRC_WORD3);
   const int q0 = qb * 128 + wave * 32;
   const int myq = q0 + l32;
   const int log2n = p.log2n;
   const int ntiles = (min(qb * 128 + 127, T_ - 1)) / BK + 1;  // key tiles up to the last query
 
-  tile_dma2<D>(Ks0, Vs0, rk, rv, 0, wave, lane);
-  if (ntiles > 1) tile_dma2<D>(Ks1, Vs1, rk, rv, BK, wave, lane);
+  tile_dma2<D>(Ks0, Vs0, rk, rv, 0, wave, lane, ld);
+  if (ntiles > 1) tile_dma2<D>(Ks1, Vs1, rk, rv, BK, wave, lane, ld);
   // Q and dO fragments of this lane's query (B operands of S^T = K Q^T, dP^T = V dO^T);
   // queries past T carry stat = 0, so their weights and score gradients are zero.
   bf16x8 qf[NF], of[NF];
@@ -845,7 +855,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
 #pragma unroll
   for (int s = 0; s < NF; ++s) {
     const bf16x8 z = {};
-    const size_t o = (size_t)myq * D + 16 * s + 8 * h;
+    const size_t o = (size_t)myq * ld + 16 * s + 8 * h;
     qf[s] = live ? ld8(Q + o) : z;
     of[s] = live ? ld8(dO + o) : z;
   }
@@ -965,8 +975,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
       rv2[0] = ld8(Vn + row_off[0]);
     }
     if (kt + 2 < ntiles) {
-      if constexpr (BUF) tile_dma2<D>(Ks1, Vs1, rk, rv, kb0 + 2 * BK, wave, lane);
-      else tile_dma2<D>(Ks0, Vs0, rk, rv, kb0 + 2 * BK, wave, lane);
+      if constexpr (BUF) tile_dma2<D>(Ks1, Vs1, rk, rv, kb0 + 2 * BK, wave, lane, ld);
+      else tile_dma2<D>(Ks0, Vs0, rk, rv, kb0 + 2 * BK, wave, lane, ld);
     }
   };
 
@@ -985,7 +995,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
 
   if (live) {
     const float slope = (float)(1 << log2n);
-    bf16* DQ = reinterpret_cast<bf16*>(p.dq) + base + (size_t)myq * D;
+    bf16* DQ = reinterpret_cast<bf16*>(p.dq) + base + (size_t)myq * ld;
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
 #pragma unroll
@@ -1006,7 +1016,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
 // post: dq and the per-head sink gradient
 // ---------------------------------------------------------------------------
 template <typename T>
-__global__ __launch_bounds__(256) void attn_bwd_post_kernel(AttnBwdParams p, size_t total, int nblk) {
+__global__ __launch_bounds__(256) void attn_bwd_post_kernel(AttnBwdParams p, size_t total, int nblk, int D) {
   const float slope = (float)(1 << p.log2n);
   // 8 consecutive elements per thread (total is a multiple of D, itself a multiple of 8).
   const size_t n8 = total / 8;
@@ -1019,11 +1029,19 @@ __global__ __launch_bounds__(256) void attn_bwd_post_kernel(AttnBwdParams p, siz
       const T dqs = (T)((j < 4 ? a0[j] : a1[j - 4]) * slope);  // kernel output dq_s (flash.py:592)
       out[j] = (T)((float)dqs * p.dq_scale);                   // chain rule through q_s
     }
+    // dq_acc is (B, H, T, D); dq is stored in the call's layout.
+    size_t dst = 8 * i;
+    if (p.layout) {
+      const size_t row = dst / D;
+      const int col = (int)(dst - row * D);
+      const int bh = (int)(row / p.T), t = (int)(row - (size_t)bh * p.T);
+      dst = head_base(bh, p.H, p.T, D, 1) + (size_t)t * row_stride(p.H, D, 1) + col;
+    }
     if constexpr (sizeof(T) == 2) {
-      *reinterpret_cast<uint4*>(reinterpret_cast<T*>(p.dq) + 8 * i) = *reinterpret_cast<const uint4*>(out);
+      *reinterpret_cast<uint4*>(reinterpret_cast<T*>(p.dq) + dst) = *reinterpret_cast<const uint4*>(out);
     } else {
-      *reinterpret_cast<uint4*>(reinterpret_cast<T*>(p.dq) + 8 * i) = *reinterpret_cast<const uint4*>(out);
-      *reinterpret_cast<uint4*>(reinterpret_cast<T*>(p.dq) + 8 * i + 4) = *reinterpret_cast<const uint4*>(out + 4);
+      *reinterpret_cast<uint4*>(reinterpret_cast<T*>(p.dq) + dst) = *reinterpret_cast<const uint4*>(out);
+      *reinterpret_cast<uint4*>(reinterpret_cast<T*>(p.dq) + dst + 4) = *reinterpret_cast<const uint4*>(out + 4);
     }
   }
   if (blockIdx.x == 0 && p.dbeta) {
@@ -1047,40 +1065,45 @@ __global__ __launch_bounds__(256) void attn_bwd_post_kernel(AttnBwdParams p, siz
 }
 
 // bf16: the dK/dV kernel, then the dQ kernel (which writes dq itself).
-template <int D>
-static hipError_t launch_bwd_main_bf16(const AttnBwdParams& p, int mode, hipStream_t st) {
+template <int D, int LAYOUT>
+static hipError_t launch_bwd_main_bf16_l(const AttnBwdParams& p, int mode, hipStream_t st) {
   dim3 grid(p.B * p.H * ceil_div(p.T, BWD_BK)), block(256);
   dim3 qgrid(p.B * p.H, ceil_div(p.T, 128));
   switch (mode) {
     case MODE_INRANGE: {
       {
         KTimer t("attn_bwd_inrange", st);
-        if (p.log2n == 4) hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_INRANGE, 4>), grid, block, 0, st, p);
-        else hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_INRANGE, 0>), grid, block, 0, st, p);
+        if (p.log2n == 4) hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_INRANGE, 4, LAYOUT>), grid, block, 0, st, p);
+        else hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_INRANGE, 0, LAYOUT>), grid, block, 0, st, p);
       }
       KTimer t("attn_bwd_dq_inrange", st);
-      if (p.log2n == 4) hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE_INRANGE, 4>), qgrid, block, 0, st, p);
-      else hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE_INRANGE, 0>), qgrid, block, 0, st, p);
+      if (p.log2n == 4) hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE_INRANGE, 4, LAYOUT>), qgrid, block, 0, st, p);
+      else hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE_INRANGE, 0, LAYOUT>), qgrid, block, 0, st, p);
     } break;
     case MODE_CLIPPED: {
       {
         KTimer t("attn_bwd_clipped", st);
-        hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_CLIPPED, 0>), grid, block, 0, st, p);
+        hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_CLIPPED, 0, LAYOUT>), grid, block, 0, st, p);
       }
       KTimer t("attn_bwd_dq_clipped", st);
-      hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE_CLIPPED, 0>), qgrid, block, 0, st, p);
+      hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE_CLIPPED, 0, LAYOUT>), qgrid, block, 0, st, p);
     } break;
     case MODE_SHIFTED: {
       {
         KTimer t("attn_bwd_shifted", st);
-        hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_SHIFTED, 0>), grid, block, 0, st, p);
+        hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_SHIFTED, 0, LAYOUT>), grid, block, 0, st, p);
       }
       KTimer t("attn_bwd_dq_shifted", st);
-      hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE_SHIFTED, 0>), qgrid, block, 0, st, p);
+      hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE_SHIFTED, 0, LAYOUT>), qgrid, block, 0, st, p);
     } break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+template <int D>
+static hipError_t launch_bwd_main_bf16(const AttnBwdParams& p, int mode, hipStream_t st) {
+  return p.layout ? launch_bwd_main_bf16_l<D, 1>(p, mode, st) : launch_bwd_main_bf16_l<D, 0>(p, mode, st);
 }
 
 template <typename T, int D>
@@ -1125,8 +1148,8 @@ hipError_t launch_attn_bwd(const AttnBwdParams& p, int D, bool bf16_io, const in
   const int blocks = (int)std::max<size_t>(std::min<size_t>((total / 8 + 255) / 256, 16384), 1);
   {
     KTimer t("attn_bwd_post", st);
-    if (bf16_io) hipLaunchKernelGGL((attn_bwd_post_kernel<bf16>), dim3(blocks), dim3(256), 0, st, p, total, nblk);
-    else hipLaunchKernelGGL((attn_bwd_post_kernel<float>), dim3(blocks), dim3(256), 0, st, p, total, nblk);
+    if (bf16_io) hipLaunchKernelGGL((attn_bwd_post_kernel<bf16>), dim3(blocks), dim3(256), 0, st, p, total, nblk, D);
+    else hipLaunchKernelGGL((attn_bwd_post_kernel<float>), dim3(blocks), dim3(256), 0, st, p, total, nblk, D);
   }
   return hipGetLastError();
 }

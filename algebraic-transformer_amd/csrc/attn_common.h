@@ -26,6 +26,7 @@ struct AttnFwdParams {
   float clamp;         // CLIPPED: positive-score clamp
   int fast_rho;        // SHIFTED: fast rho for the weights
   int inv_stat;        // CLIPPED: 1 -> stat = 1/Z, 0 -> stat = Z^(-1/n)
+  int layout;          // storage of q, k, v, o (see head_base)
 };
 
 struct AttnBwdParams {
@@ -52,9 +53,25 @@ struct AttnBwdParams {
   int inv_stat;
   int mode;            // AttnMode selected by the host when flag is nullptr
   float dq_scale;      // chain-rule factor applied after the slope (alpha), or 1
+  int layout;          // storage of q, k, v, o, dO, dq, dk, dv (see head_base)
 };
 
 __host__ __device__ inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// Storage of the (B, ., ., D) tensors of a call (q, k, v, o, dO, dq, dk, dv): 0 = (B, H, T, D),
+// 1 = (B, T, H, D), the projection layout before the head transpose (model.py:167-169, 182).
+// Per-row vectors (stat, di) and the internal f32 buffers (o_precise, dq_acc) stay (B, H, T).
+// head_base is the element offset of position 0 of head bh = b*H + h; positions are
+// row_stride elements apart.
+__host__ __device__ inline size_t head_base(int bh, int H, int T, int D, int layout) {
+  if (!layout) return (size_t)bh * T * D;
+  const int b = bh / H, h = bh - b * H;
+  return ((size_t)b * T * H + h) * D;
+}
+__host__ __device__ inline int row_stride(int H, int D, int layout) { return layout ? H * D : D; }
+// Bytes from a head's base to the end of its last row (the range of a buffer descriptor whose
+// out-of-range rows read as zeros).
+__host__ __device__ inline int head_bytes(int T, int ld, int D, int esize) { return ((T - 1) * ld + D) * esize; }
 
 // Unpadded bf16 LDS tiles with CPR 16-byte chunks per row (CPR = 16 for 256-byte rows, 8 for
 // 128-byte rows). Chunk c of row r is stored at chunk c ^ swz_chunk<CPR>(r); the mask is
@@ -120,21 +137,23 @@ constexpr int F32_PAD = 4;
 // Instruction J covers rows RPI J + r (r = lane / CPR); its swizzle is swz(r) ^ swz(RPI J), so
 // every instruction's lane offset is one XOR of a per-lane chunk term with a wave-uniform
 // value: two per-lane registers serve all of them.
+// Both matrices have rows `ld` elements apart (ld = D for (B, H, T, D) storage, H*D for
+// (B, T, H, D)); the descriptors' ranges end at the head's last row (head_bytes).
 template <int D>
 __device__ __forceinline__ void tile_dma2(bf16* la, bf16* lb, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
-                                          int r0, int wave, int lane) {
+                                          int r0, int wave, int lane, int ld = D) {
   constexpr int CPR = D / 8, RPI = 64 / CPR, PW = 64 * CPR / 64 / 4;  // PW instructions per wave
   auto lla = LDS_PTR(bf16, la);
   auto llb = LDS_PTR(bf16, lb);
   asm volatile("" : "+s"(lla), "+s"(llb));
   const int r = lane / CPR;
-  int rowb = r * D * 2;                                         // per-lane row bytes
+  int rowb = r * ld * 2;                                        // per-lane row bytes
   int chunkb = 16 * ((lane % CPR) ^ swz_chunk<CPR>(r));         // per-lane chunk bytes
   asm volatile("" : "+v"(rowb), "+v"(chunkb));                  // computed here, not kept live
 #pragma unroll
   for (int j = 0; j < PW; ++j) {
     const int J = wave * PW + j;
-    const int voff = (r0 + RPI * J) * D * 2 + rowb + (chunkb ^ (16 * swz_chunk<CPR>(RPI * J)));
+    const int voff = (r0 + RPI * J) * ld * 2 + rowb + (chunkb ^ (16 * swz_chunk<CPR>(RPI * J)));
     __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, lla + J * 512, 16, voff, 0, 0, 0);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, llb + J * 512, 16, voff, 0, 0, 0);
   }
@@ -143,17 +162,18 @@ __device__ __forceinline__ void tile_dma2(bf16* la, bf16* lb, __amdgpu_buffer_rs
 // pipeline steps).
 template <int D>
 __device__ __forceinline__ void tile_dma2_part(bf16* la, bf16* lb, __amdgpu_buffer_rsrc_t ra,
-                                               __amdgpu_buffer_rsrc_t rb, int r0, int wave, int lane, int j) {
+                                               __amdgpu_buffer_rsrc_t rb, int r0, int wave, int lane, int j,
+                                               int ld = D) {
   constexpr int CPR = D / 8, RPI = 64 / CPR, PW = 64 * CPR / 64 / 4;
   auto lla = LDS_PTR(bf16, la);
   auto llb = LDS_PTR(bf16, lb);
   asm volatile("" : "+s"(lla), "+s"(llb));
   const int r = lane / CPR;
-  int rowb = r * D * 2;
+  int rowb = r * ld * 2;
   int chunkb = 16 * ((lane % CPR) ^ swz_chunk<CPR>(r));
   asm volatile("" : "+v"(rowb), "+v"(chunkb));
   const int J = wave * PW + j;
-  const int voff = (r0 + RPI * J) * D * 2 + rowb + (chunkb ^ (16 * swz_chunk<CPR>(RPI * J)));
+  const int voff = (r0 + RPI * J) * ld * 2 + rowb + (chunkb ^ (16 * swz_chunk<CPR>(RPI * J)));
   __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, lla + J * 512, 16, voff, 0, 0, 0);
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, llb + J * 512, 16, voff, 0, 0, 0);
 }

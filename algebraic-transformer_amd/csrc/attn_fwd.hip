@@ -39,13 +39,13 @@ struct KVTile {
   static constexpr int CH = 16 / sizeof(T);
   static constexpr int CPR = D / CH;
   static constexpr int PER = FWD_BK * CPR / 256;  // chunks per thread
-  static __device__ __forceinline__ void load(uint4 (&r)[PER], const T* src, int r0, int T_) {
+  static __device__ __forceinline__ void load(uint4 (&r)[PER], const T* src, int r0, int T_, int ld) {
 #pragma unroll
     for (int c = 0; c < PER; ++c) {
       const int idx = threadIdx.x + c * 256;
       const int row = idx / CPR, col = (idx - row * CPR) * CH;
       uint4 v = make_uint4(0, 0, 0, 0);
-      if (r0 + row < T_) v = *reinterpret_cast<const uint4*>(src + (size_t)(r0 + row) * D + col);
+      if (r0 + row < T_) v = *reinterpret_cast<const uint4*>(src + (size_t)(r0 + row) * ld + col);
       r[c] = v;
     }
   }
@@ -83,10 +83,12 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
   const int bh = blockIdx.x;
   const int qb = nqb - 1 - blockIdx.y;  // heaviest causal rows first
   const int head = bh % p.H;
-  const size_t base = (size_t)bh * T_ * D;
-  const T* Q = reinterpret_cast<const T*>(p.q) + base;
-  const T* K = reinterpret_cast<const T*>(p.k) + base;
-  const T* V = reinterpret_cast<const T*>(p.v) + base;
+  const size_t base = (size_t)bh * T_ * D;  // internal (B, H, T, D) buffers (o_precise)
+  const size_t hb = head_base(bh, p.H, T_, D, p.layout);
+  const int ld = row_stride(p.H, D, p.layout);
+  const T* Q = reinterpret_cast<const T*>(p.q) + hb;
+  const T* K = reinterpret_cast<const T*>(p.k) + hb;
+  const T* V = reinterpret_cast<const T*>(p.v) + hb;
   const int q0 = qb * FWD_BQ + wave * 32;
   const int myq = q0 + l32;
   const bool wave_live = q0 < T_;
@@ -99,10 +101,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
   for (int s = 0; s < NQF; ++s) {
     if constexpr (BF) {
       bf16x8 z = {};
-      qf[s] = myq < T_ ? ld8(reinterpret_cast<const bf16*>(Q) + (size_t)myq * D + 16 * s + 8 * h) : z;
+      qf[s] = myq < T_ ? ld8(reinterpret_cast<const bf16*>(Q) + (size_t)myq * ld + 16 * s + 8 * h) : z;
     } else {
       floatx4 z = {};
-      qf[s] = myq < T_ ? *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(Q) + (size_t)myq * D + 8 * s + 4 * h) : z;
+      qf[s] = myq < T_ ? *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(Q) + (size_t)myq * ld + 8 * s + 4 * h) : z;
     }
   }
 
@@ -213,8 +215,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
   // K/V tiles are double-buffered: the next tile's global loads are in flight while the
   // current tile is consumed; one barrier per tile.
   uint4 kr[KV::PER], vr[KV::PER];
-  KV::load(kr, K, 0, T_);
-  KV::load(vr, V, 0, T_);
+  KV::load(kr, K, 0, T_, ld);
+  KV::load(vr, V, 0, T_, ld);
   KV::store(Ks[0], PITCH, kr);
   KV::store(Vs[0], PITCH, vr);
   __syncthreads();
@@ -222,8 +224,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
     const int cur = kt & 1;
     const bool more = kt + 1 < ntiles;
     if (more) {
-      KV::load(kr, K, (kt + 1) * FWD_BK, T_);
-      KV::load(vr, V, (kt + 1) * FWD_BK, T_);
+      KV::load(kr, K, (kt + 1) * FWD_BK, T_, ld);
+      KV::load(vr, V, (kt + 1) * FWD_BK, T_, ld);
     }
     if (wave_live) {
       const int kb0 = kt * FWD_BK;
@@ -264,7 +266,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
   }
   const float scale = Z;
   if (myq < T_) {
-    T* O = reinterpret_cast<T*>(p.o) + base + (size_t)myq * D;
+    T* O = reinterpret_cast<T*>(p.o) + hb + (size_t)myq * ld;
     // o_precise carries the shifted branch's unrounded output only (flash.py:322).
     float* OP = (MODE == MODE_SHIFTED && p.o_precise) ? p.o_precise + base + (size_t)myq * D : nullptr;
 #pragma unroll
@@ -299,7 +301,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
 //   R3  O^T over keys 0..31 | weights of 32..63 (MFMA | VALU)
 //   R4  O^T over keys 32..63                    (MFMA)
 // The two tiles that cross this workgroup's diagonal evaluate the causal mask per element.
-template <int D, int L2N>
+template <int D, int L2N, int LAYOUT>
 __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) {
   static_assert(D == 64 || D == 128, "head_dim");
   constexpr int BK = FWD_BK, CPR = D / 8, NDB = D / 32, NF = D / 16;
@@ -316,25 +318,27 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) 
   const int bh = blockIdx.x;
   const int qb = nqb - 1 - blockIdx.y;  // heaviest causal rows first
   const int head = bh % p.H;
-  const size_t base = (size_t)bh * T_ * D;
+  const size_t base = head_base(bh, p.H, T_, D, LAYOUT);
+  const int ld = LAYOUT ? p.H * D : D;  // elements between positions
   const bf16* Q = reinterpret_cast<const bf16*>(p.q) + base;
   const bf16* K = reinterpret_cast<const bf16*>(p.k) + base;
   const bf16* V = reinterpret_cast<const bf16*>(p.v) + base;
-  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)K, (short)0, T_ * D * 2, BUF_RSRC_WORD3);
-  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)V, (short)0, T_ * D * 2, BUF_RSRC_WORD3);
+  const int nbytes = head_bytes(T_, ld, D, 2);
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)K, (short)0, nbytes, BUF_RSRC_WORD3);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)V, (short)0, nbytes, BUF_RSRC_WORD3);
   const int myq = qb * FWD_BQ + wave * 32 + l32;
   const int log2n = p.log2n;
   const int ntiles = min(qb * FWD_BQ + FWD_BQ - 1, T_ - 1) / BK + 1;  // key tiles up to the last query
 
-  tile_dma2<D>(Ks0, Vs0, rk, rv, 0, wave, lane);
-  if (ntiles > 1) tile_dma2<D>(Ks1, Vs1, rk, rv, BK, wave, lane);
+  tile_dma2<D>(Ks0, Vs0, rk, rv, 0, wave, lane, ld);
+  if (ntiles > 1) tile_dma2<D>(Ks1, Vs1, rk, rv, BK, wave, lane, ld);
   // Query fragments (B operand of S^T = K Q^T), held for the whole kernel.
   bf16x8 qf[NF];
   const bool live = myq < T_;
 #pragma unroll
   for (int s = 0; s < NF; ++s) {
     const bf16x8 z = {};
-    qf[s] = live ? ld8(Q + (size_t)myq * D + 16 * s + 8 * h) : z;
+    qf[s] = live ? ld8(Q + (size_t)myq * ld + 16 * s + 8 * h) : z;
   }
   floatx16 oacc[NDB];
 #pragma unroll
@@ -442,8 +446,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) 
       rk3[1] = ld8(Kn + row_off[1]);
     }
     if (kt + 2 < ntiles) {
-      if constexpr (BUF) tile_dma2<D>(Ks1, Vs1, rk, rv, kb0 + 2 * BK, wave, lane);
-      else tile_dma2<D>(Ks0, Vs0, rk, rv, kb0 + 2 * BK, wave, lane);
+      if constexpr (BUF) tile_dma2<D>(Ks1, Vs1, rk, rv, kb0 + 2 * BK, wave, lane, ld);
+      else tile_dma2<D>(Ks0, Vs0, rk, rv, kb0 + 2 * BK, wave, lane, ld);
     }
   };
 
@@ -465,7 +469,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) 
   float Z = lsum + xor32(lsum);
   if (p.sink) Z += pow2n<L2N>(rho_fast(p.sink[head]), log2n);
   const float inv = 1.0f / Z;
-  bf16* O = reinterpret_cast<bf16*>(p.o) + base + (size_t)myq * D;  // (o_precise: shifted only)
+  bf16* O = reinterpret_cast<bf16*>(p.o) + base + (size_t)myq * ld;  // (o_precise: shifted only)
 #pragma unroll
   for (int db = 0; db < NDB; ++db) {
 #pragma unroll
@@ -487,8 +491,13 @@ static hipError_t launch_fwd_mode(const AttnFwdParams& p, int mode, hipStream_t 
     case MODE_INRANGE: {
       KTimer t("attn_fwd_inrange", st);
       if constexpr (sizeof(T) == 2) {
-        if (p.log2n == 4) hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, 4>), grid, block, 0, st, p);
-        else hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, 0>), grid, block, 0, st, p);
+        if (p.layout) {
+          if (p.log2n == 4) hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, 4, 1>), grid, block, 0, st, p);
+          else hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, 0, 1>), grid, block, 0, st, p);
+        } else {
+          if (p.log2n == 4) hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, 4, 0>), grid, block, 0, st, p);
+          else hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, 0, 0>), grid, block, 0, st, p);
+        }
       } else {
         if (p.log2n == 4) hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_INRANGE, 4>), grid, block, 0, st, p);
         else hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_INRANGE, 0>), grid, block, 0, st, p);

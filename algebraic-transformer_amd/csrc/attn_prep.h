@@ -33,7 +33,7 @@ struct QkPrologueParams {
   const void* q; const void* k; const void* v;  // raw projections in `layout`
   const float* q_gain; const float* k_gain;     // (D,) or nullptr (no gain)
   const float* cos; const float* sin;           // (T, D/2) or nullptr (no rotation)
-  void* q_s; void* k_r;                         // (B, H, T, D) outputs
+  void* q_s; void* k_r;                         // outputs in `layout`
   float* tau_q; float* tau_k;                   // (B, H, T) 1/rms per row
   float* part;                                  // (nblocks, 3) guard maxima
   int B, H, T, D;
@@ -47,7 +47,7 @@ struct QkPrologueBwdParams {
   const float* q_gain; const float* k_gain;
   const float* cos; const float* sin;
   const float* tau_q; const float* tau_k;
-  const void* dq_r; const void* dk_r;           // (B, H, T, D) cotangents of the rotated rows
+  const void* dq_r; const void* dk_r;           // cotangents of the rotated rows, in `layout`
   void* dq; void* dk;                           // outputs in `layout`
   float* gpart;                                 // (2, D, nblocks) gain-gradient partials
   int B, H, T, D;

@@ -7,9 +7,10 @@
 // flash.py:823-849 (q_s = round(q alpha), guard maxima), and the Cayley tables of
 // algebraic.py:124-169.
 //
-// Rows are (b, h, t) in (B, H, T, D) order on output. The raw projections may be stored
-// (B, H, T, D) or (B, T, H, D) (the projection layout before the head transpose,
-// model.py:167-169). A row of D elements is split between D/(2 CH) lanes; lane li holds the
+// The raw projections and every (B, ., ., D) output (q_s, k_r; dq, dk and the cotangents in the
+// VJP) are stored (B, H, T, D) or (B, T, H, D) (the projection layout before the head
+// transpose, model.py:167-169); the per-row 1/rms vectors are (B, H, T). A row of D elements
+// is split between D/(2 CH) lanes; lane li holds the
 // 16-byte chunk li of both halves, so the rotate-half pairs (x_j, x_{j+D/2}) sit in one lane
 // and only the row's sum of squares crosses lanes.
 //
@@ -46,21 +47,20 @@ __device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, 
 constexpr int PRO_ITER = PRO_ITER_N;
 
 struct RowAddr {
-  size_t in_base, out_base;  // element offsets of position 0 of this head
-  size_t in_stride;          // elements between consecutive positions in the input layout
+  size_t base;    // element offset of position 0 of this head
+  size_t stride;  // elements between consecutive positions
 };
 
 __device__ __forceinline__ RowAddr head_rows(int H, int T, int D, int layout) {
   const int bh = blockIdx.x;
   const int b = bh / H, h = bh - b * H;
   RowAddr a;
-  a.out_base = (size_t)bh * T * D;
   if (layout == 0) {
-    a.in_base = a.out_base;
-    a.in_stride = D;
+    a.base = (size_t)bh * T * D;
+    a.stride = D;
   } else {
-    a.in_base = ((size_t)b * T * H + h) * D;
-    a.in_stride = (size_t)H * D;
+    a.base = ((size_t)b * T * H + h) * D;
+    a.stride = (size_t)H * D;
   }
   return a;
 }
@@ -190,7 +190,7 @@ __global__ __launch_bounds__(256) void attn_qk_prologue_kernel(QkPrologueParams 
       const int t = t0 + 4 * RPW * (j + u);
       ok[u] = t < p.T;
       tt[u] = ok[u] ? t : p.T - 1;
-      const size_t in = ra.in_base + (size_t)tt[u] * ra.in_stride + c0;
+      const size_t in = ra.base + (size_t)tt[u] * ra.stride + c0;
       rq[u][0] = ld16<T>(p.q, in);
       rq[u][1] = ld16<T>(p.q, in + HALF);
       rk[u][0] = ld16<T>(p.k, in);
@@ -241,7 +241,7 @@ __global__ __launch_bounds__(256) void attn_qk_prologue_kernel(QkPrologueParams 
       sq = row_sum<LPR>(sq);
       sk = row_sum<LPR>(sk);
       if (ok[u]) {
-        const size_t out = ra.out_base + (size_t)tt[u] * D + c0;
+        const size_t out = ra.base + (size_t)tt[u] * ra.stride + c0;
         store_chunk<T, CH>(p.q_s, out, qa);
         store_chunk<T, CH>(p.q_s, out + HALF, qb);
         store_chunk<T, CH>(p.k_r, out, ka);
@@ -338,8 +338,8 @@ __global__ __launch_bounds__(256) void attn_qk_prologue_bwd_kernel(QkPrologueBwd
       const int t = t0 + 4 * RPW * (j + u);
       ok[u] = t < p.T;
       const int tc = ok[u] ? t : p.T - 1;
-      in[u] = ra.in_base + (size_t)tc * ra.in_stride + c0;
-      const size_t gr = ra.out_base + (size_t)tc * D + c0;
+      in[u] = ra.base + (size_t)tc * ra.stride + c0;
+      const size_t gr = in[u];
       rxq[u][0] = ld16<T>(p.q, in[u]);
       rxq[u][1] = ld16<T>(p.q, in[u] + HALF);
       rxk[u][0] = ld16<T>(p.k, in[u]);

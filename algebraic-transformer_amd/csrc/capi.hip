@@ -58,6 +58,16 @@ int check_attn_shape(int dtype, int B, int H, int T, int D) {
   return ALG_OK;
 }
 
+// Layout check: with (B, T, H, D) storage a head's rows are H*D elements apart, and one head's
+// rows are addressed with 32-bit byte offsets.
+int check_layout(int layout, int H, int T, int D) {
+  if (layout != ALG_LAYOUT_BHTD && layout != ALG_LAYOUT_BTHD) return fail(ALG_ERR_INVALID, "unknown layout %d", layout);
+  const double ld = layout == ALG_LAYOUT_BTHD ? (double)H * D : (double)D;
+  if ((T + 64.0) * ld * 4 >= 2147483648.0)
+    return fail(ALG_ERR_UNSUPPORTED, "T = %d with H = %d: one head's rows exceed 32-bit offsets in this layout", T, H);
+  return ALG_OK;
+}
+
 int check_n(int n) {
   const int k = log2_pow2(n);
   if (k < 1 || k > 6) return fail(ALG_ERR_INVALID, "asinh kernel needs n to be a power of two in [2, 64] (got %d)", n);
@@ -157,7 +167,7 @@ int check_prologue(int dtype, int layout, int B, int H, int T, int D, const floa
                    float eps) {
   int rc = check_attn_shape(dtype, B, H, T, D);
   if (rc) return rc;
-  if (layout != ALG_LAYOUT_BHTD && layout != ALG_LAYOUT_BTHD) return fail(ALG_ERR_INVALID, "unknown layout %d", layout);
+  if ((rc = check_layout(layout, H, T, D))) return rc;
   if ((cos_t == nullptr) != (sin_t == nullptr)) return fail(ALG_ERR_INVALID, "cos and sin are given together");
   if (!(eps > 0.0f) || !std::isfinite(eps)) return fail(ALG_ERR_INVALID, "eps must be positive and finite");
   return ALG_OK;
@@ -267,11 +277,12 @@ int alg_attn_qk_prologue_bwd(alg_stream_t stream, int dtype, int layout, int B, 
                     "alg_attn_qk_prologue_bwd");
 }
 
-int alg_attn_fwd(alg_stream_t stream, int dtype, int B, int H, int T, int D, const void* q_s, const void* k,
-                 const void* v, const float* sink_scaled, int n, int variant, const int* guard_flag, float clamp,
-                 int fast_rho, int inv_stat, void* o, float* o_precise, float* stat) {
+int alg_attn_fwd(alg_stream_t stream, int dtype, int layout, int B, int H, int T, int D, const void* q_s,
+                 const void* k, const void* v, const float* sink_scaled, int n, int variant, const int* guard_flag,
+                 float clamp, int fast_rho, int inv_stat, void* o, float* o_precise, float* stat) {
   int rc = check_attn_shape(dtype, B, H, T, D);
   if (rc) return rc;
+  if ((rc = check_layout(layout, H, T, D))) return rc;
   if ((rc = check_n(n))) return rc;
   if (!q_s || !k || !v || !o || !stat) return fail(ALG_ERR_INVALID, "q_s, k, v, o and stat are required");
   if (variant < ALG_ATTN_INRANGE || variant > ALG_ATTN_GUARDED) return fail(ALG_ERR_INVALID, "unknown variant %d", variant);
@@ -283,6 +294,7 @@ int alg_attn_fwd(alg_stream_t stream, int dtype, int B, int H, int T, int D, con
   p.B = B; p.H = H; p.T = T;
   p.log2n = log2_pow2(n);
   p.clamp = clamp; p.fast_rho = fast_rho; p.inv_stat = inv_stat;
+  p.layout = layout;
   const bool bf = dtype == ALG_DTYPE_BF16;
   hipStream_t st = (hipStream_t)stream;
   if (variant == ALG_ATTN_GUARDED) {
@@ -295,13 +307,14 @@ int alg_attn_fwd(alg_stream_t stream, int dtype, int B, int H, int T, int D, con
   return hip_status(alg::launch_attn_fwd(p, D, bf, variant, st), "alg_attn_fwd");
 }
 
-int alg_attn_bwd(alg_stream_t stream, int dtype, int B, int H, int T, int D, const void* q_s, const void* k,
-                 const void* v, const float* sink_scaled, const void* o, const float* o_precise, const float* stat,
-                 const void* dO, int n, int variant, const int* guard_flag, float clamp, int fast_rho, int inv_stat,
-                 float dq_scale, void* dq, void* dk, void* dv, float* di, float* dsink_scaled, void* workspace,
-                 size_t workspace_bytes) {
+int alg_attn_bwd(alg_stream_t stream, int dtype, int layout, int B, int H, int T, int D, const void* q_s,
+                 const void* k, const void* v, const float* sink_scaled, const void* o, const float* o_precise,
+                 const float* stat, const void* dO, int n, int variant, const int* guard_flag, float clamp,
+                 int fast_rho, int inv_stat, float dq_scale, void* dq, void* dk, void* dv, float* di,
+                 float* dsink_scaled, void* workspace, size_t workspace_bytes) {
   int rc = check_attn_shape(dtype, B, H, T, D);
   if (rc) return rc;
+  if ((rc = check_layout(layout, H, T, D))) return rc;
   if ((rc = check_n(n))) return rc;
   if (!q_s || !k || !v || !o || !stat || !dO || !dq || !dk || !dv || !di)
     return fail(ALG_ERR_INVALID, "q_s, k, v, o, stat, dO, dq, dk, dv and di are required");
@@ -323,6 +336,7 @@ int alg_attn_bwd(alg_stream_t stream, int dtype, int B, int H, int T, int D, con
   p.clamp = clamp; p.fast_rho = fast_rho; p.inv_stat = inv_stat;
   p.mode = variant == ALG_ATTN_GUARDED ? alg::MODE_INRANGE : variant;
   p.dq_scale = dq_scale;
+  p.layout = layout;
   const bool bf = dtype == ALG_DTYPE_BF16;
   hipStream_t st = (hipStream_t)stream;
   if (variant == ALG_ATTN_GUARDED) {

@@ -244,6 +244,24 @@ def time_prologue(torch, dev, iters=20, warmup=3, seed=2):
             "peak_gbs": PEAK_HBM_GBS, "fwd_frac": round(fg / PEAK_HBM_GBS, 4), "bwd_frac": round(bg / PEAK_HBM_GBS, 4)}
 
 
+def time_layout_bthd(torch, x, steps, warmup):
+    """The headline attention step with q, k, v, dO stored (B, T, H, D) (the projection
+    layout; o comes back as the (B, T, H*D) input of the output projection with no copy)."""
+    from algebraic_amd.kernels.flash import flash_attention
+    t = lambda a: a.detach().permute(0, 2, 1, 3).contiguous()
+    q, k, v = (t(x[n]).requires_grad_(True) for n in ("q", "k", "v"))
+    do = t(x["do"])
+
+    def step():
+        o = flash_attention(q, k, v, x["sink"], kind="asinh", n=ATTN["n"], c=ATTN["c"], block=512,
+                            range_guard=True, layout="bthd")
+        return torch.autograd.grad(o, (q, k, v, x["sink"]), do)
+    s = timed(torch, step, steps, warmup)
+    fa = attn_flops(**ATTN) * 3.5
+    return {"workload": "C4a attention fwd+bwd with q, k, v, o, dO, dq, dk, dv in (B, T, H, D)",
+            "ms": round(s * 1e3, 4), "tflops": round(fa / s / 1e12, 3)}
+
+
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` recorded from rocprofv3 FETCH_SIZE + WRITE_SIZE runs
     (each scaled by the same counter's reading for a device copy of known size), as listed
@@ -428,6 +446,8 @@ def main():
         log("timing the other BASELINE configs (C1, C2, C3, C5)")
         out["other_configs"] = time_other_configs(torch, dev)
         out["prologue"] = time_prologue(torch, dev)
+        out["layout_bthd"] = time_layout_bthd(torch, x, K, 1)
+        out["layout_bthd"]["vs_bhtd"] = round(out["attn"]["ms"] / out["layout_bthd"]["ms"], 4)
     if not args.no_cpu_baseline:
         log("timing the CPU baseline sample")
         out["cpu_baseline"] = cpu_baseline()

@@ -9,7 +9,8 @@
  * Return value: ALG_OK or an error code; alg_last_error() describes the last failure on
  * the calling thread.
  *
- * Tensor layouts are row-major: attention (B, H, T, D); head h (N, d), E (V, d).
+ * Tensor layouts are row-major: attention (B, H, T, D) or (B, T, H, D) (the `layout`
+ * argument); head h (N, d), E (V, d).
  * Reference interfaces replaced (paths relative to the reference repository root):
  *   src/algebraic/kernels/flash.py       flash_attention 763-857, _forward 292-326,
  *                                        _backward 630-687, _flash_bwd 718-726
@@ -41,8 +42,10 @@ enum {
 
 enum { ALG_DTYPE_BF16 = 0, ALG_DTYPE_F32 = 1 };
 
-/* Storage of the raw attention projections for the fused prologue: (B, H, T, D), or the
- * projection layout (B, T, H, D) before the head transpose of model.py:167-169. */
+/* Storage of the (B, ., ., D) tensors of an attention call (q, k, v, o, dO, dq, dk, dv and the
+ * prologue's outputs): (B, H, T, D), the reference's layout, or the projection layout
+ * (B, T, H, D) that model.py:167-169 transposes away and model.py:182 transposes back; with it
+ * o reads as (B, T, H*D) with no copy. Per-row vectors (stat, di, tau) are (B, H, T). */
 enum { ALG_LAYOUT_BHTD = 0, ALG_LAYOUT_BTHD = 1 };
 
 /* Attention variants (flash.py:59-73, 732-760, 850-852).
@@ -63,7 +66,8 @@ size_t alg_attn_workspace_size(int B, int H, int T, int D);
  * (sink_logit may be NULL; sink_count is 1 or H); guard_flag = 1 when
  *   max||q_s||^2 max||k||^2 <= (bound/1.01)^2, max|sink/c| <= bound/1.01 and
  *   max|v| <= min(1e8, 1e37/((T+has_sink)(2 bound+1)^n)), bound = min(16, clamp/2),
- * else 0; with range_guard = 0 the flag is set to 1 and k, v are not read. */
+ * else 0; with range_guard = 0 the flag is set to 1 and k, v are not read. The pass is
+ * elementwise over rows, so q_s has q's layout, whichever of the two it is. */
 int alg_attn_prepare(alg_stream_t stream, int dtype, int B, int H, int T, int D,
                      const void* q, const void* k, const void* v,
                      const float* sink_logit, int sink_count, float c, int n, int range_guard,
@@ -71,11 +75,11 @@ int alg_attn_prepare(alg_stream_t stream, int dtype, int B, int H, int T, int D,
                      void* workspace, size_t workspace_bytes);
 
 /* Forward, flash.py:189-326 / head_resident.py:25-89 (kernel contract of _forward):
- * in q_s, k, v (B,H,T,D) and sink_scaled (H) f32 or NULL; out o (B,H,T,D) in the input
+ * in q_s, k, v (in `layout`) and sink_scaled (H) f32 or NULL; out o (in `layout`) in the input
  * dtype and stat (B,H,T) f32 (1/Z, or rho(-m) Z^(-1/n) when shifted, or Z^(-1/n) when
  * CLIPPED with inv_stat = 0). o_precise (f32, optional) receives the unrounded output of
  * the SHIFTED branch (precise_output, flash.py:322). guard_flag is read for GUARDED. */
-int alg_attn_fwd(alg_stream_t stream, int dtype, int B, int H, int T, int D,
+int alg_attn_fwd(alg_stream_t stream, int dtype, int layout, int B, int H, int T, int D,
                  const void* q_s, const void* k, const void* v, const float* sink_scaled,
                  int n, int variant, const int* guard_flag, float clamp, int fast_rho, int inv_stat,
                  void* o, float* o_precise, float* stat);
@@ -83,9 +87,10 @@ int alg_attn_fwd(alg_stream_t stream, int dtype, int B, int H, int T, int D,
 /* Backward, flash.py:333-361, 515-687, 694-726 / head_resident.py:91-119:
  * in the forward residuals and dO; out dq = round(round(n * dq_s_acc) * dq_scale)
  * (dq_scale = 1 gives the kernel's dq_s; = 1/(sqrt(D) c) chains back to q), dk, dv in the
- * input dtype, di (B,H,T) f32 = sum_d dO*o and dsink_scaled (H) f32 = dL/d(sink/c)
+ * input dtype and `layout` (as are q_s, k, v, o, dO), di (B,H,T) f32 = sum_d dO*o and
+ * dsink_scaled (H) f32 = dL/d(sink/c)
  * (may be NULL). o_precise is used for di when the SHIFTED branch ran, if given. */
-int alg_attn_bwd(alg_stream_t stream, int dtype, int B, int H, int T, int D,
+int alg_attn_bwd(alg_stream_t stream, int dtype, int layout, int B, int H, int T, int D,
                  const void* q_s, const void* k, const void* v, const float* sink_scaled,
                  const void* o, const float* o_precise, const float* stat, const void* dO,
                  int n, int variant, const int* guard_flag, float clamp, int fast_rho, int inv_stat,
@@ -109,8 +114,8 @@ size_t alg_attn_prologue_workspace_size(int B, int H, int T, int D);
  *   tau = 1/sqrt(mean(x^2) + eps) per row (written to tau_q / tau_k for the backward),
  *   alpha = 1/(sqrt(D) c); the guard flag and sink_scaled exactly as alg_attn_prepare
  *   (the guard's ||q_s||^2 and ||k||^2 maxima are taken over q_s and k_r).
- * q, k, v are read in `layout`; q_s and k_r are written (B, H, T, D) for alg_attn_fwd /
- * alg_attn_bwd. Gains (D) f32 may be NULL (no gain); cos/sin (T, D/2) f32 may both be NULL
+ * q, k, v are read and q_s, k_r written in `layout`, the layout alg_attn_fwd / alg_attn_bwd
+ * then take. Gains (D) f32 may be NULL (no gain); cos/sin (T, D/2) f32 may both be NULL
  * (no rotation); the tables are rounded to the input dtype before use, like the reference. */
 int alg_attn_qk_prologue(alg_stream_t stream, int dtype, int layout, int B, int H, int T, int D,
                          const void* q, const void* k, const void* v,
@@ -120,7 +125,7 @@ int alg_attn_qk_prologue(alg_stream_t stream, int dtype, int layout, int B, int 
                          void* workspace, size_t workspace_bytes);
 
 /* VJP of the fused prologue's normalisation and rotation (JAX autodiff of
- * algebraic.py:76-83 and 172-179): dq_r, dk_r (B, H, T, D) are the cotangents of the rotated
+ * algebraic.py:76-83 and 172-179): dq_r, dk_r (in `layout`) are the cotangents of the rotated
  * rows (alg_attn_bwd's dq with dq_scale = alpha, and its dk); out dq, dk in `layout` and the
  * gain gradients dq_gain, dk_gain (D) f32 (summed over all rows; NULL to skip). */
 int alg_attn_qk_prologue_bwd(alg_stream_t stream, int dtype, int layout, int B, int H, int T, int D,

@@ -62,13 +62,20 @@ def test_invalid_arguments_fail_before_launch():
     handle = lib()
     P = ctypes.c_void_p
     # D = 96 is not built; no pointer is touched before validation.
-    rc = handle.alg_attn_fwd(None, 0, 1, 1, 64, 96, P(16), P(16), P(16), None, 16, 3, P(16), 0.0, 1, 1,
+    rc = handle.alg_attn_fwd(None, 0, 0, 1, 1, 64, 96, P(16), P(16), P(16), None, 16, 3, P(16), 0.0, 1, 1,
                              P(16), None, P(16))
     assert rc == _lib.ALG_ERR_UNSUPPORTED
     assert b"head_dim" in handle.alg_last_error()
-    rc = handle.alg_attn_fwd(None, 0, 1, 1, 64, 64, P(16), P(16), P(16), None, 12, 0, None, 0.0, 1, 1,
+    rc = handle.alg_attn_fwd(None, 0, 0, 1, 1, 64, 64, P(16), P(16), P(16), None, 12, 0, None, 0.0, 1, 1,
                              P(16), None, P(16))
     assert rc == _lib.ALG_ERR_INVALID and b"power of two" in handle.alg_last_error()
+    rc = handle.alg_attn_fwd(None, 0, 2, 1, 1, 64, 64, P(16), P(16), P(16), None, 16, 0, None, 0.0, 1, 1,
+                             P(16), None, P(16))
+    assert rc == _lib.ALG_ERR_INVALID and b"layout" in handle.alg_last_error()
+    # (B, T, H, D): one head's rows must stay within 32-bit byte offsets.
+    rc = handle.alg_attn_fwd(None, 0, 1, 1, 256, 1 << 16, 128, P(16), P(16), P(16), None, 16, 0, None, 0.0, 1, 1,
+                             P(16), None, P(16))
+    assert rc == _lib.ALG_ERR_UNSUPPORTED and b"layout" in handle.alg_last_error()
     rc = handle.alg_head_fwd(None, 128, 100, 1000, P(16), P(16), P(16), 8, 2.0, P(16), P(16), P(16), P(16),
                              None, P(16), 1 << 30)  # d = 100: rows not 16-byte aligned
     assert rc == _lib.ALG_ERR_UNSUPPORTED and b"d_model" in handle.alg_last_error()

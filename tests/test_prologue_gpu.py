@@ -118,10 +118,11 @@ def _lib():
 
 
 def _prologue_abi(q, k, v, gq, gk, cs, sn, layout, B, H, T, D, sink=None):
-    """Forward prologue through the C ABI on device tensors stored in `layout`."""
+    """Forward prologue through the C ABI on device tensors stored in `layout` (q_s and k_r
+    come back in it too)."""
     L, lib = _lib()
     dt = L.DTYPE_BF16 if q.dtype == torch.bfloat16 else L.DTYPE_F32
-    q_s = torch.empty((B, H, T, D), dtype=q.dtype, device="cuda")
+    q_s = torch.empty_like(q)
     k_r = torch.empty_like(q_s)
     tau_q = torch.empty((B, H, T), dtype=torch.float32, device="cuda")
     tau_k = torch.empty_like(tau_q)
@@ -173,11 +174,13 @@ def test_prologue_layouts_agree_bitwise(dtype):
     cs, sn = cayley_powers(w, T)
     a = _prologue_abi(q, k, v, gq, gk, cs, sn, L.LAYOUT_BHTD, B, H, T, D)
     b = _prologue_abi(_bthd(q), _bthd(k), _bthd(v), gq, gk, cs, sn, L.LAYOUT_BTHD, B, H, T, D)
-    for x, y in zip(a, b):
+    assert torch.equal(_bthd(a[0]), b[0]) and torch.equal(_bthd(a[1]), b[1])  # q_s, k_r in the layout
+    for x, y in zip(a[2:], b[2:]):  # 1/rms rows (B, H, T) and the guard flag
         assert torch.equal(x, y)
     dq_r, dk_r = rn(B, H, T, D).to(dtype), rn(B, H, T, D).to(dtype)
     da = _prologue_bwd_abi(q, k, gq, gk, cs, sn, a[2], a[3], dq_r, dk_r, L.LAYOUT_BHTD, B, H, T, D)
-    db = _prologue_bwd_abi(_bthd(q), _bthd(k), gq, gk, cs, sn, b[2], b[3], dq_r, dk_r, L.LAYOUT_BTHD, B, H, T, D)
+    db = _prologue_bwd_abi(_bthd(q), _bthd(k), gq, gk, cs, sn, b[2], b[3], _bthd(dq_r), _bthd(dk_r),
+                           L.LAYOUT_BTHD, B, H, T, D)
     assert torch.equal(_bthd(da[0]), db[0]) and torch.equal(_bthd(da[1]), db[1])
     assert torch.equal(da[2], db[2]) and torch.equal(da[3], db[3])
 
@@ -222,13 +225,14 @@ def test_prologue_full_size_c4a():
                                                  L.LAYOUT_BTHD, B, H, T, D)
     r_qs, r_kr, _, r_tq, r_tk = OP.prologue_forward(q, k, gq, gk, cos, sin, c=C_ATTN, dtype="bf16")
     np_ = lambda t: t.float().cpu().numpy()
+    q_s, k_r = q_s.permute(0, 2, 1, 3), k_r.permute(0, 2, 1, 3)  # (B, T, H, D) -> (B, H, T, D)
     errs = {"q_s": rel_l2(np_(q_s), r_qs), "k_r": rel_l2(np_(k_r), r_kr),
             "tau_q": rel_l2(np_(tau_q), r_tq), "tau_k": rel_l2(np_(tau_k), r_tk)}
     print(f"  forward: {errs}", flush=True)
     assert max(errs.values()) < 1e-3, errs
     assert int(flag.item()) == int(OA.guard_in_range(r_qs, r_kr, v, np.zeros(1, np.float32), has_sink=False))
     dq, dk, dgq, dgk = _prologue_bwd_abi(_bthd(tq), _bthd(tk), f(gq), f(gk), f(cos), f(sin), tau_q, tau_k,
-                                         dev(dq_r), dev(dk_r), L.LAYOUT_BTHD, B, H, T, D)
+                                         _bthd(dev(dq_r)), _bthd(dev(dk_r)), L.LAYOUT_BTHD, B, H, T, D)
     r_dq, r_dk, r_dgq, r_dgk = OP.prologue_backward(q, k, gq, gk, cos, sin, r_tq, r_tk, dq_r, dk_r, dtype="bf16")
     errs = {"dq": rel_l2(np_(dq).transpose(0, 2, 1, 3), r_dq), "dk": rel_l2(np_(dk).transpose(0, 2, 1, 3), r_dk),
             "dq_gain": rel_l2(np_(dgq), r_dgq), "dk_gain": rel_l2(np_(dgk), r_dgk)}
