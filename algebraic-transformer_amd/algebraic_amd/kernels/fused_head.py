@@ -106,3 +106,37 @@ def fused_head(h, embed, targets, *, kind="ce", n=16, c=16.0, block_n=128, block
         raise RuntimeError("fused_head needs GPU tensors (no CPU fallback)")
     obj, tel = _HeadFn.apply(h, embed, targets, int(n), float(c))
     return obj, tel.detach()
+
+
+@torch.no_grad()
+def head_logprob(h, embed, targets, *, head="alg_ce", n=8, c=2.0, argmax=True):
+    """Per-token ``log p(target)`` with the vocabulary streamed (no (N, V) logits), and the
+    argmax token: the scorer's head (src/algebraic/benchmarking.py:178-188) with
+    ``logprob_from_logits`` (src/algebraic/evaluation.py:13-23) for ``head="alg_ce"``.
+
+    ``h`` (N, d) bfloat16, ``embed`` (V, d), ``targets`` (N,). Returns ``(logprob, argmax)``:
+    float32 (N,) and int64 (N,) (``None`` when ``argmax=False``). Forward only.
+    """
+    if head == "ce":
+        raise NotImplementedError("head='ce' is the softmax control arm; only head='alg_ce' is built for MI355X")
+    if head != "alg_ce":
+        raise ValueError(f"unknown head {head!r}")
+    if n & (n - 1):
+        raise ValueError("n must be a power of two")
+    if h.dtype != torch.bfloat16:
+        raise NotImplementedError(f"hidden dtype {h.dtype}: the gfx950 head takes bfloat16 hidden states")
+    if not h.is_cuda:
+        raise RuntimeError("head_logprob needs GPU tensors (no CPU fallback)")
+    lib = _lib.load()
+    N, d = h.shape
+    V = embed.shape[0]
+    h = h.contiguous()
+    E = embed.to(h.dtype).contiguous()  # the cast of fused_head.py:168
+    t = targets.to(device=h.device, dtype=torch.int32).contiguous()
+    logprob = torch.empty(N, dtype=torch.float32, device=h.device)
+    am = torch.empty(N, dtype=torch.int32, device=h.device) if argmax else None
+    nbytes = lib.alg_head_workspace_size(N, d, V, 3)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=h.device)
+    _lib.check(lib.alg_head_eval(_lib.stream_of(h), N, d, V, _lib.ptr(h), _lib.ptr(E), _lib.ptr(t), int(n), float(c),
+                                 _lib.ptr(logprob), _lib.ptr(am), _lib.ptr(ws), nbytes), "head_logprob")
+    return logprob, (am.long() if argmax else None)

@@ -115,6 +115,20 @@ HeadWs head_ws(int N, int d, int V, int pass, bool residual) {
   return w;
 }
 
+// Eval workspace: [row-sum partials f32 nvt*N][tile maxima f32 nvt*N][their indices i32 nvt*N].
+struct HeadEvalWs {
+  size_t partial, pmax, pidx, total;
+};
+HeadEvalWs head_eval_ws(int N, int V) {
+  const size_t cells = (size_t)alg::head_vocab_tiles(V) * N;
+  HeadEvalWs w;
+  w.partial = 0;
+  w.pmax = align256(cells * sizeof(float));
+  w.pidx = w.pmax + align256(cells * sizeof(float));
+  w.total = w.pidx + align256(cells * sizeof(int));
+  return w;
+}
+
 int check_head(int N, int d, int V, int n, float c) {
   if (N <= 0 || d <= 0 || V <= 0) return fail(ALG_ERR_INVALID, "N, d, V must be positive (got %d, %d, %d)", N, d, V);
   if (d % 8) return fail(ALG_ERR_UNSUPPORTED, "d_model %d: head rows must be 16-byte aligned (d %% 8 == 0)", d);
@@ -352,7 +366,8 @@ int alg_attn_bwd(alg_stream_t stream, int dtype, int layout, int B, int H, int T
 
 size_t alg_head_workspace_size(int N, int d, int V, int pass) {
   if (N <= 0 || d <= 0 || V <= 0) return 0;
-  // pass 0: forward; 1: backward without a residual; 2: backward with a residual
+  // pass 0: forward; 1: backward without a residual; 2: backward with a residual; 3: eval
+  if (pass == 3) return head_eval_ws(N, V).total;
   return head_ws(N, d, V, pass ? 1 : 0, pass == 2).total;
 }
 
@@ -395,6 +410,27 @@ int alg_head_fwd(alg_stream_t stream, int N, int d, int V, const void* h, const 
     p.lsum = reinterpret_cast<float*>(static_cast<char*>(residual) + ws.res_l);
   }
   return hip_status(alg::launch_head_fwd(p, (hipStream_t)stream), "alg_head_fwd");
+}
+
+int alg_head_eval(alg_stream_t stream, int N, int d, int V, const void* h, const void* E, const int32_t* targets,
+                  int n, float c, float* logprob, int32_t* argmax, void* workspace, size_t workspace_bytes) {
+  int rc = check_head(N, d, V, n, c);
+  if (rc) return rc;
+  if (!h || !E || !targets || !logprob) return fail(ALG_ERR_INVALID, "null argument");
+  const HeadEvalWs ws = head_eval_ws(N, V);
+  if (!workspace || workspace_bytes < ws.total)
+    return fail(ALG_ERR_INVALID, "workspace too small: need %zu bytes", ws.total);
+  const HeadWs hw = head_ws(N, d, V, 0, false);
+  alg::HeadParams p = head_params(N, d, V, h, E, targets, n, c, workspace, hw);
+  char* w = static_cast<char*>(workspace);
+  p.partial = reinterpret_cast<float*>(w + ws.partial);
+  p.pmax = reinterpret_cast<float*>(w + ws.pmax);
+  p.pidx = reinterpret_cast<int*>(w + ws.pidx);
+  p.obj_part = nullptr;
+  p.zt = reinterpret_cast<float*>(logprob);  // the target logit is staged in the output
+  p.logprob = logprob;
+  p.argmax = argmax;
+  return hip_status(alg::launch_head_eval(p, (hipStream_t)stream), "alg_head_eval");
 }
 
 int alg_head_bwd(alg_stream_t stream, int N, int d, int V, const void* h, const void* E, const int32_t* targets,

@@ -179,6 +179,96 @@ __global__ __launch_bounds__(NT, 1) void head_fwd_kernel(HeadParams p) {
   }
 }
 
+// Evaluation head (src/algebraic/evaluation.py:13-23 with the argmax of
+// src/algebraic/benchmarking.py:178-188): z^T = E h^T as in the forward, the epilogue keeps
+// the per-token partial sums of w, the target logit, and the tile's largest logit with its
+// smallest vocabulary index. Nothing else is stored; head_eval_stats_kernel finishes.
+template <int L2N>
+__global__ __launch_bounds__(NT, 1) void head_eval_kernel(HeadParams p) {
+  __shared__ __attribute__((aligned(16))) GemmStage<KMAJOR, KMAJOR, HC> s0, s1;
+  __shared__ float red[HC::WM][HT_N];
+  __shared__ float redm[HC::WM][HT_N];
+  __shared__ int redi[HC::WM][HT_N];
+  const int nbm = (p.V + HT_M - 1) / HT_M, nbn = p.Npad / HT_N;
+  int tm, tn;
+  xcd_tile(blockIdx.x, nbm, nbn, tm, tn);
+  const int m0 = tm * HT_M;  // vocab
+  const int n0 = tn * HT_N;  // tokens
+  GemmOperand A{p.E, p.d, p.V, p.d, (long)p.V * p.d}, B{p.h, p.d, p.N, p.d, (long)p.N * p.d};
+  floatx16 acc[HC::MB][HC::NB];
+  gemm_mainloop<KMAJOR, KMAJOR, HC>(s0, s1, A, B, m0, n0, 0, p.d, acc);
+  const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  int wm, wn;
+  wave_coords<HC>(wm, wn);
+  const float inv_c = p.inv_c, clamp = p.clamp;
+  const int vrow0 = m0 + wm * HC::WTM;
+#pragma unroll
+  for (int nb = 0; nb < HC::NB; ++nb) {
+    const int col = wn * HC::WTN + nb * 32 + l32;
+    const int tok = n0 + col;
+    const int tgt = tok < p.N ? p.targets[tok] : -1;
+    float part = 0.0f, zm = -INFINITY;
+    int im = 0x7fffffff;
+    // This lane's vocabulary rows increase with (mb, i), so a strict comparison keeps the
+    // first index among equal maxima (argmax's tie rule).
+#pragma unroll
+    for (int mb = 0; mb < HC::MB; ++mb) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int v = vrow0 + mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+        const float z = acc[mb][nb][i];
+        if (v < p.V) {
+          const float x = fminf(z * inv_c, clamp);
+          float r;
+          part += pow2n<L2N>(rho_fast(x, r), p.log2n);
+          if (z > zm) { zm = z; im = v; }
+          if (v == tgt) p.zt[tok] = z;
+        }
+      }
+    }
+    part += xor32(part);
+    const float pz = __shfl_xor(zm, 32, 64);
+    const int pi = __shfl_xor(im, 32, 64);
+    if (pz > zm || (pz == zm && pi < im)) { zm = pz; im = pi; }
+    if (h == 0) { red[wm][col] = part; redm[wm][col] = zm; redi[wm][col] = im; }
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < HT_N; t += NT) {
+    const int tok = n0 + t;
+    float s = 0.0f, m = -INFINITY;
+    int ix = 0x7fffffff;
+#pragma unroll
+    for (int w = 0; w < HC::WM; ++w) {  // waves cover increasing vocabulary rows
+      s += red[w][t];
+      if (redm[w][t] > m) { m = redm[w][t]; ix = redi[w][t]; }
+    }
+    if (tok < p.N) {
+      p.partial[(size_t)tm * p.N + tok] = s;
+      p.pmax[(size_t)tm * p.N + tok] = m;
+      p.pidx[(size_t)tm * p.N + tok] = ix;
+    }
+  }
+}
+
+// log p(target) = n log rho(min(zt/c, X)) - log sum_v w (log of the lean likelihood's pt,
+// which src/algebraic/evaluation.py:13-23 equals: tests/test_components.py:56), in the log
+// domain so that improbable targets do not underflow; argmax over the vocabulary tiles in
+// order (first index on ties).
+__global__ __launch_bounds__(256) void head_eval_stats_kernel(HeadParams p, int nvt) {
+  const int tok = blockIdx.x * 256 + threadIdx.x;
+  if (tok >= p.N) return;
+  float l = 0.0f, m = -INFINITY;
+  int ix = 0x7fffffff;
+  for (int t = 0; t < nvt; ++t) {
+    l += p.partial[(size_t)t * p.N + tok];
+    const float pm = p.pmax[(size_t)t * p.N + tok];
+    if (pm > m) { m = pm; ix = p.pidx[(size_t)t * p.N + tok]; }
+  }
+  const float x = fminf(p.zt[tok] / p.c, p.clamp);
+  p.logprob[tok] = (float)(1 << p.log2n) * logf(rho_exact(x)) - logf(l);
+  if (p.argmax) p.argmax[tok] = ix;
+}
+
 // Per-token statistics and telemetry (fused_head.py:116-117, 219-229); with the residual
 // schedule also l and the target entries of U.
 __global__ __launch_bounds__(256) void head_stats_kernel(HeadParams p, int nvt) {
@@ -415,6 +505,21 @@ hipError_t launch_head_fwd(const HeadParams& p, hipStream_t st) {
   const int nb = head_stat_blocks(p.N);
   { KTimer t("head_stats", st); hipLaunchKernelGGL(head_stats_kernel, dim3(nb), dim3(256), 0, st, p, head_vocab_tiles(p.V)); }
   { KTimer t("head_obj", st); hipLaunchKernelGGL(head_obj_kernel, dim3(1), dim3(256), 0, st, p, nb); }
+  return hipGetLastError();
+}
+
+hipError_t launch_head_eval(const HeadParams& p, hipStream_t st) {
+  { KTimer t("head_zero", st); hipLaunchKernelGGL(head_zero_kernel, dim3((p.N + 255) / 256), dim3(256), 0, st, p.zt, p.N); }
+  const int tiles = head_vocab_tiles(p.V) * (p.Npad / HT_N);
+  {
+    KTimer t("head_eval", st);
+    if (p.log2n == 3) hipLaunchKernelGGL(head_eval_kernel<3>, dim3(tiles), dim3(NT), 0, st, p);
+    else hipLaunchKernelGGL(head_eval_kernel<0>, dim3(tiles), dim3(NT), 0, st, p);
+  }
+  {
+    KTimer t("head_eval_stats", st);
+    hipLaunchKernelGGL(head_eval_stats_kernel, dim3(head_stat_blocks(p.N)), dim3(256), 0, st, p, head_vocab_tiles(p.V));
+  }
   return hipGetLastError();
 }
 

@@ -40,6 +40,10 @@ struct HeadParams {
   int dh_kchunk;        // vocabulary entries per split (a multiple of 128)
   void* dE;             // (V, d) bf16 or f32
   int dE_f32;
+  float* pmax;          // eval: (ceil(V/HT_M), N) per-vocab-tile maximum logit
+  int* pidx;            // eval: (ceil(V/HT_M), N) its vocabulary index
+  float* logprob;       // eval: (N,) log p(target)
+  int* argmax;          // eval: (N,) argmax_v z
 };
 
 typedef GemmCfg<HT_M, HT_N, ALG_HEAD_WM, ALG_HEAD_WN> HeadGemm;

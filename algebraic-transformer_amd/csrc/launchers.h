@@ -28,5 +28,6 @@ int head_dh_split(int N, int d, int V);
 int head_dh_kchunk(int V, int split);
 hipError_t launch_head_fwd(const HeadParams& p, hipStream_t st);
 hipError_t launch_head_bwd(const HeadParams& p, hipStream_t st);
+hipError_t launch_head_eval(const HeadParams& p, hipStream_t st);
 
 }  // namespace alg

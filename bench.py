@@ -262,6 +262,32 @@ def time_layout_bthd(torch, x, steps, warmup):
             "ms": round(s * 1e3, 4), "tflops": round(fa / s / 1e12, 3)}
 
 
+def time_eval_head(torch, x, iters=20, warmup=3):
+    """Streamed evaluation head (per-token log p(target) and argmax, no logits) at the C4b
+    shape; one N x d x V product, so TFLOP/s counts 2 N d V."""
+    from algebraic_amd.kernels.fused_head import head_logprob
+    h, E, t = x["h"].detach(), x["E"].detach(), x["t"]
+
+    def call():
+        head_logprob(h, E, t, n=HEAD["n"], c=HEAD["c"])
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(iters):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        call()
+        e1.record()
+        e1.synchronize()
+        ts.append(e0.elapsed_time(e1))
+    ms = sorted(ts)[len(ts) // 2]
+    fl = 2.0 * HEAD["N"] * HEAD["d"] * HEAD["V"]
+    return {"workload": "eval head log p(target) + argmax, N16384 d2048 V32000 (C4b shape)",
+            "ms": round(ms, 4), "tflops": round(fl / (ms * 1e-3) / 1e12, 3),
+            "tokens_per_s": round(HEAD["N"] / (ms * 1e-3), 1)}
+
+
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` recorded from rocprofv3 FETCH_SIZE + WRITE_SIZE runs
     (each scaled by the same counter's reading for a device copy of known size), as listed
@@ -448,6 +474,7 @@ def main():
         out["prologue"] = time_prologue(torch, dev)
         out["layout_bthd"] = time_layout_bthd(torch, x, K, 1)
         out["layout_bthd"]["vs_bhtd"] = round(out["attn"]["ms"] / out["layout_bthd"]["ms"], 4)
+        out["eval_head"] = time_eval_head(torch, x)
     if not args.no_cpu_baseline:
         log("timing the CPU baseline sample")
         out["cpu_baseline"] = cpu_baseline()

@@ -134,8 +134,8 @@ int alg_attn_qk_prologue_bwd(alg_stream_t stream, int dtype, int layout, int B, 
                              const void* dq_r, const void* dk_r, void* dq, void* dk,
                              float* dq_gain, float* dk_gain, void* workspace, size_t workspace_bytes);
 
-/* Bytes of workspace for alg_head_fwd (pass 0), alg_head_bwd without a residual (pass 1)
- * and alg_head_bwd with a residual (pass 2). */
+/* Bytes of workspace for alg_head_fwd (pass 0), alg_head_bwd without a residual (pass 1),
+ * alg_head_bwd with a residual (pass 2) and alg_head_eval (pass 3). */
 size_t alg_head_workspace_size(int N, int d, int V, int pass);
 
 /* Bytes of the optional forward->backward residual: the vocab-major bf16 block
@@ -153,6 +153,17 @@ int alg_head_fwd(alg_stream_t stream, int N, int d, int V,
                  const void* h, const void* E, const int32_t* targets, int n, float c,
                  float* stat, float* zt, float* pt, float* obj, void* residual,
                  void* workspace, size_t workspace_bytes);
+
+/* Evaluation head, replacing the dense logits of the reference's scorer
+ * (src/algebraic/benchmarking.py:178-188 with src/algebraic/evaluation.py:13-23, head
+ * "alg_ce"): for h (N,d) bf16, E (V,d) bf16 and targets (N) int32, streams the vocabulary like
+ * alg_head_fwd and writes logprob[n] = log_softmax(n asinh(z/c))[t_n] (computed as
+ * n log rho(min(z_t/c, X)) - log sum_v rho(min(z_v/c, X))^n, X the head clamp, which equals it
+ * for every logit below c X) and, if argmax is not NULL, argmax[n] = the first index of the
+ * largest logit z_n. No logits are stored. */
+int alg_head_eval(alg_stream_t stream, int N, int d, int V,
+                  const void* h, const void* E, const int32_t* targets, int n, float c,
+                  float* logprob, int32_t* argmax, void* workspace, size_t workspace_bytes);
 
 /* Head backward, fused_head.py:120-156, 194-216, 247-254:
  * in h, E, targets, stat, g (1) f32 on the device (cotangent of obj) and optionally the

@@ -10,6 +10,11 @@
     true NLL ``-mean log softmax(n asinh(z/c))_t`` (tests/test_components.py:43-56,
     src/algebraic/evaluation.py:13-23) and ``pt`` against the same closed form.
 
+``eval_logprob`` (float64)
+    The scorer's per-token log-probability and argmax (src/algebraic/evaluation.py:13-23,
+    src/algebraic/benchmarking.py:178-188). Pin: tests/test_oracle.py checks it against the log
+    of the lean likelihood's pt (tests/test_components.py:56) and a brute-force loop.
+
 ``kernel_forward`` / ``kernel_backward`` (float32, cast-faithful)
     The Pallas fused head (src/algebraic/kernels/fused_head.py): E cast to h's dtype
     (168), z in f32, x = min(z * (1/c), X) (98), w = (x + rad rsqrt(rad))^n (99-100),
@@ -116,6 +121,18 @@ def kernel_backward(h, E, targets, stat, g=1.0, *, n=8, c=2.0, dtype="bf16", e_d
         dh[ids] = dzb @ Eb
         dE += dzb.T @ hh[ids]
     return round_to(dh, dtype), round_to(dE, e_dtype)
+
+
+def eval_logprob(h, E, targets, *, n=8, c=2.0):
+    """(logprob, argmax): log_softmax(n asinh(z/c))[t] on float64 logits
+    (src/algebraic/evaluation.py:13-23, head "alg_ce") and argmax of the logits
+    (src/algebraic/benchmarking.py:187)."""
+    z = h.astype(F64) @ E.astype(F64).T
+    a = n * np.arcsinh(z / c)
+    m = np.max(a, axis=-1, keepdims=True)
+    lse = (m + np.log(np.sum(np.exp(a - m), axis=-1, keepdims=True)))[:, 0]
+    lp = a[np.arange(z.shape[0]), targets] - lse
+    return lp, np.argmax(z, axis=-1), z
 
 
 def head_flops(N, d, V):

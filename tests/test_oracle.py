@@ -164,3 +164,20 @@ def test_head_kernel_restatement_matches_dense():
     dh, dE = OH.kernel_backward(h, E, t, stat)
     dh_r, dE_r = OH.dense_backward(h, E, t)
     assert rel_l2(dh, dh_r) < 1e-2 and rel_l2(dE, dE_r) < 1e-2
+
+
+def test_eval_logprob_is_log_of_lean_pt():
+    """evaluation.logprob_from_logits == log(pt) of the lean likelihood (test_components.py:56),
+    and == a per-token brute-force log-softmax loop; argmax == the largest logit."""
+    import math
+    from helpers import head_inputs
+    h, E, t = head_inputs(24, 32, 50, seed=13, e_std=0.5)
+    lp, am, z = OH.eval_logprob(h, E, t, n=8, c=2.0)
+    _, pt = OH.dense_forward(h, E, t, n=8, c=2.0)
+    np.testing.assert_allclose(lp, np.log(pt), rtol=1e-9)
+    for i in range(len(t)):
+        a = [8 * math.asinh(float(zz) / 2.0) for zz in z[i]]
+        mx = max(a)
+        ref = a[t[i]] - (mx + math.log(sum(math.exp(x - mx) for x in a)))
+        assert abs(lp[i] - ref) < 1e-9
+        assert am[i] == max(range(len(a)), key=lambda j: (z[i][j], -j))
