@@ -412,6 +412,49 @@ int alg_head_fwd(alg_stream_t stream, int N, int d, int V, const void* h, const 
   return hip_status(alg::launch_head_fwd(p, (hipStream_t)stream), "alg_head_fwd");
 }
 
+size_t alg_rms_norm_workspace_size(int rows, int d) {
+  if (rows <= 0 || d <= 0) return 0;
+  return align256((size_t)d * alg::rms_norm_blocks(rows) * sizeof(float));
+}
+
+static int check_rms_norm(int rows, int d, float eps) {
+  if (rows <= 0 || d <= 0) return fail(ALG_ERR_INVALID, "rows and d must be positive (got %d, %d)", rows, d);
+  if (d % 8) return fail(ALG_ERR_UNSUPPORTED, "d = %d: rows must be 16-byte aligned (d %% 8 == 0)", d);
+  if (d > alg::rms_norm_max_d()) return fail(ALG_ERR_UNSUPPORTED, "d = %d: at most %d", d, alg::rms_norm_max_d());
+  if (!(eps > 0.0f) || !std::isfinite(eps)) return fail(ALG_ERR_INVALID, "eps must be positive and finite");
+  return ALG_OK;
+}
+
+int alg_rms_norm_fwd(alg_stream_t stream, int rows, int d, const void* x, const float* gain, float eps, void* y,
+                     float* tau) {
+  int rc = check_rms_norm(rows, d, eps);
+  if (rc) return rc;
+  if (!x || !y || !tau) return fail(ALG_ERR_INVALID, "x, y and tau are required");
+  alg::RmsNormParams p;
+  std::memset(&p, 0, sizeof p);
+  p.x = static_cast<const bf16*>(x); p.gain = gain; p.y = static_cast<bf16*>(y); p.tau = tau;
+  p.rows = rows; p.d = d; p.eps = eps;
+  return hip_status(alg::launch_rms_norm_fwd(p, (hipStream_t)stream), "alg_rms_norm_fwd");
+}
+
+int alg_rms_norm_bwd(alg_stream_t stream, int rows, int d, const void* x, const float* gain, const float* tau,
+                     const void* dy, void* dx, float* dgain, void* workspace, size_t workspace_bytes) {
+  int rc = check_rms_norm(rows, d, 1.0f);
+  if (rc) return rc;
+  if (!x || !tau || !dy || !dx) return fail(ALG_ERR_INVALID, "x, tau, dy and dx are required");
+  if (dgain && !gain) return fail(ALG_ERR_INVALID, "a gain gradient needs the gain it differentiates");
+  const size_t need = alg_rms_norm_workspace_size(rows, d);
+  if (dgain && (!workspace || workspace_bytes < need))
+    return fail(ALG_ERR_INVALID, "workspace too small: need %zu bytes", need);
+  alg::RmsNormParams p;
+  std::memset(&p, 0, sizeof p);
+  p.x = static_cast<const bf16*>(x); p.gain = gain; p.tau = const_cast<float*>(tau);
+  p.dy = static_cast<const bf16*>(dy); p.dx = static_cast<bf16*>(dx);
+  p.gpart = dgain ? static_cast<float*>(workspace) : nullptr;
+  p.rows = rows; p.d = d;
+  return hip_status(alg::launch_rms_norm_bwd(p, dgain, (hipStream_t)stream), "alg_rms_norm_bwd");
+}
+
 int alg_head_eval(alg_stream_t stream, int N, int d, int V, const void* h, const void* E, const int32_t* targets,
                   int n, float c, float* logprob, int32_t* argmax, void* workspace, size_t workspace_bytes) {
   int rc = check_head(N, d, V, n, c);

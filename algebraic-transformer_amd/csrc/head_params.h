@@ -48,4 +48,17 @@ struct HeadParams {
 
 typedef GemmCfg<HT_M, HT_N, ALG_HEAD_WM, ALG_HEAD_WN> HeadGemm;
 
+// Row RMS norm with gain (the final norm before the head, model.py:208).
+struct RmsNormParams {
+  const bf16* x;        // (rows, d)
+  const float* gain;    // (d,) or nullptr
+  bf16* y;              // forward output (rows, d)
+  float* tau;           // (rows,) 1/rms, written by the forward, read by the VJP
+  const bf16* dy;       // VJP: cotangent of y
+  bf16* dx;             // VJP: (rows, d)
+  float* gpart;         // VJP: (d, nblocks) gain-gradient partials, or nullptr
+  int rows, d;
+  float eps;
+};
+
 }  // namespace alg

@@ -29,5 +29,9 @@ int head_dh_kchunk(int V, int split);
 hipError_t launch_head_fwd(const HeadParams& p, hipStream_t st);
 hipError_t launch_head_bwd(const HeadParams& p, hipStream_t st);
 hipError_t launch_head_eval(const HeadParams& p, hipStream_t st);
+int rms_norm_max_d();
+int rms_norm_blocks(int rows);
+hipError_t launch_rms_norm_fwd(const RmsNormParams& p, hipStream_t st);
+hipError_t launch_rms_norm_bwd(const RmsNormParams& p, float* dgain, hipStream_t st);
 
 }  // namespace alg

@@ -288,6 +288,38 @@ def time_eval_head(torch, x, iters=20, warmup=3):
             "tokens_per_s": round(HEAD["N"] / (ms * 1e-3), 1)}
 
 
+def time_final_norm(torch, x, iters=20, warmup=3):
+    """Final RMS norm with gain ahead of the head (model.py:208) at the C4b shape (16384 rows of
+    2048): forward reads x, writes y (+ 1/rms); the VJP reads x, dy, writes dx (+ gain partials)."""
+    from algebraic_amd.kernels.norm import rms_norm
+    h = x["h"].detach().clone().requires_grad_(True)
+    g = torch.ones(HEAD["d"], device=h.device, requires_grad=True)
+    dy = torch.randn_like(h)
+
+    def median_ms(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(iters):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            e1.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        return sorted(ts)[len(ts) // 2]
+    y = rms_norm(h, g)
+    f_ms = median_ms(lambda: rms_norm(h, g))
+    fb_ms = median_ms(lambda: torch.autograd.grad(rms_norm(h, g), (h, g), dy))
+    b_ms = fb_ms - f_ms
+    nb = HEAD["N"] * HEAD["d"] * 2
+    fg, bg = (2 * nb) / (f_ms * 1e-3) / 1e9, (3 * nb) / (b_ms * 1e-3) / 1e9
+    del y
+    return {"workload": "final RMS norm + gain, 16384 x 2048 bf16 (C4b head input)", "fwd_ms": round(f_ms, 4),
+            "fwd_gbs": round(fg, 1), "bwd_ms": round(b_ms, 4), "bwd_gbs": round(bg, 1), "peak_gbs": PEAK_HBM_GBS}
+
+
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` recorded from rocprofv3 FETCH_SIZE + WRITE_SIZE runs
     (each scaled by the same counter's reading for a device copy of known size), as listed
@@ -475,6 +507,7 @@ def main():
         out["layout_bthd"] = time_layout_bthd(torch, x, K, 1)
         out["layout_bthd"]["vs_bhtd"] = round(out["attn"]["ms"] / out["layout_bthd"]["ms"], 4)
         out["eval_head"] = time_eval_head(torch, x)
+        out["final_norm"] = time_final_norm(torch, x)
     if not args.no_cpu_baseline:
         log("timing the CPU baseline sample")
         out["cpu_baseline"] = cpu_baseline()

@@ -165,6 +165,17 @@ int alg_head_eval(alg_stream_t stream, int N, int d, int V,
                   const void* h, const void* E, const int32_t* targets, int n, float c,
                   float* logprob, int32_t* argmax, void* workspace, size_t workspace_bytes);
 
+/* Row RMS norm with a learned gain, bf16 rows of d elements (d % 8 == 0, d <= 4096): the
+ * model's final norm ahead of the head (model.py:208; rms_norm at algebraic.py:76-83).
+ * Forward: tau[r] = 1/sqrt(mean(x_r^2) + eps), y = round((x tau) gain) (gain NULL: none).
+ * Backward (JAX autodiff of the same expression): dx = round(a tau - x tau^3 sum(a x)/d) with
+ * a = gain dy, and dgain (d) f32 = sum over rows of dy x tau (NULL to skip; then no workspace). */
+size_t alg_rms_norm_workspace_size(int rows, int d);
+int alg_rms_norm_fwd(alg_stream_t stream, int rows, int d, const void* x, const float* gain, float eps,
+                     void* y, float* tau);
+int alg_rms_norm_bwd(alg_stream_t stream, int rows, int d, const void* x, const float* gain, const float* tau,
+                     const void* dy, void* dx, float* dgain, void* workspace, size_t workspace_bytes);
+
 /* Head backward, fused_head.py:120-156, 194-216, 247-254:
  * in h, E, targets, stat, g (1) f32 on the device (cotangent of obj) and optionally the
  * forward's residual; out dh (N,d) bf16 and dE (V,d) in dE_dtype (ALG_DTYPE_BF16 or
