@@ -1,0 +1,74 @@
+"""ALU-GLU feed-forward block on MI355X with the activation fused into the products.
+
+``alu_glu_ffn(h2, w_g, w_u, w_d, beta)`` is ``(h2 @ w_g * alu(h2 @ w_u, beta)) @ w_d`` as the
+model's block computes it (src/algebraic/model.py:185-193, ffn="alu_glu"; alu and its custom VJP
+src/algebraic/algebraic.py:86-113), differentiable in h2 and the three weights. The gate/up
+product over the concatenated weights [w_g | w_u] carries the activation in its epilogue (one
+HIP kernel writes y = gate*alu(up) and the gate/up residuals); in the backward, the product
+dout @ w_d^T carries the activation's VJP in its epilogue (one HIP kernel writes
+[d_gate | d_up]). The four remaining products are plain GEMMs (hipBLASLt through torch),
+each one call: y @ w_d, [d_gate | d_up] @ [w_g | w_u]^T, h2^T @ [d_gate | d_up], y^T @ dout.
+bf16 only; d_ff must be a multiple of 128. No CPU fallback for the fused parts.
+"""
+
+import torch
+
+from .. import _lib
+
+
+def _t(x):
+    """Contiguous transpose (products never take a transposed view)."""
+    return x.t().contiguous()
+
+
+def _a16(x):
+    """Contiguous and 16-byte aligned, as the fused kernels' vector accesses need."""
+    x = x.contiguous()
+    return x if x.data_ptr() % 16 == 0 else x.clone()
+
+
+class _FfnFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, h2, w_g, w_u, w_d, beta):
+        lib = _lib.load()
+        shape = h2.shape
+        d = shape[-1]
+        x = _a16(h2).reshape(-1, d)
+        N, F = x.shape[0], w_g.shape[1]
+        w_gu = torch.cat([w_g, w_u], dim=1).to(torch.bfloat16).contiguous()
+        wd = _a16(w_d.to(torch.bfloat16))
+        y, gate, up = (torch.empty((N, F), dtype=torch.bfloat16, device=x.device) for _ in range(3))
+        _lib.check(lib.alg_ffn_alu_glu_fwd(_lib.stream_of(x), N, d, F, _lib.ptr(x), _lib.ptr(w_gu), float(beta),
+                                           _lib.ptr(y), _lib.ptr(gate), _lib.ptr(up)), "alu_glu_ffn")
+        out = torch.matmul(y, wd)
+        ctx.save_for_backward(x, w_gu, wd, y, gate, up)
+        ctx.meta = (shape, beta, w_g.dtype, w_u.dtype, w_d.dtype)
+        return out.reshape(*shape[:-1], wd.shape[1])
+
+    @staticmethod
+    def backward(ctx, dout):
+        x, w_gu, wd, y, gate, up = ctx.saved_tensors
+        shape, beta, tg, tu, td = ctx.meta
+        lib = _lib.load()
+        N, d = x.shape
+        F, dm = wd.shape
+        do = _a16(dout.to(torch.bfloat16)).reshape(N, dm)
+        d_gu = torch.empty((N, 2 * F), dtype=torch.bfloat16, device=x.device)
+        _lib.check(lib.alg_ffn_alu_glu_dy(_lib.stream_of(x), N, dm, F, _lib.ptr(do), _lib.ptr(wd), _lib.ptr(gate),
+                                          _lib.ptr(up), float(beta), _lib.ptr(d_gu)), "alu_glu_ffn backward")
+        dh2 = torch.matmul(d_gu, _t(w_gu)).reshape(shape)
+        dw_gu = torch.matmul(_t(x), d_gu)
+        dw_d = torch.matmul(_t(y), do)
+        return dh2, dw_gu[:, :F].to(tg), dw_gu[:, F:].to(tu), dw_d.to(td), None
+
+
+def alu_glu_ffn(h2, w_g, w_u, w_d, beta: float = 0.5):
+    """(h2 @ w_g * alu(h2 @ w_u, beta)) @ w_d for bfloat16 GPU tensors (model.py:185-193)."""
+    if h2.dtype != torch.bfloat16:
+        raise NotImplementedError(f"dtype {h2.dtype}: the gfx950 feed-forward takes bfloat16 activations")
+    if not h2.is_cuda:
+        raise RuntimeError("alu_glu_ffn needs GPU tensors (no CPU fallback)")
+    d = h2.shape[-1]
+    if w_g.shape != w_u.shape or w_g.shape[0] != d or w_d.shape[0] != w_g.shape[1]:
+        raise ValueError("w_g, w_u must be (d, d_ff) and w_d (d_ff, d_out)")
+    return _FfnFn.apply(h2, w_g, w_u, w_d, float(beta))

@@ -8,6 +8,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <initializer_list>
 #include <string>
 
 #include "algebraic_hip.h"
@@ -453,6 +454,53 @@ int alg_rms_norm_bwd(alg_stream_t stream, int rows, int d, const void* x, const 
   p.gpart = dgain ? static_cast<float*>(workspace) : nullptr;
   p.rows = rows; p.d = d;
   return hip_status(alg::launch_rms_norm_bwd(p, dgain, (hipStream_t)stream), "alg_rms_norm_bwd");
+}
+
+static int check_ffn(int N, int d, int F) {
+  if (N <= 0 || d <= 0 || F <= 0) return fail(ALG_ERR_INVALID, "N, d, F must be positive (got %d, %d, %d)", N, d, F);
+  if (d % 8) return fail(ALG_ERR_UNSUPPORTED, "width %d: rows must be 16-byte aligned (%% 8 == 0)", d);
+  if (F % 128) return fail(ALG_ERR_UNSUPPORTED, "d_ff = %d: the fused gate/up product needs d_ff %% 128 == 0", F);
+  if ((double)N * 2 * F > 2.0e9 || (double)d * 2 * F > 2.0e9 || (double)N * d > 2.0e9)
+    return fail(ALG_ERR_INVALID, "feed-forward too large");
+  return ALG_OK;
+}
+
+// The fused epilogues move 8 bf16 per lane: every matrix must start on a 16-byte boundary.
+static bool aligned16(std::initializer_list<const void*> ptrs) {
+  for (const void* q : ptrs)
+    if (reinterpret_cast<uintptr_t>(q) & 15) return false;
+  return true;
+}
+
+int alg_ffn_alu_glu_fwd(alg_stream_t stream, int N, int d, int F, const void* h2, const void* w_gu, float beta,
+                        void* y, void* gate, void* up) {
+  int rc = check_ffn(N, d, F);
+  if (rc) return rc;
+  if (!h2 || !w_gu || !y || !gate || !up) return fail(ALG_ERR_INVALID, "null argument");
+  if (!aligned16({h2, w_gu, y, gate, up})) return fail(ALG_ERR_INVALID, "matrices must be 16-byte aligned");
+  if (!std::isfinite(beta)) return fail(ALG_ERR_INVALID, "beta must be finite");
+  alg::FfnParams p;
+  std::memset(&p, 0, sizeof p);
+  p.h2 = static_cast<const bf16*>(h2); p.w_gu = static_cast<const bf16*>(w_gu);
+  p.y = static_cast<bf16*>(y); p.gate = static_cast<bf16*>(gate); p.up = static_cast<bf16*>(up);
+  p.N = N; p.d = d; p.F = F; p.beta = beta;
+  return hip_status(alg::launch_ffn_fwd(p, (hipStream_t)stream), "alg_ffn_alu_glu_fwd");
+}
+
+int alg_ffn_alu_glu_dy(alg_stream_t stream, int N, int dm, int F, const void* dout, const void* w_d, const void* gate,
+                       const void* up, float beta, void* d_gu) {
+  int rc = check_ffn(N, dm, F);
+  if (rc) return rc;
+  if (!dout || !w_d || !gate || !up || !d_gu) return fail(ALG_ERR_INVALID, "null argument");
+  if (!aligned16({dout, w_d, gate, up, d_gu})) return fail(ALG_ERR_INVALID, "matrices must be 16-byte aligned");
+  if (!std::isfinite(beta)) return fail(ALG_ERR_INVALID, "beta must be finite");
+  alg::FfnParams p;
+  std::memset(&p, 0, sizeof p);
+  p.dout = static_cast<const bf16*>(dout); p.w_d = static_cast<const bf16*>(w_d);
+  p.gate = const_cast<bf16*>(static_cast<const bf16*>(gate)); p.up = const_cast<bf16*>(static_cast<const bf16*>(up));
+  p.d_gu = static_cast<bf16*>(d_gu);
+  p.N = N; p.dm = dm; p.F = F; p.beta = beta;
+  return hip_status(alg::launch_ffn_dy(p, (hipStream_t)stream), "alg_ffn_alu_glu_dy");
 }
 
 int alg_head_eval(alg_stream_t stream, int N, int d, int V, const void* h, const void* E, const int32_t* targets,

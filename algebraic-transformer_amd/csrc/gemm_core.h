@@ -46,7 +46,21 @@ struct GemmOperand {
   int rows_valid;  // rows of the logical matrix
   int cols_valid;  // columns of the logical matrix (ld >= cols_valid rounded up to 8)
   long extent;     // elements readable from ptr (the allocation); a multiple of 8
+  // Split m/n-contiguous operand: the logical columns alternate in 32-wide blocks between two
+  // stored halves `split` elements apart (logical block 2b -> stored columns 32b.. of the first
+  // half, block 2b+1 -> the same columns of the second half), so a product against [W1 | W2]
+  // gives each wave matching W1 and W2 columns. 0: plain operand. Logical tile columns start at
+  // mn0, stored ones at mn0 / 2.
+  long split = 0;
 };
+
+// Stored element offset, relative to a tile's stored first column, of logical chunk c
+// (8 columns) of an m/n-contiguous operand.
+__device__ __forceinline__ long split_chunk_offset(const GemmOperand& op, int c) {
+  if (!op.split) return 8L * c;
+  const int blk = c >> 2;
+  return (blk & 1) * op.split + (blk >> 1) * 32 + (c & 3) * 8;
+}
 
 // One operand tile covering TMN (m or n) x 64 (k) in LDS, unpadded and swizzled.
 template <int MODE, int TMN, int NT>
@@ -76,13 +90,14 @@ struct OperandTile {
 
   // Per-lane byte offsets (relative to the instruction's first row and the tile's first
   // column) for even and odd instructions; computed once per kernel.
-  static __device__ __forceinline__ void lane_offsets(long ld, uint32_t (&off)[2]) {
+  static __device__ __forceinline__ void lane_offsets(const GemmOperand& op, uint32_t (&off)[2]) {
     const int lane = threadIdx.x & 63;
 #pragma unroll
     for (int par = 0; par < 2; ++par) {
       const int row = RPI * par + lane / CPR;  // row inside the tile modulo the swizzle period
       const int c = (lane % CPR) ^ swz(row);   // logical chunk this lane fetches
-      off[par] = (uint32_t)((lane / CPR) * ld * 2 + 16 * c);
+      const long col = MODE == KMAJOR ? 8L * c : split_chunk_offset(op, c);
+      off[par] = (uint32_t)(((lane / CPR) * op.ld + col) * 2);
     }
   }
 
@@ -100,7 +115,7 @@ struct OperandTile {
   static __device__ __forceinline__ void copy(bf16* tile, const GemmOperand& op, const uint32_t (&off)[2], int wave,
                                               int mn0, int k0) {
     const int r0 = (MODE == KMAJOR) ? mn0 : k0;
-    const int c0 = (MODE == KMAJOR) ? k0 : mn0;
+    const int c0 = (MODE == KMAJOR) ? k0 : (op.split ? mn0 / 2 : mn0);
     if constexpr (!CHECKED) {
       const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
           (void*)(op.ptr + ((long)r0 * op.ld + c0)), (short)0, 0x7FFFFFFF, BUF_RSRC_WORD3);
@@ -129,12 +144,13 @@ struct OperandTile {
     for (int p = threadIdx.x; p < ROWS * CPR; p += NT) {
       const int row = p / CPR, c = p - row * CPR;
       const int grow = (MODE == KMAJOR) ? mn0 + row : k0 + row;
-      const int gcol = (MODE == KMAJOR) ? k0 + 8 * c : mn0 + 8 * c;
+      const int gcol = (MODE == KMAJOR) ? k0 + 8 * c : mn0 + 8 * c;  // logical column
       const int col_end = (MODE == KMAJOR) ? min(K, op.cols_valid) : op.cols_valid;
       const bool row_ok = grow < op.rows_valid && ((MODE == KMAJOR) || grow < K);
       const int nv = row_ok ? min(8, col_end - gcol) : 0;  // live elements of this chunk
+      const long scol = (MODE != KMAJOR && op.split) ? mn0 / 2 + split_chunk_offset(op, c) : gcol;
       uint4 v = make_uint4(0, 0, 0, 0);
-      if (nv > 0) v = *reinterpret_cast<const uint4*>(op.ptr + (long)grow * op.ld + gcol);
+      if (nv > 0) v = *reinterpret_cast<const uint4*>(op.ptr + (long)grow * op.ld + scol);
       if (nv < 8) {  // keep elements [0, nv): two bf16 per 32-bit word
         unsigned int* w = reinterpret_cast<unsigned int*>(&v);
 #pragma unroll
@@ -241,8 +257,8 @@ __device__ __forceinline__ void gemm_mainloop(GemmStage<AM, BM, C>& s0, GemmStag
   const bool b_full = (BM == KMAJOR ? B.rows_valid : B.cols_valid) >= n0 + C::TN;
   if (kmain > 0) {
     uint32_t aoff[2], boff[2];
-    TA::lane_offsets(A.ld, aoff);
-    TB::lane_offsets(B.ld, boff);
+    TA::lane_offsets(A, aoff);
+    TB::lane_offsets(B, boff);
     const int wave_u = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nk = kmain / GT_K;  // even, >= 2
     // One k step, software-pipelined over its four 16-deep sub-steps: fragments of sub-step

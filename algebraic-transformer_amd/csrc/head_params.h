@@ -48,6 +48,20 @@ struct HeadParams {
 
 typedef GemmCfg<HT_M, HT_N, ALG_HEAD_WM, ALG_HEAD_WN> HeadGemm;
 
+// ALU-GLU feed-forward products with fused activation epilogues (model.py:185-193).
+struct FfnParams {
+  const bf16* h2;       // (N, d) block input after its norm
+  const bf16* w_gu;     // (d, 2F) = [w_g | w_u]
+  bf16* y;              // (N, F) gate * alu(up)
+  bf16* gate;           // (N, F) residual for the backward
+  bf16* up;             // (N, F) residual for the backward
+  const bf16* dout;     // (N, dm) cotangent of the block output
+  const bf16* w_d;      // (F, dm)
+  bf16* d_gu;           // (N, 2F) = [d_gate | d_up]
+  int N, d, F, dm;
+  float beta;
+};
+
 // Row RMS norm with gain (the final norm before the head, model.py:208).
 struct RmsNormParams {
   const bf16* x;        // (rows, d)

@@ -32,6 +32,8 @@ hipError_t launch_head_eval(const HeadParams& p, hipStream_t st);
 int rms_norm_max_d();
 int rms_norm_blocks(int rows);
 hipError_t launch_rms_norm_fwd(const RmsNormParams& p, hipStream_t st);
+hipError_t launch_ffn_fwd(const FfnParams& p, hipStream_t st);
+hipError_t launch_ffn_dy(const FfnParams& p, hipStream_t st);
 hipError_t launch_rms_norm_bwd(const RmsNormParams& p, float* dgain, hipStream_t st);
 
 }  // namespace alg

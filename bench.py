@@ -320,6 +320,63 @@ def time_final_norm(torch, x, iters=20, warmup=3):
             "fwd_gbs": round(fg, 1), "bwd_ms": round(b_ms, 4), "bwd_gbs": round(bg, 1), "peak_gbs": PEAK_HBM_GBS}
 
 
+def time_ffn(torch, dev, iters=10, warmup=2, seed=3):
+    """ALU-GLU feed-forward at the 1b model's shape (N = 8 x 2048 tokens, d 1536, d_ff 4224):
+    the fused gate/up product (2 N d 2F FLOP) and the fused dy product (2 N d F), the whole
+    block forward + backward, and the same block with plain library products and torch
+    elementwise activation for comparison."""
+    from algebraic_amd import _lib as L
+    from algebraic_amd.kernels.ffn import alu_glu_ffn
+    N, d, F = 16384, 1536, 4224
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    rn = lambda *s, sc=1.0: (torch.randn(*s, device=dev, generator=g) * sc).to(torch.bfloat16)
+    h2 = rn(N, d).requires_grad_(True)
+    w_g, w_u = rn(d, F, sc=d ** -0.5).requires_grad_(True), rn(d, F, sc=d ** -0.5).requires_grad_(True)
+    w_d = rn(F, d, sc=F ** -0.5).requires_grad_(True)
+    dout = rn(N, d)
+
+    def median_ms(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(iters):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            e1.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        return sorted(ts)[len(ts) // 2]
+
+    def fused():
+        torch.autograd.grad(alu_glu_ffn(h2, w_g, w_u, w_d, 0.5), (h2, w_g, w_u, w_d), dout)
+
+    def plain():
+        up = h2 @ w_u
+        act = (0.5 * up.float() * (1 + 0.5 * up.float() * torch.rsqrt(1 + (0.5 * up.float()) ** 2))).to(up.dtype)
+        out = ((h2 @ w_g) * act) @ w_d
+        torch.autograd.grad(out, (h2, w_g, w_u, w_d), dout)
+    lib = L.load()
+    w_gu = torch.cat([w_g, w_u], 1).detach().contiguous()
+    y, gate, up = (torch.empty((N, F), dtype=torch.bfloat16, device=dev) for _ in range(3))
+    d_gu = torch.empty((N, 2 * F), dtype=torch.bfloat16, device=dev)
+    st = L.stream_of(h2)
+    k_fwd = median_ms(lambda: lib.alg_ffn_alu_glu_fwd(st, N, d, F, L.ptr(h2), L.ptr(w_gu), 0.5, L.ptr(y),
+                                                       L.ptr(gate), L.ptr(up)))
+    k_dy = median_ms(lambda: lib.alg_ffn_alu_glu_dy(st, N, d, F, L.ptr(dout), L.ptr(w_d.detach()), L.ptr(gate),
+                                                     L.ptr(up), 0.5, L.ptr(d_gu)))
+    t_f, t_p = median_ms(fused), median_ms(plain)
+    fl_gu, fl_dy = 2.0 * N * d * 2 * F, 2.0 * N * d * F
+    block = 6 * 2.0 * N * d * F + 2 * 2.0 * N * d * F  # 3 products forward (gate, up, out), 6 backward
+    return {"workload": "ALU-GLU FFN, 1b shape N16384 d1536 d_ff4224 bf16",
+            "gate_up_ms": round(k_fwd, 4), "gate_up_tflops": round(fl_gu / (k_fwd * 1e-3) / 1e12, 1),
+            "dy_ms": round(k_dy, 4), "dy_tflops": round(fl_dy / (k_dy * 1e-3) / 1e12, 1),
+            "block_fwd_bwd_ms": round(t_f, 4), "block_tflops": round(block / (t_f * 1e-3) / 1e12, 1),
+            "plain_library_ms": round(t_p, 4), "vs_plain": round(t_p / t_f, 3)}
+
+
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` recorded from rocprofv3 FETCH_SIZE + WRITE_SIZE runs
     (each scaled by the same counter's reading for a device copy of known size), as listed
@@ -508,6 +565,7 @@ def main():
         out["layout_bthd"]["vs_bhtd"] = round(out["attn"]["ms"] / out["layout_bthd"]["ms"], 4)
         out["eval_head"] = time_eval_head(torch, x)
         out["final_norm"] = time_final_norm(torch, x)
+        out["ffn"] = time_ffn(torch, dev)
     if not args.no_cpu_baseline:
         log("timing the CPU baseline sample")
         out["cpu_baseline"] = cpu_baseline()

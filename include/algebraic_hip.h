@@ -176,6 +176,18 @@ int alg_rms_norm_fwd(alg_stream_t stream, int rows, int d, const void* x, const 
 int alg_rms_norm_bwd(alg_stream_t stream, int rows, int d, const void* x, const float* gain, const float* tau,
                      const void* dy, void* dx, float* dgain, void* workspace, size_t workspace_bytes);
 
+/* ALU-GLU feed-forward (model.py:185-193, ffn = "alu_glu"; alu and its VJP algebraic.py:86-113),
+ * bf16, d_ff = F a multiple of 128. Forward: for h2 (N, d) and w_gu = [w_g | w_u] (d, 2F),
+ * gate = round(h2 w_g), up = round(h2 w_u), y = round(gate alu(up)) (alu with the negative-tail
+ * form, beta its slope), all (N, F); y w_d is then a plain product. Backward: for the block
+ * output's cotangent dout (N, dm) and w_d (F, dm), dy = round(dout w_d^T) and
+ * d_gu = [round(dy alu(up)) | round(round(dy gate) alu'(up))] (N, 2F); dh2 = d_gu w_gu^T and
+ * [dw_g | dw_u] = h2^T d_gu are then plain products. */
+int alg_ffn_alu_glu_fwd(alg_stream_t stream, int N, int d, int F, const void* h2, const void* w_gu, float beta,
+                        void* y, void* gate, void* up);
+int alg_ffn_alu_glu_dy(alg_stream_t stream, int N, int dm, int F, const void* dout, const void* w_d,
+                       const void* gate, const void* up, float beta, void* d_gu);
+
 /* Head backward, fused_head.py:120-156, 194-216, 247-254:
  * in h, E, targets, stat, g (1) f32 on the device (cotangent of obj) and optionally the
  * forward's residual; out dh (N,d) bf16 and dE (V,d) in dE_dtype (ALG_DTYPE_BF16 or
