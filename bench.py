@@ -262,6 +262,21 @@ def time_layout_bthd(torch, x, steps, warmup):
             "ms": round(s * 1e3, 4), "tflops": round(fa / s / 1e12, 3)}
 
 
+def kernel_times(torch, fn, iters):
+    """Mean duration (ms) of each library kernel over `iters` calls of fn, from the library's
+    HIP events on the launch stream (no host launch overhead)."""
+    from algebraic_amd import _lib
+    fn()
+    torch.cuda.synchronize()
+    _lib.timer_enable(True)
+    for _ in range(iters):
+        fn()
+    torch.cuda.synchronize()
+    rep = _lib.timer_report()
+    _lib.timer_enable(False)
+    return {name: r["mean_ms"] for name, r in rep.items()}
+
+
 def time_eval_head(torch, x, iters=20, warmup=3):
     """Streamed evaluation head (per-token log p(target) and argmax, no logits) at the C4b
     shape; one N x d x V product, so TFLOP/s counts 2 N d V."""
@@ -282,10 +297,13 @@ def time_eval_head(torch, x, iters=20, warmup=3):
         e1.synchronize()
         ts.append(e0.elapsed_time(e1))
     ms = sorted(ts)[len(ts) // 2]
+    k = kernel_times(torch, call, iters)
     fl = 2.0 * HEAD["N"] * HEAD["d"] * HEAD["V"]
     return {"workload": "eval head log p(target) + argmax, N16384 d2048 V32000 (C4b shape)",
             "ms": round(ms, 4), "tflops": round(fl / (ms * 1e-3) / 1e12, 3),
-            "tokens_per_s": round(HEAD["N"] / (ms * 1e-3), 1)}
+            "tokens_per_s": round(HEAD["N"] / (ms * 1e-3), 1),
+            "kernel_ms": round(k["head_eval"], 4), "kernel_tflops": round(fl / (k["head_eval"] * 1e-3) / 1e12, 3),
+            "stats_ms": round(k["head_eval_stats"], 4)}
 
 
 def time_final_norm(torch, x, iters=20, warmup=3):
@@ -309,18 +327,12 @@ def time_final_norm(torch, x, iters=20, warmup=3):
             e1.synchronize()
             ts.append(e0.elapsed_time(e1))
         return sorted(ts)[len(ts) // 2]
-    from algebraic_amd import _lib
     f_ms = median_ms(lambda: rms_norm(h, g))
     fb_ms = median_ms(lambda: torch.autograd.grad(rms_norm(h, g), (h, g), dy))
-    # Kernel durations (HIP events on the launch stream): the wrapper times above also hold
-    # the autograd and allocation overhead of a ~0.1 ms call.
-    _lib.timer_enable(True)
-    for _ in range(iters):
-        torch.autograd.grad(rms_norm(h, g), (h, g), dy)
-    torch.cuda.synchronize()
-    k = _lib.timer_report()
-    _lib.timer_enable(False)
-    kf, kb, kr = (k[n]["mean_ms"] for n in ("rms_norm_fwd", "rms_norm_bwd", "rms_norm_gain_reduce"))
+    # Kernel durations: the wrapper times above also hold the autograd and allocation
+    # overhead of a ~0.1 ms call.
+    k = kernel_times(torch, lambda: torch.autograd.grad(rms_norm(h, g), (h, g), dy), iters)
+    kf, kb, kr = (k[n] for n in ("rms_norm_fwd", "rms_norm_bwd", "rms_norm_gain_reduce"))
     nb = HEAD["N"] * HEAD["d"] * 2
     fg, bg = (2 * nb) / (kf * 1e-3) / 1e9, (3 * nb) / (kb * 1e-3) / 1e9
     return {"workload": "final RMS norm + gain, 16384 x 2048 bf16 (C4b head input)",
@@ -373,10 +385,13 @@ def time_ffn(torch, dev, iters=10, warmup=2, seed=3):
     y, gate, up = (torch.empty((N, F), dtype=torch.bfloat16, device=dev) for _ in range(3))
     d_gu = torch.empty((N, 2 * F), dtype=torch.bfloat16, device=dev)
     st = L.stream_of(h2)
-    k_fwd = median_ms(lambda: lib.alg_ffn_alu_glu_fwd(st, N, d, F, L.ptr(h2), L.ptr(w_gu), 0.5, L.ptr(y),
-                                                       L.ptr(gate), L.ptr(up)))
-    k_dy = median_ms(lambda: lib.alg_ffn_alu_glu_dy(st, N, d, F, L.ptr(dout), L.ptr(w_d.detach()), L.ptr(gate),
-                                                     L.ptr(up), 0.5, L.ptr(d_gu)))
+    def both():
+        L.check(lib.alg_ffn_alu_glu_fwd(st, N, d, F, L.ptr(h2), L.ptr(w_gu), 0.5, L.ptr(y), L.ptr(gate), L.ptr(up)),
+                "ffn fwd")
+        L.check(lib.alg_ffn_alu_glu_dy(st, N, d, F, L.ptr(dout), L.ptr(w_d.detach()), L.ptr(gate), L.ptr(up), 0.5,
+                                       L.ptr(d_gu)), "ffn dy")
+    k = kernel_times(torch, both, iters)
+    k_fwd, k_dy = k["ffn_gate_up"], k["ffn_dy"]
     t_f, t_p = median_ms(fused), median_ms(plain)
     fl_gu, fl_dy = 2.0 * N * d * 2 * F, 2.0 * N * d * F
     block = 6 * 2.0 * N * d * F + 2 * 2.0 * N * d * F  # 3 products forward (gate, up, out), 6 backward

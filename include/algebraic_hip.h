@@ -182,7 +182,8 @@ int alg_rms_norm_bwd(alg_stream_t stream, int rows, int d, const void* x, const 
  * form, beta its slope), all (N, F); y w_d is then a plain product. Backward: for the block
  * output's cotangent dout (N, dm) and w_d (F, dm), dy = round(dout w_d^T) and
  * d_gu = [round(dy alu(up)) | round(round(dy gate) alu'(up))] (N, 2F); dh2 = d_gu w_gu^T and
- * [dw_g | dw_u] = h2^T d_gu are then plain products. */
+ * [dw_g | dw_u] = h2^T d_gu are then plain products. Every matrix is row-major, contiguous and
+ * 16-byte aligned (ALG_ERR_INVALID otherwise). */
 int alg_ffn_alu_glu_fwd(alg_stream_t stream, int N, int d, int F, const void* h2, const void* w_gu, float beta,
                         void* y, void* gate, void* up);
 int alg_ffn_alu_glu_dy(alg_stream_t stream, int N, int dm, int F, const void* dout, const void* w_d,

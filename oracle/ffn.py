@@ -13,7 +13,8 @@
 Pins (tests/test_ffn_oracle.py): alu against its closed form x/2 (1 + bx/sqrt(1 + b^2 x^2))
 and its VJP against torch float64 autograd of that closed form on [-40, 40]
 (tests/test_components.py:71-78), and the whole block's gradients against torch float64
-autograd in float32 mode.
+autograd in float32 mode; planted mistakes (the derivative without 0.5 u r^2, gate and up
+weights swapped) fail that pin.
 """
 
 import numpy as np

@@ -52,3 +52,26 @@ def test_ffn_block_gradients_match_torch_autograd():
         assert rel_l2(a, b.numpy()) < 1e-5, name
     out_o, *_ = OF.ffn_forward(h2, w_g, w_u, w_d, 0.5, "f32")
     assert rel_l2(out_o, out.detach().numpy()) < 1e-6
+
+
+@pytest.mark.parametrize("mistake", ["drop_r2_term", "transposed_gate_up"])
+def test_planted_mistakes_fail_the_pins(mistake, monkeypatch):
+    """Plausible slips planted in the oracle (the derivative without its 0.5 u r^2 term; gate
+    and up weights swapped in the backward) must fail the float64 autograd pin above."""
+    rng = np.random.default_rng(7)
+    N, d, F = 24, 32, 48
+    h2, w_g, w_u, w_d, dout = (rng.standard_normal(s).astype(np.float32) * sc for s, sc in
+                               [((N, d), 1.0), ((d, F), 0.4), ((d, F), 0.4), ((F, d), 0.2), ((N, d), 1.0)])
+    if mistake == "drop_r2_term":
+        monkeypatch.setattr(OF, "alu_vjp", lambda u, r, g, dtype="bf16":
+                            OF.round_to((np.asarray(g, np.float32) * np.float32(0.5) * (1 + u)).astype(np.float32), dtype))
+        dh2, dw_g, dw_u, dw_d, _, _ = OF.ffn_backward(h2, w_g, w_u, w_d, dout, 0.5, "f32")
+    else:
+        dh2, dw_g, dw_u, dw_d, _, _ = OF.ffn_backward(h2, w_u, w_g, w_d, dout, 0.5, "f32")
+    t = lambda a: torch.tensor(a.astype(np.float64), requires_grad=True)
+    th, tg, tu, td = t(h2), t(w_g), t(w_u), t(w_d)
+    up = th @ tu
+    act = 0.5 * up * (1 + 0.5 * up / torch.sqrt(1 + (0.5 * up) ** 2))
+    (((th @ tg) * act) @ td * torch.tensor(dout.astype(np.float64))).sum().backward()
+    worst = max(rel_l2(a, b.numpy()) for a, b in [(dh2, th.grad), (dw_u, tu.grad)])
+    assert worst > 1e-3, f"planted mistake {mistake} passes the pin ({worst:.1e})"
