@@ -109,10 +109,15 @@ __device__ __forceinline__ float inv_root(float l, int n) {
 
 __device__ __forceinline__ float bf2f(bf16 x) { return (float)x; }
 __device__ __forceinline__ bf16 f2bf(float x) { return (bf16)x; }
-// Two floats rounded to bf16 and packed (a in the low half).
+// Two floats rounded to bf16 and packed (a in the low half). Built as a 2-vector so the
+// compiler emits one v_cvt_pk_bf16_f32 (the shift-and-or form cost two conversions and a
+// merge per pair).
 __device__ __forceinline__ unsigned int pack_bf16x2(float a, float b) {
-  return (unsigned int)__builtin_bit_cast(unsigned short, f2bf(a)) |
-         ((unsigned int)__builtin_bit_cast(unsigned short, f2bf(b)) << 16);
+  typedef bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  bf16x2_t v;
+  v[0] = f2bf(a);
+  v[1] = f2bf(b);
+  return __builtin_bit_cast(unsigned int, v);
 }
 
 __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }

@@ -46,6 +46,17 @@ __global__ void head_zero_kernel(float* p, int n) {
 
 // z^T = E h^T with the forward epilogue (row sums, target logit, optional U residual).
 // L2N > 0 fixes n = 2^L2N at compile time (0: taken from the parameters).
+// acc[mb][nb][4g + e] for the row offset dt = mb*32 + 8g + e (bit 2 of dt, the lane half,
+// already matched).
+__device__ __forceinline__ float select_row(const floatx16 (&acc)[HC::MB][HC::NB], int nb, int dt) {
+  float z = 0.0f;
+#pragma unroll
+  for (int mb = 0; mb < HC::MB; ++mb)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) z = dt == mb * 32 + 8 * (i >> 2) + (i & 3) ? acc[mb][nb][i] : z;
+  return z;
+}
+
 template <int L2N>
 __global__ __launch_bounds__(NT, 1) void head_fwd_kernel(HeadParams p) {
   __shared__ __attribute__((aligned(16))) GemmStage<KMAJOR, KMAJOR, HC> s0, s1;
@@ -90,8 +101,7 @@ __global__ __launch_bounds__(NT, 1) void head_fwd_kernel(HeadParams p) {
       const int col = wn * HC::WTN + nb * 32 + l32;
       const int tok = n0 + col;
       const int dt = p.targets[tok] - vrow0 - 4 * h;  // target row relative to this lane's rows
-      float part = 0.0f, ztv = 0.0f;
-      bool hit = false;
+      float part = 0.0f;
 #pragma unroll
       for (int mb = 0; mb < HC::MB; ++mb) {
 #pragma unroll
@@ -99,15 +109,12 @@ __global__ __launch_bounds__(NT, 1) void head_fwd_kernel(HeadParams p) {
           float u[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const int c = mb * 32 + 8 * g + e;  // lane row offset (without 4h)
             const float z = acc[mb][nb][4 * g + e];
             const float x = fminf(z * inv_c, clamp);  // fused_head.py:98
             float r;
             const float w = pow2n<L2N>(rho_fast(x, r), p.log2n);
             part += w;
             u[e] = w * r;
-            ztv = dt == c ? z : ztv;
-            hit = hit || dt == c;
           }
           if constexpr (WITH_U) {
             u32x2 pk;
@@ -117,7 +124,17 @@ __global__ __launch_bounds__(NT, 1) void head_fwd_kernel(HeadParams p) {
           }
         }
       }
-      if (hit) p.zt[tok] = ztv;
+      // The lane holds rows mb*32 + 8g + e (+4h) of the block: the target's row is one of them
+      // when its offset dt has bit 2 clear and lies in [0, WTM). That is rare (WTM of V rows
+      // per token), so the select runs behind a wave-uniform branch, skipped by every wave
+      // where no lane hits.
+      const bool mine = (unsigned)dt < (unsigned)HC::WTM && !(dt & 4);
+      if (__builtin_amdgcn_ballot_w64(mine)) {
+        int dsel = dt;
+        asm volatile("" : "+v"(dsel));  // keeps the select inside the branch (not speculated)
+        const float z = select_row(acc, nb, dsel);
+        if (mine) p.zt[tok] = z;
+      }
       part += xor32(part);
       if (h == 0) red[wm][col] = part;
     }

@@ -477,8 +477,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip timing BASELINE configs 1, 2, 3 and 5 beside the headline")
-    ap.add_argument("--only", choices=["attn", "head", "step"],
-                    help="run only W+K launches of one part (for profiler runs) and print its time")
+    ap.add_argument("--only", choices=["attn", "head", "step", "neighbours"],
+                    help="run only W+K launches of one part (for profiler runs) and print its time; "
+                         "'neighbours' runs the timings of the fused prologue, eval head, final norm "
+                         "and feed-forward")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="with --only: also run K device copies of this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -499,6 +501,11 @@ def main():
 
     K, W = args.steps, args.warmup
     log = lambda msg: print(f"bench: {msg}", file=sys.stderr, flush=True)
+    if args.only == "neighbours":
+        out = {"only": "neighbours", "prologue": time_prologue(torch, dev), "eval_head": time_eval_head(torch, x),
+               "final_norm": time_final_norm(torch, x), "ffn": time_ffn(torch, dev)}
+        print(json.dumps(out), flush=True)
+        return 0
     if args.only:
         fn = {"attn": attn_step, "head": head_step, "step": full_step}[args.only]
         t = timed(torch, fn, K, W)
