@@ -103,6 +103,13 @@ def timer_report():
     return json.loads(buf.value.decode())
 
 
+def aligned16(t):
+    """``t`` contiguous and starting on a 16-byte boundary (copied if needed), as the kernels
+    that move 8 bf16 per lane require."""
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 def ptr(t):
     """Device pointer of a tensor (or None)."""
     return None if t is None else ctypes.c_void_p(t.data_ptr())

@@ -21,22 +21,16 @@ def _t(x):
     return x.t().contiguous()
 
 
-def _a16(x):
-    """Contiguous and 16-byte aligned, as the fused kernels' vector accesses need."""
-    x = x.contiguous()
-    return x if x.data_ptr() % 16 == 0 else x.clone()
-
-
 class _FfnFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, h2, w_g, w_u, w_d, beta):
         lib = _lib.load()
         shape = h2.shape
         d = shape[-1]
-        x = _a16(h2).reshape(-1, d)
+        x = _lib.aligned16(h2).reshape(-1, d)
         N, F = x.shape[0], w_g.shape[1]
         w_gu = torch.cat([w_g, w_u], dim=1).to(torch.bfloat16).contiguous()
-        wd = _a16(w_d.to(torch.bfloat16))
+        wd = _lib.aligned16(w_d.to(torch.bfloat16))
         y, gate, up = (torch.empty((N, F), dtype=torch.bfloat16, device=x.device) for _ in range(3))
         _lib.check(lib.alg_ffn_alu_glu_fwd(_lib.stream_of(x), N, d, F, _lib.ptr(x), _lib.ptr(w_gu), float(beta),
                                            _lib.ptr(y), _lib.ptr(gate), _lib.ptr(up)), "alu_glu_ffn")
@@ -52,7 +46,7 @@ class _FfnFn(torch.autograd.Function):
         lib = _lib.load()
         N, d = x.shape
         F, dm = wd.shape
-        do = _a16(dout.to(torch.bfloat16)).reshape(N, dm)
+        do = _lib.aligned16(dout.to(torch.bfloat16)).reshape(N, dm)
         d_gu = torch.empty((N, 2 * F), dtype=torch.bfloat16, device=x.device)
         _lib.check(lib.alg_ffn_alu_glu_dy(_lib.stream_of(x), N, dm, F, _lib.ptr(do), _lib.ptr(wd), _lib.ptr(gate),
                                           _lib.ptr(up), float(beta), _lib.ptr(d_gu)), "alu_glu_ffn backward")

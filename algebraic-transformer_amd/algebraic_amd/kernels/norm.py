@@ -17,7 +17,7 @@ class _RmsNormFn(torch.autograd.Function):
     def forward(ctx, x, gain, eps):
         lib = _lib.load()
         d = x.shape[-1]
-        x2 = x.contiguous().reshape(-1, d)
+        x2 = _lib.aligned16(x).reshape(-1, d)
         rows = x2.shape[0]
         g = None if gain is None else gain.detach().to(device=x.device, dtype=torch.float32).contiguous()
         y = torch.empty_like(x2)
@@ -34,7 +34,7 @@ class _RmsNormFn(torch.autograd.Function):
         x2, g, tau = ctx.saved_tensors
         lib = _lib.load()
         rows, d = x2.shape
-        dy2 = dy.to(x2.dtype).contiguous().reshape(rows, d)
+        dy2 = _lib.aligned16(dy.to(x2.dtype)).reshape(rows, d)
         dx = torch.empty_like(x2)
         dg = torch.empty(d, dtype=torch.float32, device=x2.device) if g is not None else None
         nbytes = lib.alg_rms_norm_workspace_size(rows, d)

@@ -418,6 +418,13 @@ size_t alg_rms_norm_workspace_size(int rows, int d) {
   return align256((size_t)d * alg::rms_norm_blocks(rows) * sizeof(float));
 }
 
+// Kernels that move 8 bf16 (16 bytes) per lane need every matrix on a 16-byte boundary.
+static bool aligned16(std::initializer_list<const void*> ptrs) {
+  for (const void* q : ptrs)
+    if (reinterpret_cast<uintptr_t>(q) & 15) return false;
+  return true;
+}
+
 static int check_rms_norm(int rows, int d, float eps) {
   if (rows <= 0 || d <= 0) return fail(ALG_ERR_INVALID, "rows and d must be positive (got %d, %d)", rows, d);
   if (d % 8) return fail(ALG_ERR_UNSUPPORTED, "d = %d: rows must be 16-byte aligned (d %% 8 == 0)", d);
@@ -431,6 +438,7 @@ int alg_rms_norm_fwd(alg_stream_t stream, int rows, int d, const void* x, const 
   int rc = check_rms_norm(rows, d, eps);
   if (rc) return rc;
   if (!x || !y || !tau) return fail(ALG_ERR_INVALID, "x, y and tau are required");
+  if (!aligned16({x, y})) return fail(ALG_ERR_INVALID, "x and y must be 16-byte aligned");
   alg::RmsNormParams p;
   std::memset(&p, 0, sizeof p);
   p.x = static_cast<const bf16*>(x); p.gain = gain; p.y = static_cast<bf16*>(y); p.tau = tau;
@@ -443,6 +451,7 @@ int alg_rms_norm_bwd(alg_stream_t stream, int rows, int d, const void* x, const 
   int rc = check_rms_norm(rows, d, 1.0f);
   if (rc) return rc;
   if (!x || !tau || !dy || !dx) return fail(ALG_ERR_INVALID, "x, tau, dy and dx are required");
+  if (!aligned16({x, dy, dx})) return fail(ALG_ERR_INVALID, "x, dy and dx must be 16-byte aligned");
   if (dgain && !gain) return fail(ALG_ERR_INVALID, "a gain gradient needs the gain it differentiates");
   const size_t need = alg_rms_norm_workspace_size(rows, d);
   if (dgain && (!workspace || workspace_bytes < need))
@@ -463,13 +472,6 @@ static int check_ffn(int N, int d, int F) {
   if ((double)N * 2 * F > 2.0e9 || (double)d * 2 * F > 2.0e9 || (double)N * d > 2.0e9)
     return fail(ALG_ERR_INVALID, "feed-forward too large");
   return ALG_OK;
-}
-
-// The fused epilogues move 8 bf16 per lane: every matrix must start on a 16-byte boundary.
-static bool aligned16(std::initializer_list<const void*> ptrs) {
-  for (const void* q : ptrs)
-    if (reinterpret_cast<uintptr_t>(q) & 15) return false;
-  return true;
 }
 
 int alg_ffn_alu_glu_fwd(alg_stream_t stream, int N, int d, int F, const void* h2, const void* w_gu, float beta,

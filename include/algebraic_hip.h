@@ -169,7 +169,8 @@ int alg_head_eval(alg_stream_t stream, int N, int d, int V,
  * model's final norm ahead of the head (model.py:208; rms_norm at algebraic.py:76-83).
  * Forward: tau[r] = 1/sqrt(mean(x_r^2) + eps), y = round((x tau) gain) (gain NULL: none).
  * Backward (JAX autodiff of the same expression): dx = round(a tau - x tau^3 sum(a x)/d) with
- * a = gain dy, and dgain (d) f32 = sum over rows of dy x tau (NULL to skip; then no workspace). */
+ * a = gain dy, and dgain (d) f32 = sum over rows of dy x tau (NULL to skip; then no workspace).
+ * x, y, dy and dx are row-major and 16-byte aligned (ALG_ERR_INVALID otherwise). */
 size_t alg_rms_norm_workspace_size(int rows, int d);
 int alg_rms_norm_fwd(alg_stream_t stream, int rows, int d, const void* x, const float* gain, float eps,
                      void* y, float* tau);

@@ -84,3 +84,56 @@ def test_invalid_arguments_fail_before_launch():
     assert rc == _lib.ALG_ERR_INVALID and b"workspace" in handle.alg_last_error()
     with pytest.raises(ValueError):
         _lib.check(_lib.ALG_ERR_INVALID, "probe")
+
+
+def test_neighbour_entry_points_validate_before_launch():
+    """The prologue, eval head, final norm and feed-forward entry points reject bad shapes,
+    missing workspaces, non-finite scalars and misaligned matrices before any launch."""
+    from algebraic_amd import _lib
+    handle = lib()
+    P = ctypes.c_void_p
+    err = lambda: handle.alg_last_error()
+    # Fused prologue: cos without sin, bad eps, workspace too small.
+    args = [None, 0, 1, 2, 4, 128, 128, P(16), P(16), P(16), None, None, P(16), None, 1e-5, None, 0, 8.0, 16, 1,
+            P(16), P(16), P(16), P(16), None, P(16), P(16), 1 << 30]
+    rc = handle.alg_attn_qk_prologue(*args)
+    assert rc == _lib.ALG_ERR_INVALID and b"cos and sin" in err()
+    args[12] = None
+    args[14] = 0.0
+    rc = handle.alg_attn_qk_prologue(*args)
+    assert rc == _lib.ALG_ERR_INVALID and b"eps" in err()
+    args[14] = 1e-5
+    args[-1] = 16
+    rc = handle.alg_attn_qk_prologue(*args)
+    assert rc == _lib.ALG_ERR_INVALID and b"workspace" in err()
+    assert handle.alg_attn_prologue_workspace_size(2, 4, 128, 128) > 16
+    rc = handle.alg_cayley_tables(None, P(16), 0, 128, P(16), P(16))
+    assert rc == _lib.ALG_ERR_INVALID and b"positive" in err()
+    # Eval head: pass 3 sizes its workspace; too small is refused.
+    need = handle.alg_head_workspace_size(512, 256, 1000, 3)
+    assert need > 0
+    rc = handle.alg_head_eval(None, 512, 256, 1000, P(16), P(16), P(16), 8, 2.0, P(16), P(16), P(16), need - 1)
+    assert rc == _lib.ALG_ERR_INVALID and b"workspace" in err()
+    # Final norm: width limits, eps, gain gradient without a gain, alignment.
+    rc = handle.alg_rms_norm_fwd(None, 4, 100, P(16), None, 1e-5, P(16), P(16))
+    assert rc == _lib.ALG_ERR_UNSUPPORTED and b"16-byte" in err()
+    rc = handle.alg_rms_norm_fwd(None, 4, 8192, P(16), None, 1e-5, P(16), P(16))
+    assert rc == _lib.ALG_ERR_UNSUPPORTED and b"at most" in err()
+    rc = handle.alg_rms_norm_fwd(None, 4, 256, P(16), None, float("nan"), P(16), P(16))
+    assert rc == _lib.ALG_ERR_INVALID and b"eps" in err()
+    rc = handle.alg_rms_norm_fwd(None, 4, 256, P(18), None, 1e-5, P(16), P(16))
+    assert rc == _lib.ALG_ERR_INVALID and b"aligned" in err()
+    rc = handle.alg_rms_norm_bwd(None, 4, 256, P(16), None, P(16), P(16), P(16), P(16), P(16), 1 << 20)
+    assert rc == _lib.ALG_ERR_INVALID and b"gain" in err()
+    rc = handle.alg_rms_norm_bwd(None, 4, 256, P(16), P(16), P(16), P(16), P(16), P(16), P(16), 4)
+    assert rc == _lib.ALG_ERR_INVALID and b"workspace" in err()
+    assert handle.alg_rms_norm_workspace_size(16384, 2048) >= 2048 * 4
+    # Feed-forward: d_ff % 128, non-finite beta, misaligned matrices.
+    rc = handle.alg_ffn_alu_glu_fwd(None, 256, 128, 200, P(16), P(16), 0.5, P(16), P(16), P(16))
+    assert rc == _lib.ALG_ERR_UNSUPPORTED and b"128" in err()
+    rc = handle.alg_ffn_alu_glu_fwd(None, 256, 128, 256, P(16), P(16), float("inf"), P(16), P(16), P(16))
+    assert rc == _lib.ALG_ERR_INVALID and b"beta" in err()
+    rc = handle.alg_ffn_alu_glu_fwd(None, 256, 128, 256, P(16), P(16), 0.5, P(16), P(24), P(16))
+    assert rc == _lib.ALG_ERR_INVALID and b"aligned" in err()
+    rc = handle.alg_ffn_alu_glu_dy(None, 256, 128, 256, P(16), P(16), P(16), P(16), 0.5, P(20))
+    assert rc == _lib.ALG_ERR_INVALID and b"aligned" in err()
