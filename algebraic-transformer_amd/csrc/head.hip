@@ -39,11 +39,6 @@ __device__ __forceinline__ float head_w(float z, const HeadParams& p, float& r) 
   return t;
 }
 
-__global__ void head_zero_kernel(float* p, int n) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0.0f;
-}
-
 // z^T = E h^T with the forward epilogue (row sums, target logit, optional U residual).
 // L2N > 0 fixes n = 2^L2N at compile time (0: taken from the parameters).
 // acc[mb][nb][4g + e] for the row offset dt = mb*32 + 8g + e (bit 2 of dt, the lane half,
@@ -271,17 +266,58 @@ __global__ __launch_bounds__(NT, 1) void head_eval_kernel(HeadParams p) {
 // which src/algebraic/evaluation.py:13-23 equals: tests/test_components.py:56), in the log
 // domain so that improbable targets do not underflow; argmax over the vocabulary tiles in
 // order (first index on ties).
+// The per-token reductions over vocabulary tiles below read one value per tile (stride N) and
+// combine them in tile order; the loads are issued TB at a time so their latencies overlap,
+// while the order of the combining steps (and so every result bit) stays that of a plain loop.
+constexpr int TB = 16;
+
+// sum over t in [0, nvt) of part[t * N + tok], added in increasing t.
+__device__ __forceinline__ float sum_tiles(const float* part, int N, int tok, int nvt) {
+  float l = 0.0f;
+  int t = 0;
+  for (; t + TB <= nvt; t += TB) {
+    float v[TB];
+#pragma unroll
+    for (int u = 0; u < TB; ++u) v[u] = part[(size_t)(t + u) * N + tok];
+#pragma unroll
+    for (int u = 0; u < TB; ++u) l += v[u];
+  }
+  for (; t < nvt; ++t) l += part[(size_t)t * N + tok];
+  return l;
+}
+
 __global__ __launch_bounds__(256) void head_eval_stats_kernel(HeadParams p, int nvt) {
   const int tok = blockIdx.x * 256 + threadIdx.x;
   if (tok >= p.N) return;
   float l = 0.0f, m = -INFINITY;
   int ix = 0x7fffffff;
-  for (int t = 0; t < nvt; ++t) {
-    l += p.partial[(size_t)t * p.N + tok];
-    const float pm = p.pmax[(size_t)t * p.N + tok];
-    if (pm > m) { m = pm; ix = p.pidx[(size_t)t * p.N + tok]; }
+  // Sum of the partials and the first tile holding the largest maximum, in tile order.
+  auto take = [&](float pl, float pm, int pi) {
+    l += pl;
+    if (pm > m) { m = pm; ix = pi; }
+  };
+  int t = 0;
+  for (; t + TB <= nvt; t += TB) {
+    float vl[TB], vm[TB];
+    int vi[TB];
+#pragma unroll
+    for (int u = 0; u < TB; ++u) {
+      const size_t o = (size_t)(t + u) * p.N + tok;
+      vl[u] = p.partial[o];
+      vm[u] = p.pmax[o];
+      vi[u] = p.pidx[o];
+    }
+#pragma unroll
+    for (int u = 0; u < TB; ++u) take(vl[u], vm[u], vi[u]);
   }
-  const float x = fminf(p.zt[tok] / p.c, p.clamp);
+  for (; t < nvt; ++t) {
+    const size_t o = (size_t)t * p.N + tok;
+    take(p.partial[o], p.pmax[o], p.pidx[o]);
+  }
+  // The target logit is written by the tile holding the target; out-of-range targets read 0.
+  const int tgt = p.targets[tok];
+  const float zt = tgt >= 0 && tgt < p.V ? p.zt[tok] : 0.0f;
+  const float x = fminf(zt / p.c, p.clamp);
   p.logprob[tok] = (float)(1 << p.log2n) * logf(rho_exact(x)) - logf(l);
   if (p.argmax) p.argmax[tok] = ix;
 }
@@ -293,20 +329,23 @@ __global__ __launch_bounds__(256) void head_stats_kernel(HeadParams p, int nvt) 
   const int tok = blockIdx.x * 256 + threadIdx.x;
   float miss = 0.0f;
   if (tok < p.N) {
-    float l = 0.0f;
-    for (int t = 0; t < nvt; ++t) l += p.partial[(size_t)t * p.N + tok];
+    const float l = sum_tiles(p.partial, p.N, tok, nvt);
     const int n = 1 << p.log2n;
     const float st = inv_root(l, n);
     p.stat[tok] = st;
-    const float zt = p.zt[tok];
+    // The forward wrote zt only where the target lies in [0, V); elsewhere it is 0
+    // (fused_head.py:87 sums no column).
+    const int tgt = p.targets[tok];
+    const bool valid = tgt >= 0 && tgt < p.V;
+    const float zt = valid ? p.zt[tok] : 0.0f;
+    if (!valid) p.zt[tok] = 0.0f;
     const float x = fminf(zt / p.c, p.clamp);
     const float pt = ipow_rt(rho_exact(x) * st, n);
     p.pt[tok] = pt;
     miss = 1.0f - pt;
     if (p.lsum) p.lsum[tok] = l;
     if (p.ut) {
-      const int tgt = p.targets[tok];
-      if (tgt >= 0 && tgt < p.V) {
+      if (valid) {
         float r;
         const float w = head_w(zt, p, r);
         p.ut[(size_t)tok * p.Vp + tgt] = f2bf((w - l) * r);
@@ -512,7 +551,6 @@ int head_dh_split(int N, int d, int V) {
 int head_dh_kchunk(int V, int split) { return ((V + split - 1) / split + 127) / 128 * 128; }
 
 hipError_t launch_head_fwd(const HeadParams& p, hipStream_t st) {
-  { KTimer t("head_zero", st); hipLaunchKernelGGL(head_zero_kernel, dim3((p.N + 255) / 256), dim3(256), 0, st, p.zt, p.N); }
   const int tiles = head_vocab_tiles(p.V) * (p.Npad / HT_N);
   {
     KTimer t("head_fwd", st);
@@ -526,7 +564,6 @@ hipError_t launch_head_fwd(const HeadParams& p, hipStream_t st) {
 }
 
 hipError_t launch_head_eval(const HeadParams& p, hipStream_t st) {
-  { KTimer t("head_zero", st); hipLaunchKernelGGL(head_zero_kernel, dim3((p.N + 255) / 256), dim3(256), 0, st, p.zt, p.N); }
   const int tiles = head_vocab_tiles(p.V) * (p.Npad / HT_N);
   {
     KTimer t("head_eval", st);
