@@ -35,14 +35,15 @@ constexpr int PRE_ROWS = 256;  // rows per pre-kernel workgroup
 // ---------------------------------------------------------------------------
 // pre: di, dq_acc = 0, sink partials
 // ---------------------------------------------------------------------------
-template <typename T>
-__global__ __launch_bounds__(256) void attn_bwd_pre_kernel(AttnBwdParams p, int D, bool zero_dq) {
+// PRECISE: o is read from the f32 o_precise buffer (the shifted fallback saved it) rather
+// than from o. The choice is uniform over the grid (it follows the guard flag), so the kernel
+// branches once into one of two straight-line bodies whose loads are all issued before any is
+// waited for.
+template <typename T, bool PRECISE, int D>
+__device__ __forceinline__ void attn_bwd_pre_body(const AttnBwdParams& p, bool zero_dq, bool shifted) {
   const int bh = blockIdx.x;
   const int head = bh % p.H;
   const int T_ = p.T;
-  bool shifted = p.mode == MODE_SHIFTED;
-  if (p.flag) shifted = *p.flag == 0;
-  const bool precise = shifted && p.o_precise != nullptr;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row0 = blockIdx.y * PRE_ROWS;
   const size_t hb = head_base(bh, p.H, T_, D, p.layout);
@@ -57,15 +58,16 @@ __global__ __launch_bounds__(256) void attn_bwd_pre_kernel(AttnBwdParams p, int 
   // 8 elements per lane, D/8 lanes per row (vector loads of dO, o; vector zero-fill of dq_acc);
   // each lane loads PRE_U rows before reducing any, to keep more bytes in flight.
   constexpr int PRE_U = 4;
-  const int lpr = D / 8, rpw = 64 / lpr;
+  constexpr int lpr = D / 8, rpw = 64 / lpr;
   const int sub = lane / lpr, li = lane - sub * lpr;
   const int rend = min(row0 + PRE_ROWS, T_);
   for (int r0 = row0 + wave * rpw; r0 < rend; r0 += 4 * rpw * PRE_U) {
-    float dov[PRE_U][8], ov[PRE_U][8];
+    float dov[PRE_U][8], ov[PRE_U][8], stv[PRE_U];
 #pragma unroll
     for (int u = 0; u < PRE_U; ++u) {
       const int r = r0 + u * 4 * rpw + sub;
       const int rc = min(r, rend - 1);
+      stv[u] = p.stat[(size_t)bh * T_ + rc];
       const size_t off = ((size_t)bh * T_ + rc) * D + li * 8;  // internal (B, H, T, D) buffers
       const size_t xoff = hb + (size_t)rc * ld + li * 8;        // dO and o in the call's layout
       if constexpr (sizeof(T) == 2) {
@@ -78,8 +80,8 @@ __global__ __launch_bounds__(256) void attn_bwd_pre_kernel(AttnBwdParams p, int 
 #pragma unroll
         for (int j = 0; j < 4; ++j) { dov[u][j] = a0[j]; dov[u][4 + j] = a1[j]; }
       }
-      if (precise || sizeof(T) == 4) {
-        const float* src = precise ? p.o_precise + off : reinterpret_cast<const float*>(p.o) + xoff;
+      if constexpr (PRECISE || sizeof(T) == 4) {
+        const float* src = PRECISE ? p.o_precise + off : reinterpret_cast<const float*>(p.o) + xoff;
         const floatx4 b0 = *reinterpret_cast<const floatx4*>(src);
         const floatx4 b1 = *reinterpret_cast<const floatx4*>(src + 4);
 #pragma unroll
@@ -103,10 +105,11 @@ __global__ __launch_bounds__(256) void attn_bwd_pre_kernel(AttnBwdParams p, int 
         *reinterpret_cast<floatx4*>(p.dq_acc + off) = z;
         *reinterpret_cast<floatx4*>(p.dq_acc + off + 4) = z;
       }
+#pragma unroll
       for (int m = 1; m < lpr; m <<= 1) s += __shfl_xor(s, m, 64);
       if (ok && li == 0) {
         p.di[(size_t)bh * T_ + r] = s;
-        const float st = p.stat[(size_t)bh * T_ + r];
+        const float st = stv[u];
         const float mass = inv_stat ? rbn * st : ipow_rt(rb * st, n);
         part += mass * s;
       }
@@ -117,6 +120,20 @@ __global__ __launch_bounds__(256) void attn_bwd_pre_kernel(AttnBwdParams p, int 
   if (lane == 0) red[wave] = part;
   __syncthreads();
   if (threadIdx.x == 0) p.sink_part[(size_t)bh * gridDim.y + blockIdx.y] = red[0] + red[1] + red[2] + red[3];
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void attn_bwd_pre_kernel(AttnBwdParams p, int D, bool zero_dq) {
+  bool shifted = p.mode == MODE_SHIFTED;
+  if (p.flag) shifted = *p.flag == 0;
+  const bool precise = shifted && p.o_precise != nullptr;
+  if (D == 128) {
+    if (precise) attn_bwd_pre_body<T, true, 128>(p, zero_dq, shifted);
+    else attn_bwd_pre_body<T, false, 128>(p, zero_dq, shifted);
+  } else {
+    if (precise) attn_bwd_pre_body<T, true, 64>(p, zero_dq, shifted);
+    else attn_bwd_pre_body<T, false, 64>(p, zero_dq, shifted);
+  }
 }
 
 // ---------------------------------------------------------------------------

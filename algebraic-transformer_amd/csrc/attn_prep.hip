@@ -12,18 +12,19 @@ namespace alg {
 
 __device__ __forceinline__ float nanmax(float a, float b) { return (a > b || a != a) ? a : b; }
 
-
-
-template <typename T>
-__global__ __launch_bounds__(256) void attn_prep_kernel(PrepParams p) {
+// Head dim D and whether the guard maxima are wanted are fixed per launch, so the kernel
+// branches once into a straight-line body: all PREP_U rows' loads are issued before any is
+// waited for, and the row sums are unrolled shuffles.
+template <typename T, int D, bool GUARD>
+__device__ __forceinline__ void attn_prep_body(const PrepParams& p) {
   constexpr int CH = 16 / sizeof(T);
-  const int lpr = p.D / CH;                 // lanes per row
-  const int rpw = 64 / lpr;                 // rows per wave per step
+  constexpr int lpr = D / CH;               // lanes per row
+  constexpr int rpw = 64 / lpr;             // rows per wave per step
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane / lpr, li = lane - sub * lpr;
   float mq = 0.0f, mk = 0.0f, mv = 0.0f;
   // Each lane loads PREP_U rows before reducing any (more bytes in flight per lane).
-  constexpr int PREP_U = 2;
+  constexpr int PREP_U = 4;
   const size_t step = (size_t)gridDim.x * 4 * rpw;
   for (size_t r0 = ((size_t)blockIdx.x * 4 + wave) * rpw; r0 < p.rows; r0 += step * PREP_U) {
     T qv[PREP_U][CH], kv[PREP_U][CH], vv[PREP_U][CH];
@@ -32,7 +33,7 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(PrepParams p) {
       const size_t r = r0 + u * step + sub;
       const size_t off = (r < p.rows ? r : p.rows - 1) * p.D + li * CH;
       *reinterpret_cast<uint4*>(qv[u]) = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.q) + off);
-      if (p.want_guard) {
+      if constexpr (GUARD) {
         *reinterpret_cast<uint4*>(kv[u]) = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.k) + off);
         *reinterpret_cast<uint4*>(vv[u]) = *reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(p.v) + off);
       }
@@ -52,7 +53,7 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(PrepParams p) {
           sq += f * f;
         }
         *reinterpret_cast<uint4*>(reinterpret_cast<T*>(p.q_s) + off) = *reinterpret_cast<uint4*>(out);
-        if (p.want_guard) {
+        if constexpr (GUARD) {
 #pragma unroll
           for (int j = 0; j < CH; ++j) {
             const float kf = (float)kv[u][j];
@@ -62,6 +63,7 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(PrepParams p) {
         }
       }
       // Row sums across the lanes of one row.
+#pragma unroll
       for (int m = 1; m < lpr; m <<= 1) {
         sq += __shfl_xor(sq, m, 64);
         sk += __shfl_xor(sk, m, 64);
@@ -83,6 +85,17 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(PrepParams p) {
     float m = red[0][threadIdx.x];
     for (int w = 1; w < 4; ++w) m = nanmax(m, red[w][threadIdx.x]);
     p.part[blockIdx.x * 3 + threadIdx.x] = m;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void attn_prep_kernel(PrepParams p) {
+  if (p.D == 128) {
+    if (p.want_guard) attn_prep_body<T, 128, true>(p);
+    else attn_prep_body<T, 128, false>(p);
+  } else {
+    if (p.want_guard) attn_prep_body<T, 64, true>(p);
+    else attn_prep_body<T, 64, false>(p);
   }
 }
 
