@@ -1064,11 +1064,21 @@ __global__ __launch_bounds__(256) void attn_bwd_post_kernel(AttnBwdParams p, siz
   if (blockIdx.x == 0 && p.dbeta) {
     bool shifted = p.mode == MODE_SHIFTED;
     if (p.flag) shifted = *p.flag == 0;
-    for (int hh = threadIdx.x; hh < p.H; hh += blockDim.x) {
-      if (!p.sink) { p.dbeta[hh] = 0.0f; continue; }
+    // One wave per head: lane l adds partials l, l + 64, ... of the head's B * nblk, then a
+    // butterfly over the wave (a fixed order for a given shape).
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwave = blockDim.x >> 6;
+    const int cnt = p.B * nblk;
+    for (int hh = wave; hh < p.H; hh += nwave) {
       float s = 0.0f;
-      for (int b = 0; b < p.B; ++b)
-        for (int k = 0; k < nblk; ++k) s += p.sink_part[(size_t)(b * p.H + hh) * nblk + k];
+      if (p.sink)
+        for (int i = lane; i < cnt; i += 64) {
+          const int b = i / nblk, k = i - b * nblk;
+          s += p.sink_part[(size_t)(b * p.H + hh) * nblk + k];
+        }
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
+      if (lane != 0) continue;
+      if (!p.sink) { p.dbeta[hh] = 0.0f; continue; }
       float beta = p.sink[hh];
       const bool clipped = !shifted && p.mode == MODE_CLIPPED && !p.flag;
       float bb = clipped ? fminf(beta, p.clamp) : beta;
