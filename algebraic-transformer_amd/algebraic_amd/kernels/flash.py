@@ -105,7 +105,7 @@ class _FlashFn(torch.autograd.Function):
         dt = _DTYPES[q.dtype]
         dev = q.device
         st = _lib.stream_of(q)
-        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        q, k, v = _lib.aligned16(q), _lib.aligned16(k), _lib.aligned16(v)
         has_sink = sink_logit is not None
         sink_in = None
         if has_sink:
@@ -144,7 +144,7 @@ class _FlashFn(torch.autograd.Function):
         dt = _DTYPES[q_s.dtype]
         dev = q_s.device
         st = _lib.stream_of(q_s)
-        do = do.to(q_s.dtype).contiguous()
+        do = _lib.aligned16(do.to(q_s.dtype))
         ws_bytes = lib.alg_attn_workspace_size(B, H, T, D)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         dq = torch.empty_like(q_s)

@@ -41,8 +41,8 @@ class _HeadFn(torch.autograd.Function):
         lib = _lib.load()
         dev = h.device
         st = _lib.stream_of(h)
-        h = h.contiguous()
-        e = embed.detach().to(h.dtype).contiguous()        # fused_head.py:168
+        h = _lib.aligned16(h)
+        e = _lib.aligned16(embed.detach().to(h.dtype))        # fused_head.py:168
         t = targets.to(device=dev, dtype=torch.int32).contiguous()
         ws_bytes = lib.alg_head_workspace_size(N, d, V, 0)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
@@ -130,8 +130,8 @@ def head_logprob(h, embed, targets, *, head="alg_ce", n=8, c=2.0, argmax=True):
     lib = _lib.load()
     N, d = h.shape
     V = embed.shape[0]
-    h = h.contiguous()
-    E = embed.to(h.dtype).contiguous()  # the cast of fused_head.py:168
+    h = _lib.aligned16(h)
+    E = _lib.aligned16(embed.to(h.dtype))  # the cast of fused_head.py:168
     t = targets.to(device=h.device, dtype=torch.int32).contiguous()
     logprob = torch.empty(N, dtype=torch.float32, device=h.device)
     am = torch.empty(N, dtype=torch.int32, device=h.device) if argmax else None

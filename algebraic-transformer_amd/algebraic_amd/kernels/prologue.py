@@ -71,7 +71,7 @@ class _PrologueFlashFn(torch.autograd.Function):
         dt = _DTYPES[q.dtype]
         dev = q.device
         st = _lib.stream_of(q)
-        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        q, k, v = _lib.aligned16(q), _lib.aligned16(k), _lib.aligned16(v)
         gq, gk = _f32_or_none(q_gain, dev), _f32_or_none(k_gain, dev)
         cs, sn = _f32_or_none(cos, dev), _f32_or_none(sin, dev)
         if cs is not None and (cs.shape[0] < T or cs.shape[1] != D // 2 or sn.shape != cs.shape):
@@ -122,7 +122,7 @@ class _PrologueFlashFn(torch.autograd.Function):
         dt = _DTYPES[q.dtype]
         dev = q.device
         st = _lib.stream_of(q)
-        do = do.to(q.dtype).contiguous()
+        do = _lib.aligned16(do.to(q.dtype))
         ws_bytes = lib.alg_attn_workspace_size(B, H, T, D)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         dq_r, dk_r, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)

@@ -188,6 +188,15 @@ int check_prologue(int dtype, int layout, int B, int H, int T, int D, const floa
   return ALG_OK;
 }
 
+// Every matrix (and workspace) is read or written 16 bytes per lane: its base must sit on a
+// 16-byte boundary (rows stay aligned because row lengths are multiples of 8 elements).
+// Null pointers (optional arguments) pass.
+bool aligned16(std::initializer_list<const void*> ptrs) {
+  for (const void* q : ptrs)
+    if (reinterpret_cast<uintptr_t>(q) & 15) return false;
+  return true;
+}
+
 }  // namespace
 
 extern "C" {
@@ -208,6 +217,7 @@ int alg_attn_prepare(alg_stream_t stream, int dtype, int B, int H, int T, int D,
   if ((rc = check_n(n))) return rc;
   if (!(c > 0.0f) || !std::isfinite(c)) return fail(ALG_ERR_INVALID, "asinh scale c must be positive and finite");
   if (!q || !q_s || !guard_flag) return fail(ALG_ERR_INVALID, "q, q_s and guard_flag are required");
+  if (!aligned16({q, k, v, q_s, workspace})) return fail(ALG_ERR_INVALID, "matrices must be 16-byte aligned");
   if (range_guard && (!k || !v)) return fail(ALG_ERR_INVALID, "range_guard needs k and v");
   if (sink_logit && sink_count != 1 && sink_count != H) return fail(ALG_ERR_INVALID, "sink_count must be 1 or H");
   if (sink_logit && !sink_scaled) return fail(ALG_ERR_INVALID, "sink_scaled output required with a sink");
@@ -249,6 +259,7 @@ int alg_attn_qk_prologue(alg_stream_t stream, int dtype, int layout, int B, int 
   if (!(c > 0.0f) || !std::isfinite(c)) return fail(ALG_ERR_INVALID, "asinh scale c must be positive and finite");
   if (!q || !k || !q_s || !k_r || !tau_q || !tau_k || !guard_flag)
     return fail(ALG_ERR_INVALID, "q, k, q_s, k_r, tau_q, tau_k and guard_flag are required");
+  if (!aligned16({q, k, v, q_s, k_r, workspace})) return fail(ALG_ERR_INVALID, "matrices must be 16-byte aligned");
   if (range_guard && !v) return fail(ALG_ERR_INVALID, "range_guard needs v");
   if (sink_logit && sink_count != 1 && sink_count != H) return fail(ALG_ERR_INVALID, "sink_count must be 1 or H");
   if (sink_logit && !sink_scaled) return fail(ALG_ERR_INVALID, "sink_scaled output required with a sink");
@@ -278,6 +289,8 @@ int alg_attn_qk_prologue_bwd(alg_stream_t stream, int dtype, int layout, int B, 
   if (rc) return rc;
   if (!q || !k || !tau_q || !tau_k || !dq_r || !dk_r || !dq || !dk)
     return fail(ALG_ERR_INVALID, "q, k, tau_q, tau_k, dq_r, dk_r, dq and dk are required");
+  if (!aligned16({q, k, dq_r, dk_r, dq, dk, workspace}))
+    return fail(ALG_ERR_INVALID, "matrices must be 16-byte aligned");
   if ((dq_gain && !q_gain) || (dk_gain && !k_gain))
     return fail(ALG_ERR_INVALID, "a gain gradient needs the gain it differentiates");
   const PrologueWs ws = prologue_ws(B, H, T, D);
@@ -300,6 +313,7 @@ int alg_attn_fwd(alg_stream_t stream, int dtype, int layout, int B, int H, int T
   if ((rc = check_layout(layout, H, T, D))) return rc;
   if ((rc = check_n(n))) return rc;
   if (!q_s || !k || !v || !o || !stat) return fail(ALG_ERR_INVALID, "q_s, k, v, o and stat are required");
+  if (!aligned16({q_s, k, v, o, o_precise})) return fail(ALG_ERR_INVALID, "matrices must be 16-byte aligned");
   if (variant < ALG_ATTN_INRANGE || variant > ALG_ATTN_GUARDED) return fail(ALG_ERR_INVALID, "unknown variant %d", variant);
   if (variant == ALG_ATTN_GUARDED && !guard_flag) return fail(ALG_ERR_INVALID, "GUARDED needs guard_flag");
   alg::AttnFwdParams p;
@@ -333,6 +347,8 @@ int alg_attn_bwd(alg_stream_t stream, int dtype, int layout, int B, int H, int T
   if ((rc = check_n(n))) return rc;
   if (!q_s || !k || !v || !o || !stat || !dO || !dq || !dk || !dv || !di)
     return fail(ALG_ERR_INVALID, "q_s, k, v, o, stat, dO, dq, dk, dv and di are required");
+  if (!aligned16({q_s, k, v, o, o_precise, dO, dq, dk, dv, workspace}))
+    return fail(ALG_ERR_INVALID, "matrices must be 16-byte aligned");
   if (variant < ALG_ATTN_INRANGE || variant > ALG_ATTN_GUARDED) return fail(ALG_ERR_INVALID, "unknown variant %d", variant);
   if (variant == ALG_ATTN_GUARDED && !guard_flag) return fail(ALG_ERR_INVALID, "GUARDED needs guard_flag");
   const AttnWs ws = attn_ws(B, H, T, D);
@@ -401,6 +417,7 @@ int alg_head_fwd(alg_stream_t stream, int N, int d, int V, const void* h, const 
   int rc = check_head(N, d, V, n, c);
   if (rc) return rc;
   if (!h || !E || !targets || !stat || !zt || !pt || !obj) return fail(ALG_ERR_INVALID, "null argument");
+  if (!aligned16({h, E, residual, workspace})) return fail(ALG_ERR_INVALID, "matrices must be 16-byte aligned");
   const HeadWs ws = head_ws(N, d, V, 0, residual != nullptr);
   if (!workspace || workspace_bytes < ws.total)
     return fail(ALG_ERR_INVALID, "workspace too small: need %zu bytes", ws.total);
@@ -416,13 +433,6 @@ int alg_head_fwd(alg_stream_t stream, int N, int d, int V, const void* h, const 
 size_t alg_rms_norm_workspace_size(int rows, int d) {
   if (rows <= 0 || d <= 0) return 0;
   return align256((size_t)d * alg::rms_norm_blocks(rows) * sizeof(float));
-}
-
-// Kernels that move 8 bf16 (16 bytes) per lane need every matrix on a 16-byte boundary.
-static bool aligned16(std::initializer_list<const void*> ptrs) {
-  for (const void* q : ptrs)
-    if (reinterpret_cast<uintptr_t>(q) & 15) return false;
-  return true;
 }
 
 static int check_rms_norm(int rows, int d, float eps) {
@@ -510,6 +520,7 @@ int alg_head_eval(alg_stream_t stream, int N, int d, int V, const void* h, const
   int rc = check_head(N, d, V, n, c);
   if (rc) return rc;
   if (!h || !E || !targets || !logprob) return fail(ALG_ERR_INVALID, "null argument");
+  if (!aligned16({h, E, workspace})) return fail(ALG_ERR_INVALID, "matrices must be 16-byte aligned");
   const HeadEvalWs ws = head_eval_ws(N, V);
   if (!workspace || workspace_bytes < ws.total)
     return fail(ALG_ERR_INVALID, "workspace too small: need %zu bytes", ws.total);
@@ -532,6 +543,7 @@ int alg_head_bwd(alg_stream_t stream, int N, int d, int V, const void* h, const 
   int rc = check_head(N, d, V, n, c);
   if (rc) return rc;
   if (!h || !E || !targets || !stat || !g || !dh || !dE) return fail(ALG_ERR_INVALID, "null argument");
+  if (!aligned16({h, E, residual, dh, dE, workspace})) return fail(ALG_ERR_INVALID, "matrices must be 16-byte aligned");
   if (dE_dtype != ALG_DTYPE_BF16 && dE_dtype != ALG_DTYPE_F32) return fail(ALG_ERR_INVALID, "dE dtype must be bf16 or f32");
   const HeadWs ws = head_ws(N, d, V, 1, residual != nullptr);
   if (!workspace || workspace_bytes < ws.total)

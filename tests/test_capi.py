@@ -137,3 +137,17 @@ def test_neighbour_entry_points_validate_before_launch():
     assert rc == _lib.ALG_ERR_INVALID and b"aligned" in err()
     rc = handle.alg_ffn_alu_glu_dy(None, 256, 128, 256, P(16), P(16), P(16), P(16), 0.5, P(20))
     assert rc == _lib.ALG_ERR_INVALID and b"aligned" in err()
+
+
+def test_hot_path_entry_points_reject_misaligned_matrices():
+    """Attention and head matrices are moved 16 bytes per lane: a base off a 16-byte boundary
+    is refused before any launch."""
+    from algebraic_amd import _lib
+    handle = lib()
+    P = ctypes.c_void_p
+    rc = handle.alg_attn_fwd(None, 0, 0, 1, 1, 64, 64, P(18), P(16), P(16), None, 16, 0, None, 0.0, 1, 1,
+                             P(16), None, P(16))
+    assert rc == _lib.ALG_ERR_INVALID and b"aligned" in handle.alg_last_error()
+    rc = handle.alg_head_fwd(None, 128, 256, 1000, P(16), P(40), P(16), 8, 2.0, P(16), P(16), P(16), P(16),
+                             None, P(16), 1 << 30)
+    assert rc == _lib.ALG_ERR_INVALID and b"aligned" in handle.alg_last_error()
