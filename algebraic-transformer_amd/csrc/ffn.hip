@@ -23,12 +23,17 @@ constexpr int FNT = FC::THREADS;
 
 namespace {
 
-// alu(z) with the reference's negative-tail form; u, r returned for the derivative.
+// alu(z) with the reference's negative-tail form; u, r returned for the derivative
+// (algebraic.py:84-91). r is the hardware reciprocal square root, as the reference's
+// lax.rsqrt; the tail's r^2 / (1 - u) (1 - u in (1, 2)) is a reciprocal multiply, within
+// 2 ulp of the f32 quotient before the result is rounded to bf16. An IEEE sqrt and two IEEE
+// divisions here cost about three times the VALU of the rest of the epilogue.
 __device__ __forceinline__ float alu_f32(float z, float beta, float& u, float& r) {
   const float bz = __fmul_rn(beta, z);
-  r = 1.0f / sqrtf(__fadd_rn(1.0f, __fmul_rn(bz, bz)));
+  r = rsq(__fadd_rn(1.0f, __fmul_rn(bz, bz)));
   u = __fmul_rn(bz, r);
-  const float one_plus_u = bz < 0.0f ? __fmul_rn(r, r) / __fsub_rn(1.0f, u) : __fadd_rn(1.0f, u);
+  const float one_plus_u =
+      bz < 0.0f ? __fmul_rn(__fmul_rn(r, r), __builtin_amdgcn_rcpf(__fsub_rn(1.0f, u))) : __fadd_rn(1.0f, u);
   return __fmul_rn(__fmul_rn(0.5f, z), one_plus_u);
 }
 
