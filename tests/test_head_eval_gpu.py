@@ -89,3 +89,31 @@ def test_head_logprob_full_size(shape):
     gap = float(torch.cat(gaps).max())
     print(f"  max |logprob - float64| = {err:.2e}, argmax agreement {agree:.5f}, worst gap {gap:.1e}", flush=True)
     assert err < 1e-4 and agree >= 0.99 and gap <= 1e-5
+
+
+def test_out_of_range_targets_read_a_zero_logit():
+    """A target outside [0, V) contributes no column (fused_head.py:87 sums none), so its
+    logit reads 0: the training head's telemetry is rho(0)^n stat^n = 1/l and the eval head's
+    log p is -log l, with l (and stat) unchanged from a run with valid targets. Covers the
+    interior and the edge vocabulary tiles (V not a multiple of the tile)."""
+    from algebraic_amd.kernels.fused_head import fused_head, head_logprob
+    N, d, V = 512, 256, 1000
+    h, E, t = head_inputs(N, d, V, seed=23)
+    bad = t.copy()
+    bad[::7] = -1
+    bad[3::7] = V
+    bad[5::7] = V + 37
+    invalid = (bad < 0) | (bad >= V)
+    stat, _, pt_ref, _ = OH.kernel_forward(h, E, t, n=8, c=2.0)
+    th = torch.tensor(h, device="cuda").to(torch.bfloat16)
+    tE = torch.tensor(E, device="cuda").to(torch.bfloat16)
+    tb = torch.tensor(bad, device="cuda")
+    _, tel = fused_head(th, tE, tb, kind="alg_ce", n=8, c=2.0)
+    lp, _ = head_logprob(th, tE, tb, n=8, c=2.0)
+    torch.cuda.synchronize()
+    tel = tel.cpu().numpy().astype(np.float64)
+    lp = lp.cpu().numpy().astype(np.float64)
+    st = stat.astype(np.float64)
+    np.testing.assert_allclose(tel[invalid], st[invalid] ** 8, rtol=2e-5)
+    np.testing.assert_allclose(lp[invalid], 8 * np.log(st[invalid]), atol=2e-5)
+    np.testing.assert_allclose(tel[~invalid], pt_ref[~invalid], rtol=1e-4, atol=1e-9)
