@@ -29,17 +29,20 @@ def _dev(a):
     return torch.tensor(a, device="cuda").to(torch.bfloat16)
 
 
-@pytest.mark.parametrize("N,d,F", [(256, 128, 256), (300, 256, 384), (512, 384, 1024), (200, 72, 128)])
-def test_ffn_matches_oracle(N, d, F):
+@pytest.mark.parametrize("N,d,F,beta", [(256, 128, 256, 0.5), (300, 256, 384, 0.5), (512, 384, 1024, 0.5),
+                                         (200, 72, 128, 0.5), (300, 256, 384, 1.0), (200, 72, 128, 0.8)])
+def test_ffn_matches_oracle(N, d, F, beta):
+    """beta 0.5 is the model's SiLU-matched slope, 1.0 the reference's default (algebraic.py:97)
+    and 0.8 its GELU-matched one."""
     from algebraic_amd.kernels.ffn import alu_glu_ffn
     h2, w_g, w_u, w_d, dout = _inputs(N, d, F, d, seed=N + F)
-    print(f"[ffn] N={N} d={d} F={F}", flush=True)
+    print(f"[ffn] N={N} d={d} F={F} beta={beta}", flush=True)
     t = [_dev(a).requires_grad_(True) for a in (h2, w_g, w_u, w_d)]
-    out = alu_glu_ffn(*t, beta=0.5)
+    out = alu_glu_ffn(*t, beta=beta)
     out.backward(_dev(dout))
     torch.cuda.synchronize()
-    o_ref, _, _, _ = OF.ffn_forward(h2, w_g, w_u, w_d, 0.5)
-    dh2, dw_g, dw_u, dw_d, _, _ = OF.ffn_backward(h2, w_g, w_u, w_d, dout, 0.5)
+    o_ref, _, _, _ = OF.ffn_forward(h2, w_g, w_u, w_d, beta)
+    dh2, dw_g, dw_u, dw_d, _, _ = OF.ffn_backward(h2, w_g, w_u, w_d, dout, beta)
     g = lambda x: x.detach().float().cpu().numpy()
     errs = {"out": rel_l2(g(out), o_ref), "dh2": rel_l2(g(t[0].grad), dh2), "dw_g": rel_l2(g(t[1].grad), dw_g),
             "dw_u": rel_l2(g(t[2].grad), dw_u), "dw_d": rel_l2(g(t[3].grad), dw_d)}
