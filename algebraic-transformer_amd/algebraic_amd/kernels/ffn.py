@@ -60,9 +60,9 @@ def alu_glu_ffn(h2, w_g, w_u, w_d, beta: float = 0.5):
     """(h2 @ w_g * alu(h2 @ w_u, beta)) @ w_d for bfloat16 GPU tensors (model.py:185-193)."""
     if h2.dtype != torch.bfloat16:
         raise NotImplementedError(f"dtype {h2.dtype}: the gfx950 feed-forward takes bfloat16 activations")
-    if not h2.is_cuda:
-        raise RuntimeError("alu_glu_ffn needs GPU tensors (no CPU fallback)")
     d = h2.shape[-1]
     if w_g.shape != w_u.shape or w_g.shape[0] != d or w_d.shape[0] != w_g.shape[1]:
         raise ValueError("w_g, w_u must be (d, d_ff) and w_d (d_ff, d_out)")
+    if not h2.is_cuda:
+        raise RuntimeError("alu_glu_ffn needs GPU tensors (no CPU fallback)")
     return _FfnFn.apply(h2, w_g, w_u, w_d, float(beta))

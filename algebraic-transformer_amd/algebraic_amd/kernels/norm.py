@@ -50,8 +50,8 @@ def rms_norm(x, gain=None, eps: float = 1e-5):
     """``round((x rsqrt(mean(x^2) + eps)) gain)`` over the last axis of a bfloat16 GPU tensor."""
     if x.dtype != torch.bfloat16:
         raise NotImplementedError(f"dtype {x.dtype}: the gfx950 norm takes bfloat16 rows")
-    if not x.is_cuda:
-        raise RuntimeError("rms_norm needs a GPU tensor (no CPU fallback)")
     if gain is not None and gain.numel() != x.shape[-1]:
         raise ValueError(f"gain must have {x.shape[-1]} entries")
+    if not x.is_cuda:
+        raise RuntimeError("rms_norm needs a GPU tensor (no CPU fallback)")
     return _RmsNormFn.apply(x, gain, float(eps))

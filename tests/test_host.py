@@ -66,3 +66,41 @@ def test_fused_head_validation():
         fused_head(h.float(), E, t, kind="alg_ce")
     with pytest.raises(RuntimeError):
         fused_head(h, E, t, kind="alg_ce", n=8, c=2.0)               # CPU tensors: no fallback
+
+
+def test_neighbour_mirrors_validate_before_any_launch():
+    """The final norm, feed-forward, eval head and prologue mirrors refuse unsupported dtypes,
+    CPU tensors (no host fallback) and inconsistent shapes before touching a GPU."""
+    from algebraic_amd.kernels.ffn import alu_glu_ffn
+    from algebraic_amd.kernels.fused_head import head_logprob
+    from algebraic_amd.kernels.norm import rms_norm
+    from algebraic_amd.kernels.prologue import cayley_powers, cayley_table_geometric
+    x = torch.zeros(4, 256, dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError):
+        rms_norm(x.float())
+    with pytest.raises(RuntimeError):
+        rms_norm(x)
+    with pytest.raises(ValueError):
+        rms_norm(x, torch.ones(128))
+    h2, wg, wd = torch.zeros(8, 64, dtype=torch.bfloat16), torch.zeros(64, 128), torch.zeros(128, 64)
+    with pytest.raises(NotImplementedError):
+        alu_glu_ffn(h2.float(), wg, wg, wd)
+    with pytest.raises(ValueError):
+        alu_glu_ffn(h2, wg, wg[:, :64], wd)
+    with pytest.raises(RuntimeError):
+        alu_glu_ffn(h2, wg, wg, wd)
+    h, E, t = torch.zeros(16, 64, dtype=torch.bfloat16), torch.zeros(100, 64), torch.zeros(16, dtype=torch.int32)
+    with pytest.raises(NotImplementedError):
+        head_logprob(h, E, t, head="ce")
+    with pytest.raises(ValueError):
+        head_logprob(h, E, t, n=6)
+    with pytest.raises(NotImplementedError):
+        head_logprob(h.float(), E, t)
+    with pytest.raises(RuntimeError):
+        head_logprob(h, E, t)
+    with pytest.raises(ValueError):
+        cayley_table_geometric(96, 128)           # head_dim / 2 = 48: not a power of two
+    with pytest.raises(ValueError):
+        cayley_powers(torch.zeros(2, 4), 8)
+    with pytest.raises(RuntimeError):
+        cayley_powers(torch.zeros(4), 8)
