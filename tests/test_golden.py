@@ -4,7 +4,9 @@ Fixtures (tests/golden/*.npz, written by tests/golden/make_golden.py) hold bf16-
 the float64 closed-form outputs of softmax attention over n*asinh(s/c) logits with a sink column
 and of the algebraic head's true NLL (tests/test_components.py:27-56 in the reference), stored
 as float32. The dense float64 oracle must reproduce them to float32 storage precision; the
-cast-faithful kernel restatements must meet the north-star bars (bf16 2e-2, fp32 1e-5).
+cast-faithful kernel restatements must meet the north-star bars (bf16 2e-2, fp32 1e-5). The
+final RMS norm and ALU-GLU fixtures hold their float64 definitions (algebraic.py:76-103,
+model.py:185-193) and gradients; the oracle meets them the same way.
 """
 
 import glob
@@ -80,3 +82,41 @@ def test_kernel_head_oracle_within_bar_of_golden(path):
     assert rel_l2(pt, g["pt"]) < 2e-2
     assert rel_l2(dh, g["dh"]) < 1e-2
     assert rel_l2(dE, g["dE"]) < 1e-2
+
+
+NORM = sorted(glob.glob(os.path.join(GOLDEN, "norm_*.npz")))
+FFN = sorted(glob.glob(os.path.join(GOLDEN, "ffn_*.npz")))
+
+
+def test_neighbour_fixtures_present():
+    assert len(NORM) >= 2 and len(FFN) >= 2
+
+
+@pytest.mark.parametrize("dtype,tol", [("f32", 1e-5), ("bf16", 2e-2)])
+@pytest.mark.parametrize("path", NORM, ids=os.path.basename)
+def test_norm_oracle_matches_golden(path, dtype, tol):
+    """oracle/prologue.py rms_norm and rms_norm_vjp against the float64 definition
+    (algebraic.py:76-83): f32 to storage precision, the bf16 cast-faithful form within 2e-2."""
+    from oracle import prologue as OP
+    z = load(path)
+    g = z.get("gain")
+    y, tau = OP.rms_norm(z["x"], g, float(z["eps"]), dtype)
+    dx, dg = OP.rms_norm_vjp(z["x"], g, tau, z["dy"], dtype)
+    errs = {"y": rel_l2(y, z["y"]), "dx": rel_l2(dx, z["dx"])}
+    if g is not None:
+        errs["dgain"] = rel_l2(dg, z["dgain"])
+    assert max(errs.values()) < tol, errs
+
+
+@pytest.mark.parametrize("dtype,tol", [("f32", 1e-5), ("bf16", 2e-2)])
+@pytest.mark.parametrize("path", FFN, ids=os.path.basename)
+def test_ffn_oracle_matches_golden(path, dtype, tol):
+    """oracle/ffn.py against the float64 ALU-GLU block (model.py:185-193, algebraic.py:84-103)."""
+    from oracle import ffn as OF
+    z = load(path)
+    beta = float(z["beta"])
+    out, *_ = OF.ffn_forward(z["h2"], z["w_g"], z["w_u"], z["w_d"], beta, dtype)
+    dh2, dw_g, dw_u, dw_d, _, _ = OF.ffn_backward(z["h2"], z["w_g"], z["w_u"], z["w_d"], z["dout"], beta, dtype)
+    errs = {"out": rel_l2(out, z["out"]), "dh2": rel_l2(dh2, z["dh2"]), "dw_g": rel_l2(dw_g, z["dw_g"]),
+            "dw_u": rel_l2(dw_u, z["dw_u"]), "dw_d": rel_l2(dw_d, z["dw_d"])}
+    assert max(errs.values()) < tol, errs

@@ -4,7 +4,9 @@ The HIP attention (flash_attention mirror, guarded asinh path) and fused head (f
 mirror, alg_ce) run on the fixture inputs through the C ABI; outputs and gradients must meet
 the north-star bars against the float64 closed forms: bf16 relative L2 2e-2 (attention),
 head objective rtol 2e-3, telemetry 2e-2 and gradients 1e-2 (tests/test_fused_head_tpu.py:33-43
-in the reference); fp32 attention 1e-5.
+in the reference); fp32 attention 1e-5. The final RMS norm and the ALU-GLU block run on their
+fixtures at the bf16 bar (2e-2); the streamed eval head on the head fixtures gives log pt of
+the closed form (1e-4 absolute) and a float64 argmax.
 """
 
 import glob
@@ -68,3 +70,58 @@ def test_head_matches_golden(path):
     assert rel_l2(f64(pt), g["pt"]) < 2e-2
     assert rel_l2(f64(h.grad), g["dh"]) < 1e-2
     assert rel_l2(f64(E.grad), g["dE"]) < 1e-2
+
+
+NORM = sorted(glob.glob(os.path.join(GOLDEN, "norm_*.npz")))
+FFN = sorted(glob.glob(os.path.join(GOLDEN, "ffn_*.npz")))
+
+
+@pytest.mark.parametrize("path", NORM, ids=os.path.basename)
+def test_norm_matches_golden(path):
+    """The HIP final RMS norm (bf16 rows) against the float64 definition: bf16 bar 2e-2."""
+    from algebraic_amd.kernels.norm import rms_norm
+    z = load(path)
+    x = torch.tensor(z["x"], device="cuda").to(torch.bfloat16).requires_grad_(True)
+    g = torch.tensor(z["gain"], device="cuda", requires_grad=True) if "gain" in z else None
+    print(f"[golden] {os.path.basename(path)}", flush=True)
+    y = rms_norm(x, g, eps=float(z["eps"]))
+    y.backward(torch.tensor(z["dy"], device="cuda").to(torch.bfloat16))
+    torch.cuda.synchronize()
+    errs = {"y": rel_l2(f64(y), z["y"]), "dx": rel_l2(f64(x.grad), z["dx"])}
+    if g is not None:
+        errs["dgain"] = rel_l2(f64(g.grad), z["dgain"])
+    assert max(errs.values()) < 2e-2, errs
+
+
+@pytest.mark.parametrize("path", FFN, ids=os.path.basename)
+def test_ffn_matches_golden(path):
+    """The HIP ALU-GLU block (fused activation epilogues) against the float64 definition."""
+    from algebraic_amd.kernels.ffn import alu_glu_ffn
+    z = load(path)
+    t = [torch.tensor(z[k], device="cuda").to(torch.bfloat16).requires_grad_(True) for k in ("h2", "w_g", "w_u", "w_d")]
+    print(f"[golden] {os.path.basename(path)}", flush=True)
+    out = alu_glu_ffn(*t, beta=float(z["beta"]))
+    out.backward(torch.tensor(z["dout"], device="cuda").to(torch.bfloat16))
+    torch.cuda.synchronize()
+    errs = {"out": rel_l2(f64(out), z["out"]), "dh2": rel_l2(f64(t[0].grad), z["dh2"]),
+            "dw_g": rel_l2(f64(t[1].grad), z["dw_g"]), "dw_u": rel_l2(f64(t[2].grad), z["dw_u"]),
+            "dw_d": rel_l2(f64(t[3].grad), z["dw_d"])}
+    assert max(errs.values()) < 2e-2, errs
+
+
+@pytest.mark.parametrize("path", HEAD, ids=os.path.basename)
+def test_eval_head_matches_golden(path):
+    """The streamed eval head on the head fixtures: log p(target) = log pt of the float64
+    closed form (the identity the reference's scorer relies on), argmax a float64 maximum."""
+    from algebraic_amd.kernels.fused_head import head_logprob
+    z = load(path)
+    h = torch.tensor(z["h"], device="cuda").to(torch.bfloat16)
+    E = torch.tensor(z["E"], device="cuda").to(torch.bfloat16)
+    print(f"[golden] eval {os.path.basename(path)}", flush=True)
+    lp, am = head_logprob(h, E, torch.tensor(z["targets"], device="cuda"), n=int(z["n"]), c=float(z["c"]))
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(f64(lp), np.log(z["pt"].astype(np.float64)), atol=1e-4)
+    logits = z["h"].astype(np.float64) @ z["E"].astype(np.float64).T
+    best = logits.max(axis=1)
+    got = logits[np.arange(len(best)), am.cpu().numpy()]
+    assert np.all(got >= best - 1e-5 * (np.abs(best) + 1))
