@@ -192,9 +192,40 @@ __global__ __launch_bounds__(NT, 1) void head_fwd_kernel(HeadParams p) {
 }
 
 // Evaluation head (src/algebraic/evaluation.py:13-23 with the argmax of
-// src/algebraic/benchmarking.py:178-188): z^T = E h^T as in the forward, the epilogue keeps
-// the per-token partial sums of w, the target logit, and the tile's largest logit with its
-// smallest vocabulary index. Nothing else is stored; head_eval_stats_kernel finishes.
+// src/algebraic/benchmarking.py:178-188): z^T = E h^T as in the forward. The scorer's
+// log_softmax(n asinh(z/c)) has no clamp, so the weights are evaluated relative to the largest
+// logit z_m of a group of logits: w' = (rho(z/c) rho(-z_m/c))^n = exp(n (asinh(z/c) - asinh(z_m/c)))
+// <= 1, which neither overflows however large the logits grow nor loses the group's leading
+// terms. The epilogue keeps, per token and vocabulary tile, the tile's largest logit with its
+// first index (the argmax), the sum of w' relative to that logit, and the target logit.
+// Nothing per (token, vocab) pair is stored; head_eval_stats_kernel combines the tiles.
+constexpr int EVAL_NO_INDEX = 0x7fffffff;
+
+// Argmax order over increasing vocabulary indices (jnp.argmax): the first NaN wins, else the
+// first of the largest values. (z, i) replaces the running (zm, im) when it comes first in that
+// order; the running value starts empty (EVAL_NO_INDEX).
+__device__ __forceinline__ bool eval_better(float z, int i, float zm, int im) {
+  if (im == EVAL_NO_INDEX) return true;
+  if (zm != zm) return z != z && i < im;
+  if (z != z) return true;
+  return z > zm || (z == zm && i < im);
+}
+
+// Stable rho (reciprocal form below zero) with the hardware reciprocal: rho(x) = e^asinh(x).
+__device__ __forceinline__ float eval_rho(float x) {
+  const float rad = __builtin_fmaf(x, x, 1.0f);
+  const float t = __builtin_fmaf(rad, rsq(rad), __builtin_fabsf(x));
+  return x >= 0.0f ? t : __builtin_amdgcn_rcpf(t);
+}
+
+// Factor that moves a sum of weights relative to logit za onto logit zb >= za:
+// (rho(za/c) rho(-zb/c))^n, exactly 1 when za == zb.
+template <int L2N>
+__device__ __forceinline__ float eval_rescale(float za, float zb, float inv_c, int log2n) {
+  if (za == zb) return 1.0f;
+  return pow2n<L2N>(eval_rho(za * inv_c) * eval_rho(-zb * inv_c), log2n);
+}
+
 template <int L2N>
 __global__ __launch_bounds__(NT, 1) void head_eval_kernel(HeadParams p) {
   __shared__ __attribute__((aligned(16))) GemmStage<KMAJOR, KMAJOR, HC> s0, s1;
@@ -212,17 +243,17 @@ __global__ __launch_bounds__(NT, 1) void head_eval_kernel(HeadParams p) {
   const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
   int wm, wn;
   wave_coords<HC>(wm, wn);
-  const float inv_c = p.inv_c, clamp = p.clamp;
+  const float inv_c = p.inv_c;
   const int vrow0 = m0 + wm * HC::WTM;
 #pragma unroll
   for (int nb = 0; nb < HC::NB; ++nb) {
     const int col = wn * HC::WTN + nb * 32 + l32;
     const int tok = n0 + col;
     const int tgt = tok < p.N ? p.targets[tok] : -1;
-    float part = 0.0f, zm = -INFINITY;
-    int im = 0x7fffffff;
-    // This lane's vocabulary rows increase with (mb, i), so a strict comparison keeps the
-    // first index among equal maxima (argmax's tie rule).
+    // Pass 1: this lane's largest logit and its first index (the lane's vocabulary rows
+    // increase with (mb, i)), and the target logit.
+    float zm = -INFINITY;
+    int im = EVAL_NO_INDEX;
 #pragma unroll
     for (int mb = 0; mb < HC::MB; ++mb) {
 #pragma unroll
@@ -230,30 +261,46 @@ __global__ __launch_bounds__(NT, 1) void head_eval_kernel(HeadParams p) {
         const int v = vrow0 + mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
         const float z = acc[mb][nb][i];
         if (v < p.V) {
-          const float x = fminf(z * inv_c, clamp);
-          float r;
-          part += pow2n<L2N>(rho_fast(x, r), p.log2n);
-          if (z > zm) { zm = z; im = v; }
+          // Rows increase along the lane: take z if it is larger, or the first NaN.
+          if (!(z <= zm) && zm == zm) { zm = z; im = v; }
           if (v == tgt) p.zt[tok] = z;
         }
       }
     }
-    part += xor32(part);
+    // Pass 2: the sum of weights relative to that logit.
+    const float sh = eval_rho(-zm * inv_c);
+    float part = 0.0f;
+#pragma unroll
+    for (int mb = 0; mb < HC::MB; ++mb) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int v = vrow0 + mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+        if (v < p.V) part += pow2n<L2N>(eval_rho(acc[mb][nb][i] * inv_c) * sh, p.log2n);
+      }
+    }
+    // The other lane half holds the same token's remaining rows of this wave's block.
     const float pz = __shfl_xor(zm, 32, 64);
+    const float pp = __shfl_xor(part, 32, 64);
     const int pi = __shfl_xor(im, 32, 64);
-    if (pz > zm || (pz == zm && pi < im)) { zm = pz; im = pi; }
-    if (h == 0) { red[wm][col] = part; redm[wm][col] = zm; redi[wm][col] = im; }
+    const bool take = pi != EVAL_NO_INDEX && eval_better(pz, pi, zm, im);
+    const float zn = take ? pz : zm;
+    const float mine = part == 0.0f ? 0.0f : part * eval_rescale<L2N>(zm, zn, inv_c, p.log2n);
+    const float other = pp == 0.0f ? 0.0f : pp * eval_rescale<L2N>(pz, zn, inv_c, p.log2n);
+    if (take) { zm = pz; im = pi; }
+    if (h == 0) { red[wm][col] = mine + other; redm[wm][col] = zm; redi[wm][col] = im; }
   }
   __syncthreads();
   for (int t = threadIdx.x; t < HT_N; t += NT) {
     const int tok = n0 + t;
-    float s = 0.0f, m = -INFINITY;
-    int ix = 0x7fffffff;
+    float m = -INFINITY;
+    int ix = EVAL_NO_INDEX;
 #pragma unroll
-    for (int w = 0; w < HC::WM; ++w) {  // waves cover increasing vocabulary rows
-      s += red[w][t];
-      if (redm[w][t] > m) { m = redm[w][t]; ix = redi[w][t]; }
-    }
+    for (int w = 0; w < HC::WM; ++w)  // waves cover increasing vocabulary rows
+      if (redi[w][t] != EVAL_NO_INDEX && eval_better(redm[w][t], redi[w][t], m, ix)) { m = redm[w][t]; ix = redi[w][t]; }
+    float s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < HC::WM; ++w)
+      if (red[w][t] != 0.0f) s += red[w][t] * eval_rescale<L2N>(redm[w][t], m, inv_c, p.log2n);
     if (tok < p.N) {
       p.partial[(size_t)tm * p.N + tok] = s;
       p.pmax[(size_t)tm * p.N + tok] = m;
@@ -262,10 +309,6 @@ __global__ __launch_bounds__(NT, 1) void head_eval_kernel(HeadParams p) {
   }
 }
 
-// log p(target) = n log rho(min(zt/c, X)) - log sum_v w (log of the lean likelihood's pt,
-// which src/algebraic/evaluation.py:13-23 equals: tests/test_components.py:56), in the log
-// domain so that improbable targets do not underflow; argmax over the vocabulary tiles in
-// order (first index on ties).
 // The per-token reductions over vocabulary tiles below read one value per tile (stride N) and
 // combine them in tile order; the loads are issued TB at a time so their latencies overlap,
 // while the order of the combining steps (and so every result bit) stays that of a plain loop.
@@ -286,40 +329,59 @@ __device__ __forceinline__ float sum_tiles(const float* part, int N, int tok, in
   return l;
 }
 
+// log p(target) = log_softmax(n asinh(z/c))[t] (src/algebraic/evaluation.py:13-23) from the
+// tiles' (largest logit, shifted sum) pairs: with z_m the largest logit of the row and
+// L = sum over tiles of S_tile (rho(z_tile/c) rho(-z_m/c))^n = sum_v (rho(z_v/c) rho(-z_m/c))^n,
+//   log p = n (log rho(z_t/c) + log rho(-z_m/c)) - log L,
+// all in the log domain so that neither large logits nor improbable targets overflow or
+// underflow. argmax: the first index of the largest logit over the tiles in vocabulary order
+// (the first NaN if there is one, as jnp.argmax).
 __global__ __launch_bounds__(256) void head_eval_stats_kernel(HeadParams p, int nvt) {
   const int tok = blockIdx.x * 256 + threadIdx.x;
   if (tok >= p.N) return;
-  float l = 0.0f, m = -INFINITY;
-  int ix = 0x7fffffff;
-  // Sum of the partials and the first tile holding the largest maximum, in tile order.
-  auto take = [&](float pl, float pm, int pi) {
-    l += pl;
-    if (pm > m) { m = pm; ix = pi; }
+  float m = -INFINITY;
+  int ix = EVAL_NO_INDEX;
+  auto take = [&](float pm, int pi) {
+    if (pi != EVAL_NO_INDEX && eval_better(pm, pi, m, ix)) { m = pm; ix = pi; }
   };
   int t = 0;
   for (; t + TB <= nvt; t += TB) {
-    float vl[TB], vm[TB];
+    float vm[TB];
     int vi[TB];
 #pragma unroll
     for (int u = 0; u < TB; ++u) {
       const size_t o = (size_t)(t + u) * p.N + tok;
-      vl[u] = p.partial[o];
       vm[u] = p.pmax[o];
       vi[u] = p.pidx[o];
     }
 #pragma unroll
-    for (int u = 0; u < TB; ++u) take(vl[u], vm[u], vi[u]);
+    for (int u = 0; u < TB; ++u) take(vm[u], vi[u]);
   }
-  for (; t < nvt; ++t) {
-    const size_t o = (size_t)t * p.N + tok;
-    take(p.partial[o], p.pmax[o], p.pidx[o]);
+  for (; t < nvt; ++t) take(p.pmax[(size_t)t * p.N + tok], p.pidx[(size_t)t * p.N + tok]);
+  // Sum of the tiles' sums, each moved onto m, in tile order.
+  float l = 0.0f;
+  auto add = [&](float s, float pm) {
+    if (s != 0.0f) l += s * eval_rescale<0>(pm, m, p.inv_c, p.log2n);
+  };
+  t = 0;
+  for (; t + TB <= nvt; t += TB) {
+    float vs[TB], vm[TB];
+#pragma unroll
+    for (int u = 0; u < TB; ++u) {
+      const size_t o = (size_t)(t + u) * p.N + tok;
+      vs[u] = p.partial[o];
+      vm[u] = p.pmax[o];
+    }
+#pragma unroll
+    for (int u = 0; u < TB; ++u) add(vs[u], vm[u]);
   }
+  for (; t < nvt; ++t) add(p.partial[(size_t)t * p.N + tok], p.pmax[(size_t)t * p.N + tok]);
   // The target logit is written by the tile holding the target; out-of-range targets read 0.
   const int tgt = p.targets[tok];
   const float zt = tgt >= 0 && tgt < p.V ? p.zt[tok] : 0.0f;
-  const float x = fminf(zt / p.c, p.clamp);
-  p.logprob[tok] = (float)(1 << p.log2n) * logf(rho_exact(x)) - logf(l);
-  if (p.argmax) p.argmax[tok] = ix;
+  const float rel = zt == m ? 0.0f : logf(rho_exact(zt * p.inv_c)) + logf(rho_exact(-m * p.inv_c));
+  p.logprob[tok] = (float)(1 << p.log2n) * rel - logf(l);
+  if (p.argmax) p.argmax[tok] = ix == EVAL_NO_INDEX ? 0 : ix;  // every logit -inf: index 0
 }
 
 // Per-token statistics and telemetry (fused_head.py:116-117, 219-229); with the residual

@@ -157,10 +157,11 @@ int alg_head_fwd(alg_stream_t stream, int N, int d, int V,
 /* Evaluation head, replacing the dense logits of the reference's scorer
  * (src/algebraic/benchmarking.py:178-188 with src/algebraic/evaluation.py:13-23, head
  * "alg_ce"): for h (N,d) bf16, E (V,d) bf16 and targets (N) int32, streams the vocabulary like
- * alg_head_fwd and writes logprob[n] = log_softmax(n asinh(z/c))[t_n] (computed as
- * n log rho(min(z_t/c, X)) - log sum_v rho(min(z_v/c, X))^n, X the head clamp, which equals it
- * for every logit below c X) and, if argmax is not NULL, argmax[n] = the first index of the
- * largest logit z_n. No logits are stored. */
+ * alg_head_fwd and writes logprob[n] = log_softmax(n asinh(z/c))[t_n] with no clamp (computed
+ * as n (log rho(z_t/c) + log rho(-z_m/c)) - log sum_v (rho(z_v/c) rho(-z_m/c))^n, z_m the row's
+ * largest logit, so no term overflows) and, if argmax is not NULL, argmax[n] = the first index
+ * of the largest logit z_n (the first NaN if the row holds one, as jnp.argmax). No logits are
+ * stored. */
 int alg_head_eval(alg_stream_t stream, int N, int d, int V,
                   const void* h, const void* E, const int32_t* targets, int n, float c,
                   float* logprob, int32_t* argmax, void* workspace, size_t workspace_bytes);

@@ -117,3 +117,40 @@ def test_out_of_range_targets_read_a_zero_logit():
     np.testing.assert_allclose(tel[invalid], st[invalid] ** 8, rtol=2e-5)
     np.testing.assert_allclose(lp[invalid], 8 * np.log(st[invalid]), atol=2e-5)
     np.testing.assert_allclose(tel[~invalid], pt_ref[~invalid], rtol=1e-4, atol=1e-9)
+
+
+@pytest.mark.parametrize("n,c", [(8, 2.0), (16, 16.0)])
+def test_head_logprob_logits_beyond_the_training_clamp(n, c):
+    """The scorer's log_softmax(n asinh(z/c)) has no clamp (src/algebraic/evaluation.py:13-23).
+    One embedding row is aligned with token 0's hidden state so that logit reaches several times
+    c X (X = 1/4 (1e38/V)^(1/n), the training head's clamp), and through it the other tokens see
+    large positive and negative logits: log p and the argmax against the float64 oracle."""
+    from oracle.numerics import head_clamp, round_bf16
+    N, d, V = 256, 256, 1000
+    h, E, t = head_inputs(N, d, V, seed=29, e_std=0.05)
+    big = 4.0 * c * head_clamp(V, n)
+    E[7] = round_bf16(h[0] * np.float32(big / d))
+    t[0] = 7
+    lp, am = _run(h, E, t, n, c)
+    lp_ref, _, z = OH.eval_logprob(h, E, t, n=n, c=c)
+    assert z[0, 7] > 3.0 * c * head_clamp(V, n) and z[:, 7].min() < -c * head_clamp(V, n) / 10
+    err = float(np.max(np.abs(lp - lp_ref)))
+    print(f"  logit max {z.max():.0f} (c X = {c * head_clamp(V, n):.0f}): max |logprob - oracle| = {err:.2e}",
+          flush=True)
+    assert err < 1e-4
+    _check_argmax(am, z)
+
+
+def test_head_argmax_takes_the_first_nan():
+    """jnp.argmax returns the first NaN's index: a token whose hidden state is NaN has only NaN
+    logits (argmax 0, log p NaN); an embedding row of NaN gives every token a NaN logit there."""
+    N, d, V = 256, 128, 700
+    h, E, t = head_inputs(N, d, V, seed=31)
+    h[5] = np.nan
+    lp, am = _run(h, E, t)
+    assert am[5] == 0 and np.isnan(lp[5])
+    assert np.isfinite(lp[np.arange(N) != 5]).all()
+    E[300] = np.nan
+    lp, am = _run(h, E, t)
+    assert am[5] == 0
+    np.testing.assert_array_equal(am[np.arange(N) != 5], 300)
