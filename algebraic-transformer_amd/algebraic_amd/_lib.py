@@ -24,10 +24,10 @@ _S = ctypes.c_size_t
 _SIGNATURES = {
     "alg_last_error": (ctypes.c_char_p, []),
     "alg_version": (ctypes.c_char_p, []),
-    "alg_attn_workspace_size": (_S, [_I, _I, _I, _I]),
+    "alg_attn_workspace_size": (_S, [_I, _I, _I, _I, _I]),
     "alg_attn_prepare": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _F, _I, _I, _P, _P, _P, _P, _S]),
     "alg_attn_fwd": (_I, [_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _P, _F, _I, _I, _P, _P, _P]),
-    "alg_attn_bwd": (_I, [_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P, _F, _I, _I, _F,
+    "alg_attn_bwd": (_I, [_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P, _F, _I, _I, _F,
                           _P, _P, _P, _P, _P, _P, _S]),
     "alg_attn_prologue_workspace_size": (_S, [_I, _I, _I, _I]),
     "alg_cayley_tables": (_I, [_P, _P, _I, _I, _P, _P]),

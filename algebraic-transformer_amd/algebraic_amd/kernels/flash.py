@@ -112,7 +112,7 @@ class _FlashFn(torch.autograd.Function):
             sink_in = sink_logit.detach().to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
             if sink_in.numel() not in (1, H):
                 raise ValueError(f"sink_logit must broadcast to ({H},)")
-        ws_bytes = lib.alg_attn_workspace_size(B, H, T, D)
+        ws_bytes = lib.alg_attn_workspace_size(dt, B, H, T, D)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         q_s = torch.empty_like(q)
         sink = torch.empty(H, dtype=torch.float32, device=dev) if has_sink else None
@@ -122,22 +122,20 @@ class _FlashFn(torch.autograd.Function):
             sink_in.numel() if has_sink else 0, plan.c, plan.n, int(plan.range_guard),
             _lib.ptr(q_s), _lib.ptr(sink), _lib.ptr(flag), _lib.ptr(ws), ws_bytes), "flash_attention prologue")
         o = torch.empty_like(q)
-        need_precise = plan.variant == _lib.ATTN_GUARDED
-        o_precise = torch.empty(q.shape, dtype=torch.float32, device=dev) if need_precise else None
         stat = torch.empty((B, H, T), dtype=torch.float32, device=dev)
         _lib.check(lib.alg_attn_fwd(
             st, dt, plan.layout, B, H, T, D, _lib.ptr(q_s), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink), plan.n, plan.variant,
             _lib.ptr(flag), plan.clamp, int(plan.fast_rho), int(plan.inv_stat),
-            _lib.ptr(o), _lib.ptr(o_precise), _lib.ptr(stat)), "flash_attention forward")
+            _lib.ptr(o), None, _lib.ptr(stat)), "flash_attention forward")
         ctx.plan = plan
         ctx.sink_shape = None if not has_sink else tuple(sink_logit.shape)
         ctx.sink_dtype = None if not has_sink else sink_logit.dtype
-        ctx.save_for_backward(q_s, k, v, sink, o, o_precise, stat, flag)
+        ctx.save_for_backward(q_s, k, v, sink, o, stat, flag)
         return o
 
     @staticmethod
     def backward(ctx, do):
-        q_s, k, v, sink, o, o_precise, stat, flag = ctx.saved_tensors
+        q_s, k, v, sink, o, stat, flag = ctx.saved_tensors
         plan = ctx.plan
         B, H, T, D = _bhtd(q_s.shape, plan.layout)
         lib = _lib.load()
@@ -145,7 +143,7 @@ class _FlashFn(torch.autograd.Function):
         dev = q_s.device
         st = _lib.stream_of(q_s)
         do = _lib.aligned16(do.to(q_s.dtype))
-        ws_bytes = lib.alg_attn_workspace_size(B, H, T, D)
+        ws_bytes = lib.alg_attn_workspace_size(dt, B, H, T, D)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         dq = torch.empty_like(q_s)
         dk = torch.empty_like(k)
@@ -155,7 +153,7 @@ class _FlashFn(torch.autograd.Function):
         alpha = 1.0 / (math.sqrt(D) * plan.c)
         _lib.check(lib.alg_attn_bwd(
             st, dt, plan.layout, B, H, T, D, _lib.ptr(q_s), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink), _lib.ptr(o),
-            _lib.ptr(o_precise), _lib.ptr(stat), _lib.ptr(do), plan.n, plan.variant, _lib.ptr(flag), plan.clamp,
+            _lib.ptr(stat), _lib.ptr(do), plan.n, plan.variant, _lib.ptr(flag), plan.clamp,
             int(plan.fast_rho), int(plan.inv_stat), alpha, _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(di),
             _lib.ptr(dbeta), _lib.ptr(ws), ws_bytes), "flash_attention backward")
         dsink = None

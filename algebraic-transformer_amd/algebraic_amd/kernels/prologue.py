@@ -100,22 +100,21 @@ class _PrologueFlashFn(torch.autograd.Function):
             plan.n, int(plan.range_guard), _lib.ptr(q_s), _lib.ptr(k_r), _lib.ptr(tau_q), _lib.ptr(tau_k),
             _lib.ptr(sink), _lib.ptr(flag), _lib.ptr(ws), ws_bytes), "attention prologue")
         o = torch.empty_like(q)
-        o_precise = torch.empty(q.shape, dtype=torch.float32, device=dev) if plan.variant == _lib.ATTN_GUARDED else None
         stat = torch.empty((B, H, T), dtype=torch.float32, device=dev)
         _lib.check(lib.alg_attn_fwd(
             st, dt, plan.layout, B, H, T, D, _lib.ptr(q_s), _lib.ptr(k_r), _lib.ptr(v), _lib.ptr(sink), plan.n, plan.variant,
             _lib.ptr(flag), plan.clamp, int(plan.fast_rho), int(plan.inv_stat),
-            _lib.ptr(o), _lib.ptr(o_precise), _lib.ptr(stat)), "attention forward")
+            _lib.ptr(o), None, _lib.ptr(stat)), "attention forward")
         ctx.plan = plan
         ctx.sink_shape = None if not has_sink else tuple(sink_logit.shape)
         ctx.sink_dtype = None if not has_sink else sink_logit.dtype
         ctx.gain_meta = [None if g is None else (g.shape, g.dtype) for g in (q_gain, k_gain)]
-        ctx.save_for_backward(q, k, v, gq, gk, cs, sn, q_s, k_r, tau_q, tau_k, sink, o, o_precise, stat, flag)
+        ctx.save_for_backward(q, k, v, gq, gk, cs, sn, q_s, k_r, tau_q, tau_k, sink, o, stat, flag)
         return o
 
     @staticmethod
     def backward(ctx, do):
-        q, k, v, gq, gk, cs, sn, q_s, k_r, tau_q, tau_k, sink, o, o_precise, stat, flag = ctx.saved_tensors
+        q, k, v, gq, gk, cs, sn, q_s, k_r, tau_q, tau_k, sink, o, stat, flag = ctx.saved_tensors
         plan = ctx.plan
         B, H, T, D = _bhtd(q.shape, plan.layout)
         lib = _lib.load()
@@ -123,7 +122,7 @@ class _PrologueFlashFn(torch.autograd.Function):
         dev = q.device
         st = _lib.stream_of(q)
         do = _lib.aligned16(do.to(q.dtype))
-        ws_bytes = lib.alg_attn_workspace_size(B, H, T, D)
+        ws_bytes = lib.alg_attn_workspace_size(dt, B, H, T, D)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         dq_r, dk_r, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
         di = torch.empty((B, H, T), dtype=torch.float32, device=dev)
@@ -131,7 +130,7 @@ class _PrologueFlashFn(torch.autograd.Function):
         alpha = 1.0 / (math.sqrt(D) * plan.c)
         _lib.check(lib.alg_attn_bwd(
             st, dt, plan.layout, B, H, T, D, _lib.ptr(q_s), _lib.ptr(k_r), _lib.ptr(v), _lib.ptr(sink), _lib.ptr(o),
-            _lib.ptr(o_precise), _lib.ptr(stat), _lib.ptr(do), plan.n, plan.variant, _lib.ptr(flag), plan.clamp,
+            _lib.ptr(stat), _lib.ptr(do), plan.n, plan.variant, _lib.ptr(flag), plan.clamp,
             int(plan.fast_rho), int(plan.inv_stat), alpha, _lib.ptr(dq_r), _lib.ptr(dk_r), _lib.ptr(dv),
             _lib.ptr(di), _lib.ptr(dbeta), _lib.ptr(ws), ws_bytes), "attention backward")
         pws_bytes = lib.alg_attn_prologue_workspace_size(B, H, T, D)

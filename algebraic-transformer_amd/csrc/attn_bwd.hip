@@ -4,22 +4,27 @@
 // resident backward schedules), 630-645 (di), 694-726 (sink VJP) and
 // src/algebraic/kernels/head_resident.py:91-119.
 //
-// Launches:
-//   pre   di = sum_d dO*o per row (from the rounded output in range, the f32 output when
-//         shifted; flash.py:633), per-(b,h,block) partial sums of mass*di for the sink
-//         gradient (flash.py:694-705, 721-723); for f32 inputs also zeroes the dQ accumulator.
-//   main  key-stationary: one workgroup = 4 waves = 128 keys of one (b,h); dK/dV accumulate
-//         in registers while the kernel streams 64-query tiles of Q and dO through LDS.
-//         Scores are formed as S = Q K^T so a lane owns one key column; P^T and dS^T feed
-//         dV += P^T dO and dK += dS^T Q directly as MFMA A operands, with dO/Q fragments
-//         transposed by ds_read_b64_tr_b16.
-//   dq    (bf16) query-stationary: one workgroup = 128 queries; S^T and dP^T are formed
-//         again and dQ^T += K^T dS^T accumulates in registers, written once. No atomics and
-//         no per-key-block dQ partials (unlike flash.py:537-544); f32 atomics run at about
-//         a sixth of the store bandwidth on this GPU, so recomputing two products is cheaper.
-//         f32 inputs keep the single key-stationary kernel with dQ added to an f32
-//         accumulator by atomics (one per element per key block).
-//   post  the per-head sink gradient; for f32, dq = round(round(n * acc) * dq_scale).
+// bf16 launches, in order:
+//   dq    query-stationary: one workgroup = 128 queries of one (b,h). It first forms
+//         di = sum_d dO*o for its queries (from the rounded output, flash.py:633; on the
+//         shifted fallback from a first pass over the keys, see attn_bwd_dq_kernel) and the
+//         per-(b,h,query block) partial sums of mass*di for the sink gradient
+//         (flash.py:694-705, 721-723), writes di, then forms S^T and dP^T again and
+//         accumulates dQ^T += K^T dS^T in registers, written once. No atomics and no
+//         per-key-block dQ partials (unlike flash.py:537-544): f32 atomics run at about a
+//         sixth of the store bandwidth on this GPU, so recomputing two products is cheaper.
+//   dkdv  key-stationary: one workgroup = 4 waves = 128 keys of one (b,h); dK/dV accumulate
+//         in registers while the kernel streams 64-query tiles of Q, dO, stat and di through
+//         LDS. Scores are formed as S = Q K^T so a lane owns one key column; P^T and dS^T
+//         feed dV += P^T dO and dK += dS^T Q directly as MFMA A operands, with dO/Q
+//         fragments transposed by ds_read_b64_tr_b16.
+//   post  the per-head sink gradient.
+// f32 launches: pre (di from the f32 output, sink partials, zeroed dQ accumulator), one
+// key-stationary kernel adding dQ to an f32 accumulator with atomics, post (dq from the
+// accumulator: round(round(n * acc) * dq_scale), and the sink gradient).
+// The fallback variants (shifted, clipped) loop over their work items (grid-stride), so the
+// guarded path's launch of the branch the device flag did not select is a small grid that
+// exits at once.
 #include <type_traits>
 
 #include "attn_common.h"
@@ -30,22 +35,22 @@ constexpr int BWD_BK = 128;  // keys per workgroup
 // Queries per streamed tile: 64, or 32 where 64 would not fit in LDS (f32 with D=128).
 template <typename T, int D>
 constexpr int bwd_bq() { return (sizeof(T) == 4 && D == 128) ? 32 : 64; }
-constexpr int PRE_ROWS = 256;  // rows per pre-kernel workgroup
+// Rows per pre-kernel workgroup, and per block of the sink-gradient partials: the bf16 dQ
+// kernel writes one partial per 128-query workgroup, the f32 pre kernel one per 128 rows.
+constexpr int SINK_ROWS = 128;
 
 // ---------------------------------------------------------------------------
-// pre: di, dq_acc = 0, sink partials
+// pre (f32): di, dq_acc = 0, sink partials
 // ---------------------------------------------------------------------------
-// PRECISE: o is read from the f32 o_precise buffer (the shifted fallback saved it) rather
-// than from o. The choice is uniform over the grid (it follows the guard flag), so the kernel
-// branches once into one of two straight-line bodies whose loads are all issued before any is
-// waited for.
-template <typename T, bool PRECISE, int D>
-__device__ __forceinline__ void attn_bwd_pre_body(const AttnBwdParams& p, bool zero_dq, bool shifted) {
+// The branch taken (the guard flag or the host's mode) is uniform over the grid; the body is
+// straight-line, with every row's loads issued before any is waited for.
+template <typename T, int D>
+__device__ __forceinline__ void attn_bwd_pre_body(const AttnBwdParams& p, bool shifted) {
   const int bh = blockIdx.x;
   const int head = bh % p.H;
   const int T_ = p.T;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int row0 = blockIdx.y * PRE_ROWS;
+  const int row0 = blockIdx.y * SINK_ROWS;
   const size_t hb = head_base(bh, p.H, T_, D, p.layout);
   const int ld = row_stride(p.H, D, p.layout);
   const int n = 1 << p.log2n;
@@ -57,10 +62,10 @@ __device__ __forceinline__ void attn_bwd_pre_body(const AttnBwdParams& p, bool z
   float part = 0.0f;
   // 8 elements per lane, D/8 lanes per row (vector loads of dO, o; vector zero-fill of dq_acc);
   // each lane loads PRE_U rows before reducing any, to keep more bytes in flight.
-  constexpr int PRE_U = 4;
+  constexpr int PRE_U = 2;
   constexpr int lpr = D / 8, rpw = 64 / lpr;
   const int sub = lane / lpr, li = lane - sub * lpr;
-  const int rend = min(row0 + PRE_ROWS, T_);
+  const int rend = min(row0 + SINK_ROWS, T_);
   for (int r0 = row0 + wave * rpw; r0 < rend; r0 += 4 * rpw * PRE_U) {
     float dov[PRE_U][8], ov[PRE_U][8], stv[PRE_U];
 #pragma unroll
@@ -68,28 +73,22 @@ __device__ __forceinline__ void attn_bwd_pre_body(const AttnBwdParams& p, bool z
       const int r = r0 + u * 4 * rpw + sub;
       const int rc = min(r, rend - 1);
       stv[u] = p.stat[(size_t)bh * T_ + rc];
-      const size_t off = ((size_t)bh * T_ + rc) * D + li * 8;  // internal (B, H, T, D) buffers
-      const size_t xoff = hb + (size_t)rc * ld + li * 8;        // dO and o in the call's layout
+      const size_t xoff = hb + (size_t)rc * ld + li * 8;  // dO and o in the call's layout
+      const T* dsrc = reinterpret_cast<const T*>(p.dO) + xoff;
+      const T* osrc = reinterpret_cast<const T*>(p.o) + xoff;
       if constexpr (sizeof(T) == 2) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p.dO) + xoff);
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(dsrc);
+        const bf16x8 c = *reinterpret_cast<const bf16x8*>(osrc);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dov[u][j] = (float)a[j];
+        for (int j = 0; j < 8; ++j) { dov[u][j] = (float)a[j]; ov[u][j] = (float)c[j]; }
       } else {
-        const floatx4 a0 = *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(p.dO) + xoff);
-        const floatx4 a1 = *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(p.dO) + xoff + 4);
+        const floatx4 a0 = *reinterpret_cast<const floatx4*>(dsrc), a1 = *reinterpret_cast<const floatx4*>(dsrc + 4);
+        const floatx4 c0 = *reinterpret_cast<const floatx4*>(osrc), c1 = *reinterpret_cast<const floatx4*>(osrc + 4);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) { dov[u][j] = a0[j]; dov[u][4 + j] = a1[j]; }
-      }
-      if constexpr (PRECISE || sizeof(T) == 4) {
-        const float* src = PRECISE ? p.o_precise + off : reinterpret_cast<const float*>(p.o) + xoff;
-        const floatx4 b0 = *reinterpret_cast<const floatx4*>(src);
-        const floatx4 b1 = *reinterpret_cast<const floatx4*>(src + 4);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) { ov[u][j] = b0[j]; ov[u][4 + j] = b1[j]; }
-      } else {
-        const bf16x8 b = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p.o) + xoff);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) ov[u][j] = (float)b[j];
+        for (int j = 0; j < 4; ++j) {
+          dov[u][j] = a0[j]; dov[u][4 + j] = a1[j];
+          ov[u][j] = c0[j]; ov[u][4 + j] = c1[j];
+        }
       }
     }
 #pragma unroll
@@ -99,8 +98,8 @@ __device__ __forceinline__ void attn_bwd_pre_body(const AttnBwdParams& p, bool z
       float s = 0.0f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) s += dov[u][j] * ov[u][j];
-      if (ok && zero_dq) {
-        const size_t off = ((size_t)bh * T_ + r) * D + li * 8;
+      if (ok) {
+        const size_t off = ((size_t)bh * T_ + r) * D + li * 8;  // dq_acc is (B, H, T, D)
         const floatx4 z = {};
         *reinterpret_cast<floatx4*>(p.dq_acc + off) = z;
         *reinterpret_cast<floatx4*>(p.dq_acc + off + 4) = z;
@@ -123,17 +122,11 @@ __device__ __forceinline__ void attn_bwd_pre_body(const AttnBwdParams& p, bool z
 }
 
 template <typename T>
-__global__ __launch_bounds__(256) void attn_bwd_pre_kernel(AttnBwdParams p, int D, bool zero_dq) {
+__global__ __launch_bounds__(256) void attn_bwd_pre_kernel(AttnBwdParams p, int D) {
   bool shifted = p.mode == MODE_SHIFTED;
   if (p.flag) shifted = *p.flag == 0;
-  const bool precise = shifted && p.o_precise != nullptr;
-  if (D == 128) {
-    if (precise) attn_bwd_pre_body<T, true, 128>(p, zero_dq, shifted);
-    else attn_bwd_pre_body<T, false, 128>(p, zero_dq, shifted);
-  } else {
-    if (precise) attn_bwd_pre_body<T, true, 64>(p, zero_dq, shifted);
-    else attn_bwd_pre_body<T, false, 64>(p, zero_dq, shifted);
-  }
+  if (D == 128) attn_bwd_pre_body<T, 128>(p, shifted);
+  else attn_bwd_pre_body<T, 64>(p, shifted);
 }
 
 // ---------------------------------------------------------------------------
@@ -195,8 +188,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
   const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int T_ = p.T;
-  const int bh = blockIdx.x;
-  const int k0 = blockIdx.y * BWD_BK;  // blockIdx.y = 0 has the most causal work
+  // One 128-key block of one head. The in-range kernel takes one per workgroup from its 2-D
+  // grid; the fallbacks loop over them (grid-stride), key block 0 (the most causal work) first.
+  auto run = [&](int bh, int kblk) __attribute__((always_inline)) {
+  const int k0 = kblk * BWD_BK;
   const size_t base = (size_t)bh * T_ * D;  // internal (B, H, T, D) buffers (dq_acc)
   const size_t hb = head_base(bh, p.H, T_, D, p.layout);
   const int ld = row_stride(p.H, D, p.layout);
@@ -485,6 +480,16 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_kernel(AttnBwdParams p) {
       }
     }
   }
+  };
+  if constexpr (MODE == MODE_INRANGE) {
+    run(blockIdx.x, blockIdx.y);
+  } else {
+    const int nbh = p.B * p.H, total = nbh * ceil_div(T_, BWD_BK);
+    for (int L = blockIdx.x; L < total; L += gridDim.x) {
+      run(L % nbh, L / nbh);
+      __syncthreads();  // the next block's K tile overwrites LDS
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -524,13 +529,13 @@ constexpr int BF_BQ = 64;  // queries per streamed tile (bf16 kernel)
 constexpr int BWD_XCDS = 8;    // workgroup i runs on XCD i % 8
 constexpr int BWD_GROUP = 4;   // heads whose key blocks one XCD interleaves
 
-// Workgroup -> (head, key block) of the bf16 main kernel (1-D grid). Each XCD works through
-// its own share of the heads in groups of BWD_GROUP, key block by key block within a group
-// (heaviest causal blocks first), so the dQ rows and query tiles of only a few heads are live
-// in that XCD's L2 at a time. Head counts that do not split evenly over the XCDs use the
-// plain key-block-major order.
-__device__ __forceinline__ void bwd_block_coords(int nbh, int nkb, int& bh, int& kblk) {
-  const int L = blockIdx.x;
+// Work item L -> (head, key block) of the bf16 dK/dV kernel (1-D grid; L is the workgroup id,
+// or for the grid-stride fallbacks the workgroup id plus multiples of a grid size that is a
+// multiple of 8, so L % 8 is still the XCD). Each XCD works through its own share of the heads
+// in groups of BWD_GROUP, key block by key block within a group (heaviest causal blocks
+// first), so the query tiles of only a few heads are live in that XCD's L2 at a time. Head
+// counts that do not split evenly over the XCDs use the plain key-block-major order.
+__device__ __forceinline__ void bwd_block_coords(int L, int nbh, int nkb, int& bh, int& kblk) {
   if (nbh % (BWD_XCDS * BWD_GROUP) == 0) {
     const int xcd = L % BWD_XCDS, idx = L / BWD_XCDS;
     const int g = idx / (BWD_GROUP * nkb), r = idx - g * BWD_GROUP * nkb;
@@ -589,8 +594,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
   const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int T_ = p.T;
+  const int nbh = p.B * p.H, nkb = ceil_div(T_, BWD_BK);
+  auto run = [&](int L) __attribute__((always_inline)) {
   int bh, kblk;
-  bwd_block_coords(p.B * p.H, ceil_div(T_, BWD_BK), bh, kblk);
+  bwd_block_coords(L, nbh, nkb, bh, kblk);
   const int k0 = kblk * BWD_BK;
   const size_t base = head_base(bh, p.H, T_, D, LAYOUT);
   const int ld = LAYOUT ? p.H * D : D;  // elements between positions
@@ -817,6 +824,15 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
       }
     }
   }
+  };
+  if constexpr (MODE == MODE_INRANGE) {
+    run(blockIdx.x);
+  } else {
+    for (int L = blockIdx.x; L < nbh * nkb; L += gridDim.x) {
+      run(L);
+      __syncthreads();  // the next item's first copies overwrite both LDS buffer sets
+    }
+  }
 }
 
 // dQ kernel for bf16 inputs (query-stationary; no atomics): one workgroup = 4 waves = 128
@@ -830,6 +846,15 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
 //   R3  dQ^T over keys 0..31     | dS of 32..63  (MFMA | VALU)
 //   R4  dQ^T over keys 32..63                    (MFMA)
 // The output is dq = round(round(n * acc) * dq_scale) (flash.py:592 and the q_s chain rule).
+//
+// Before the tiles the kernel forms this workgroup's di (written for the dK/dV kernel, which
+// runs after it) and its partial sum of mass * di for the sink gradient (flash.py:694-705,
+// 721-723). Unshifted variants take di = sum_d dO o from the rounded output, as
+// flash.py:633 does. The shifted fallback saves no f32 copy of its output (the reference's
+// precise_output, flash.py:322, exists to make this sum exact); it takes
+// di = sum_j p_ij dP_ij from a first pass over the keys with the same f32 weights p and
+// products dP that its score gradients use, so that sum_j p_ij (dP_ij - di_i) vanishes to
+// f32 rounding however the weights are spread. In exact arithmetic both are <dO_i, o_i>.
 template <int D, int MODE, int L2N, int LAYOUT>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
   static_assert(D == 64 || D == 128, "head_dim");
@@ -838,6 +863,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
   __shared__ __attribute__((aligned(16))) bf16 Ks1[BK * D];
   __shared__ __attribute__((aligned(16))) bf16 Vs0[BK * D];
   __shared__ __attribute__((aligned(16))) bf16 Vs1[BK * D];
+  __shared__ float red[4];
 
   if (p.flag) {
     const bool in_range = *p.flag != 0;
@@ -847,20 +873,36 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int T_ = p.T;
   const int nqb = ceil_div(T_, 128);
-  const int bh = blockIdx.x;
-  const int qb = nqb - 1 - blockIdx.y;  // heaviest causal rows first
-  const size_t base = head_base(bh, p.H, T_, D, LAYOUT);
+  const int nbh = p.B * p.H;
   const int ld = LAYOUT ? p.H * D : D;  // elements between positions
+  const int log2n = p.log2n;
+  const int nbytes = head_bytes(T_, ld, D, 2);
+
+  // Per-lane swizzled offsets (the swizzle repeats every 16 rows).
+  const int trow = (lane & 15) >> 2;
+  int row_off[NF];  // row fragments of K / V: row l32, k chunk 2 st + h
+#pragma unroll
+  for (int st = 0; st < NF; ++st) row_off[st] = swz_at<CPR>(l32, 16 * st + 8 * h);
+  int tk_lo[NDB], tk_hi[NDB];  // transposed K fragments: rows 4h + (0..3), 4h + 8 + (0..3)
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+    tk_lo[db] = swz_at<CPR>(4 * h + trow, tr_col(db * 32, lane));
+    tk_hi[db] = swz_at<CPR>(4 * h + 8 + trow, tr_col(db * 32, lane));
+  }
+  constexpr int VE = bwd_valu_per_elem<MODE>();
+
+  // One 128-query block qb of head bh.
+  auto run = [&](int bh, int qb) __attribute__((always_inline)) {
+  const int head = bh % p.H;
+  const size_t base = head_base(bh, p.H, T_, D, LAYOUT);
   const bf16* Q = reinterpret_cast<const bf16*>(p.q) + base;
   const bf16* K = reinterpret_cast<const bf16*>(p.k) + base;
   const bf16* V = reinterpret_cast<const bf16*>(p.v) + base;
   const bf16* dO = reinterpret_cast<const bf16*>(p.dO) + base;
-  const int nbytes = head_bytes(T_, ld, D, 2);
   const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)K, (short)0, nbytes, BUF_RSRC_WORD3);
   const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)V, (short)0, nbytes, BUF_RSRC_WORD3);
   const int q0 = qb * 128 + wave * 32;
   const int myq = q0 + l32;
-  const int log2n = p.log2n;
   const int ntiles = (min(qb * 128 + 127, T_ - 1)) / BK + 1;  // key tiles up to the last query
 
   tile_dma2<D>(Ks0, Vs0, rk, rv, 0, wave, lane, ld);
@@ -877,33 +919,38 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
     of[s] = live ? ld8(dO + o) : z;
   }
   const float stq = live ? p.stat[(size_t)bh * T_ + myq] : 0.0f;
-  const float diq = live ? p.di[(size_t)bh * T_ + myq] : 0.0f;
+  float diq = 0.0f;
+  if constexpr (MODE != MODE_SHIFTED) {
+    // di = sum_d dO o over the rounded output (flash.py:633); the two lane halves hold
+    // alternate 8-element chunks of the row.
+    const bf16* O = reinterpret_cast<const bf16*>(p.o) + base + (size_t)myq * ld;
+    float s = 0.0f;
+#pragma unroll
+    for (int st = 0; st < NF; ++st) {
+      const bf16x8 z = {};
+      const bf16x8 ov = live ? ld8(O + 16 * st + 8 * h) : z;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s += (float)of[st][j] * (float)ov[j];
+    }
+    diq = s + xor32(s);
+  }
   floatx16 dqa[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db) dqa[db] = floatx16{};
-
-  // Per-lane swizzled offsets (the swizzle repeats every 16 rows).
-  const int trow = (lane & 15) >> 2;
-  int row_off[NF];  // row fragments of K / V: row l32, k chunk 2 st + h
-#pragma unroll
-  for (int st = 0; st < NF; ++st) row_off[st] = swz_at<CPR>(l32, 16 * st + 8 * h);
-  int tk_lo[NDB], tk_hi[NDB];  // transposed K fragments: rows 4h + (0..3), 4h + 8 + (0..3)
-#pragma unroll
-  for (int db = 0; db < NDB; ++db) {
-    tk_lo[db] = swz_at<CPR>(4 * h + trow, tr_col(db * 32, lane));
-    tk_hi[db] = swz_at<CPR>(4 * h + 8 + trow, tr_col(db * 32, lane));
-  }
+  float di_acc = 0.0f;  // shifted fallback: this lane's share of sum_j p_ij dP_ij
 
   bf16x8 rk2[2], rv2[2];  // row fragments of K / V, one step ahead (R1, R2)
   __builtin_amdgcn_s_waitcnt(VMCNT0);
   __syncthreads();
   rk2[0] = ld8(Ks0 + row_off[0]);
   rv2[0] = ld8(Vs0 + row_off[0]);
-  constexpr int VE = bwd_valu_per_elem<MODE>();
 
-  auto tile = [&](auto bufc, auto maskc, int kt) {
+  // One key tile. BUF selects the LDS buffer set, MASKED the tiles that cross the diagonal,
+  // DIPASS the shifted fallback's first pass (weights and dP only, summed into di_acc).
+  auto tile = [&](auto bufc, auto maskc, auto dipassc, int kt) {
     constexpr int BUF = decltype(bufc)::value;
     constexpr bool MASKED = decltype(maskc)::value;
+    constexpr bool DIPASS = decltype(dipassc)::value;
     const bf16* Ks = BUF ? Ks1 : Ks0;
     const bf16* Vs = BUF ? Vs1 : Vs0;
     const int kb0 = kt * BK;
@@ -921,11 +968,14 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
       s[blk] = mfma_bf16(rk2[g % 2], qf[st], s[blk]);
       dp[blk] = mfma_bf16(rv2[g % 2], of[st], dp[blk]);
     };
-    // Score gradient of key element i of block blk (this lane's query), rounded to bf16.
+    // Score gradient of key element i of block blk (this lane's query), rounded to bf16; in
+    // the first pass of the shifted fallback, the weight times dP instead.
     auto elem = [&](int blk, int i) {
       const bool masked = MASKED && kb0 + blk * 32 + 8 * (i >> 2) + 4 * h + (i & 3) > myq;
       bwd_elem<MODE, L2N>(s[blk][i], dp[blk][i], stq, diq, masked, p, log2n, pv[i], dsv[i]);
-      if (i & 1) {
+      if constexpr (DIPASS) {
+        di_acc += pv[i] * dp[blk][i];
+      } else if (i & 1) {
         da[blk][i >> 3][(i & 7) - 1] = f2bf(dsv[i - 1]);
         da[blk][i >> 3][i & 7] = f2bf(dsv[i]);
       }
@@ -957,30 +1007,35 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
       sdp_step(g);
 #pragma unroll
       for (int k = 0; k < E2; ++k) elem(0, E2 * (g - NF) + k);
-      if (g == 2 * NF - 1) dq_load(0, 0, ft[0]);
+      if (!DIPASS && g == 2 * NF - 1) dq_load(0, 0, ft[0]);
       step_order<2, VE * E2, 4 + 4, 0>();
     }
-    // R3: dQ^T over keys 0..31 under dS of keys 32..63.
-    constexpr int E3 = 16 / NDB;
+    if constexpr (DIPASS) {
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-      const int c = db & 1;
-      if (db + 1 < NDB) dq_load(0, db + 1, ft[c ^ 1]);
-      else dq_load(1, 0, ft[c ^ 1]);
-      dqa[db] = mfma_bf16(ft[c][0], da[0][0], dqa[db]);
-      dqa[db] = mfma_bf16(ft[c][1], da[0][1], dqa[db]);
+      for (int i = 0; i < 16; ++i) elem(1, i);
+    } else {
+      // R3: dQ^T over keys 0..31 under dS of keys 32..63.
+      constexpr int E3 = 16 / NDB;
 #pragma unroll
-      for (int k = 0; k < E3; ++k) elem(1, E3 * db + k);
-      step_order<2, VE * E3, 4, 0>();
-    }
-    // R4: dQ^T over keys 32..63.
+      for (int db = 0; db < NDB; ++db) {
+        const int c = db & 1;
+        if (db + 1 < NDB) dq_load(0, db + 1, ft[c ^ 1]);
+        else dq_load(1, 0, ft[c ^ 1]);
+        dqa[db] = mfma_bf16(ft[c][0], da[0][0], dqa[db]);
+        dqa[db] = mfma_bf16(ft[c][1], da[0][1], dqa[db]);
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-      const int c = (db + NDB) & 1;
-      if (db + 1 < NDB) dq_load(1, db + 1, ft[c ^ 1]);
-      dqa[db] = mfma_bf16(ft[c][0], da[1][0], dqa[db]);
-      dqa[db] = mfma_bf16(ft[c][1], da[1][1], dqa[db]);
-      step_order<2, 0, 4, 0>();
+        for (int k = 0; k < E3; ++k) elem(1, E3 * db + k);
+        step_order<2, VE * E3, 4, 0>();
+      }
+      // R4: dQ^T over keys 32..63.
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const int c = (db + NDB) & 1;
+        if (db + 1 < NDB) dq_load(1, db + 1, ft[c ^ 1]);
+        dqa[db] = mfma_bf16(ft[c][0], da[1][0], dqa[db]);
+        dqa[db] = mfma_bf16(ft[c][1], da[1][1], dqa[db]);
+        step_order<2, 0, 4, 0>();
+      }
     }
 
     __builtin_amdgcn_s_waitcnt(VMCNT0);  // this wave's copies of the next tile have landed
@@ -1000,15 +1055,45 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
   // Key tiles 0 .. 2 qb - 1 lie wholly before this workgroup's queries; tiles 2 qb and
   // 2 qb + 1 cross the diagonal.
   const int nfull = min(2 * qb, ntiles);
-  int kt = 0;
-  for (; kt < nfull; kt += 2) {
-    tile(std::integral_constant<int, 0>{}, std::false_type{}, kt);
-    tile(std::integral_constant<int, 1>{}, std::false_type{}, kt + 1);
+  auto sweep = [&](auto dipassc) {
+    int kt = 0;
+    for (; kt < nfull; kt += 2) {
+      tile(std::integral_constant<int, 0>{}, std::false_type{}, dipassc, kt);
+      tile(std::integral_constant<int, 1>{}, std::false_type{}, dipassc, kt + 1);
+    }
+    if (kt < ntiles) {
+      tile(std::integral_constant<int, 0>{}, std::true_type{}, dipassc, kt);
+      if (kt + 1 < ntiles) tile(std::integral_constant<int, 1>{}, std::true_type{}, dipassc, kt + 1);
+    }
+  };
+  if constexpr (MODE == MODE_SHIFTED) {
+    sweep(std::true_type{});
+    diq = di_acc + xor32(di_acc);
+    __syncthreads();  // every wave is done with the last tile's fragments
+    tile_dma2<D>(Ks0, Vs0, rk, rv, 0, wave, lane, ld);
+    if (ntiles > 1) tile_dma2<D>(Ks1, Vs1, rk, rv, BK, wave, lane, ld);
+    __builtin_amdgcn_s_waitcnt(VMCNT0);
+    __syncthreads();
+    rk2[0] = ld8(Ks0 + row_off[0]);
+    rv2[0] = ld8(Vs0 + row_off[0]);
   }
-  if (kt < ntiles) {
-    tile(std::integral_constant<int, 0>{}, std::true_type{}, kt);
-    if (kt + 1 < ntiles) tile(std::integral_constant<int, 1>{}, std::true_type{}, kt + 1);
+  // di for the dK/dV kernel, and this block's share of the sink gradient: the sink's weight
+  // relative to the row, mass = rho(b)^n stat (unshifted, 1/Z statistic) or (rho(b) stat)^n.
+  if (live && h == 0) p.di[(size_t)bh * T_ + myq] = diq;
+  if (p.sink) {
+    float b = p.sink[head];
+    if constexpr (MODE == MODE_CLIPPED) b = fminf(b, p.clamp);
+    const float rb = rho_exact(b);
+    const bool inv_stat = MODE == MODE_INRANGE || (MODE == MODE_CLIPPED && p.inv_stat);
+    const float mass = inv_stat ? pow2n<L2N>(rb, log2n) * stq : pow2n<L2N>(rb * stq, log2n);
+    float part = live && h == 0 ? mass * diq : 0.0f;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) part += __shfl_xor(part, m, 64);
+    if (lane == 0) red[wave] = part;
+    __syncthreads();
+    if (threadIdx.x == 0) p.sink_part[(size_t)bh * nqb + qb] = red[0] + red[1] + red[2] + red[3];
   }
+  sweep(std::false_type{});
 
   if (live) {
     const float slope = (float)(1 << log2n);
@@ -1025,6 +1110,15 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
         }
         *reinterpret_cast<bf16x4*>(DQ + db * 32 + 8 * g + 4 * h) = ob;
       }
+    }
+  }
+  };
+  if constexpr (MODE == MODE_INRANGE) {
+    run(blockIdx.x, nqb - 1 - blockIdx.y);  // heaviest causal rows first
+  } else {
+    for (int L = blockIdx.x; L < nbh * nqb; L += gridDim.x) {
+      run(L % nbh, nqb - 1 - L / nbh);
+      __syncthreads();  // the next item's first copies overwrite both LDS buffer sets
     }
   }
 }
@@ -1091,85 +1185,118 @@ __global__ __launch_bounds__(256) void attn_bwd_post_kernel(AttnBwdParams p, siz
   }
 }
 
-// bf16: the dK/dV kernel, then the dQ kernel (which writes dq itself).
+// Grid of a fallback (grid-stride) kernel: every work item gets its own workgroup when the
+// variant was chosen on the host; when it is one branch of the device guard it usually exits
+// at once, so it is launched as a small grid (a multiple of 8, so work item % 8 stays the XCD).
+constexpr int FALLBACK_GRID = 512;
+static int fallback_grid(const AttnBwdParams& p, int items) {
+  return p.flag ? std::min(items, FALLBACK_GRID) : items;
+}
+
+// bf16, one variant: the dQ kernel (which also writes di and the sink partials) or the dK/dV
+// kernel (which reads di).
 template <int D, int LAYOUT>
-static hipError_t launch_bwd_main_bf16_l(const AttnBwdParams& p, int mode, hipStream_t st) {
-  dim3 grid(p.B * p.H * ceil_div(p.T, BWD_BK)), block(256);
-  dim3 qgrid(p.B * p.H, ceil_div(p.T, 128));
-  switch (mode) {
-    case MODE_INRANGE: {
-      {
+static hipError_t launch_bwd_bf16_l(const AttnBwdParams& p, int mode, bool dq, hipStream_t st) {
+  const int nbh = p.B * p.H, nkb = ceil_div(p.T, BWD_BK), nqb = ceil_div(p.T, 128);
+  dim3 block(256);
+  if (dq) {
+    switch (mode) {
+      case MODE_INRANGE: {
+        KTimer t("attn_bwd_dq_inrange", st);
+        dim3 qgrid(nbh, nqb);
+        if (p.log2n == 4) hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE_INRANGE, 4, LAYOUT>), qgrid, block, 0, st, p);
+        else hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE_INRANGE, 0, LAYOUT>), qgrid, block, 0, st, p);
+      } break;
+      case MODE_CLIPPED: {
+        KTimer t("attn_bwd_dq_clipped", st);
+        hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE_CLIPPED, 0, LAYOUT>), dim3(fallback_grid(p, nbh * nqb)), block,
+                           0, st, p);
+      } break;
+      case MODE_SHIFTED: {
+        KTimer t("attn_bwd_dq_shifted", st);
+        hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE_SHIFTED, 0, LAYOUT>), dim3(fallback_grid(p, nbh * nqb)), block,
+                           0, st, p);
+      } break;
+      default: return hipErrorInvalidValue;
+    }
+  } else {
+    switch (mode) {
+      case MODE_INRANGE: {
         KTimer t("attn_bwd_inrange", st);
+        dim3 grid(nbh * nkb);
         if (p.log2n == 4) hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_INRANGE, 4, LAYOUT>), grid, block, 0, st, p);
         else hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_INRANGE, 0, LAYOUT>), grid, block, 0, st, p);
-      }
-      KTimer t("attn_bwd_dq_inrange", st);
-      if (p.log2n == 4) hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE_INRANGE, 4, LAYOUT>), qgrid, block, 0, st, p);
-      else hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE_INRANGE, 0, LAYOUT>), qgrid, block, 0, st, p);
-    } break;
-    case MODE_CLIPPED: {
-      {
+      } break;
+      case MODE_CLIPPED: {
         KTimer t("attn_bwd_clipped", st);
-        hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_CLIPPED, 0, LAYOUT>), grid, block, 0, st, p);
-      }
-      KTimer t("attn_bwd_dq_clipped", st);
-      hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE_CLIPPED, 0, LAYOUT>), qgrid, block, 0, st, p);
-    } break;
-    case MODE_SHIFTED: {
-      {
+        hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_CLIPPED, 0, LAYOUT>), dim3(fallback_grid(p, nbh * nkb)), block,
+                           0, st, p);
+      } break;
+      case MODE_SHIFTED: {
         KTimer t("attn_bwd_shifted", st);
-        hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_SHIFTED, 0, LAYOUT>), grid, block, 0, st, p);
-      }
-      KTimer t("attn_bwd_dq_shifted", st);
-      hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE_SHIFTED, 0, LAYOUT>), qgrid, block, 0, st, p);
-    } break;
-    default: return hipErrorInvalidValue;
+        hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_SHIFTED, 0, LAYOUT>), dim3(fallback_grid(p, nbh * nkb)), block,
+                           0, st, p);
+      } break;
+      default: return hipErrorInvalidValue;
+    }
   }
   return hipGetLastError();
 }
 
 template <int D>
-static hipError_t launch_bwd_main_bf16(const AttnBwdParams& p, int mode, hipStream_t st) {
-  return p.layout ? launch_bwd_main_bf16_l<D, 1>(p, mode, st) : launch_bwd_main_bf16_l<D, 0>(p, mode, st);
+static hipError_t launch_bwd_bf16(const AttnBwdParams& p, int mode, bool dq, hipStream_t st) {
+  return p.layout ? launch_bwd_bf16_l<D, 1>(p, mode, dq, st) : launch_bwd_bf16_l<D, 0>(p, mode, dq, st);
 }
 
-template <typename T, int D>
-static hipError_t launch_bwd_main(const AttnBwdParams& p, int mode, hipStream_t st) {
-  if constexpr (sizeof(T) == 2) return launch_bwd_main_bf16<D>(p, mode, st);
-  dim3 grid(p.B * p.H, ceil_div(p.T, BWD_BK)), block(256);
+// f32: the key-stationary kernel with dQ atomics.
+template <int D>
+static hipError_t launch_bwd_f32(const AttnBwdParams& p, int mode, hipStream_t st) {
+  const int nbh = p.B * p.H, nkb = ceil_div(p.T, BWD_BK);
+  dim3 block(256);
   switch (mode) {
     case MODE_INRANGE: {
       KTimer t("attn_bwd_inrange", st);
-      if (p.log2n == 4) hipLaunchKernelGGL((attn_bwd_kernel<T, D, MODE_INRANGE, 4>), grid, block, 0, st, p);
-      else hipLaunchKernelGGL((attn_bwd_kernel<T, D, MODE_INRANGE, 0>), grid, block, 0, st, p);
+      dim3 grid(nbh, nkb);
+      if (p.log2n == 4) hipLaunchKernelGGL((attn_bwd_kernel<float, D, MODE_INRANGE, 4>), grid, block, 0, st, p);
+      else hipLaunchKernelGGL((attn_bwd_kernel<float, D, MODE_INRANGE, 0>), grid, block, 0, st, p);
     } break;
-    case MODE_CLIPPED: { KTimer t("attn_bwd_clipped", st); hipLaunchKernelGGL((attn_bwd_kernel<T, D, MODE_CLIPPED, 0>), grid, block, 0, st, p); } break;
-    case MODE_SHIFTED: { KTimer t("attn_bwd_shifted", st); hipLaunchKernelGGL((attn_bwd_kernel<T, D, MODE_SHIFTED, 0>), grid, block, 0, st, p); } break;
+    case MODE_CLIPPED: {
+      KTimer t("attn_bwd_clipped", st);
+      hipLaunchKernelGGL((attn_bwd_kernel<float, D, MODE_CLIPPED, 0>), dim3(fallback_grid(p, nbh * nkb)), block, 0, st,
+                         p);
+    } break;
+    case MODE_SHIFTED: {
+      KTimer t("attn_bwd_shifted", st);
+      hipLaunchKernelGGL((attn_bwd_kernel<float, D, MODE_SHIFTED, 0>), dim3(fallback_grid(p, nbh * nkb)), block, 0, st,
+                         p);
+    } break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
-int attn_bwd_sink_blocks(int T) { return ceil_div(T, PRE_ROWS); }
+int attn_bwd_sink_blocks(int T) { return ceil_div(T, SINK_ROWS); }
 
-// modes: list of main-kernel variants to launch (each exits early unless the guard selects it).
+// modes: list of variants to launch (each exits early unless the guard selects it).
 hipError_t launch_attn_bwd(const AttnBwdParams& p, int D, bool bf16_io, const int* modes, int nmodes,
                            hipStream_t st) {
   const int nblk = attn_bwd_sink_blocks(p.T);
-  dim3 pgrid(p.B * p.H, nblk);
-  {
-    KTimer t("attn_bwd_pre", st);
-    // bf16: dq comes from the dQ kernel, the f32 accumulator is not used.
-    if (bf16_io) hipLaunchKernelGGL((attn_bwd_pre_kernel<bf16>), pgrid, dim3(256), 0, st, p, D, false);
-    else hipLaunchKernelGGL((attn_bwd_pre_kernel<float>), pgrid, dim3(256), 0, st, p, D, true);
+  hipError_t e = hipSuccess;
+  if (bf16_io) {
+    // dQ first (it writes di), then dK/dV; the sink partials come from the dQ kernel.
+    for (int pass = 0; pass < 2 && e == hipSuccess; ++pass)
+      for (int m = 0; m < nmodes && e == hipSuccess; ++m)
+        e = D == 64 ? launch_bwd_bf16<64>(p, modes[m], pass == 0, st) : launch_bwd_bf16<128>(p, modes[m], pass == 0, st);
+  } else {
+    {
+      KTimer t("attn_bwd_pre", st);
+      hipLaunchKernelGGL((attn_bwd_pre_kernel<float>), dim3(p.B * p.H, nblk), dim3(256), 0, st, p, D);
+    }
+    e = hipGetLastError();
+    for (int m = 0; m < nmodes && e == hipSuccess; ++m)
+      e = D == 64 ? launch_bwd_f32<64>(p, modes[m], st) : launch_bwd_f32<128>(p, modes[m], st);
   }
-  hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  for (int m = 0; m < nmodes; ++m) {
-    if (bf16_io) e = D == 64 ? launch_bwd_main<bf16, 64>(p, modes[m], st) : launch_bwd_main<bf16, 128>(p, modes[m], st);
-    else e = D == 64 ? launch_bwd_main<float, 64>(p, modes[m], st) : launch_bwd_main<float, 128>(p, modes[m], st);
-    if (e != hipSuccess) return e;
-  }
   // f32: dq from the accumulator; bf16: only the sink gradient is left to do.
   const size_t total = bf16_io ? 0 : (size_t)p.B * p.H * p.T * D;
   const int blocks = (int)std::max<size_t>(std::min<size_t>((total / 8 + 255) / 256, 16384), 1);

@@ -33,14 +33,14 @@ struct AttnBwdParams {
   const void* q;       // q_s
   const void* k;
   const void* v;
-  const void* o;       // forward output in the input dtype (di source in range)
-  const float* o_precise;  // f32 forward output (di source when shifted) or nullptr
+  const void* o;       // forward output in the input dtype (the di source, except on the
+                       // bf16 shifted fallback, which forms di from its weights)
   const void* dO;      // (B,H,T,D) upstream cotangent in the input dtype
   const float* stat;   // (B,H,T)
   const float* sink;   // (H,) or nullptr
   const int* flag;
-  float* di;           // (B,H,T) f32, written by the pre kernel
-  float* dq_acc;       // (B,H,T,D) f32 accumulator (workspace)
+  float* di;           // (B,H,T) f32, written by the dQ kernel (bf16) or the pre kernel (f32)
+  float* dq_acc;       // (B,H,T,D) f32 accumulator (workspace; f32 inputs only)
   float* sink_part;    // (B*H*nblk) f32 partial sums of mass*di (workspace)
   void* dq;            // (B,H,T,D) output
   void* dk;
@@ -60,7 +60,7 @@ __host__ __device__ inline int ceil_div(int a, int b) { return (a + b - 1) / b; 
 
 // Storage of the (B, ., ., D) tensors of a call (q, k, v, o, dO, dq, dk, dv): 0 = (B, H, T, D),
 // 1 = (B, T, H, D), the projection layout before the head transpose (model.py:167-169, 182).
-// Per-row vectors (stat, di) and the internal f32 buffers (o_precise, dq_acc) stay (B, H, T).
+// Per-row vectors (stat, di) and the internal f32 buffers (o_precise, dq_acc) stay (B, H, T, .).
 // head_base is the element offset of position 0 of head bh = b*H + h; positions are
 // row_stride elements apart.
 __host__ __device__ inline size_t head_base(int bh, int H, int T, int D, int layout) {

@@ -80,8 +80,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, l32 = lane & 31;
   const int T_ = p.T;
   const int nqb = ceil_div(T_, FWD_BQ);
-  const int bh = blockIdx.x;
-  const int qb = nqb - 1 - blockIdx.y;  // heaviest causal rows first
+  // One 128-query block of one head. The in-range kernel takes one per workgroup from its 2-D
+  // grid; the fallbacks loop over them (grid-stride), heaviest causal rows first.
+  auto run = [&](int bh, int qb) __attribute__((always_inline)) {
   const int head = bh % p.H;
   const size_t base = (size_t)bh * T_ * D;  // internal (B, H, T, D) buffers (o_precise)
   const size_t hb = head_base(bh, p.H, T_, D, p.layout);
@@ -290,6 +291,16 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
     }
     if (h == 0) p.stat[(size_t)bh * T_ + myq] = stat;
   }
+  };
+  if constexpr (MODE == MODE_INRANGE) {
+    run(blockIdx.x, nqb - 1 - blockIdx.y);
+  } else {
+    const int nbh = p.B * p.H;
+    for (int L = blockIdx.x; L < nbh * nqb; L += gridDim.x) {
+      run(L % nbh, nqb - 1 - L / nbh);
+      __syncthreads();  // the next block's first K/V tile overwrites LDS
+    }
+  }
 }
 
 // In-range forward for bf16 inputs (the guarded "low" variant): same decomposition as
@@ -487,6 +498,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) 
 template <typename T, int D>
 static hipError_t launch_fwd_mode(const AttnFwdParams& p, int mode, hipStream_t st) {
   dim3 grid(p.B * p.H, ceil_div(p.T, FWD_BQ)), block(256);
+  // The fallbacks loop over (head, query block) items: one workgroup each when the host chose
+  // the variant, a small grid (a multiple of 8) when it is the branch the device guard
+  // usually skips.
+  const int items = p.B * p.H * ceil_div(p.T, FWD_BQ);
+  const int fallback_items = p.flag ? std::min(items, 512) : items;
   switch (mode) {
     case MODE_INRANGE: {
       KTimer t("attn_fwd_inrange", st);
@@ -503,8 +519,14 @@ static hipError_t launch_fwd_mode(const AttnFwdParams& p, int mode, hipStream_t 
         else hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_INRANGE, 0>), grid, block, 0, st, p);
       }
     } break;
-    case MODE_CLIPPED: { KTimer t("attn_fwd_clipped", st); hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_CLIPPED, 0>), grid, block, 0, st, p); } break;
-    case MODE_SHIFTED: { KTimer t("attn_fwd_shifted", st); hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_SHIFTED, 0>), grid, block, 0, st, p); } break;
+    case MODE_CLIPPED: {
+      KTimer t("attn_fwd_clipped", st);
+      hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_CLIPPED, 0>), dim3(fallback_items), block, 0, st, p);
+    } break;
+    case MODE_SHIFTED: {
+      KTimer t("attn_fwd_shifted", st);
+      hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_SHIFTED, 0>), dim3(fallback_items), block, 0, st, p);
+    } break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

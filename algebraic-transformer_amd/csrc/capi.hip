@@ -75,16 +75,17 @@ int check_n(int n) {
   return ALG_OK;
 }
 
-// Workspace layout for attention: [dq_acc f32 B*H*T*D][sink partials B*H*nblk][prep partials 3*1024]
+// Workspace layout for attention: [sink partials f32 B*H*nblk][prep partials f32 3*1024], and
+// for f32 inputs then [dq accumulator f32 B*H*T*D] (the bf16 dQ kernel needs none).
 struct AttnWs {
-  size_t dq_acc, sink_part, prep_part, total;
+  size_t sink_part, prep_part, dq_acc, total;
 };
-AttnWs attn_ws(int B, int H, int T, int D) {
+AttnWs attn_ws(int dtype, int B, int H, int T, int D) {
   AttnWs w;
-  w.dq_acc = 0;
-  w.sink_part = align256((size_t)B * H * T * D * sizeof(float));
-  w.prep_part = w.sink_part + align256((size_t)B * H * alg::attn_bwd_sink_blocks(T) * sizeof(float));
-  w.total = w.prep_part + align256(3 * 1024 * sizeof(float));
+  w.sink_part = 0;
+  w.prep_part = align256((size_t)B * H * alg::attn_bwd_sink_blocks(T) * sizeof(float));
+  w.dq_acc = w.prep_part + align256(3 * 1024 * sizeof(float));
+  w.total = w.dq_acc + (dtype == ALG_DTYPE_F32 ? align256((size_t)B * H * T * D * sizeof(float)) : 0);
   return w;
 }
 
@@ -204,9 +205,10 @@ extern "C" {
 const char* alg_last_error(void) { return g_err.c_str(); }
 const char* alg_version(void) { return "algebraic_hip 0.1 gfx950"; }
 
-size_t alg_attn_workspace_size(int B, int H, int T, int D) {
+size_t alg_attn_workspace_size(int dtype, int B, int H, int T, int D) {
   if (B <= 0 || H <= 0 || T <= 0 || D <= 0) return 0;
-  return attn_ws(B, H, T, D).total;
+  if (dtype != ALG_DTYPE_BF16 && dtype != ALG_DTYPE_F32) return 0;
+  return attn_ws(dtype, B, H, T, D).total;
 }
 
 int alg_attn_prepare(alg_stream_t stream, int dtype, int B, int H, int T, int D, const void* q, const void* k,
@@ -221,7 +223,7 @@ int alg_attn_prepare(alg_stream_t stream, int dtype, int B, int H, int T, int D,
   if (range_guard && (!k || !v)) return fail(ALG_ERR_INVALID, "range_guard needs k and v");
   if (sink_logit && sink_count != 1 && sink_count != H) return fail(ALG_ERR_INVALID, "sink_count must be 1 or H");
   if (sink_logit && !sink_scaled) return fail(ALG_ERR_INVALID, "sink_scaled output required with a sink");
-  const AttnWs ws = attn_ws(B, H, T, D);
+  const AttnWs ws = attn_ws(dtype, B, H, T, D);
   if (!workspace || workspace_bytes < ws.total)
     return fail(ALG_ERR_INVALID, "workspace too small: need %zu bytes", ws.total);
   alg::PrepParams pp;
@@ -337,29 +339,29 @@ int alg_attn_fwd(alg_stream_t stream, int dtype, int layout, int B, int H, int T
 }
 
 int alg_attn_bwd(alg_stream_t stream, int dtype, int layout, int B, int H, int T, int D, const void* q_s,
-                 const void* k, const void* v, const float* sink_scaled, const void* o, const float* o_precise,
-                 const float* stat, const void* dO, int n, int variant, const int* guard_flag, float clamp,
-                 int fast_rho, int inv_stat, float dq_scale, void* dq, void* dk, void* dv, float* di,
-                 float* dsink_scaled, void* workspace, size_t workspace_bytes) {
+                 const void* k, const void* v, const float* sink_scaled, const void* o, const float* stat,
+                 const void* dO, int n, int variant, const int* guard_flag, float clamp, int fast_rho, int inv_stat,
+                 float dq_scale, void* dq, void* dk, void* dv, float* di, float* dsink_scaled, void* workspace,
+                 size_t workspace_bytes) {
   int rc = check_attn_shape(dtype, B, H, T, D);
   if (rc) return rc;
   if ((rc = check_layout(layout, H, T, D))) return rc;
   if ((rc = check_n(n))) return rc;
   if (!q_s || !k || !v || !o || !stat || !dO || !dq || !dk || !dv || !di)
     return fail(ALG_ERR_INVALID, "q_s, k, v, o, stat, dO, dq, dk, dv and di are required");
-  if (!aligned16({q_s, k, v, o, o_precise, dO, dq, dk, dv, workspace}))
+  if (!aligned16({q_s, k, v, o, dO, dq, dk, dv, workspace}))
     return fail(ALG_ERR_INVALID, "matrices must be 16-byte aligned");
   if (variant < ALG_ATTN_INRANGE || variant > ALG_ATTN_GUARDED) return fail(ALG_ERR_INVALID, "unknown variant %d", variant);
   if (variant == ALG_ATTN_GUARDED && !guard_flag) return fail(ALG_ERR_INVALID, "GUARDED needs guard_flag");
-  const AttnWs ws = attn_ws(B, H, T, D);
+  const AttnWs ws = attn_ws(dtype, B, H, T, D);
   if (!workspace || workspace_bytes < ws.total)
     return fail(ALG_ERR_INVALID, "workspace too small: need %zu bytes", ws.total);
   alg::AttnBwdParams p;
-  p.q = q_s; p.k = k; p.v = v; p.o = o; p.o_precise = o_precise; p.dO = dO; p.stat = stat;
+  p.q = q_s; p.k = k; p.v = v; p.o = o; p.dO = dO; p.stat = stat;
   p.sink = sink_scaled;
   p.flag = variant == ALG_ATTN_GUARDED ? guard_flag : nullptr;
   p.di = di;
-  p.dq_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + ws.dq_acc);
+  p.dq_acc = dtype == ALG_DTYPE_F32 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + ws.dq_acc) : nullptr;
   p.sink_part = reinterpret_cast<float*>(static_cast<char*>(workspace) + ws.sink_part);
   p.dq = dq; p.dk = dk; p.dv = dv; p.dbeta = dsink_scaled;
   p.B = B; p.H = H; p.T = T;
@@ -372,7 +374,7 @@ int alg_attn_bwd(alg_stream_t stream, int dtype, int layout, int B, int H, int T
   hipStream_t st = (hipStream_t)stream;
   if (variant == ALG_ATTN_GUARDED) {
     // Both branches are launched; each exits unless the device flag selects it. The
-    // fallback's fast_rho is forced off in the SHIFTED kernel via the params below.
+    // fallback uses stable rho (flash.py:851); the in-range kernels do not read fast_rho.
     const int modes[2] = {alg::MODE_INRANGE, alg::MODE_SHIFTED};
     p.fast_rho = 0;
     return hip_status(alg::launch_attn_bwd(p, D, bf, modes, 2, st), "alg_attn_bwd");

@@ -58,8 +58,10 @@ enum { ALG_ATTN_INRANGE = 0, ALG_ATTN_CLIPPED = 1, ALG_ATTN_SHIFTED = 2, ALG_ATT
 const char* alg_last_error(void);
 const char* alg_version(void);
 
-/* Bytes of workspace alg_attn_prepare / alg_attn_bwd need for this shape. */
-size_t alg_attn_workspace_size(int B, int H, int T, int D);
+/* Bytes of workspace alg_attn_prepare / alg_attn_bwd need for this dtype and shape: the sink
+ * gradient's and the guard's partials, and for ALG_DTYPE_F32 also an f32 dQ accumulator
+ * (B*H*T*D floats). 0 for an invalid dtype or shape. */
+size_t alg_attn_workspace_size(int dtype, int B, int H, int T, int D);
 
 /* Prologue and range guard, flash.py:823-849.
  * q_s = round(q * 1/(sqrt(D) c)) in the input dtype; sink_scaled[h] = sink_logit[h or 0] / c
@@ -85,14 +87,15 @@ int alg_attn_fwd(alg_stream_t stream, int dtype, int layout, int B, int H, int T
                  void* o, float* o_precise, float* stat);
 
 /* Backward, flash.py:333-361, 515-687, 694-726 / head_resident.py:91-119:
- * in the forward residuals and dO; out dq = round(round(n * dq_s_acc) * dq_scale)
- * (dq_scale = 1 gives the kernel's dq_s; = 1/(sqrt(D) c) chains back to q), dk, dv in the
- * input dtype and `layout` (as are q_s, k, v, o, dO), di (B,H,T) f32 = sum_d dO*o and
- * dsink_scaled (H) f32 = dL/d(sink/c)
- * (may be NULL). o_precise is used for di when the SHIFTED branch ran, if given. */
+ * in the forward residuals (q_s, k, v, sink_scaled, o, stat) and dO; out
+ * dq = round(round(n * dq_s_acc) * dq_scale) (dq_scale = 1 gives the kernel's dq_s;
+ * = 1/(sqrt(D) c) chains back to q), dk, dv in the input dtype and `layout` (as are q_s, k, v,
+ * o, dO), di (B,H,T) f32 = sum_d dO*o and dsink_scaled (H) f32 = dL/d(sink/c) (may be NULL).
+ * The bf16 SHIFTED branch needs no f32 copy of the output: it forms di = sum_j p_ij dP_ij from
+ * its own weights (equal to sum_d dO*o in exact arithmetic). */
 int alg_attn_bwd(alg_stream_t stream, int dtype, int layout, int B, int H, int T, int D,
                  const void* q_s, const void* k, const void* v, const float* sink_scaled,
-                 const void* o, const float* o_precise, const float* stat, const void* dO,
+                 const void* o, const float* stat, const void* dO,
                  int n, int variant, const int* guard_flag, float clamp, int fast_rho, int inv_stat,
                  float dq_scale,
                  void* dq, void* dk, void* dv, float* di, float* dsink_scaled,

@@ -21,7 +21,9 @@ Two restatements of the reference:
     slope n applied once (flash.py:591-597), sink VJP (flash.py:694-726), and the
     chain rule through ``q_s`` back to ``q``. ``shifted=True`` restates the guarded
     fallback (flash.py:235-259, 280, 347-350, 851-852): max-shifted stable rho,
-    ``stat = rho(-m) Z^(-1/n)``, precise (f32) output.
+    ``stat = rho(-m) Z^(-1/n)``, precise (f32) output; for bf16 the backward's ``di`` is
+    ``sum_j p_ij dP_ij`` from the f32 weights, as the HIP fallback forms it (it keeps no f32
+    copy of the output), instead of ``<dO_i, o_i>`` over that copy.
     Pin: equal to the dense float64 oracle within the bf16/fp32 tolerances
     (tests/test_oracle.py), and to its own float64 evaluation.
 
@@ -207,13 +209,15 @@ def kernel_forward(q_s, k, v, sink, *, n=16, dtype="bf16", shifted=False, heads=
 
 
 def kernel_backward(q_s, k, v, sink, o, stat, do, *, n=16, alpha=None, dtype="bf16",
-                    shifted=False, heads=None):
+                    shifted=False, heads=None, di_from_weights=False):
     """Backward of the kernel; returns (dq_s, dk, dv, di, dbeta[, dq]).
 
     Per tile (flash.py:333-361): p = rho^n * stat (in range, inv_stat) or (rho*stat)^n
     (shifted); dp = dO v^T; ds = p (dp - di) r. dV = round(p)^T dO; dK = n round(ds)^T q_s;
     dq_s = n round(ds) k (flash.py:573-597). di = sum(dO*o) from the given ``o``
-    (the rounded output in range, the precise output when shifted; flash.py:633, 715).
+    (flash.py:633, 715), or with ``di_from_weights`` di = sum_j p_ij dp_ij from the f32
+    weights (the HIP bf16 shifted fallback, which keeps no f32 copy of its output; the two
+    agree in exact arithmetic, and this one makes sum_j p_ij (dp_ij - di_i) vanish).
     dbeta_h = -sum_{b,t} mass*di * n r(beta) with mass = rho(beta)^n stat (in range) or
     (rho(beta) stat)^n (shifted), rho stable (flash.py:694-705, 721-723).
     If ``alpha`` is given also returns dq = round(dq_s * alpha) (chain rule through q_s).
@@ -223,6 +227,8 @@ def kernel_backward(q_s, k, v, sink, o, stat, do, *, n=16, alpha=None, dtype="bf
     dk = np.zeros((B, H, T, D), F32)
     dv = np.zeros((B, H, T, D), F32)
     di = np.sum(do.astype(F32) * o.astype(F32), axis=-1, dtype=F32)
+    if di_from_weights:
+        di = np.zeros((B, H, T), F32)
     mask = np.tril(np.ones((T, T), bool))
     pairs = heads if heads is not None else [(b, h) for b in range(B) for h in range(H)]
     for b, h in pairs:
@@ -237,6 +243,8 @@ def kernel_backward(q_s, k, v, sink, o, stat, do, *, n=16, alpha=None, dtype="bf
             p = np.where(mask, int_pow(rho * st, n), F32(0))
         p = p.astype(F32)
         dp = dob @ vb.T
+        if di_from_weights:
+            di[b, h] = np.sum(p * dp, axis=1, dtype=F32)
         ds = (p * (dp - di[b, h][:, None]) * r).astype(F32)
         dsb = round_to(ds, dtype)
         dv[b, h] = round_to(round_to(p, dtype).T @ dob, dtype)
@@ -270,9 +278,10 @@ def flash_attention_oracle(q, k, v, sink_logit, do=None, *, n=16, c=8.0, dtype="
     o, stat, o_precise = kernel_forward(q_s, k, v, sink, n=n, dtype=dtype, shifted=not ok)
     res = dict(o=o, stat=stat, q_s=q_s, in_range=ok, o_precise=o_precise)
     if do is not None:
-        o_res = o if ok else o_precise
-        dq_s, dk, dv, di, dbeta, dq = kernel_backward(q_s, k, v, sink, o_res, stat, do, n=n, alpha=alpha,
-                                                       dtype=dtype, shifted=not ok)
+        # The f32 output is exact; the bf16 fallback forms di from its weights.
+        dq_s, dk, dv, di, dbeta, dq = kernel_backward(q_s, k, v, sink, o, stat, do, n=n, alpha=alpha,
+                                                       dtype=dtype, shifted=not ok,
+                                                       di_from_weights=dtype == "bf16" and not ok)
         res.update(dq=dq, dk=dk, dv=dv, di=di)
         if sink_logit is not None:
             shape = np.shape(sink_logit)

@@ -44,11 +44,15 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_workspace_sizes():
+    from algebraic_amd import _lib
     handle = lib()
     B, H, T, D = 8, 16, 2048, 128
-    ws = handle.alg_attn_workspace_size(B, H, T, D)
-    assert ws >= B * H * T * D * 4           # f32 dQ accumulator
-    assert handle.alg_attn_workspace_size(0, H, T, D) == 0
+    ws32 = handle.alg_attn_workspace_size(_lib.DTYPE_F32, B, H, T, D)
+    ws16 = handle.alg_attn_workspace_size(_lib.DTYPE_BF16, B, H, T, D)
+    assert ws32 >= B * H * T * D * 4           # f32 dQ accumulator
+    assert 0 < ws16 < 1 << 20                  # bf16: the sink and guard partials only
+    assert handle.alg_attn_workspace_size(_lib.DTYPE_BF16, 0, H, T, D) == 0
+    assert handle.alg_attn_workspace_size(7, B, H, T, D) == 0
     fwd = handle.alg_head_workspace_size(16384, 2048, 32000, 0)
     bwd = handle.alg_head_workspace_size(16384, 2048, 32000, 1)
     assert bwd - fwd >= 32000 * 16384 * 2     # bf16 logit-gradient block (recompute schedule)

@@ -109,12 +109,42 @@ def test_kernel_restatement_matches_dense(dtype, tol, shifted):
     o, stat, op = OA.kernel_forward(q_s, k, v, sk, dtype=dtype, shifted=shifted)
     o_res = op if shifted else o
     dq_s, dk, dv, di, dbeta, dq = OA.kernel_backward(q_s, k, v, sk, o_res, stat, do, alpha=alpha, dtype=dtype,
-                                                      shifted=shifted)
+                                                      shifted=shifted, di_from_weights=shifted and dtype == "bf16")
     o_ref = OA.dense_forward(q, k, v, sink)
     dq_r, dk_r, dv_r, ds_r = OA.dense_backward(q, k, v, sink, do)
     assert rel_l2(o, o_ref) < tol
     assert rel_l2(dq, dq_r) < tol and rel_l2(dk, dk_r) < tol and rel_l2(dv, dv_r) < tol
     assert rel_l2(dbeta / 8.0, ds_r.reshape(-1)) < tol
+
+
+@pytest.mark.parametrize("dtype,tol", [("f32", 2e-6), ("bf16", 1e-2)])
+def test_shifted_di_from_weights_is_the_output_dot(dtype, tol):
+    """di = sum_j p_ij dP_ij (the HIP bf16 fallback's rule) against the reference's
+    di = <dO_i, o_i> over the f32 output (flash.py:633 with precise_output): equal up to f32
+    rounding in f32, and up to the bf16 rounding of the weights before PV in bf16."""
+    q, k, v, do, sink = attention_inputs(1, 2, 80, 64, seed=6, dtype=dtype, qk_norm=False, scale=3.0)
+    q_s, sk, alpha = OA.prologue(q, sink, dtype=dtype)
+    o, stat, op = OA.kernel_forward(q_s, k, v, sk, dtype=dtype, shifted=True)
+    di_out = OA.kernel_backward(q_s, k, v, sk, op, stat, do, dtype=dtype, shifted=True)[3]
+    di_w = OA.kernel_backward(q_s, k, v, sk, op, stat, do, dtype=dtype, shifted=True, di_from_weights=True)[3]
+    assert rel_l2(di_w, di_out) < tol
+    assert rel_l2(di_w, np.sum(do.astype(np.float64) * OA.dense_forward(q, k, v, sink), -1)) < max(tol, 1e-5)
+
+
+def test_shifted_di_from_weights_centres_equal_keys():
+    """With every score equal the weights are uniform and sum_j p_ij (dP_ij - di_i) = 0, so the
+    exact dq is 0. Without the bf16 rounding of the score gradients (f32) the weights rule
+    leaves only f32 rounding in dq_s, two orders below what a di off by 2^-12 leaves."""
+    shape = (1, 1, 64, 64)
+    q = np.full(shape, np.sqrt(1000.0), np.float32)
+    v = attention_inputs(1, 1, 64, 64, seed=7, dtype="f32")[2]
+    do = np.ones(shape, np.float32)
+    q_s, _, alpha = OA.prologue(q, None, dtype="f32")
+    o, stat, op = OA.kernel_forward(q_s, q, v, None, dtype="f32", shifted=True)
+    dq_w = OA.kernel_backward(q_s, q, v, None, op, stat, do, dtype="f32", shifted=True, di_from_weights=True)[0]
+    dq_bad = OA.kernel_backward(q_s, q, v, None, op * np.float32(1 + 2.0 ** -12), stat, do, dtype="f32",
+                                shifted=True)[0]
+    assert np.linalg.norm(dq_w) < 1e-2 * np.linalg.norm(dq_bad)
 
 
 def test_planted_mistakes_fail_the_pins():
