@@ -29,6 +29,8 @@ _SIGNATURES = {
     "alg_attn_fwd": (_I, [_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _P, _F, _I, _I, _P, _P, _P]),
     "alg_attn_bwd": (_I, [_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P, _F, _I, _I, _F,
                           _P, _P, _P, _P, _P, _P, _S]),
+    "alg_attn_bwd_noalloc": (_I, [_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P, _F, _I, _I,
+                                  _F, _P, _P, _P, _P, _P]),
     "alg_attn_prologue_workspace_size": (_S, [_I, _I, _I, _I]),
     "alg_cayley_tables": (_I, [_P, _P, _I, _I, _P, _P]),
     "alg_attn_qk_prologue": (_I, [_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _F, _P, _I, _F, _I, _I,

@@ -9,10 +9,19 @@
 #include <cstdio>
 #include <cstring>
 #include <initializer_list>
+#include <mutex>
 #include <string>
 
 #include "algebraic_hip.h"
 #include "launchers.h"
+
+// Scratch of alg_attn_bwd_noalloc: the sink-gradient and guard partials and, for f32 inputs,
+// the dQ accumulator (the layout of attn_ws below), for callers that cannot allocate. Each GPU
+// the library runs on holds its own copy of this array until the process ends. Host code never
+// uses its name as an address: the device address comes from hipGetSymbolAddress, once per
+// device (noalloc_scratch below).
+constexpr size_t NOALLOC_SCRATCH_BYTES = ALG_ATTN_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -198,6 +207,29 @@ bool aligned16(std::initializer_list<const void*> ptrs) {
   return true;
 }
 
+// Device address of `scratch` on the current device, looked up with that device current on the
+// first call that runs there and kept per device.
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[MAX_DEVICES];
+
+int noalloc_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e, "alg_attn_bwd_noalloc: hipGetDevice");
+  if (dev < 0 || dev >= MAX_DEVICES) return fail(ALG_ERR_UNSUPPORTED, "device %d: at most %d devices", dev, MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_status(e, "alg_attn_bwd_noalloc: hipGetSymbolAddress");
+    if (!ptr) return fail(ALG_ERR_HIP, "alg_attn_bwd_noalloc: no device address for the scratch array");
+    g_scratch_dev[dev] = ptr;
+  }
+  *out = g_scratch_dev[dev];
+  return ALG_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -381,6 +413,24 @@ int alg_attn_bwd(alg_stream_t stream, int dtype, int layout, int B, int H, int T
   }
   const int modes[1] = {variant};
   return hip_status(alg::launch_attn_bwd(p, D, bf, modes, 1, st), "alg_attn_bwd");
+}
+
+int alg_attn_bwd_noalloc(alg_stream_t stream, int dtype, int layout, int B, int H, int T, int D, const void* q_s,
+                         const void* k, const void* v, const float* sink_scaled, const void* o, const float* stat,
+                         const void* dO, int n, int variant, const int* guard_flag, float clamp, int fast_rho,
+                         int inv_stat, float dq_scale, void* dq, void* dk, void* dv, float* di, float* dsink_scaled) {
+  int rc = check_attn_shape(dtype, B, H, T, D);
+  if (rc) return rc;
+  const size_t need = attn_ws(dtype, B, H, T, D).total;
+  if (need > NOALLOC_SCRATCH_BYTES)
+    return fail(ALG_ERR_UNSUPPORTED,
+                "alg_attn_bwd_noalloc: this call needs %zu bytes of scratch, above the %zu bytes the library "
+                "holds per GPU; use alg_attn_bwd with a workspace",
+                need, NOALLOC_SCRATCH_BYTES);
+  void* ptr = nullptr;
+  if ((rc = noalloc_scratch(&ptr))) return rc;
+  return alg_attn_bwd(stream, dtype, layout, B, H, T, D, q_s, k, v, sink_scaled, o, stat, dO, n, variant, guard_flag,
+                      clamp, fast_rho, inv_stat, dq_scale, dq, dk, dv, di, dsink_scaled, ptr, NOALLOC_SCRATCH_BYTES);
 }
 
 size_t alg_head_workspace_size(int N, int d, int V, int pass) {

@@ -101,6 +101,27 @@ int alg_attn_bwd(alg_stream_t stream, int dtype, int layout, int B, int H, int T
                  void* dq, void* dk, void* dv, float* di, float* dsink_scaled,
                  void* workspace, size_t workspace_bytes);
 
+/* Allocation-free variant of alg_attn_bwd. It has no counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving or
+ * training loops, harnesses that forbid allocation). Same arguments, results and errors as
+ * alg_attn_bwd without the workspace: the scratch (the sink-gradient and guard partials, and
+ * for ALG_DTYPE_F32 the f32 dQ accumulator) is a device array the library holds per GPU,
+ * ALG_ATTN_NOALLOC_SCRATCH_BYTES bytes on each GPU it runs on, until the process ends. A call
+ * whose scratch would exceed it (alg_attn_workspace_size above that limit; f32 inputs with
+ * more than about two million B*H*T*D elements) fails with ALG_ERR_UNSUPPORTED. The call
+ * allocates no device memory (with the measurement hook of alg_timer_enable off, the
+ * default); its first call on a device looks up that device's scratch address. Every call on
+ * one GPU shares that GPU's scratch: calls that overlap on one GPU (concurrent streams or
+ * threads) race and must be ordered by the caller. Nothing in the scratch needs to start at
+ * zero: every launch writes what it later reads. */
+#define ALG_ATTN_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
+int alg_attn_bwd_noalloc(alg_stream_t stream, int dtype, int layout, int B, int H, int T, int D,
+                         const void* q_s, const void* k, const void* v, const float* sink_scaled,
+                         const void* o, const float* stat, const void* dO,
+                         int n, int variant, const int* guard_flag, float clamp, int fast_rho, int inv_stat,
+                         float dq_scale,
+                         void* dq, void* dk, void* dv, float* di, float* dsink_scaled);
+
 /* Cayley rotation tables, src/algebraic/algebraic.py:124-149 (cayley_powers): for the
  * frequencies w (half) f32, cos/sin (seq_len, half) f32 hold the rows
  * ((1 + i w)^2 / (1 + w^2))^m, m < seq_len, by binary exponentiation with a renormalisation

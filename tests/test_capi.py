@@ -143,6 +143,22 @@ def test_neighbour_entry_points_validate_before_launch():
     assert rc == _lib.ALG_ERR_INVALID and b"aligned" in err()
 
 
+def test_noalloc_backward_rejects_scratch_beyond_its_limit():
+    """alg_attn_bwd_noalloc refuses, before any launch or device call, a shape whose scratch
+    (here an f32 dQ accumulator of 2 x 12 x 1024 x 128 floats) exceeds the per-GPU array."""
+    from algebraic_amd import _lib
+    handle = lib()
+    P = ctypes.c_void_p
+    B, H, T, D = 2, 12, 1024, 128
+    assert handle.alg_attn_workspace_size(_lib.DTYPE_F32, B, H, T, D) > 8 << 20
+    rc = handle.alg_attn_bwd_noalloc(None, _lib.DTYPE_F32, 0, B, H, T, D, P(16), P(16), P(16), None, P(16), P(16),
+                                     P(16), 16, 3, P(16), 60.0, 1, 1, 0.01, P(16), P(16), P(16), P(16), None)
+    assert rc == _lib.ALG_ERR_UNSUPPORTED and b"scratch" in handle.alg_last_error()
+    rc = handle.alg_attn_bwd_noalloc(None, _lib.DTYPE_BF16, 0, B, H, T, 96, P(16), P(16), P(16), None, P(16),
+                                     P(16), P(16), 16, 3, P(16), 60.0, 1, 1, 0.01, P(16), P(16), P(16), P(16), None)
+    assert rc == _lib.ALG_ERR_UNSUPPORTED and b"head_dim" in handle.alg_last_error()
+
+
 def test_hot_path_entry_points_reject_misaligned_matrices():
     """Attention and head matrices are moved 16 bytes per lane: a base off a 16-byte boundary
     is refused before any launch."""
