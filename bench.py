@@ -427,46 +427,101 @@ def timed(torch, fn, steps, warmup):
     return (time.perf_counter() - t0) / steps
 
 
-def cpu_baseline(seconds_hint=True):
-    """Time the NumPy oracle on a bounded sample of the step on the host cores."""
+def _cpu_model():
+    """The host CPU's model name (first processor in /proc/cpuinfo), or None."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def _median_time(fn, runs=3, warmup=1):
+    """Median wall time of `runs` calls after `warmup` untimed ones, and every timed sample."""
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2], ts
+
+
+def cpu_baseline(c1_gpu_ms=None):
+    """The NumPy oracle (float32, the cast-faithful restatement of the reference's algorithm)
+    timed on the host cores: one warmup and the median of three runs each of a bounded sample
+    of the step (attention fwd+bwd on a few heads, head fwd+bwd on a few tokens, scaled to the
+    full step) and of BASELINE config 1 (attention forward, fp32, B2 H12 T1024 D64) at full
+    shape. BLAS threads: the affinity mask's cores, capped at OMP_NUM_THREADS when the host
+    sets it (a GPU box's share of the host)."""
     import numpy as np
     from oracle import attention as OA
     from oracle import head as OH
     from oracle.numerics import round_bf16
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
-    except Exception:  # pragma: no cover
-        threads = len(os.sched_getaffinity(0))
+    from threadpoolctl import threadpool_info, threadpool_limits
+    affinity = len(os.sched_getaffinity(0))
+    threads = min(affinity, int(os.environ.get("OMP_NUM_THREADS") or affinity))
     rng = np.random.default_rng(0)
     B, H, T, D = (ATTN[k] for k in "BHTD")
-    nh = 2
+    nh = 4
     mk = lambda: round_bf16(rng.standard_normal((1, nh, T, D)).astype(np.float32))
     q, k, v, do = mk(), mk(), mk(), mk()
     sink = (rng.standard_normal((1, nh, 1, 1)) * 0.1).astype(np.float32)
-    t0 = time.perf_counter()
-    r = OA.flash_attention_oracle(q, k, v, sink, do, n=ATTN["n"], c=ATTN["c"], dtype="bf16")
-    t_attn = (time.perf_counter() - t0) / nh * (B * H)
     N, d, V = HEAD["N"], HEAD["d"], HEAD["V"]
-    ns = 512
-    h = round_bf16(rng.standard_normal((ns, d)).astype(np.float32))
+    ns = (128, 384)  # two token counts: per-call work (E's cast, dE's rounding) is not per token
+    h = round_bf16(rng.standard_normal((ns[1], d)).astype(np.float32))
     E = round_bf16((rng.standard_normal((V, d)) * 0.02).astype(np.float32))
-    tg = rng.integers(0, V, ns)
-    t0 = time.perf_counter()
-    stat, zt, pt, obj = OH.kernel_forward(h, E, tg, n=HEAD["n"], c=HEAD["c"], chunk=256)
-    OH.kernel_backward(h, E, tg, stat, 1.0, n=HEAD["n"], c=HEAD["c"], chunk=256)
-    t_head = (time.perf_counter() - t0) * (N / ns)
+    tg = rng.integers(0, V, ns[1])
+    c1 = OTHER_CONFIGS["C1"]
+    c1x = [rng.standard_normal((c1["B"], c1["H"], c1["T"], c1["D"])).astype(np.float32) for _ in range(3)]
+    c1s = (rng.standard_normal((1, c1["H"], 1, 1)) * 0.1).astype(np.float32)
+
+    def attn_sample():
+        OA.flash_attention_oracle(q, k, v, sink, do, n=ATTN["n"], c=ATTN["c"], dtype="bf16")
+
+    def head_sample(m):
+        stat, _, _, _ = OH.kernel_forward(h[:m], E, tg[:m], n=HEAD["n"], c=HEAD["c"], chunk=128)
+        OH.kernel_backward(h[:m], E, tg[:m], stat, 1.0, n=HEAD["n"], c=HEAD["c"], chunk=128)
+
+    def c1_forward():
+        OA.flash_attention_oracle(*c1x, c1s, n=ATTN["n"], c=ATTN["c"], dtype="f32")
+
+    with threadpool_limits(limits=threads):
+        blas = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+        ta, ta_runs = _median_time(attn_sample)
+        th0, th0_runs = _median_time(lambda: head_sample(ns[0]))
+        th1, th1_runs = _median_time(lambda: head_sample(ns[1]), warmup=0)
+        tc1, tc1_runs = _median_time(c1_forward)
+    t_attn = ta / nh * (B * H)
+    per_token = max(th1 - th0, 0.0) / (ns[1] - ns[0])
+    t_head = th0 + per_token * (N - ns[0])  # the per-call part once, the per-token part N times
     total = attn_flops(**ATTN) * 3.5 + head_flops(**HEAD)
     step_s = t_attn + t_head
-    del r
-    return {
-        "value": round(total / step_s / 1e12, 6), "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
+    c1_flops = attn_flops(**c1)
+    out = {
+        "value": round(total / step_s / 1e12, 6), "unit": "TFLOP/s", "cores": int(blas), "kind": "port",
         "sample": (f"NumPy float32 oracle (oracle/attention.py kernel_forward/backward, oracle/head.py "
-                   f"kernel_forward/backward): attention fwd+bwd on {nh} of {B * H} heads "
-                   f"(T={T}, D={D}) scaled x{B * H // nh}, head fwd+bwd on {ns} of {N} tokens "
-                   f"(d={d}, V={V}) scaled x{N // ns}; est. CPU step {step_s:.1f} s "
-                   f"(attention {t_attn:.1f} s, head {t_head:.1f} s)"),
+                   f"kernel_forward/backward), one warmup then the median of 3 runs: attention fwd+bwd on "
+                   f"{nh} of {B * H} heads (T={T}, D={D}) scaled x{B * H // nh}, head fwd+bwd on {ns[0]} and "
+                   f"{ns[1]} of {N} tokens (d={d}, V={V}) extrapolated linearly to {N} tokens; est. CPU "
+                   f"step {step_s:.1f} s (attention {t_attn:.1f} s, head {t_head:.1f} s)"),
+        "cpu_model": _cpu_model(),
+        "affinity_cores": affinity,
+        "blas_threads": int(blas),
+        "runs_s": {"attention_sample": [round(x, 4) for x in ta_runs],
+                   f"head_sample_{ns[0]}": [round(x, 4) for x in th0_runs],
+                   f"head_sample_{ns[1]}": [round(x, 4) for x in th1_runs]},
+        "C1": {"workload": c1["workload"] + ", full shape", "ms": round(tc1 * 1e3, 3),
+               "tflops": round(c1_flops / tc1 / 1e12, 6), "runs_ms": [round(x * 1e3, 3) for x in tc1_runs]},
     }
+    if c1_gpu_ms:
+        out["C1"]["gpu_ms"] = c1_gpu_ms
+        out["C1"]["gpu_speedup"] = round(tc1 * 1e3 / c1_gpu_ms, 1)
+    return out
 
 
 def main():
@@ -544,6 +599,14 @@ def main():
     dom = max(per_step, key=per_step.get)
     dom_ms = kernels[dom]["mean_ms"]
     achieved = algo.get(dom, 0.0) / (dom_ms * 1e-3) / 1e12 if dom in algo else None
+
+    def in_step(prefix, flops):
+        """A part's time inside the full step: the sum of its kernels' HIP-event durations
+        in the timed step pass (the standalone loop above runs the part alone, back to back)."""
+        ms = sum(v for n, v in per_step.items() if n.startswith(prefix))
+        tf = flops / (ms * 1e-3) / 1e12
+        return {"in_step_kernels_ms": round(ms, 4), "in_step_tflops": round(tf, 3),
+                "in_step_frac_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
     roofline = {
         "kernel": dom,
         "bound": "mfma",
@@ -578,11 +641,13 @@ def main():
             "ms": round(attn_s * 1e3, 4), "tflops": round(attn_tf, 3),
             "tokens_per_s": round(ATTN["B"] * ATTN["T"] / attn_s, 1),
             "frac_peak": round(attn_tf / PEAK_BF16_TFLOPS, 4),
+            **in_step("attn_", fa),
         },
         "head": {
             "ms": round(head_s * 1e3, 4), "tflops": round(head_tf, 3),
             "tokens_per_s": round(HEAD["N"] / head_s, 1),
             "frac_peak": round(head_tf / PEAK_BF16_TFLOPS, 4),
+            **in_step("head_", fh),
         },
         "kernels": {n: {"launches_per_step": r["launches"] / K, "mean_ms": round(r["mean_ms"], 4),
                         **({"tflops": round(algo[n] / (r["mean_ms"] * 1e-3) / 1e12, 2)} if n in algo else {})}
@@ -600,7 +665,8 @@ def main():
         out["ffn"] = time_ffn(torch, dev)
     if not args.no_cpu_baseline:
         log("timing the CPU baseline sample")
-        out["cpu_baseline"] = cpu_baseline()
+        c1_ms = out.get("other_configs", {}).get("C1", {}).get("ms")
+        out["cpu_baseline"] = cpu_baseline(c1_ms)
     print(json.dumps(out), flush=True)
     return 0
 

@@ -96,10 +96,18 @@ def round_bf16(x):
     This is the rounding of ``astype(jnp.bfloat16)`` at every cast point of the reference.
     """
     x = np.ascontiguousarray(np.asarray(x, np.float32))
-    u = x.view(np.uint32).astype(np.uint64)
-    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
-    out = (r & 0xFFFFFFFF).astype(np.uint32).view(np.float32)
-    return np.where(np.isnan(x), x, out).astype(np.float32)
+    u = x.view(np.uint32)
+    # u + 0x7FFF + lsb stays below 2^32 for every non-NaN pattern (the largest, -inf, is
+    # 0xFF800000); NaN patterns may wrap and are restored below.
+    r = (u >> 16) & np.uint32(1)
+    r += u
+    r += np.uint32(0x7FFF)
+    r &= np.uint32(0xFFFF0000)
+    out = r.view(np.float32)
+    nan = np.isnan(x)
+    if nan.any():
+        out[nan] = x[nan]
+    return out
 
 
 def round_to(x, dtype):
