@@ -840,8 +840,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
 // dP^T = V dO^T (Q and dO fragments held in registers, so each lane owns one query and its
 // stat / di are per-lane scalars); dS^T feeds dQ^T += K^T dS^T directly as the B operand,
 // with K^T fragments read transposed from the K tile. K/V stream through LDS in 64-key tiles
-// that ping-pong between two buffer sets, copied a full tile ahead. Per tile:
-//   R1  S^T, dP^T of keys 0..31                  (MFMA)
+// that ping-pong between two buffer sets, each copied during the previous tile's first steps.
+// Per tile:
+//   R1  S^T, dP^T of keys 0..31 | next tile's copy (MFMA | VMEM)
 //   R2  S^T, dP^T of keys 32..63 | dS of 0..31   (MFMA | VALU)
 //   R3  dQ^T over keys 0..31     | dS of 32..63  (MFMA | VALU)
 //   R4  dQ^T over keys 32..63                    (MFMA)
@@ -859,6 +860,7 @@ template <int D, int MODE, int L2N, int LAYOUT>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
   static_assert(D == 64 || D == 128, "head_dim");
   constexpr int BK = 64, CPR = D / 8, NDB = D / 32, NF = D / 16;
+  constexpr int PW = 64 * CPR / 64 / 4;  // copy instruction pairs per wave and tile
   __shared__ __attribute__((aligned(16))) bf16 Ks0[BK * D];
   __shared__ __attribute__((aligned(16))) bf16 Ks1[BK * D];
   __shared__ __attribute__((aligned(16))) bf16 Vs0[BK * D];
@@ -906,7 +908,6 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
   const int ntiles = (min(qb * 128 + 127, T_ - 1)) / BK + 1;  // key tiles up to the last query
 
   tile_dma2<D>(Ks0, Vs0, rk, rv, 0, wave, lane, ld);
-  if (ntiles > 1) tile_dma2<D>(Ks1, Vs1, rk, rv, BK, wave, lane, ld);
   // Q and dO fragments of this lane's query (B operands of S^T = K Q^T, dP^T = V dO^T);
   // queries past T carry stat = 0, so their weights and score gradients are zero.
   bf16x8 qf[NF], of[NF];
@@ -989,15 +990,24 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
       f[1] = tr_frag_at(kb + 16 * D, tk_lo[db], tk_hi[db]);
     };
 
-    // R1: S^T and dP^T of keys 0..31.
+    // R1: S^T and dP^T of keys 0..31, with the copy of the next tile into the other buffer
+    // set (free since the barrier that ended the previous tile) spread over its steps: issued
+    // in one burst, the copies of the CU's eight waves queue on the vector memory path and
+    // stall the waves. Past the last tile the rows lie beyond the descriptors' ranges (no
+    // memory is read; zeros land in the unused buffer set).
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       s[b] = floatx16{};
       dp[b] = floatx16{};
     }
+    const int r_next = kt + 1 < ntiles ? kb0 + BK : T_ + BK;
 #pragma unroll
     for (int g = 0; g < NF; ++g) {
       sdp_step(g);
+      if (g < PW) {
+        if constexpr (BUF) tile_dma2_part<D>(Ks0, Vs0, rk, rv, r_next, wave, lane, g, ld);
+        else tile_dma2_part<D>(Ks1, Vs1, rk, rv, r_next, wave, lane, g, ld);
+      }
       step_order<2, 0, 4, 0>();
     }
     // R2: S^T and dP^T of keys 32..63 under dS of keys 0..31.
@@ -1039,16 +1049,12 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
     }
 
     __builtin_amdgcn_s_waitcnt(VMCNT0);  // this wave's copies of the next tile have landed
-    __syncthreads();                     // this buffer set is no longer read
+    __syncthreads();                     // the next tile is complete; this buffer set is free
     {
       const bf16* Kn = BUF ? Ks0 : Ks1;
       const bf16* Vn = BUF ? Vs0 : Vs1;
       rk2[0] = ld8(Kn + row_off[0]);
       rv2[0] = ld8(Vn + row_off[0]);
-    }
-    if (kt + 2 < ntiles) {
-      if constexpr (BUF) tile_dma2<D>(Ks1, Vs1, rk, rv, kb0 + 2 * BK, wave, lane, ld);
-      else tile_dma2<D>(Ks0, Vs0, rk, rv, kb0 + 2 * BK, wave, lane, ld);
     }
   };
 
@@ -1071,7 +1077,6 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
     diq = di_acc + xor32(di_acc);
     __syncthreads();  // every wave is done with the last tile's fragments
     tile_dma2<D>(Ks0, Vs0, rk, rv, 0, wave, lane, ld);
-    if (ntiles > 1) tile_dma2<D>(Ks1, Vs1, rk, rv, BK, wave, lane, ld);
     __builtin_amdgcn_s_waitcnt(VMCNT0);
     __syncthreads();
     rk2[0] = ld8(Ks0 + row_off[0]);

@@ -139,10 +139,12 @@ constexpr int F32_PAD = 4;
 // value: two per-lane registers serve all of them.
 // Both matrices have rows `ld` elements apart (ld = D for (B, H, T, D) storage, H*D for
 // (B, T, H, D)); the descriptors' ranges end at the head's last row (head_bytes).
-template <int D>
+// ROWS (64 by default, or 32) is the tile height; the four waves share the copy instructions.
+template <int D, int ROWS = 64>
 __device__ __forceinline__ void tile_dma2(bf16* la, bf16* lb, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
                                           int r0, int wave, int lane, int ld = D) {
-  constexpr int CPR = D / 8, RPI = 64 / CPR, PW = 64 * CPR / 64 / 4;  // PW instructions per wave
+  constexpr int CPR = D / 8, RPI = 64 / CPR, PW = ROWS * CPR / 64 / 4;  // PW instructions per wave
+  static_assert(PW >= 1 && PW * 4 * RPI == ROWS, "tile height");
   auto lla = LDS_PTR(bf16, la);
   auto llb = LDS_PTR(bf16, lb);
   asm volatile("" : "+s"(lla), "+s"(llb));
@@ -160,11 +162,11 @@ __device__ __forceinline__ void tile_dma2(bf16* la, bf16* lb, __amdgpu_buffer_rs
 }
 // Instruction pair j of tile_dma2 alone (lets a kernel spread a tile copy over several
 // pipeline steps).
-template <int D>
+template <int D, int ROWS = 64>
 __device__ __forceinline__ void tile_dma2_part(bf16* la, bf16* lb, __amdgpu_buffer_rsrc_t ra,
                                                __amdgpu_buffer_rsrc_t rb, int r0, int wave, int lane, int j,
                                                int ld = D) {
-  constexpr int CPR = D / 8, RPI = 64 / CPR, PW = 64 * CPR / 64 / 4;
+  constexpr int CPR = D / 8, RPI = 64 / CPR, PW = ROWS * CPR / 64 / 4;
   auto lla = LDS_PTR(bf16, la);
   auto llb = LDS_PTR(bf16, lb);
   asm volatile("" : "+s"(lla), "+s"(llb));

@@ -305,9 +305,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
 
 // In-range forward for bf16 inputs (the guarded "low" variant): same decomposition as
 // attn_fwd_kernel (4 waves x 32 queries, lane = query, S^T = K Q^T, O^T += V^T P^T), with K/V
-// tiles copied into LDS a full tile ahead by range-checked buffer copies (two ping-pong buffer
-// sets) and each 64-key tile software-pipelined over its two 32-key blocks:
-//   R1  S^T of keys 0..31                       (MFMA)
+// tiles in two ping-pong LDS buffer sets, each filled by range-checked buffer copies issued
+// during the previous tile's first steps, and each 64-key tile software-pipelined over its two
+// 32-key blocks:
+//   R1  S^T of keys 0..31 | copy of the next tile (MFMA | VMEM)
 //   R2  S^T of keys 32..63 | weights of 0..31   (MFMA | VALU)
 //   R3  O^T over keys 0..31 | weights of 32..63 (MFMA | VALU)
 //   R4  O^T over keys 32..63                    (MFMA)
@@ -341,8 +342,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) 
   const int log2n = p.log2n;
   const int ntiles = min(qb * FWD_BQ + FWD_BQ - 1, T_ - 1) / BK + 1;  // key tiles up to the last query
 
+  constexpr int PW = 64 * CPR / 64 / 4;  // copy instruction pairs per wave and tile
   tile_dma2<D>(Ks0, Vs0, rk, rv, 0, wave, lane, ld);
-  if (ntiles > 1) tile_dma2<D>(Ks1, Vs1, rk, rv, BK, wave, lane, ld);
   // Query fragments (B operand of S^T = K Q^T), held for the whole kernel.
   bf16x8 qf[NF];
   const bool live = myq < T_;
@@ -408,12 +409,21 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) 
       f[1] = tr_frag_at(vb + 16 * D, tv_lo[db], tv_hi[db]);
     };
 
-    // R1: S^T of keys 0..31.
+    // R1: S^T of keys 0..31, with the copy of the next tile into the other buffer set (free
+    // since the barrier that ended the previous tile) spread over its steps, one instruction
+    // pair per step: issued in one burst, the copies of the CU's eight waves queue on the
+    // vector memory path and stall the waves. Past the last tile the rows lie beyond the
+    // descriptors' ranges (no memory is read; zeros land in the unused buffer set).
     s[0] = floatx16{};
     s[1] = floatx16{};
+    const int r_next = kt + 1 < ntiles ? kb0 + BK : T_ + BK;
 #pragma unroll
     for (int g = 0; g < NF; ++g) {
       s_step(g);
+      if (g < PW) {
+        if constexpr (BUF) tile_dma2_part<D>(Ks0, Vs0, rk, rv, r_next, wave, lane, g, ld);
+        else tile_dma2_part<D>(Ks1, Vs1, rk, rv, r_next, wave, lane, g, ld);
+      }
       step_order<1, 0, 2, 0>();
     }
     // R2: S^T of keys 32..63 under the weights of keys 0..31.
@@ -450,15 +460,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) 
     }
 
     __builtin_amdgcn_s_waitcnt(VMCNT0);  // this wave's copies of the next tile have landed
-    __syncthreads();                     // this buffer set is no longer read
+    __syncthreads();                     // the next tile is complete; this buffer set is free
     {
       const bf16* Kn = BUF ? Ks0 : Ks1;
       rk3[0] = ld8(Kn + row_off[0]);
       rk3[1] = ld8(Kn + row_off[1]);
-    }
-    if (kt + 2 < ntiles) {
-      if constexpr (BUF) tile_dma2<D>(Ks1, Vs1, rk, rv, kb0 + 2 * BK, wave, lane, ld);
-      else tile_dma2<D>(Ks0, Vs0, rk, rv, kb0 + 2 * BK, wave, lane, ld);
     }
   };
 

@@ -34,8 +34,10 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 #define BUF_NT 2
 
 namespace alg {
-// s_waitcnt immediate for vmcnt(0) with expcnt/lgkmcnt left at their maxima (gfx9 encoding).
-constexpr int VMCNT0 = 0x0F70;
+// s_waitcnt immediate for vmcnt(n) with expcnt/lgkmcnt left at their maxima (gfx9 encoding:
+// vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
+constexpr int VMCNT0 = vmcnt_imm(0);
 }  // namespace alg
 
 namespace alg {
