@@ -142,11 +142,17 @@ __global__ __launch_bounds__(NT, 1) void head_fwd_kernel(HeadParams p) {
       constexpr int RPS = 64 / UCH;  // token rows per store instruction
       const int ch = lane % UCH;
       const int voff = ((lane / UCH) * p.Vp + ch * 8) * 2;
+      // The row offset goes into the per-lane offset and the scalar offset stays the constant
+      // 0. A 16-byte store needs one wait state before a VALU instruction may overwrite its
+      // data registers; the compiler inserts it only when the scalar offset is not an SGPR.
+      // With the row offset in an SGPR (an earlier form of this loop) the next instruction
+      // reused the data registers of the store just issued, and on gfx950 the store wrote the
+      // new values (measured: about 0.1 % of the U entries replaced by address arithmetic).
 #pragma unroll
       for (int j = 0; j < HC::WTN / RPS; ++j) {
         const int tl = RPS * j + lane / UCH;
         const u32x4 v = *reinterpret_cast<const u32x4*>(ub + ub_at(tl, ch * 8));
-        __builtin_amdgcn_raw_buffer_store_b128(v, urs, voff, RPS * j * p.Vp * 2, BUF_NT);
+        __builtin_amdgcn_raw_buffer_store_b128(v, urs, voff + RPS * j * p.Vp * 2, 0, BUF_NT);
       }
     }
   };

@@ -162,8 +162,10 @@ int alg_attn_qk_prologue_bwd(alg_stream_t stream, int dtype, int layout, int B, 
  * alg_head_bwd with a residual (pass 2) and alg_head_eval (pass 3). */
 size_t alg_head_workspace_size(int N, int d, int V, int pass);
 
-/* Bytes of the optional forward->backward residual: the vocab-major bf16 block
- * U = w*r (target entries (w_t - l) r_t) and the row sums l. With it the backward needs no
+/* Bytes of the optional forward->backward residual: the token-major bf16 block
+ * U = w*r (target entries (w_t - l) r_t) of Npad x Vp entries (U[tok, v] at tok * Vp + v,
+ * Npad = N rounded up to 256, Vp = V rounded up to 8), then, at the next 256-byte boundary,
+ * the row sums l (N floats). With it the backward needs no
  * logit recompute (3 products instead of 4); it has no counterpart in the reference, whose
  * residuals are (h, E, targets, stat) (fused_head.py:244). */
 size_t alg_head_residual_size(int N, int d, int V);

@@ -100,3 +100,45 @@ def test_head_confident_targets_no_cancellation(schedule):
     np.testing.assert_allclose(obj, obj_r, rtol=2e-2, atol=2e-4)
     assert rel_l2(dh, dh_r) < 2e-2
     assert rel_l2(dE, dE_r) < 2e-2
+
+
+@pytest.mark.parametrize("N,d,V,n,c", [(1024, 256, 4096, 16, 16.0), (1024, 256, 32768, 16, 16.0),
+                                       (1024, 256, 4096, 8, 2.0), (384, 256, 1000, 16, 16.0)])
+def test_residual_block_every_entry(N, d, V, n, c):
+    """Every entry of the forward's residual block U (token-major, Npad x Vp bf16) against
+    bf16(w r), target entries bf16((w_t - l) r_t), on two calls in a row. A relative L2 bar on
+    dh misses a few hundred wrong entries among millions; this compares each one."""
+    from algebraic_amd import _lib
+    from oracle.numerics import head_clamp, int_pow, round_bf16
+    lib, P = _lib.load(), _lib.ptr
+    rng = np.random.default_rng(100 + V + n)
+    h = round_bf16(rng.standard_normal((N, d)).astype(np.float32))
+    E = round_bf16((rng.standard_normal((V, d)) * 0.15).astype(np.float32))
+    t = rng.integers(0, V, N).astype(np.int32)
+    z = h @ E.T
+    x = np.minimum(z * np.float32(1.0 / c), np.float32(head_clamp(V, n)))
+    rad = np.float32(1.0) + x * x
+    r = np.float32(1.0) / np.sqrt(rad)
+    w = int_pow(x + rad * r, n).astype(np.float32)
+    l = w.sum(1, dtype=np.float64).astype(np.float32)
+    U_ref = w * r
+    rows = np.arange(N)
+    U_ref[rows, t] = (w[rows, t] - l) * r[rows, t]
+    th = torch.tensor(h, device="cuda").to(torch.bfloat16)
+    tE = torch.tensor(E, device="cuda").to(torch.bfloat16)
+    tt = torch.tensor(t, device="cuda")
+    ws_b = lib.alg_head_workspace_size(N, d, V, 0)
+    ws = torch.empty(ws_b, dtype=torch.uint8, device="cuda")
+    Npad, Vp = (N + 255) // 256 * 256, (V + 7) // 8 * 8
+    outs = [torch.empty(N, device="cuda") for _ in range(3)] + [torch.empty(1, device="cuda")]
+    for call in range(2):
+        res = torch.full((lib.alg_head_residual_size(N, d, V),), 0x7F, dtype=torch.uint8, device="cuda")
+        _lib.check(lib.alg_head_fwd(_lib.stream_of(th), N, d, V, P(th), P(tE), P(tt), n, c, *map(P, outs),
+                                    P(res), P(ws), ws_b), "alg_head_fwd")
+        torch.cuda.synchronize()
+        U = res[:Npad * Vp * 2].view(torch.bfloat16).view(Npad, Vp)[:N, :V].float().cpu().numpy()
+        err = np.abs(U - U_ref) / np.abs(U_ref)
+        bad = np.argwhere(err > 1e-2)
+        assert len(bad) == 0, f"call {call}: {len(bad)} wrong entries, first {bad[:4].tolist()}"
+        l_k = res[(Npad * Vp * 2 + 255) // 256 * 256:].view(torch.float32)[:N].cpu().numpy()
+        np.testing.assert_allclose(l_k, l, rtol=1e-4)
