@@ -4,10 +4,10 @@
 Mirrors ``fused_head(h, embed, targets, *, kind, n, c, block_n, block_v)``
 (src/algebraic/kernels/fused_head.py:260-275) and its custom VJP (232-257) over torch
 tensors on the GPU. The logits are never materialised: the forward is one tiled
-``E h^T`` MFMA pass with the row statistics fused into its epilogue; the backward
-recomputes the tiles, forms the bf16 logit gradient in a bounded workspace and runs the two
-gradient GEMMs in HIP (including the embedding gradient the reference leaves to XLA,
-fused_head.py:215). Returns ``(objective, telemetry)``: the mean target-miss probability
+``E h^T`` MFMA pass with the row statistics fused into its epilogue; the backward reads the
+forward's bf16 residual, or recomputes the tiles and forms the logit gradient (bf16, or f32
+for f32 hidden states) in a bounded workspace, and runs the two gradient GEMMs in HIP
+(including the embedding gradient the reference leaves to XLA, fused_head.py:215). Returns ``(objective, telemetry)``: the mean target-miss probability
 (whose gradient is the exact NLL gradient) and the per-token target probability, which
 receives no gradient. ``kind="ce"`` (the softmax control arm) raises NotImplementedError.
 """
@@ -18,10 +18,13 @@ import torch
 
 from .. import _lib
 
-# Backward schedule: "residual" keeps the vocab-major bf16 block U = w r (and l) from the
+# Backward schedule: "residual" keeps the token-major bf16 block U = w r (and l) from the
 # forward so the backward runs 3 products; "recompute" keeps only (h, E, targets, stat) as
-# the reference does (fused_head.py:244) and recomputes the logits (4 products).
+# the reference does (fused_head.py:244) and recomputes the logits (4 products). f32 hidden
+# states always take the recompute schedule, in f32 throughout as the reference runs it.
 SCHEDULE = os.environ.get("ALGEBRAIC_HEAD_SCHEDULE", "residual")
+
+_DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float32: _lib.DTYPE_F32}
 
 
 def _root(value, n):
@@ -44,16 +47,17 @@ class _HeadFn(torch.autograd.Function):
         h = _lib.aligned16(h)
         e = _lib.aligned16(embed.detach().to(h.dtype))        # fused_head.py:168
         t = targets.to(device=dev, dtype=torch.int32).contiguous()
-        ws_bytes = lib.alg_head_workspace_size(N, d, V, 0)
+        dt = _DTYPES[h.dtype]
+        ws_bytes = lib.alg_head_workspace_size(dt, N, d, V, 0)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         stat = torch.empty(N, dtype=torch.float32, device=dev)
         zt = torch.empty(N, dtype=torch.float32, device=dev)
         pt = torch.empty(N, dtype=torch.float32, device=dev)
         obj = torch.empty((), dtype=torch.float32, device=dev)
         residual = None
-        if SCHEDULE == "residual" and any(ctx.needs_input_grad[:2]):
+        if SCHEDULE == "residual" and dt == _lib.DTYPE_BF16 and any(ctx.needs_input_grad[:2]):
             residual = torch.empty(lib.alg_head_residual_size(N, d, V), dtype=torch.uint8, device=dev)
-        _lib.check(lib.alg_head_fwd(st, N, d, V, _lib.ptr(h), _lib.ptr(e), _lib.ptr(t), n, c, _lib.ptr(stat),
+        _lib.check(lib.alg_head_fwd(st, dt, N, d, V, _lib.ptr(h), _lib.ptr(e), _lib.ptr(t), n, c, _lib.ptr(stat),
                                     _lib.ptr(zt), _lib.ptr(pt), _lib.ptr(obj), _lib.ptr(residual),
                                     _lib.ptr(ws), ws_bytes),
                    "fused_head forward")
@@ -72,12 +76,13 @@ class _HeadFn(torch.autograd.Function):
         dev = h.device
         st = _lib.stream_of(h)
         g = (g_obj if g_obj is not None else torch.zeros((), device=dev)).to(torch.float32).reshape(1).contiguous()
-        ws_bytes = lib.alg_head_workspace_size(N, d, V, 2 if residual is not None else 1)
+        dt = _DTYPES[h.dtype]
+        ws_bytes = lib.alg_head_workspace_size(dt, N, d, V, 2 if residual is not None else 1)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         dh = torch.empty_like(h)
         de_f32 = ctx.embed_dtype == torch.float32
         dE = torch.empty((V, d), dtype=torch.float32 if de_f32 else torch.bfloat16, device=dev)
-        _lib.check(lib.alg_head_bwd(st, N, d, V, _lib.ptr(h), _lib.ptr(e), _lib.ptr(t), _lib.ptr(stat), _lib.ptr(g),
+        _lib.check(lib.alg_head_bwd(st, dt, N, d, V, _lib.ptr(h), _lib.ptr(e), _lib.ptr(t), _lib.ptr(stat), _lib.ptr(g),
                                     ctx.n, ctx.c, _lib.ptr(residual), _lib.ptr(dh), _lib.ptr(dE),
                                     _lib.DTYPE_F32 if de_f32 else _lib.DTYPE_BF16, _lib.ptr(ws), ws_bytes),
                    "fused_head backward")
@@ -87,8 +92,9 @@ class _HeadFn(torch.autograd.Function):
 def fused_head(h, embed, targets, *, kind="ce", n=16, c=16.0, block_n=128, block_v=512):
     """Fused tied-embedding projection and likelihood objective (fused_head.py:260-275).
 
-    ``h`` (N, d) bfloat16 hidden states, ``embed`` (V, d), ``targets`` (N,). Returns
-    ``(objective, telemetry)``; the telemetry carries no gradient.
+    ``h`` (N, d) bfloat16 or float32 hidden states, ``embed`` (V, d) (cast to ``h``'s dtype
+    as fused_head.py:168 does), ``targets`` (N,). Returns ``(objective, telemetry)``; the
+    telemetry carries no gradient. ``dh`` comes back in ``h``'s dtype, ``dE`` in ``embed``'s.
     """
     if kind not in ("ce", "alg_ce"):
         raise ValueError(kind)
@@ -100,8 +106,8 @@ def fused_head(h, embed, targets, *, kind="ce", n=16, c=16.0, block_n=128, block
         raise ValueError(f"token count {N} must be divisible by block {bn}")
     if kind == "ce":
         raise NotImplementedError("kind='ce' is the softmax control arm; only kind='alg_ce' is built for MI355X")
-    if h.dtype != torch.bfloat16:
-        raise NotImplementedError(f"hidden dtype {h.dtype}: the gfx950 head takes bfloat16 hidden states")
+    if h.dtype not in _DTYPES:
+        raise NotImplementedError(f"hidden dtype {h.dtype}: the gfx950 head takes bfloat16 or float32 hidden states")
     if not h.is_cuda:
         raise RuntimeError("fused_head needs GPU tensors (no CPU fallback)")
     obj, tel = _HeadFn.apply(h, embed, targets, int(n), float(c))
@@ -114,7 +120,7 @@ def head_logprob(h, embed, targets, *, head="alg_ce", n=8, c=2.0, argmax=True):
     argmax token: the scorer's head (src/algebraic/benchmarking.py:178-188) with
     ``logprob_from_logits`` (src/algebraic/evaluation.py:13-23) for ``head="alg_ce"``.
 
-    ``h`` (N, d) bfloat16, ``embed`` (V, d), ``targets`` (N,). Returns ``(logprob, argmax)``:
+    ``h`` (N, d) bfloat16 or float32, ``embed`` (V, d), ``targets`` (N,). Returns ``(logprob, argmax)``:
     float32 (N,) and int64 (N,) (``None`` when ``argmax=False``). Forward only.
     """
     if head == "ce":
@@ -123,8 +129,8 @@ def head_logprob(h, embed, targets, *, head="alg_ce", n=8, c=2.0, argmax=True):
         raise ValueError(f"unknown head {head!r}")
     if n & (n - 1):
         raise ValueError("n must be a power of two")
-    if h.dtype != torch.bfloat16:
-        raise NotImplementedError(f"hidden dtype {h.dtype}: the gfx950 head takes bfloat16 hidden states")
+    if h.dtype not in _DTYPES:
+        raise NotImplementedError(f"hidden dtype {h.dtype}: the gfx950 head takes bfloat16 or float32 hidden states")
     if not h.is_cuda:
         raise RuntimeError("head_logprob needs GPU tensors (no CPU fallback)")
     lib = _lib.load()
@@ -135,8 +141,9 @@ def head_logprob(h, embed, targets, *, head="alg_ce", n=8, c=2.0, argmax=True):
     t = targets.to(device=h.device, dtype=torch.int32).contiguous()
     logprob = torch.empty(N, dtype=torch.float32, device=h.device)
     am = torch.empty(N, dtype=torch.int32, device=h.device) if argmax else None
-    nbytes = lib.alg_head_workspace_size(N, d, V, 3)
+    dt = _DTYPES[h.dtype]
+    nbytes = lib.alg_head_workspace_size(dt, N, d, V, 3)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=h.device)
-    _lib.check(lib.alg_head_eval(_lib.stream_of(h), N, d, V, _lib.ptr(h), _lib.ptr(E), _lib.ptr(t), int(n), float(c),
+    _lib.check(lib.alg_head_eval(_lib.stream_of(h), dt, N, d, V, _lib.ptr(h), _lib.ptr(E), _lib.ptr(t), int(n), float(c),
                                  _lib.ptr(logprob), _lib.ptr(am), _lib.ptr(ws), nbytes), "head_logprob")
     return logprob, (am.long() if argmax else None)

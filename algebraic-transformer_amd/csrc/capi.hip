@@ -126,12 +126,30 @@ HeadWs head_ws(int N, int d, int V, int pass, bool residual) {
   return w;
 }
 
+// f32 hidden states (head_f32.hip, the reference's recompute schedule in f32): [partials f32
+// nvt*N over 128-entry vocabulary tiles][obj parts] (+ bwd: dZ f32 N*Vp, then the f32 partials
+// split*N*d of a vocabulary-split dh product). No residual.
+HeadWs head_ws_f32(int N, int d, int V, int pass) {
+  HeadWs w;
+  w.Npad = N;
+  w.Vp = alg::head_vocab_pitch(V);
+  w.partial = 0;
+  w.obj_part = align256((size_t)alg::head_f32_vocab_tiles(V) * N * sizeof(float));
+  w.bwd = w.obj_part + align256((size_t)alg::head_stat_blocks(N) * sizeof(float));
+  w.dh_split = alg::head_f32_dh_split(N, d, V);
+  w.dh_part = w.bwd + align256((size_t)N * w.Vp * sizeof(float));
+  const size_t part_bytes = w.dh_split > 1 ? (size_t)w.dh_split * N * d * sizeof(float) : 0;
+  w.total = pass == 0 ? w.bwd : w.dh_part + align256(part_bytes);
+  w.res_ut = w.res_l = w.res_total = 0;
+  return w;
+}
+
 // Eval workspace: [row-sum partials f32 nvt*N][tile maxima f32 nvt*N][their indices i32 nvt*N].
 struct HeadEvalWs {
   size_t partial, pmax, pidx, total;
 };
-HeadEvalWs head_eval_ws(int N, int V) {
-  const size_t cells = (size_t)alg::head_vocab_tiles(V) * N;
+HeadEvalWs head_eval_ws(int N, int V, bool f32) {
+  const size_t cells = (size_t)(f32 ? alg::head_f32_vocab_tiles(V) : alg::head_vocab_tiles(V)) * N;
   HeadEvalWs w;
   w.partial = 0;
   w.pmax = align256(cells * sizeof(float));
@@ -433,10 +451,13 @@ int alg_attn_bwd_noalloc(alg_stream_t stream, int dtype, int layout, int B, int 
                       clamp, fast_rho, inv_stat, dq_scale, dq, dk, dv, di, dsink_scaled, ptr, NOALLOC_SCRATCH_BYTES);
 }
 
-size_t alg_head_workspace_size(int N, int d, int V, int pass) {
+size_t alg_head_workspace_size(int dtype, int N, int d, int V, int pass) {
   if (N <= 0 || d <= 0 || V <= 0) return 0;
+  if (dtype != ALG_DTYPE_BF16 && dtype != ALG_DTYPE_F32) return 0;
+  const bool f32 = dtype == ALG_DTYPE_F32;
   // pass 0: forward; 1: backward without a residual; 2: backward with a residual; 3: eval
-  if (pass == 3) return head_eval_ws(N, V).total;
+  if (pass == 3) return head_eval_ws(N, V, f32).total;
+  if (f32) return pass == 2 ? 0 : head_ws_f32(N, d, V, pass ? 1 : 0).total;  // no residual in f32
   return head_ws(N, d, V, pass ? 1 : 0, pass == 2).total;
 }
 
@@ -445,12 +466,26 @@ size_t alg_head_residual_size(int N, int d, int V) {
   return head_ws(N, d, V, 0, true).res_total;
 }
 
-static alg::HeadParams head_params(int N, int d, int V, const void* h, const void* E, const int32_t* targets, int n,
-                                   float c, void* workspace, const HeadWs& ws) {
+// Head dtype check: bf16 (the tuned kernels, both schedules) or f32 (the reference's recompute
+// schedule in f32; no residual).
+static int check_head_dtype(int dtype, const void* residual) {
+  if (dtype != ALG_DTYPE_BF16 && dtype != ALG_DTYPE_F32) return fail(ALG_ERR_INVALID, "dtype must be bf16 or f32");
+  if (dtype == ALG_DTYPE_F32 && residual)
+    return fail(ALG_ERR_UNSUPPORTED, "the residual schedule is built for bf16 hidden states only; pass NULL");
+  return ALG_OK;
+}
+
+static alg::HeadParams head_params(int dtype, int N, int d, int V, const void* h, const void* E,
+                                   const int32_t* targets, int n, float c, void* workspace, const HeadWs& ws) {
   alg::HeadParams p;
   std::memset(&p, 0, sizeof p);
-  p.h = static_cast<const bf16*>(h);
-  p.E = static_cast<const bf16*>(E);
+  if (dtype == ALG_DTYPE_F32) {
+    p.h32 = static_cast<const float*>(h);
+    p.E32 = static_cast<const float*>(E);
+  } else {
+    p.h = static_cast<const bf16*>(h);
+    p.E = static_cast<const bf16*>(E);
+  }
   p.targets = targets;
   p.N = N; p.d = d; p.V = V; p.Npad = ws.Npad; p.Vp = ws.Vp;
   p.log2n = log2_pow2(n);
@@ -463,18 +498,21 @@ static alg::HeadParams head_params(int N, int d, int V, const void* h, const voi
   return p;
 }
 
-int alg_head_fwd(alg_stream_t stream, int N, int d, int V, const void* h, const void* E, const int32_t* targets,
-                 int n, float c, float* stat, float* zt, float* pt, float* obj, void* residual,
-                 void* workspace, size_t workspace_bytes) {
+int alg_head_fwd(alg_stream_t stream, int dtype, int N, int d, int V, const void* h, const void* E,
+                 const int32_t* targets, int n, float c, float* stat, float* zt, float* pt, float* obj,
+                 void* residual, void* workspace, size_t workspace_bytes) {
   int rc = check_head(N, d, V, n, c);
+  if (!rc) rc = check_head_dtype(dtype, residual);
   if (rc) return rc;
+  const bool f32 = dtype == ALG_DTYPE_F32;
   if (!h || !E || !targets || !stat || !zt || !pt || !obj) return fail(ALG_ERR_INVALID, "null argument");
   if (!aligned16({h, E, residual, workspace})) return fail(ALG_ERR_INVALID, "matrices must be 16-byte aligned");
-  const HeadWs ws = head_ws(N, d, V, 0, residual != nullptr);
+  const HeadWs ws = f32 ? head_ws_f32(N, d, V, 0) : head_ws(N, d, V, 0, residual != nullptr);
   if (!workspace || workspace_bytes < ws.total)
     return fail(ALG_ERR_INVALID, "workspace too small: need %zu bytes", ws.total);
-  alg::HeadParams p = head_params(N, d, V, h, E, targets, n, c, workspace, ws);
+  alg::HeadParams p = head_params(dtype, N, d, V, h, E, targets, n, c, workspace, ws);
   p.stat = stat; p.zt = zt; p.pt = pt; p.obj = obj;
+  if (f32) return hip_status(alg::launch_head_fwd_f32(p, (hipStream_t)stream), "alg_head_fwd");
   if (residual) {
     p.ut = reinterpret_cast<bf16*>(static_cast<char*>(residual) + ws.res_ut);
     p.lsum = reinterpret_cast<float*>(static_cast<char*>(residual) + ws.res_l);
@@ -567,17 +605,20 @@ int alg_ffn_alu_glu_dy(alg_stream_t stream, int N, int dm, int F, const void* do
   return hip_status(alg::launch_ffn_dy(p, (hipStream_t)stream), "alg_ffn_alu_glu_dy");
 }
 
-int alg_head_eval(alg_stream_t stream, int N, int d, int V, const void* h, const void* E, const int32_t* targets,
-                  int n, float c, float* logprob, int32_t* argmax, void* workspace, size_t workspace_bytes) {
+int alg_head_eval(alg_stream_t stream, int dtype, int N, int d, int V, const void* h, const void* E,
+                  const int32_t* targets, int n, float c, float* logprob, int32_t* argmax, void* workspace,
+                  size_t workspace_bytes) {
   int rc = check_head(N, d, V, n, c);
+  if (!rc) rc = check_head_dtype(dtype, nullptr);
   if (rc) return rc;
+  const bool f32 = dtype == ALG_DTYPE_F32;
   if (!h || !E || !targets || !logprob) return fail(ALG_ERR_INVALID, "null argument");
   if (!aligned16({h, E, workspace})) return fail(ALG_ERR_INVALID, "matrices must be 16-byte aligned");
-  const HeadEvalWs ws = head_eval_ws(N, V);
+  const HeadEvalWs ws = head_eval_ws(N, V, f32);
   if (!workspace || workspace_bytes < ws.total)
     return fail(ALG_ERR_INVALID, "workspace too small: need %zu bytes", ws.total);
-  const HeadWs hw = head_ws(N, d, V, 0, false);
-  alg::HeadParams p = head_params(N, d, V, h, E, targets, n, c, workspace, hw);
+  const HeadWs hw = f32 ? head_ws_f32(N, d, V, 0) : head_ws(N, d, V, 0, false);
+  alg::HeadParams p = head_params(dtype, N, d, V, h, E, targets, n, c, workspace, hw);
   char* w = static_cast<char*>(workspace);
   p.partial = reinterpret_cast<float*>(w + ws.partial);
   p.pmax = reinterpret_cast<float*>(w + ws.pmax);
@@ -586,24 +627,37 @@ int alg_head_eval(alg_stream_t stream, int N, int d, int V, const void* h, const
   p.zt = reinterpret_cast<float*>(logprob);  // the target logit is staged in the output
   p.logprob = logprob;
   p.argmax = argmax;
+  if (f32) return hip_status(alg::launch_head_eval_f32(p, (hipStream_t)stream), "alg_head_eval");
   return hip_status(alg::launch_head_eval(p, (hipStream_t)stream), "alg_head_eval");
 }
 
-int alg_head_bwd(alg_stream_t stream, int N, int d, int V, const void* h, const void* E, const int32_t* targets,
-                 const float* stat, const float* g, int n, float c, const void* residual, void* dh, void* dE,
-                 int dE_dtype, void* workspace, size_t workspace_bytes) {
+int alg_head_bwd(alg_stream_t stream, int dtype, int N, int d, int V, const void* h, const void* E,
+                 const int32_t* targets, const float* stat, const float* g, int n, float c, const void* residual,
+                 void* dh, void* dE, int dE_dtype, void* workspace, size_t workspace_bytes) {
   int rc = check_head(N, d, V, n, c);
+  if (!rc) rc = check_head_dtype(dtype, residual);
   if (rc) return rc;
+  const bool f32 = dtype == ALG_DTYPE_F32;
   if (!h || !E || !targets || !stat || !g || !dh || !dE) return fail(ALG_ERR_INVALID, "null argument");
   if (!aligned16({h, E, residual, dh, dE, workspace})) return fail(ALG_ERR_INVALID, "matrices must be 16-byte aligned");
   if (dE_dtype != ALG_DTYPE_BF16 && dE_dtype != ALG_DTYPE_F32) return fail(ALG_ERR_INVALID, "dE dtype must be bf16 or f32");
-  const HeadWs ws = head_ws(N, d, V, 1, residual != nullptr);
+  const HeadWs ws = f32 ? head_ws_f32(N, d, V, 1) : head_ws(N, d, V, 1, residual != nullptr);
   if (!workspace || workspace_bytes < ws.total)
     return fail(ALG_ERR_INVALID, "workspace too small: need %zu bytes", ws.total);
-  alg::HeadParams p = head_params(N, d, V, h, E, targets, n, c, workspace, ws);
+  alg::HeadParams p = head_params(dtype, N, d, V, h, E, targets, n, c, workspace, ws);
   p.stat = const_cast<float*>(stat);
   p.g = g;
   char* w = static_cast<char*>(workspace);
+  p.dE = dE;
+  p.dE_f32 = dE_dtype == ALG_DTYPE_F32;
+  if (f32) {
+    p.dz32 = reinterpret_cast<float*>(w + ws.bwd);
+    p.dh32 = static_cast<float*>(dh);
+    p.dh_split = ws.dh_split;
+    p.dh_kchunk = alg::head_f32_dh_kchunk(V, ws.dh_split);
+    p.dh_part = ws.dh_split > 1 ? reinterpret_cast<float*>(w + ws.dh_part) : nullptr;
+    return hip_status(alg::launch_head_bwd_f32(p, (hipStream_t)stream), "alg_head_bwd");
+  }
   if (residual) {
     p.ut = reinterpret_cast<bf16*>(static_cast<char*>(const_cast<void*>(residual)) + ws.res_ut);
     p.lsum = reinterpret_cast<float*>(static_cast<char*>(const_cast<void*>(residual)) + ws.res_l);
@@ -615,8 +669,6 @@ int alg_head_bwd(alg_stream_t stream, int N, int d, int V, const void* h, const 
   p.dh_split = ws.dh_split;
   p.dh_kchunk = alg::head_dh_kchunk(V, ws.dh_split);
   p.dh_part = ws.dh_split > 1 ? reinterpret_cast<float*>(w + ws.dh_part) : nullptr;
-  p.dE = dE;
-  p.dE_f32 = dE_dtype == ALG_DTYPE_F32;
   return hip_status(alg::launch_head_bwd(p, (hipStream_t)stream), "alg_head_bwd");
 }
 

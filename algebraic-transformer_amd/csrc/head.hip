@@ -25,7 +25,9 @@
 #include <type_traits>
 
 #include "gemm_core.h"
+#include "head_eval.h"
 #include "head_params.h"
+#include "launchers.h"
 
 namespace alg {
 
@@ -205,32 +207,6 @@ __global__ __launch_bounds__(NT, 1) void head_fwd_kernel(HeadParams p) {
 // terms. The epilogue keeps, per token and vocabulary tile, the tile's largest logit with its
 // first index (the argmax), the sum of w' relative to that logit, and the target logit.
 // Nothing per (token, vocab) pair is stored; head_eval_stats_kernel combines the tiles.
-constexpr int EVAL_NO_INDEX = 0x7fffffff;
-
-// Argmax order over increasing vocabulary indices (jnp.argmax): the first NaN wins, else the
-// first of the largest values. (z, i) replaces the running (zm, im) when it comes first in that
-// order; the running value starts empty (EVAL_NO_INDEX).
-__device__ __forceinline__ bool eval_better(float z, int i, float zm, int im) {
-  if (im == EVAL_NO_INDEX) return true;
-  if (zm != zm) return z != z && i < im;
-  if (z != z) return true;
-  return z > zm || (z == zm && i < im);
-}
-
-// Stable rho (reciprocal form below zero) with the hardware reciprocal: rho(x) = e^asinh(x).
-__device__ __forceinline__ float eval_rho(float x) {
-  const float rad = __builtin_fmaf(x, x, 1.0f);
-  const float t = __builtin_fmaf(rad, rsq(rad), __builtin_fabsf(x));
-  return x >= 0.0f ? t : __builtin_amdgcn_rcpf(t);
-}
-
-// Factor that moves a sum of weights relative to logit za onto logit zb >= za:
-// (rho(za/c) rho(-zb/c))^n, exactly 1 when za == zb.
-template <int L2N>
-__device__ __forceinline__ float eval_rescale(float za, float zb, float inv_c, int log2n) {
-  if (za == zb) return 1.0f;
-  return pow2n<L2N>(eval_rho(za * inv_c) * eval_rho(-zb * inv_c), log2n);
-}
 
 template <int L2N>
 __global__ __launch_bounds__(NT, 1) void head_eval_kernel(HeadParams p) {
@@ -442,10 +418,6 @@ __global__ __launch_bounds__(256) void head_obj_kernel(HeadParams p, int nblocks
   if (threadIdx.x == 0) p.obj[0] = red[0] / (float)p.N;
 }
 
-__device__ __forceinline__ float head_grad_scale(const HeadParams& p) {
-  return p.g[0] * (((float)(1 << p.log2n) * p.inv_c) / (float)p.N);  // fused_head.py:251
-}
-
 // Recompute schedule: z^T again, dZ^T = bf16(s (p - y) r).
 __global__ __launch_bounds__(NT, 1) void head_dz_kernel(HeadParams p) {
   __shared__ __attribute__((aligned(16))) GemmStage<KMAJOR, KMAJOR, HC> s0, s1;
@@ -625,9 +597,21 @@ hipError_t launch_head_fwd(const HeadParams& p, hipStream_t st) {
     if (p.log2n == 3) hipLaunchKernelGGL(head_fwd_kernel<3>, dim3(tiles), dim3(NT), 0, st, p);
     else hipLaunchKernelGGL(head_fwd_kernel<0>, dim3(tiles), dim3(NT), 0, st, p);
   }
+  return launch_head_stats(p, head_vocab_tiles(p.V), st);
+}
+
+// Statistics, telemetry and objective from the forward's per-tile partial sums (any tiling:
+// vocab_tiles partial rows of N).
+hipError_t launch_head_stats(const HeadParams& p, int vocab_tiles, hipStream_t st) {
   const int nb = head_stat_blocks(p.N);
-  { KTimer t("head_stats", st); hipLaunchKernelGGL(head_stats_kernel, dim3(nb), dim3(256), 0, st, p, head_vocab_tiles(p.V)); }
+  { KTimer t("head_stats", st); hipLaunchKernelGGL(head_stats_kernel, dim3(nb), dim3(256), 0, st, p, vocab_tiles); }
   { KTimer t("head_obj", st); hipLaunchKernelGGL(head_obj_kernel, dim3(1), dim3(256), 0, st, p, nb); }
+  return hipGetLastError();
+}
+
+hipError_t launch_head_eval_stats(const HeadParams& p, int vocab_tiles, hipStream_t st) {
+  KTimer t("head_eval_stats", st);
+  hipLaunchKernelGGL(head_eval_stats_kernel, dim3(head_stat_blocks(p.N)), dim3(256), 0, st, p, vocab_tiles);
   return hipGetLastError();
 }
 
@@ -638,11 +622,7 @@ hipError_t launch_head_eval(const HeadParams& p, hipStream_t st) {
     if (p.log2n == 3) hipLaunchKernelGGL(head_eval_kernel<3>, dim3(tiles), dim3(NT), 0, st, p);
     else hipLaunchKernelGGL(head_eval_kernel<0>, dim3(tiles), dim3(NT), 0, st, p);
   }
-  {
-    KTimer t("head_eval_stats", st);
-    hipLaunchKernelGGL(head_eval_stats_kernel, dim3(head_stat_blocks(p.N)), dim3(256), 0, st, p, head_vocab_tiles(p.V));
-  }
-  return hipGetLastError();
+  return launch_head_eval_stats(p, head_vocab_tiles(p.V), st);
 }
 
 hipError_t launch_head_bwd(const HeadParams& p, hipStream_t st) {

@@ -44,9 +44,19 @@ struct HeadParams {
   int* pidx;            // eval: (ceil(V/HT_M), N) its vocabulary index
   float* logprob;       // eval: (N,) log p(target)
   int* argmax;          // eval: (N,) argmax_v z
+  // f32 hidden states (the head_f32 kernels; the bf16 pointers above are then unused):
+  const float* h32;     // (N, d)
+  const float* E32;     // (V, d), already cast to f32
+  float* dz32;          // recompute workspace (N, Vp): s (p - y) r, token-major
+  float* dh32;          // (N, d)
 };
 
 typedef GemmCfg<HT_M, HT_N, ALG_HEAD_WM, ALG_HEAD_WN> HeadGemm;
+
+// Scale of the logit gradient, g n / (c N) (fused_head.py:249-251).
+__device__ __forceinline__ float head_grad_scale(const HeadParams& p) {
+  return p.g[0] * (((float)(1 << p.log2n) * p.inv_c) / (float)p.N);
+}
 
 // ALU-GLU feed-forward products with fused activation epilogues (model.py:185-193).
 struct FfnParams {

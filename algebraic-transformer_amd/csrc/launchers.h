@@ -29,6 +29,14 @@ int head_dh_kchunk(int V, int split);
 hipError_t launch_head_fwd(const HeadParams& p, hipStream_t st);
 hipError_t launch_head_bwd(const HeadParams& p, hipStream_t st);
 hipError_t launch_head_eval(const HeadParams& p, hipStream_t st);
+hipError_t launch_head_stats(const HeadParams& p, int vocab_tiles, hipStream_t st);
+hipError_t launch_head_eval_stats(const HeadParams& p, int vocab_tiles, hipStream_t st);
+int head_f32_vocab_tiles(int V);
+int head_f32_dh_split(int N, int d, int V);
+int head_f32_dh_kchunk(int V, int split);
+hipError_t launch_head_fwd_f32(const HeadParams& p, hipStream_t st);
+hipError_t launch_head_bwd_f32(const HeadParams& p, hipStream_t st);
+hipError_t launch_head_eval_f32(const HeadParams& p, hipStream_t st);
 int rms_norm_max_d();
 int rms_norm_blocks(int rows);
 hipError_t launch_rms_norm_fwd(const RmsNormParams& p, hipStream_t st);

@@ -159,8 +159,9 @@ int alg_attn_qk_prologue_bwd(alg_stream_t stream, int dtype, int layout, int B, 
                              float* dq_gain, float* dk_gain, void* workspace, size_t workspace_bytes);
 
 /* Bytes of workspace for alg_head_fwd (pass 0), alg_head_bwd without a residual (pass 1),
- * alg_head_bwd with a residual (pass 2) and alg_head_eval (pass 3). */
-size_t alg_head_workspace_size(int N, int d, int V, int pass);
+ * alg_head_bwd with a residual (pass 2) and alg_head_eval (pass 3), for hidden states of
+ * dtype ALG_DTYPE_BF16 or ALG_DTYPE_F32 (0 for f32 pass 2: the residual is bf16 only). */
+size_t alg_head_workspace_size(int dtype, int N, int d, int V, int pass);
 
 /* Bytes of the optional forward->backward residual: the token-major bf16 block
  * U = w*r (target entries (w_t - l) r_t) of Npad x Vp entries (U[tok, v] at tok * Vp + v,
@@ -171,24 +172,27 @@ size_t alg_head_workspace_size(int N, int d, int V, int pass);
 size_t alg_head_residual_size(int N, int d, int V);
 
 /* Head forward, fused_head.py:72-117, 174-191, 219-229 (kind="alg_ce"):
- * in h (N,d) bf16, E (V,d) bf16 (already cast to h's dtype), targets (N) int32;
+ * in h (N,d) and E (V,d) of dtype ALG_DTYPE_BF16 or ALG_DTYPE_F32 (E already cast to h's
+ * dtype, fused_head.py:168), targets (N) int32;
  * out stat (N) = l^(-1/n), zt (N) = target logits, pt (N) telemetry, obj (1) = mean(1-pt),
- * and, when residual is not NULL, the residual for alg_head_bwd. The clamp
+ * and, when residual is not NULL (bf16 only; ALG_ERR_UNSUPPORTED for f32), the residual for
+ * alg_head_bwd. f32 runs the reference's computation in f32 throughout. The clamp
  * X = 1/4 (1e38/V)^(1/n) is derived from V and n. d must be a multiple of 8 and N at most 2^23. */
-int alg_head_fwd(alg_stream_t stream, int N, int d, int V,
+int alg_head_fwd(alg_stream_t stream, int dtype, int N, int d, int V,
                  const void* h, const void* E, const int32_t* targets, int n, float c,
                  float* stat, float* zt, float* pt, float* obj, void* residual,
                  void* workspace, size_t workspace_bytes);
 
 /* Evaluation head, replacing the dense logits of the reference's scorer
  * (src/algebraic/benchmarking.py:178-188 with src/algebraic/evaluation.py:13-23, head
- * "alg_ce"): for h (N,d) bf16, E (V,d) bf16 and targets (N) int32, streams the vocabulary like
+ * "alg_ce"): for h (N,d) and E (V,d) of dtype ALG_DTYPE_BF16 or ALG_DTYPE_F32 and targets
+ * (N) int32, streams the vocabulary like
  * alg_head_fwd and writes logprob[n] = log_softmax(n asinh(z/c))[t_n] with no clamp (computed
  * as n (log rho(z_t/c) + log rho(-z_m/c)) - log sum_v (rho(z_v/c) rho(-z_m/c))^n, z_m the row's
  * largest logit, so no term overflows) and, if argmax is not NULL, argmax[n] = the first index
  * of the largest logit z_n (the first NaN if the row holds one, as jnp.argmax). No logits are
  * stored. */
-int alg_head_eval(alg_stream_t stream, int N, int d, int V,
+int alg_head_eval(alg_stream_t stream, int dtype, int N, int d, int V,
                   const void* h, const void* E, const int32_t* targets, int n, float c,
                   float* logprob, int32_t* argmax, void* workspace, size_t workspace_bytes);
 
@@ -218,10 +222,12 @@ int alg_ffn_alu_glu_dy(alg_stream_t stream, int N, int dm, int F, const void* do
                        const void* gate, const void* up, float beta, void* d_gu);
 
 /* Head backward, fused_head.py:120-156, 194-216, 247-254:
- * in h, E, targets, stat, g (1) f32 on the device (cotangent of obj) and optionally the
- * forward's residual; out dh (N,d) bf16 and dE (V,d) in dE_dtype (ALG_DTYPE_BF16 or
- * ALG_DTYPE_F32). Without a residual the logits are recomputed (the reference's schedule). */
-int alg_head_bwd(alg_stream_t stream, int N, int d, int V,
+ * in h, E (of dtype ALG_DTYPE_BF16 or ALG_DTYPE_F32), targets, stat, g (1) f32 on the device
+ * (cotangent of obj) and optionally the forward's residual (bf16 only); out dh (N,d) in h's
+ * dtype and dE (V,d) in dE_dtype (ALG_DTYPE_BF16 or ALG_DTYPE_F32). Without a residual the
+ * logits are recomputed (the reference's schedule; f32 keeps dZ in f32 as the reference does
+ * for f32 h). */
+int alg_head_bwd(alg_stream_t stream, int dtype, int N, int d, int V,
                  const void* h, const void* E, const int32_t* targets, const float* stat,
                  const float* g, int n, float c, const void* residual, void* dh, void* dE, int dE_dtype,
                  void* workspace, size_t workspace_bytes);

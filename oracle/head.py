@@ -91,8 +91,11 @@ def kernel_forward(h, E, targets, *, n=8, c=2.0, dtype="bf16", rows=None, chunk=
 
 
 def kernel_backward(h, E, targets, stat, g=1.0, *, n=8, c=2.0, dtype="bf16", e_dtype="bf16",
-                    chunk=2048, rows=None):
-    """(dh, dE) of the fused head backward with the kernel's rounding points.
+                    chunk=2048, rows=None, dz_dtype=None):
+    """(dh, dE) of the fused head backward with the kernel's rounding points: the logit
+    gradient is stored in the hidden dtype (``dzb.astype(dz_ref.dtype)``, fused_head.py:145;
+    bf16, or f32 for f32 hidden states), dh in that dtype and dE in ``e_dtype``. ``dz_dtype``
+    overrides the logit gradient's storage dtype (the tests plant a wrong rounding with it).
 
     ``rows`` restricts the work to a token subset (bounded CPU samples): dh is exact on those
     rows (0 elsewhere) and dE then sums only their contributions. The scale keeps the full
@@ -117,7 +120,7 @@ def kernel_backward(h, E, targets, stat, g=1.0, *, n=8, c=2.0, dtype="bf16", e_d
         p = int_pow((x + rad * r) * stat[ids][:, None], n)
         y = np.zeros_like(p)
         y[np.arange(len(ids)), targets[ids]] = 1
-        dzb = round_to((p - y) * r * scale, "bf16")
+        dzb = round_to((p - y) * r * scale, dz_dtype or dtype)
         dh[ids] = dzb @ Eb
         dE += dzb.T @ hh[ids]
     return round_to(dh, dtype), round_to(dE, e_dtype)

@@ -53,12 +53,20 @@ def test_workspace_sizes():
     assert 0 < ws16 < 1 << 20                  # bf16: the sink and guard partials only
     assert handle.alg_attn_workspace_size(_lib.DTYPE_BF16, 0, H, T, D) == 0
     assert handle.alg_attn_workspace_size(7, B, H, T, D) == 0
-    fwd = handle.alg_head_workspace_size(16384, 2048, 32000, 0)
-    bwd = handle.alg_head_workspace_size(16384, 2048, 32000, 1)
+    bf, f32 = _lib.DTYPE_BF16, _lib.DTYPE_F32
+    fwd = handle.alg_head_workspace_size(bf, 16384, 2048, 32000, 0)
+    bwd = handle.alg_head_workspace_size(bf, 16384, 2048, 32000, 1)
     assert bwd - fwd >= 32000 * 16384 * 2     # bf16 logit-gradient block (recompute schedule)
-    bwd_res = handle.alg_head_workspace_size(16384, 2048, 32000, 2)
+    bwd_res = handle.alg_head_workspace_size(bf, 16384, 2048, 32000, 2)
     assert bwd_res - fwd >= 16384 * 2048 * 2  # bf16 s*h/l (residual schedule)
     assert handle.alg_head_residual_size(16384, 2048, 32000) >= 32000 * 16384 * 2 + 16384 * 4
+    # f32 hidden states: the f32 logit-gradient block, no residual schedule.
+    fwd32 = handle.alg_head_workspace_size(f32, 16384, 2048, 32000, 0)
+    bwd32 = handle.alg_head_workspace_size(f32, 16384, 2048, 32000, 1)
+    assert fwd32 > 0 and bwd32 - fwd32 >= 32000 * 16384 * 4
+    assert handle.alg_head_workspace_size(f32, 16384, 2048, 32000, 2) == 0
+    assert handle.alg_head_workspace_size(f32, 512, 256, 1000, 3) > 0
+    assert handle.alg_head_workspace_size(7, 512, 256, 1000, 0) == 0
 
 
 def test_invalid_arguments_fail_before_launch():
@@ -80,11 +88,21 @@ def test_invalid_arguments_fail_before_launch():
     rc = handle.alg_attn_fwd(None, 0, 1, 1, 256, 1 << 16, 128, P(16), P(16), P(16), None, 16, 0, None, 0.0, 1, 1,
                              P(16), None, P(16))
     assert rc == _lib.ALG_ERR_UNSUPPORTED and b"layout" in handle.alg_last_error()
-    rc = handle.alg_head_fwd(None, 128, 100, 1000, P(16), P(16), P(16), 8, 2.0, P(16), P(16), P(16), P(16),
+    rc = handle.alg_head_fwd(None, 0, 128, 100, 1000, P(16), P(16), P(16), 8, 2.0, P(16), P(16), P(16), P(16),
                              None, P(16), 1 << 30)  # d = 100: rows not 16-byte aligned
     assert rc == _lib.ALG_ERR_UNSUPPORTED and b"d_model" in handle.alg_last_error()
-    rc = handle.alg_head_bwd(None, 128, 256, 1000, P(16), P(16), P(16), P(16), P(16), 8, 2.0, None, P(16), P(16),
-                             0, P(16), 16)
+    rc = handle.alg_head_bwd(None, 0, 128, 256, 1000, P(16), P(16), P(16), P(16), P(16), 8, 2.0, None, P(16),
+                             P(16), 0, P(16), 16)
+    assert rc == _lib.ALG_ERR_INVALID and b"workspace" in handle.alg_last_error()
+    # f32 hidden states take no residual; an unknown dtype is refused.
+    rc = handle.alg_head_fwd(None, _lib.DTYPE_F32, 128, 256, 1000, P(16), P(16), P(16), 8, 2.0, P(16), P(16),
+                             P(16), P(16), P(16), P(16), 1 << 30)
+    assert rc == _lib.ALG_ERR_UNSUPPORTED and b"residual" in handle.alg_last_error()
+    rc = handle.alg_head_bwd(None, 5, 128, 256, 1000, P(16), P(16), P(16), P(16), P(16), 8, 2.0, None, P(16),
+                             P(16), 0, P(16), 1 << 30)
+    assert rc == _lib.ALG_ERR_INVALID and b"dtype" in handle.alg_last_error()
+    rc = handle.alg_head_bwd(None, _lib.DTYPE_F32, 128, 256, 1000, P(16), P(16), P(16), P(16), P(16), 8, 2.0, None,
+                             P(16), P(16), 1, P(16), 16)
     assert rc == _lib.ALG_ERR_INVALID and b"workspace" in handle.alg_last_error()
     with pytest.raises(ValueError):
         _lib.check(_lib.ALG_ERR_INVALID, "probe")
@@ -114,10 +132,12 @@ def test_neighbour_entry_points_validate_before_launch():
     rc = handle.alg_cayley_tables(None, P(16), 0, 128, P(16), P(16))
     assert rc == _lib.ALG_ERR_INVALID and b"positive" in err()
     # Eval head: pass 3 sizes its workspace; too small is refused.
-    need = handle.alg_head_workspace_size(512, 256, 1000, 3)
-    assert need > 0
-    rc = handle.alg_head_eval(None, 512, 256, 1000, P(16), P(16), P(16), 8, 2.0, P(16), P(16), P(16), need - 1)
-    assert rc == _lib.ALG_ERR_INVALID and b"workspace" in err()
+    for dt in (_lib.DTYPE_BF16, _lib.DTYPE_F32):
+        need = handle.alg_head_workspace_size(dt, 512, 256, 1000, 3)
+        assert need > 0
+        rc = handle.alg_head_eval(None, dt, 512, 256, 1000, P(16), P(16), P(16), 8, 2.0, P(16), P(16), P(16),
+                                  need - 1)
+        assert rc == _lib.ALG_ERR_INVALID and b"workspace" in err()
     # Final norm: width limits, eps, gain gradient without a gain, alignment.
     rc = handle.alg_rms_norm_fwd(None, 4, 100, P(16), None, 1e-5, P(16), P(16))
     assert rc == _lib.ALG_ERR_UNSUPPORTED and b"16-byte" in err()
@@ -168,6 +188,6 @@ def test_hot_path_entry_points_reject_misaligned_matrices():
     rc = handle.alg_attn_fwd(None, 0, 0, 1, 1, 64, 64, P(18), P(16), P(16), None, 16, 0, None, 0.0, 1, 1,
                              P(16), None, P(16))
     assert rc == _lib.ALG_ERR_INVALID and b"aligned" in handle.alg_last_error()
-    rc = handle.alg_head_fwd(None, 128, 256, 1000, P(16), P(40), P(16), 8, 2.0, P(16), P(16), P(16), P(16),
+    rc = handle.alg_head_fwd(None, 0, 128, 256, 1000, P(16), P(40), P(16), 8, 2.0, P(16), P(16), P(16), P(16),
                              None, P(16), 1 << 30)
     assert rc == _lib.ALG_ERR_INVALID and b"aligned" in handle.alg_last_error()

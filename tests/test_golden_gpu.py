@@ -72,6 +72,25 @@ def test_head_matches_golden(path):
     assert rel_l2(f64(E.grad), g["dE"]) < 1e-2
 
 
+@pytest.mark.parametrize("path", HEAD, ids=os.path.basename)
+def test_head_f32_matches_golden(path):
+    """The f32 head (h and E float32; the fixture inputs are bf16-exact, so exact in f32)
+    against the float64 closed forms at the f32 bar, 1e-5."""
+    from algebraic_amd.kernels.fused_head import fused_head
+    g = load(path)
+    h = torch.tensor(g["h"], device="cuda", dtype=torch.float32, requires_grad=True)
+    E = torch.tensor(g["E"], device="cuda", dtype=torch.float32, requires_grad=True)
+    t = torch.tensor(g["targets"], device="cuda")
+    print(f"golden head f32 {os.path.basename(path)}", flush=True)
+    obj, pt = fused_head(h, E, t, kind="alg_ce", n=int(g["n"]), c=float(g["c"]))
+    (obj * float(g["g"])).backward()
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(float(obj.detach()), float(g["obj"]), rtol=1e-5, atol=1e-8)
+    assert rel_l2(f64(pt), g["pt"]) < 1e-5
+    assert rel_l2(f64(h.grad), g["dh"]) < 1e-5
+    assert rel_l2(f64(E.grad), g["dE"]) < 1e-5
+
+
 NORM = sorted(glob.glob(os.path.join(GOLDEN, "norm_*.npz")))
 FFN = sorted(glob.glob(os.path.join(GOLDEN, "ffn_*.npz")))
 

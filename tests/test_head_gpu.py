@@ -127,13 +127,13 @@ def test_residual_block_every_entry(N, d, V, n, c):
     th = torch.tensor(h, device="cuda").to(torch.bfloat16)
     tE = torch.tensor(E, device="cuda").to(torch.bfloat16)
     tt = torch.tensor(t, device="cuda")
-    ws_b = lib.alg_head_workspace_size(N, d, V, 0)
+    ws_b = lib.alg_head_workspace_size(_lib.DTYPE_BF16, N, d, V, 0)
     ws = torch.empty(ws_b, dtype=torch.uint8, device="cuda")
     Npad, Vp = (N + 255) // 256 * 256, (V + 7) // 8 * 8
     outs = [torch.empty(N, device="cuda") for _ in range(3)] + [torch.empty(1, device="cuda")]
     for call in range(2):
         res = torch.full((lib.alg_head_residual_size(N, d, V),), 0x7F, dtype=torch.uint8, device="cuda")
-        _lib.check(lib.alg_head_fwd(_lib.stream_of(th), N, d, V, P(th), P(tE), P(tt), n, c, *map(P, outs),
+        _lib.check(lib.alg_head_fwd(_lib.stream_of(th), _lib.DTYPE_BF16, N, d, V, P(th), P(tE), P(tt), n, c, *map(P, outs),
                                     P(res), P(ws), ws_b), "alg_head_fwd")
         torch.cuda.synchronize()
         U = res[:Npad * Vp * 2].view(torch.bfloat16).view(Npad, Vp)[:N, :V].float().cpu().numpy()

@@ -63,9 +63,11 @@ def test_fused_head_validation():
     with pytest.raises(NotImplementedError):
         fused_head(h, E, t, kind="ce")
     with pytest.raises(NotImplementedError):
-        fused_head(h.float(), E, t, kind="alg_ce")
+        fused_head(h.half(), E, t, kind="alg_ce")                    # bf16 or f32 hidden states only
     with pytest.raises(RuntimeError):
         fused_head(h, E, t, kind="alg_ce", n=8, c=2.0)               # CPU tensors: no fallback
+    with pytest.raises(RuntimeError):
+        fused_head(h.float(), E, t, kind="alg_ce", n=8, c=2.0)
 
 
 def test_neighbour_mirrors_validate_before_any_launch():
@@ -95,9 +97,11 @@ def test_neighbour_mirrors_validate_before_any_launch():
     with pytest.raises(ValueError):
         head_logprob(h, E, t, n=6)
     with pytest.raises(NotImplementedError):
-        head_logprob(h.float(), E, t)
+        head_logprob(h.half(), E, t)
     with pytest.raises(RuntimeError):
         head_logprob(h, E, t)
+    with pytest.raises(RuntimeError):
+        head_logprob(h.float(), E, t)
     with pytest.raises(ValueError):
         cayley_table_geometric(96, 128)           # head_dim / 2 = 48: not a power of two
     with pytest.raises(ValueError):

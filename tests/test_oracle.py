@@ -196,6 +196,26 @@ def test_head_kernel_restatement_matches_dense():
     assert rel_l2(dh, dh_r) < 1e-2 and rel_l2(dE, dE_r) < 1e-2
 
 
+@pytest.mark.parametrize("n,c", [(8, 2.0), (16, 16.0)])
+def test_head_kernel_restatement_f32_matches_dense(n, c):
+    """With f32 hidden states nothing is rounded to bf16 (the logit gradient is stored in the
+    hidden dtype, fused_head.py:145): the f32 restatement meets the dense float64 head at f32
+    precision, and planting a bf16 rounding of the logit gradient breaks that."""
+    rng = np.random.default_rng(40 + n)
+    h = rng.standard_normal((192, 96)).astype(np.float32)
+    E = (rng.standard_normal((517, 96)) * 0.15).astype(np.float32)
+    t = rng.integers(0, 517, 192).astype(np.int32)
+    stat, zt, pt, obj = OH.kernel_forward(h, E, t, n=n, c=c, dtype="f32")
+    obj_r, pt_r = OH.dense_forward(h, E, t, n=n, c=c)
+    np.testing.assert_allclose(obj, obj_r, rtol=1e-6)
+    np.testing.assert_allclose(pt, pt_r, rtol=1e-5)
+    dh, dE = OH.kernel_backward(h, E, t, stat, 0.7, n=n, c=c, dtype="f32", e_dtype="f32")
+    dh_r, dE_r = OH.dense_backward(h, E, t, 0.7, n=n, c=c)
+    assert rel_l2(dh, dh_r) < 2e-6 and rel_l2(dE, dE_r) < 2e-6
+    dh_b, _ = OH.kernel_backward(h, E, t, stat, 0.7, n=n, c=c, dtype="f32", e_dtype="f32", dz_dtype="bf16")
+    assert rel_l2(dh_b, dh_r) > 1e-4
+
+
 def test_eval_logprob_is_log_of_lean_pt():
     """evaluation.logprob_from_logits == log(pt) of the lean likelihood (test_components.py:56),
     and == a per-token brute-force log-softmax loop; argmax == the largest logit."""
