@@ -303,6 +303,187 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
   }
 }
 
+// In-range forward for f32 inputs at D = 64 with each row's keys split over several waves:
+// one workgroup = QG groups of 32 queries of one (b, h) (lane = query), and each group's
+// causal key range (its 32-key tiles) is split over KS = 4 / QG waves, wave part j taking the
+// j-th run of ceil(tiles / KS) tiles. Every part streams its own K/V tiles (all 256 threads
+// stage the parts' next tiles in registers while the current ones are consumed). At the end
+// parts 1.. add their O^T partials and row sums to part 0's through LDS, in part order, and
+// part 0 finalizes. An fp32 MFMA (v_mfma_f32_32x32x2f32) takes 64 cycles and a row's work
+// grows along the causal range, so at small batch (24 heads of 1024 positions) the longest
+// rows set the time: the split divides that path by KS and multiplies the workgroups by
+// 4 / QG. The row sum is accumulated in KS parts and added at the end, an order of f32
+// additions of its own (the mathematics is that of attn_fwd_kernel's in-range branch).
+constexpr int F32S_BK = 32;  // keys per tile
+template <int QG, int L2N>
+__global__ __launch_bounds__(256, 2) void attn_fwd_f32_split_kernel(AttnFwdParams p) {
+  static_assert(QG == 1 || QG == 2, "query groups per workgroup");
+  constexpr int KS = 4 / QG, BQ = 32 * QG;
+  constexpr int D = 64, PITCH = D + F32_PAD, TILE = F32S_BK * PITCH, NDB = D / 32, NQF = D / 8;
+  constexpr int CPR = D / 4;                 // 16-byte chunks per row
+  constexpr int PER = F32S_BK * CPR / 256;   // chunks per thread and tile
+  __shared__ __attribute__((aligned(16))) float Ks[KS][TILE];  // [part]
+  __shared__ __attribute__((aligned(16))) float Vs[KS][TILE];
+
+  if (p.flag && *p.flag == 0) return;  // device-side guard dispatch (flash.py:853-856)
+  const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int qg = wave % QG, part = wave / QG;
+  const int T_ = p.T;
+  const int nqb = ceil_div(T_, BQ);
+  const int bh = blockIdx.x;
+  const int qb = nqb - 1 - blockIdx.y;  // heaviest causal rows first
+  const int head = bh % p.H;
+  const size_t hb = head_base(bh, p.H, T_, D, p.layout);
+  const int ld = row_stride(p.H, D, p.layout);
+  const float* Q = reinterpret_cast<const float*>(p.q) + hb;
+  const float* K = reinterpret_cast<const float*>(p.k) + hb;
+  const float* V = reinterpret_cast<const float*>(p.v) + hb;
+  const int q0 = qb * BQ + qg * 32;
+  const int myq = q0 + l32;
+  const bool wave_live = q0 < T_;
+
+  floatx4 qf[NQF];  // query fragments (B operand of S^T = K Q^T)
+#pragma unroll
+  for (int s = 0; s < NQF; ++s) {
+    const floatx4 z = {};
+    qf[s] = myq < T_ ? *reinterpret_cast<const floatx4*>(Q + (size_t)myq * ld + 8 * s + 4 * h) : z;
+  }
+  const int log2n = p.log2n;
+  floatx16 oacc[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) oacc[db] = floatx16{};
+  float lsum = 0.0f;
+
+  // One 32-key tile: S^T, weights, O^T += V^T P^T (the in-range branch of attn_fwd_kernel,
+  // flash.py:215-233).
+  auto block = [&](const float* Kt, const float* Vt, int kb, bool diag) {
+    const float* krow = Kt + l32 * PITCH;
+    floatx16 s = {};
+#pragma unroll
+    for (int st = 0; st < NQF; ++st) {
+      const floatx4 kf = *reinterpret_cast<const floatx4*>(krow + 8 * st + 4 * h);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) s = mfma_f32(kf[u], qf[st][u], s);
+    }
+    float w[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) w[i] = pow2n<L2N>(rho_fast(s[i]), log2n);
+    if (diag) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = kb + 8 * (i >> 2) + 4 * h + (i & 3);
+        if (key > myq) w[i] = 0.0f;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) lsum += w[i];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int krow_i = 8 * (i >> 2) + 4 * h + (i & 3);
+        oacc[db] = mfma_f32(Vt[krow_i * PITCH + db * 32 + l32], w[i], oacc[db]);
+      }
+    }
+  };
+
+  // Registers <-> LDS staging of one 32-row tile; rows at or past T read as zeros.
+  auto load_tile = [&](uint4 (&r)[PER], const float* src, int r0) {
+#pragma unroll
+    for (int c = 0; c < PER; ++c) {
+      const int idx = threadIdx.x + c * 256;
+      const int row = idx / CPR, col = (idx - row * CPR) * 4;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (r0 + row < T_) v = *reinterpret_cast<const uint4*>(src + (size_t)(r0 + row) * ld + col);
+      r[c] = v;
+    }
+  };
+  auto store_tile = [&](float* dst, const uint4 (&r)[PER]) {
+#pragma unroll
+    for (int c = 0; c < PER; ++c) {
+      const int idx = threadIdx.x + c * 256;
+      const int row = idx / CPR, col = (idx - row * CPR) * 4;
+      *reinterpret_cast<uint4*>(dst + row * PITCH + col) = r[c];
+    }
+  };
+
+  const int q_last = min(qb * BQ + BQ, T_) - 1;
+  const int ntiles = q_last / F32S_BK + 1;
+  const int nper = ceil_div(ntiles, KS);  // tiles per part (the last parts may have fewer)
+  uint4 kr[KS][PER], vr[KS][PER];
+  // Step j's tile of every part into registers; a part's rows past its range start at T
+  // (read as zeros, never consumed).
+  auto load_step = [&](int j) {
+#pragma unroll
+    for (int q = 0; q < KS; ++q) {
+      const int t = q * nper + j;
+      const int r0 = t < ntiles ? t * F32S_BK : T_;
+      load_tile(kr[q], K, r0);
+      load_tile(vr[q], V, r0);
+    }
+  };
+  load_step(0);
+  for (int j = 0; j < nper; ++j) {
+#pragma unroll
+    for (int q = 0; q < KS; ++q) {
+      store_tile(Ks[q], kr[q]);
+      store_tile(Vs[q], vr[q]);
+    }
+    __syncthreads();
+    if (j + 1 < nper) load_step(j + 1);  // in flight while this step's tiles are consumed
+    const int t = part * nper + j;
+    const int kb = t * F32S_BK;
+    // Tiles past the range, or keys past this wave's last query (or past T), are skipped.
+    if (wave_live && t < ntiles && kb <= q0 + 31) block(Ks[part], Vs[part], kb, kb + 31 > q0);
+    __syncthreads();  // every wave is done with the tiles before the next step stores
+  }
+
+  // Parts 1.. hand their O^T partials and row sums to part 0 through LDS (the tiles are free
+  // after the loop's last barrier): RS floats per lane, an odd stride (no bank conflicts).
+  constexpr int RS = 16 * NDB + 1;
+  static_assert((KS - 1) * QG * 64 * RS <= KS * TILE, "partials fit the K tiles");
+  float* red = &Ks[0][0];
+  if (part > 0) {
+    float* dst = red + (((part - 1) * QG + qg) * 64 + lane) * RS;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) dst[db * 16 + i] = oacc[db][i];
+    dst[16 * NDB] = lsum;
+  }
+  __syncthreads();
+  if (part > 0 || !wave_live) return;
+#pragma unroll
+  for (int q = 1; q < KS; ++q) {
+    const float* src = red + (((q - 1) * QG + qg) * 64 + lane) * RS;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) oacc[db][i] += src[db * 16 + i];
+    lsum += src[16 * NDB];
+  }
+
+  // Finalize (flash.py:271-284): Z over both lane halves (+ the sink's weight), stat = 1/Z.
+  float Z = lsum + xor32(lsum);
+  if (p.sink) Z += pow2n<L2N>(rho_fast(p.sink[head]), log2n);
+  const float inv = 1.0f / Z;
+  if (myq < T_) {
+    float* O = reinterpret_cast<float*>(p.o) + hb + (size_t)myq * ld;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        floatx4 val;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) val[e] = oacc[db][4 * g + e] * inv;
+        *reinterpret_cast<floatx4*>(O + db * 32 + 8 * g + 4 * h) = val;
+      }
+    }
+    if (h == 0) p.stat[(size_t)bh * T_ + myq] = inv;
+  }
+}
+
 // In-range forward for bf16 inputs (the guarded "low" variant): same decomposition as
 // attn_fwd_kernel (4 waves x 32 queries, lane = query, S^T = K Q^T, O^T += V^T P^T), with K/V
 // tiles in two ping-pong LDS buffer sets, each filled by range-checked buffer copies issued
@@ -519,6 +700,18 @@ static hipError_t launch_fwd_mode(const AttnFwdParams& p, int mode, hipStream_t 
         } else {
           if (p.log2n == 4) hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, 4, 0>), grid, block, 0, st, p);
           else hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, 0, 0>), grid, block, 0, st, p);
+        }
+      } else if constexpr (D == 64) {
+        // Four-way key split (32 queries per workgroup) while two-way workgroups would not
+        // fill two rounds of the CUs; two-way (64 queries) above that.
+        if (p.B * p.H * ceil_div(p.T, 64) < 512) {
+          const dim3 g32(p.B * p.H, ceil_div(p.T, 32));
+          if (p.log2n == 4) hipLaunchKernelGGL((attn_fwd_f32_split_kernel<1, 4>), g32, block, 0, st, p);
+          else hipLaunchKernelGGL((attn_fwd_f32_split_kernel<1, 0>), g32, block, 0, st, p);
+        } else {
+          const dim3 g64(p.B * p.H, ceil_div(p.T, 64));
+          if (p.log2n == 4) hipLaunchKernelGGL((attn_fwd_f32_split_kernel<2, 4>), g64, block, 0, st, p);
+          else hipLaunchKernelGGL((attn_fwd_f32_split_kernel<2, 0>), g64, block, 0, st, p);
         }
       } else {
         if (p.log2n == 4) hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_INRANGE, 4>), grid, block, 0, st, p);
