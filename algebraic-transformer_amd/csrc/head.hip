@@ -470,6 +470,50 @@ __global__ __launch_bounds__(256) void head_hscale_kernel(HeadParams p) {
   }
 }
 
+// Store of a wave's WTM x WTN accumulator block, scaled per row and rounded to bf16, into a
+// row-major matrix (interior tiles). Stored straight from the accumulators, each store
+// instruction would cover 64 bytes of two rows at 2 bytes a lane; instead the block is staged
+// in `stage` (this wave's share of the idle pipeline buffers) as [row][col] rows of WTN
+// elements, 16-byte chunks XOR-swizzled by the row, and written back with 16-byte stores
+// that cover whole 128-byte row segments. f(r) is the scale of block row r.
+template <class RowScale>
+__device__ __forceinline__ void store_block_bf16(const floatx16 (&acc)[HC::MB][HC::NB], bf16* stage, bf16* out,
+                                                 long ld, RowScale f) {
+  constexpr int CH = HC::WTN / 8;  // 16-byte chunks per staged row
+  static_assert(CH <= 64 && 64 % CH == 0 && (CH & (CH - 1)) == 0, "staged row width");
+  const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  auto at = [](int r, int c) { return r * HC::WTN + (((c >> 3) ^ (r & (CH - 1))) << 3) + (c & 7); };
+#pragma unroll
+  for (int mb = 0; mb < HC::MB; ++mb) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+      const float fr = f(r);
+#pragma unroll
+      for (int nb = 0; nb < HC::NB; ++nb) stage[at(r, nb * 32 + l32)] = f2bf(acc[mb][nb][i] * fr);
+    }
+  }
+  constexpr int RPS = 64 / CH;  // rows per store instruction
+  const int c = lane % CH;
+#pragma unroll
+  for (int j = 0; j < HC::WTM / RPS; ++j) {
+    const int r = RPS * j + lane / CH;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(stage + at(r, c * 8));
+    *reinterpret_cast<u32x4*>(out + (long)r * ld + c * 8) = v;
+  }
+}
+
+// This wave's share of the pipeline buffers (idle after the main loop; the caller has passed
+// a barrier after which no wave reads them): half the waves stage in s0, half in s1.
+template <class Stage>
+__device__ __forceinline__ bf16* wave_stage(Stage& s0, Stage& s1, int wm, int wn) {
+  constexpr int NWAVES = HC::THREADS / 64, UWAVE = HC::WTM * HC::WTN;
+  static_assert((NWAVES / 2) * UWAVE * 2 <= (int)sizeof(Stage), "half the waves per stage");
+  const int wi = wm * HC::WN + wn;
+  return reinterpret_cast<bf16*>(wi < NWAVES / 2 ? static_cast<void*>(&s0) : static_cast<void*>(&s1)) +
+         (wi % (NWAVES / 2)) * UWAVE;
+}
+
 // dh = (U' or dZ) E: A stored token-major [n][v] (k-contiguous), B = E stored [v][d]
 // (n-contiguous). The residual schedule scales token rows by s/l. When the product has too
 // few output tiles to fill the chip (small N*d, long V) the vocabulary is split into
@@ -493,6 +537,17 @@ __global__ __launch_bounds__(NT, 1) void head_dh_kernel(HeadParams p) {
   wave_coords<HC>(wm, wn);
   const float s = p.ut ? head_grad_scale(p) : 1.0f;
   float* part = p.dh_part ? p.dh_part + (size_t)split * p.N * p.d : nullptr;
+  if (!part && m0 + HT_M <= p.N && n0 + HT_N <= p.d) {
+    // Interior tile, bf16 output: the row scales s/l once per row (the expression of
+    // head_hscale_kernel), then the staged 16-byte stores.
+    __shared__ float fsc[HT_M];
+    for (int t = threadIdx.x; t < HT_M; t += NT) fsc[t] = p.ut ? s / p.lsum[m0 + t] : 1.0f;
+    __syncthreads();  // fsc is written and every wave is done with the pipeline buffers
+    const int r0 = wm * HC::WTM;
+    store_block_bf16(acc, wave_stage(s0, s1, wm, wn), p.dh + (size_t)(m0 + r0) * p.d + n0 + wn * HC::WTN, p.d,
+                     [&](int r) { return fsc[r0 + r]; });
+    return;
+  }
 #pragma unroll
   for (int mb = 0; mb < HC::MB; ++mb) {
 #pragma unroll
@@ -551,6 +606,13 @@ __global__ __launch_bounds__(NT, 1) void head_de_kernel(HeadParams p) {
   const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
   int wm, wn;
   wave_coords<HC>(wm, wn);
+  if (!p.dE_f32 && m0 + HT_M <= p.V && n0 + HT_N <= p.d) {  // interior tile, bf16 output
+    __syncthreads();  // every wave is done with the pipeline buffers
+    store_block_bf16(acc, wave_stage(s0, s1, wm, wn),
+                     reinterpret_cast<bf16*>(p.dE) + (size_t)(m0 + wm * HC::WTM) * p.d + n0 + wn * HC::WTN, p.d,
+                     [](int) { return 1.0f; });
+    return;
+  }
 #pragma unroll
   for (int mb = 0; mb < HC::MB; ++mb) {
 #pragma unroll

@@ -6,7 +6,8 @@ scalar offset is a constant, not an SGPR; with an SGPR offset, gfx950 was measur
 overwritten values (the residual block of the fused head lost about 0.1 % of its entries to
 address arithmetic issued right after the store). The kernels therefore keep every wide buffer
 store's scalar offset constant; this test compiles each source that issues raw buffer stores
-and checks the generated assembly for both conditions.
+and checks the generated assembly for both conditions. Wide global stores (the head's staged
+epilogues) are checked for the second condition too.
 """
 
 import re
@@ -21,6 +22,7 @@ CSRC = ROOT / "algebraic-transformer_amd" / "csrc"
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 
 WIDE_STORE = re.compile(r"^\s*buffer_store_(dwordx3|dwordx4|b96|b128)\s+(.*)$")
+WIDE_GLOBAL_STORE = re.compile(r"^\s*global_store_(dwordx3|dwordx4|b96|b128)\s+(.*)$")
 
 
 def _regs(tok):
@@ -55,6 +57,12 @@ def scan(asm):
     ins = _instructions(asm)
     problems = []
     for k, s in enumerate(ins):
+        g = WIDE_GLOBAL_STORE.match(s)
+        if g:  # global_store vaddr, vdata, off
+            data = _regs(re.split(r",\s*", g.group(2))[1])
+            if k + 1 < len(ins) and _valu_dst(ins[k + 1]) & data:
+                problems.append(f"data overwritten by the next instruction: {s} / {ins[k + 1]}")
+            continue
         m = WIDE_STORE.match(s)
         if not m:
             continue
@@ -80,9 +88,11 @@ def test_scan_flags_the_hazard_forms():
     """
     assert len(scan(bad)) == 2
     assert scan(good) == []
+    assert len(scan("global_store_dwordx4 v[2:3], v[8:11], off\nv_mov_b32_e32 v9, 0")) == 1
+    assert scan("global_store_dwordx4 v[2:3], v[8:11], off\ns_nop 0\nv_mov_b32_e32 v9, 0") == []
 
 
-SOURCES = sorted(p for p in CSRC.glob("*.hip") if "buffer_store" in p.read_text())
+SOURCES = sorted(p for p in CSRC.glob("*.hip") if "buffer_store" in p.read_text() or "store_block_bf16" in p.read_text())
 
 
 @pytest.mark.skipif(not Path(HIPCC).exists(), reason="hipcc not available")
