@@ -92,6 +92,18 @@ def test_guarded_fp32_matches_dense(shape, with_sink):
     check_dense(res, q, k, v, do, sink, F32_DENSE)
 
 
+@pytest.mark.parametrize("shape", [(8, 16, 256, 64), (8, 16, 200, 64)])
+@pytest.mark.parametrize("with_sink", [True, False])
+def test_guarded_fp32_two_way_key_split(shape, with_sink):
+    """f32 D = 64 grids of at least 512 two-way workgroups (B H ceil(T/64) >= 512) split each
+    row's keys over two waves (64 queries per workgroup); smaller grids, as in the other f32
+    cases, split them four ways. Both against the dense float64 reference at the f32 bar."""
+    B, H, T, D = shape
+    q, k, v, do, sink = attention_inputs(B, H, T, D, seed=7, dtype="f32", sink=with_sink)
+    res = run_hip(q, k, v, do, sink, "f32", range_guard=True, block=T)
+    check_dense(res, q, k, v, do, sink, F32_DENSE)
+
+
 def test_config1_fp32_125m_shape():
     """B=2, H=12, T=1024, D=64 fp32 forward (+ backward) at 1e-5."""
     q, k, v, do, sink = attention_inputs(2, 12, 1024, 64, seed=11, dtype="f32")
