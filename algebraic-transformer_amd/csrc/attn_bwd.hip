@@ -17,8 +17,8 @@
 //         in registers while the kernel streams 64-query tiles of Q, dO, stat and di through
 //         LDS. Scores are formed as S = Q K^T so a lane owns one key column; P^T and dS^T
 //         feed dV += P^T dO and dK += dS^T Q directly as MFMA A operands, with dO/Q
-//         fragments transposed by ds_read_b64_tr_b16.
-//   post  the per-head sink gradient.
+//         fragments transposed by ds_read_b64_tr_b16. Its last workgroup also reduces the
+//         dQ kernel's partials into the per-head sink gradient (no separate launch).
 // f32 launches: pre (di from the f32 output, sink partials, zeroed dQ accumulator), one
 // key-stationary kernel adding dQ to an f32 accumulator with atomics, post (dq from the
 // accumulator: round(round(n * acc) * dq_scale), and the sink gradient).
@@ -525,6 +525,39 @@ __device__ __forceinline__ void bwd_elem(float x, float dp, float stq, float diq
   }
 }
 
+// Per-head sink gradient (flash.py:694-705, 721-723) from the partial sums of mass * di that
+// the dQ kernel (bf16) or the pre kernel (f32) wrote, in one workgroup: one wave per head,
+// lane l adds partials l, l + 64, ... of the head's B * nblk, then a butterfly over the wave
+// (a fixed order for a given shape). Run by the bf16 dK/dV kernel's last workgroup (after the
+// dQ kernel that wrote the partials) and by the f32 post kernel.
+__device__ __forceinline__ void attn_sink_grad(const AttnBwdParams& p, int nblk) {
+  if (!p.dbeta) return;
+  bool shifted = p.mode == MODE_SHIFTED;
+  if (p.flag) shifted = *p.flag == 0;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwave = blockDim.x >> 6;
+  const int cnt = p.B * nblk;
+  for (int hh = wave; hh < p.H; hh += nwave) {
+    float s = 0.0f;
+    if (p.sink)
+      for (int i = lane; i < cnt; i += 64) {
+        const int b = i / nblk, k = i - b * nblk;
+        s += p.sink_part[(size_t)(b * p.H + hh) * nblk + k];
+      }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
+    if (lane != 0) continue;
+    if (!p.sink) { p.dbeta[hh] = 0.0f; continue; }
+    float beta = p.sink[hh];
+    const bool clipped = !shifted && p.mode == MODE_CLIPPED && !p.flag;
+    float bb = clipped ? fminf(beta, p.clamp) : beta;
+    float r;
+    rho_exact(bb, r);
+    float sl = (float)(1 << p.log2n) * r;
+    if (clipped && !(beta < p.clamp)) sl = 0.0f;  // flash.py:703-704
+    p.dbeta[hh] = -s * sl;
+  }
+}
+
 constexpr int BF_BQ = 64;  // queries per streamed tile (bf16 kernel)
 constexpr int BWD_XCDS = 8;    // workgroup i runs on XCD i % 8
 constexpr int BWD_GROUP = 4;   // heads whose key blocks one XCD interleaves
@@ -833,6 +866,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
       __syncthreads();  // the next item's first copies overwrite both LDS buffer sets
     }
   }
+  // The last workgroup (the lightest causal key block) also forms the sink gradient.
+  if (blockIdx.x == gridDim.x - 1) attn_sink_grad(p, ceil_div(T_, SINK_ROWS));
 }
 
 // dQ kernel for bf16 inputs (query-stationary; no atomics): one workgroup = 4 waves = 128
@@ -1160,34 +1195,7 @@ __global__ __launch_bounds__(256) void attn_bwd_post_kernel(AttnBwdParams p, siz
       *reinterpret_cast<uint4*>(reinterpret_cast<T*>(p.dq) + dst + 4) = *reinterpret_cast<const uint4*>(out + 4);
     }
   }
-  if (blockIdx.x == 0 && p.dbeta) {
-    bool shifted = p.mode == MODE_SHIFTED;
-    if (p.flag) shifted = *p.flag == 0;
-    // One wave per head: lane l adds partials l, l + 64, ... of the head's B * nblk, then a
-    // butterfly over the wave (a fixed order for a given shape).
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwave = blockDim.x >> 6;
-    const int cnt = p.B * nblk;
-    for (int hh = wave; hh < p.H; hh += nwave) {
-      float s = 0.0f;
-      if (p.sink)
-        for (int i = lane; i < cnt; i += 64) {
-          const int b = i / nblk, k = i - b * nblk;
-          s += p.sink_part[(size_t)(b * p.H + hh) * nblk + k];
-        }
-#pragma unroll
-      for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
-      if (lane != 0) continue;
-      if (!p.sink) { p.dbeta[hh] = 0.0f; continue; }
-      float beta = p.sink[hh];
-      const bool clipped = !shifted && p.mode == MODE_CLIPPED && !p.flag;
-      float bb = clipped ? fminf(beta, p.clamp) : beta;
-      float r;
-      rho_exact(bb, r);
-      float sl = (float)(1 << p.log2n) * r;
-      if (clipped && !(beta < p.clamp)) sl = 0.0f;  // flash.py:703-704
-      p.dbeta[hh] = -s * sl;
-    }
-  }
+  if (blockIdx.x == 0) attn_sink_grad(p, nblk);
 }
 
 // Grid of a fallback (grid-stride) kernel: every work item gets its own workgroup when the
@@ -1301,14 +1309,13 @@ hipError_t launch_attn_bwd(const AttnBwdParams& p, int D, bool bf16_io, const in
     for (int m = 0; m < nmodes && e == hipSuccess; ++m)
       e = D == 64 ? launch_bwd_f32<64>(p, modes[m], st) : launch_bwd_f32<128>(p, modes[m], st);
   }
-  if (e != hipSuccess) return e;
-  // f32: dq from the accumulator; bf16: only the sink gradient is left to do.
-  const size_t total = bf16_io ? 0 : (size_t)p.B * p.H * p.T * D;
+  if (e != hipSuccess || bf16_io) return e;  // bf16: the dK/dV kernel formed the sink gradient
+  // f32: dq from the accumulator, and the sink gradient.
+  const size_t total = (size_t)p.B * p.H * p.T * D;
   const int blocks = (int)std::max<size_t>(std::min<size_t>((total / 8 + 255) / 256, 16384), 1);
   {
     KTimer t("attn_bwd_post", st);
-    if (bf16_io) hipLaunchKernelGGL((attn_bwd_post_kernel<bf16>), dim3(blocks), dim3(256), 0, st, p, total, nblk, D);
-    else hipLaunchKernelGGL((attn_bwd_post_kernel<float>), dim3(blocks), dim3(256), 0, st, p, total, nblk, D);
+    hipLaunchKernelGGL((attn_bwd_post_kernel<float>), dim3(blocks), dim3(256), 0, st, p, total, nblk, D);
   }
   return hipGetLastError();
 }
