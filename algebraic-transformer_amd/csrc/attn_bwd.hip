@@ -591,6 +591,11 @@ __device__ __forceinline__ void bwd_stat_dma(float* lst, float* ldi, __amdgpu_bu
 // VALU instructions per score element (scheduling hint).
 template <int MODE>
 constexpr int bwd_valu_per_elem() { return MODE == MODE_INRANGE ? 14 : 20; }
+// Waves per SIMD the dK/dV kernel is built for: at D = 64 its dK/dV accumulators, K/V
+// fragments and one tile's S/dP fit in 256 registers, so two waves share a SIMD (VGPR-held
+// accumulators); at D = 128 they take about 420 and the kernel runs one wave per SIMD.
+template <int D>
+constexpr int bwd_bf16_waves_per_simd() { return D == 64 ? 2 : 1; }
 
 // dK/dV kernel for bf16 inputs: 128 keys per workgroup, 32 per wave (lane = key), dK/dV
 // accumulated in registers over the 64-query tiles of the causal range. dQ is formed by
@@ -607,7 +612,7 @@ constexpr int bwd_valu_per_elem() { return MODE == MODE_INRANGE ? 14 : 20; }
 // mask is evaluated only on the two tiles that cross the diagonal; every LDS access is a
 // per-lane swizzled offset computed once plus an immediate.
 template <int D, int MODE, int L2N, int LAYOUT>
-__global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) {
+__global__ __launch_bounds__(256, bwd_bf16_waves_per_simd<D>()) void attn_bwd_bf16_kernel(AttnBwdParams p) {
   static_assert(D == 64 || D == 128, "head_dim");
   constexpr int BQ = BF_BQ, CPR = D / 8, NDB = D / 32, NF = D / 16;
   constexpr int PW = 64 * CPR / 64 / 4;  // copy instruction pairs per wave and tile
@@ -705,7 +710,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
 
     floatx16 s[2], dp[2];
     bf16x8 pa[2][2], da[2][2];
-    floatx4 stq[2][4], diq[2][4];
+    floatx4 sq[2][2], dq4[2][2];  // stat and di of a quarter's queries (slot = quarter & 1)
     float pv[16], dsv[16];
 
     // R1/R2 step g = NF * sub + st: MFMAs on the fragments of step g, reads for step g + 3.
@@ -719,11 +724,13 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
       s[sub] = mfma_bf16(rq4[g % 4], kf[st], s[sub]);
       dp[sub] = mfma_bf16(ro4[g % 4], vf[st], dp[sub]);
     };
-    auto load_stats = [&](int sub) {
+    // Stat and di of the lane's 8 queries of quarter k (queries 16 k ..; elements 8 (k & 1)
+    // .. + 7 of block k >> 1), loaded one phase before they are used.
+    auto load_stats = [&](int k) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        stq[sub][g] = *reinterpret_cast<const floatx4*>(sts + sub * 32 + 8 * g + 4 * h);
-        diq[sub][g] = *reinterpret_cast<const floatx4*>(dis + sub * 32 + 8 * g + 4 * h);
+      for (int gl = 0; gl < 2; ++gl) {
+        sq[k & 1][gl] = *reinterpret_cast<const floatx4*>(sts + 16 * k + 8 * gl + 4 * h);
+        dq4[k & 1][gl] = *reinterpret_cast<const floatx4*>(dis + 16 * k + 8 * gl + 4 * h);
       }
     };
     // Weight P and score gradient dS of element i of block sub, rounded to bf16 as the
@@ -731,7 +738,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
     auto elem = [&](int sub, int i) {
       const int g = i >> 2, e = i & 3;
       const bool masked = MASKED && mykey > qbase + sub * 32 + 8 * g + 4 * h + e;
-      bwd_elem<MODE, L2N>(s[sub][i], dp[sub][i], stq[sub][g][e], diq[sub][g][e], masked, p, log2n, pv[i], dsv[i]);
+      const int k = 2 * sub + (i >> 3);
+      bwd_elem<MODE, L2N>(s[sub][i], dp[sub][i], sq[k & 1][g & 1][e], dq4[k & 1][g & 1][e], masked, p, log2n, pv[i],
+                          dsv[i]);
       if (i & 1) {
         pa[sub][i >> 3][(i & 7) - 1] = f2bf(pv[i - 1]);
         pa[sub][i >> 3][i & 7] = f2bf(pv[i]);
@@ -775,11 +784,12 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
         if constexpr (BUF) bwd_stat_dma(st0, di0, rst, rdi, qbase + BQ, wave, lane);
         else bwd_stat_dma(st1, di1, rst, rdi, qbase + BQ, wave, lane);
       }
-      if (g == 0) step_order<2, 0, 4 + 8, 0>();
+      if (g == 0) step_order<2, 0, 4 + 4, 0>();
       else step_order<2, 0, 4, 0>();
     }
     // R2: S and dP of block 1 under elements 0..7 of block 0.
     constexpr int E2 = 8 / NF > 0 ? 8 / NF : 1;
+    load_stats(1);
 #pragma unroll
     for (int g = NF; g < 2 * NF; ++g) {
       sdp_step(g);
@@ -790,14 +800,17 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
       if (g == 2 * NF - 3) c_load(0);
       if (g == 2 * NF - 2) c_load(1);
       if (g == 2 * NF - 1) c_load(2);
-      step_order<2, VE * E2, 4 + 4, 0>();
+      if (g == NF) step_order<2, VE * E2, 4 + 4 + 4, 0>();
+      else step_order<2, VE * E2, 4 + 4, 0>();
     }
     // C steps: quarter 0 under elements 8..15 of block 0, quarter 1 under 0..7 of block 1,
-    // quarter 2 under 8..15 of block 1, quarter 3 alone.
-    load_stats(1);
+    // quarter 2 under 8..15 of block 1, quarter 3 alone. Quarters 0 and 1 read the stats of
+    // the quarters weighed after them.
     constexpr int EC = 8 / NDB;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
+      if (c == 0) load_stats(2);
+      if (c == NDB) load_stats(3);
       if (c + 3 < NC) c_load(c + 3);
       c_mma(c);
       const int qq = c / NDB, db = c % NDB;
@@ -807,7 +820,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_bf16_kernel(AttnBwdParams p) 
           const int idx = EC * db + k;  // quarter 0: 8..15 of block 0; 1: 0..7 of block 1; 2: 8..15
           elem(qq == 0 ? 0 : 1, qq == 1 ? idx : 8 + idx);
         }
-        step_order<2, VE * EC, 4, 0>();
+        if (c == 0 || c == NDB) step_order<2, VE * EC, 4 + 4, 0>();
+        else step_order<2, VE * EC, 4, 0>();
       } else {
         step_order<2, 0, 4, 0>();
       }
