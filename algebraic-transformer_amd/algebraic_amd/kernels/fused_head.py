@@ -100,6 +100,10 @@ def fused_head(h, embed, targets, *, kind="ce", n=16, c=16.0, block_n=128, block
         raise ValueError(kind)
     if kind == "alg_ce" and (n & (n - 1)):
         raise ValueError("n must be a power of two")
+    if kind == "alg_ce" and n == 1:
+        # fused_head.py:59-65 forms l^(-1/n) as rsqrt(l) then y * rsqrt(y) while n/2 > 1,
+        # which for n = 1 is rsqrt(l), not 1/l: the reference's fused head is wrong there.
+        raise NotImplementedError("n = 1: the fused head's statistic l^(-1/n) is built for n >= 2")
     N = h.shape[0]
     bn = min(block_n, N)
     if N % bn:

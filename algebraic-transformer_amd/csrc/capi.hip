@@ -78,9 +78,15 @@ int check_layout(int layout, int H, int T, int D) {
   return ALG_OK;
 }
 
+// The reference takes any power of two (flash.py:740-741, fused_head.py:269-270); the kernels
+// form powers by repeated squaring with the exponent's log2 as a loop count, so the C ABI
+// takes exponents up to 2^20 (beyond that every weight but the largest underflows in f32).
+constexpr int MAX_LOG2N = 20;
+
 int check_n(int n) {
   const int k = log2_pow2(n);
-  if (k < 1 || k > 6) return fail(ALG_ERR_INVALID, "asinh kernel needs n to be a power of two in [2, 64] (got %d)", n);
+  if (k < 1 || k > MAX_LOG2N)
+    return fail(ALG_ERR_INVALID, "asinh kernel needs n to be a power of two in [2, 2^%d] (got %d)", MAX_LOG2N, n);
   return ALG_OK;
 }
 
@@ -167,8 +173,19 @@ int check_head(int N, int d, int V, int n, float c) {
       (double)alg::head_vocab_pitch(V) * alg::head_token_pad(N) > 4.0e9)
     return fail(ALG_ERR_INVALID, "head too large");
   const int k = log2_pow2(n);
-  if (k < 0 || k > 6) return fail(ALG_ERR_INVALID, "n must be a power of two in [1, 64] (got %d)", n);
+  if (k < 0 || k > MAX_LOG2N) return fail(ALG_ERR_INVALID, "n must be a power of two in [1, 2^%d] (got %d)", MAX_LOG2N, n);
   if (!(c > 0.0f) || !std::isfinite(c)) return fail(ALG_ERR_INVALID, "c must be positive and finite");
+  return ALG_OK;
+}
+
+// The training head's statistic is l^(-1/n), formed as the reference's _inv_root does
+// (fused_head.py:59-65: rsqrt, then y * rsqrt(y) while k = n/2 > 1). For n = 1 that loop gives
+// rsqrt(l) rather than 1/l, so the reference's fused head returns a wrong probability and
+// gradient there; the training head here takes n >= 2 (the evaluation head, which works in
+// the log domain, takes n = 1 too).
+int check_train_head_n(int n) {
+  if (n == 1)
+    return fail(ALG_ERR_UNSUPPORTED, "n = 1: the training head needs n >= 2 (l^(-1/n) by repeated rsqrt)");
   return ALG_OK;
 }
 
@@ -502,6 +519,7 @@ int alg_head_fwd(alg_stream_t stream, int dtype, int N, int d, int V, const void
                  const int32_t* targets, int n, float c, float* stat, float* zt, float* pt, float* obj,
                  void* residual, void* workspace, size_t workspace_bytes) {
   int rc = check_head(N, d, V, n, c);
+  if (!rc) rc = check_train_head_n(n);
   if (!rc) rc = check_head_dtype(dtype, residual);
   if (rc) return rc;
   const bool f32 = dtype == ALG_DTYPE_F32;
@@ -635,6 +653,7 @@ int alg_head_bwd(alg_stream_t stream, int dtype, int N, int d, int V, const void
                  const int32_t* targets, const float* stat, const float* g, int n, float c, const void* residual,
                  void* dh, void* dE, int dE_dtype, void* workspace, size_t workspace_bytes) {
   int rc = check_head(N, d, V, n, c);
+  if (!rc) rc = check_train_head_n(n);
   if (!rc) rc = check_head_dtype(dtype, residual);
   if (rc) return rc;
   const bool f32 = dtype == ALG_DTYPE_F32;

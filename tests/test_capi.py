@@ -81,6 +81,13 @@ def test_invalid_arguments_fail_before_launch():
     rc = handle.alg_attn_fwd(None, 0, 0, 1, 1, 64, 64, P(16), P(16), P(16), None, 12, 0, None, 0.0, 1, 1,
                              P(16), None, P(16))
     assert rc == _lib.ALG_ERR_INVALID and b"power of two" in handle.alg_last_error()
+    # Any power of two up to 2^20 (the reference takes any power of two, flash.py:740-741).
+    rc = handle.alg_attn_fwd(None, 0, 0, 1, 1, 64, 64, P(16), P(16), P(16), None, 1 << 21, 0, None, 0.0, 1, 1,
+                             P(16), None, P(16))
+    assert rc == _lib.ALG_ERR_INVALID and b"2^20" in handle.alg_last_error()
+    rc = handle.alg_head_fwd(None, 0, 128, 256, 1000, P(16), P(16), P(16), 3, 2.0, P(16), P(16), P(16), P(16),
+                             None, P(16), 1 << 30)
+    assert rc == _lib.ALG_ERR_INVALID and b"power of two" in handle.alg_last_error()
     rc = handle.alg_attn_fwd(None, 0, 2, 1, 1, 64, 64, P(16), P(16), P(16), None, 16, 0, None, 0.0, 1, 1,
                              P(16), None, P(16))
     assert rc == _lib.ALG_ERR_INVALID and b"layout" in handle.alg_last_error()

@@ -92,6 +92,11 @@ def test_neighbour_mirrors_validate_before_any_launch():
     with pytest.raises(RuntimeError):
         alu_glu_ffn(h2, wg, wg, wd)
     h, E, t = torch.zeros(16, 64, dtype=torch.bfloat16), torch.zeros(100, 64), torch.zeros(16, dtype=torch.int32)
+    # n = 1 passes the reference's power-of-two check, but its statistic l^(-1/n) is formed by
+    # repeated rsqrt (fused_head.py:59-65), which gives rsqrt(l) there: refused before the device.
+    from algebraic_amd.kernels.fused_head import fused_head
+    with pytest.raises(NotImplementedError, match="n = 1"):
+        fused_head(h, E, t, kind="alg_ce", n=1, c=2.0)
     with pytest.raises(NotImplementedError):
         head_logprob(h, E, t, head="ce")
     with pytest.raises(ValueError):

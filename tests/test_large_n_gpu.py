@@ -1,0 +1,95 @@
+"""GPU parity for exponents beyond the model presets (n = 2^k, k up to 20 in the C ABI).
+
+The reference takes any power of two for both kernels (src/algebraic/kernels/flash.py:740-741,
+fused_head.py:269-270); the presets use n = 16 (attention) and n = 8 (head). For n > 32 the
+reference's range guard does not apply (flash.py:834) and make_variant selects the shifted
+variant, whose clamp (t - 1/t)/2 with (T + 1) t^n = 1e37 falls below 20 (flash.py:747-751);
+the HIP path follows the same selection. Checked against the float64 dense oracles
+(oracle.attention.dense_forward / dense_backward, oracle.head.dense_forward /
+dense_backward) at the bars of the reference's own tests: attention f32 atol/rtol 2e-3 on o
+and 3e-3 on max-scaled gradients (tests/test_flash_kernel_tpu.py:35-77), bf16 relative L2
+2e-2; head objective rtol 2e-3, telemetry 2e-2, gradients 1e-2 (tests/test_fused_head_tpu.py).
+"""
+
+import numpy as np
+import pytest
+
+from helpers import head_inputs, rel_l2
+from oracle import attention as OA
+from oracle import head as OH
+from oracle.numerics import round_bf16
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+
+def _attn(q, k, v, g, sink, dtype, **kw):
+    from algebraic_amd.kernels.flash import flash_attention
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    tq, tk, tv = (torch.tensor(a, device="cuda").to(tdt).requires_grad_(True) for a in (q, k, v))
+    ts = torch.tensor(sink, device="cuda", requires_grad=True)
+    o = flash_attention(tq, tk, tv, ts, kind="asinh", **kw)
+    o.backward(torch.tensor(g, device="cuda").to(tdt))
+    torch.cuda.synchronize()
+    f = lambda t: t.detach().float().cpu().numpy().astype(np.float64)
+    return f(o), f(tq.grad), f(tk.grad), f(tv.grad), f(ts.grad)
+
+
+@pytest.mark.parametrize("n,c", [(64, 8.0), (256, 16.0), (1024, 8.0)])
+def test_attention_large_n_f32(n, c):
+    B, H, T, D = 1, 2, 512, 64
+    rng = np.random.default_rng(7 + n)
+    q, k = (rng.standard_normal((B, H, T, D)).astype(np.float32) * 1.5 for _ in range(2))
+    v, g = (rng.standard_normal((B, H, T, D)).astype(np.float32) for _ in range(2))
+    sink = (rng.standard_normal(H) * 0.5).astype(np.float32)[None, :, None, None]
+    res = _attn(q, k, v, g, sink, "f32", n=n, c=c, block=128, range_guard=True)
+    o_ref = OA.dense_forward(q, k, v, sink, n=n, c=c)
+    grads = OA.dense_backward(q, k, v, sink, g, n=n, c=c)
+    np.testing.assert_allclose(res[0], o_ref, atol=2e-3, rtol=2e-3)
+    for a, b in zip(res[1:], grads):
+        scale = float(np.max(np.abs(b))) + 1e-6
+        np.testing.assert_allclose(a / scale, np.asarray(b) / scale, atol=3e-3)
+
+
+def test_attention_large_n_bf16():
+    B, H, T, D, n, c = 1, 2, 512, 128, 128, 8.0
+    rng = np.random.default_rng(11)
+    q, k, v, g = (round_bf16(rng.standard_normal((B, H, T, D)).astype(np.float32)) for _ in range(4))
+    sink = (rng.standard_normal(H) * 0.1).astype(np.float32)[None, :, None, None]
+    res = _attn(q, k, v, g, sink, "bf16", n=n, c=c, range_guard=True)
+    want = [OA.dense_forward(q, k, v, sink, n=n, c=c)] + list(OA.dense_backward(q, k, v, sink, g, n=n, c=c))
+    for name, a, b in zip(("o", "dq", "dk", "dv", "dsink"), res, want):
+        assert rel_l2(a, b) < 2e-2, (name, rel_l2(a, b))
+
+
+@pytest.mark.parametrize("n,c", [(32, 2.0), (128, 16.0)])
+def test_head_large_n(n, c):
+    from algebraic_amd.kernels.fused_head import fused_head
+    N, d, V = 256, 128, 1000
+    h, E, t = head_inputs(N, d, V, seed=5 + n, e_std=0.15)
+    th = torch.tensor(h, device="cuda").to(torch.bfloat16).requires_grad_(True)
+    tE = torch.tensor(E, device="cuda").to(torch.bfloat16).requires_grad_(True)
+    obj, tel = fused_head(th, tE, torch.tensor(t, device="cuda"), kind="alg_ce", n=n, c=c)
+    obj.backward()
+    torch.cuda.synchronize()
+    obj_r, pt_r = OH.dense_forward(h, E, t, n=n, c=c)
+    dh_r, dE_r = OH.dense_backward(h, E, t, 1.0, n=n, c=c)
+    assert abs(obj.item() - obj_r) <= 2e-3 * abs(obj_r) + 2e-4, (obj.item(), obj_r)
+    assert rel_l2(tel.float().cpu().numpy(), pt_r) < 2e-2
+    assert rel_l2(th.grad.float().cpu().numpy(), dh_r) < 1e-2
+    assert rel_l2(tE.grad.float().cpu().numpy(), dE_r) < 1e-2
+
+
+@pytest.mark.parametrize("n,c", [(1, 2.0), (128, 16.0)])
+def test_eval_head_n(n, c):
+    """The streamed evaluation head works in the log domain, so it takes n = 1 as well."""
+    from algebraic_amd.kernels.fused_head import head_logprob
+    N, d, V = 256, 128, 1000
+    h, E, t = head_inputs(N, d, V, seed=9 + n, e_std=0.15)
+    th = torch.tensor(h, device="cuda").to(torch.bfloat16)
+    tE = torch.tensor(E, device="cuda").to(torch.bfloat16)
+    out = head_logprob(th, tE, torch.tensor(t, device="cuda"), n=n, c=c)
+    logp = (out[0] if isinstance(out, tuple) else out).float().cpu().numpy()
+    ref = OH.eval_logprob(h, E, t, n=n, c=c)
+    ref = ref[0] if isinstance(ref, tuple) else ref
+    np.testing.assert_allclose(logp, ref, atol=1e-4 * max(1.0, n / 16), rtol=1e-4)
