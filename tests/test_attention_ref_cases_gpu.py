@@ -12,6 +12,9 @@ Reference cases covered:
   test_model_attention_statistics         :80-101  (root, inverse, compact, guarded; f32, bf16)
   test_guarded_attention_tail             :104-123 (f32 tails, gradients checked too)
   test_explicit_clipping_vjp_is_zero_above_cap :126-142 (f32 and bf16)
+  test_resident_backward_matches_dense    :145-181 (asinh modes inverse, root, shifted, guarded;
+                                                    bf16, T = 512 and 2048; the schedule knobs
+                                                    give bit-identical gradients)
   test_diagonal_forward_matches_dense     :181-235 (ordinary, negative_no_sink)
   test_resident_guarded_tail              :238-255 (bf16, D = 64 as there and D = 128)
   test_whole_head_residency_matches_dense :258-334 (the six asinh modes, incl. the
@@ -149,6 +152,32 @@ def test_explicit_clipping_vjp_is_zero_above_cap(dtype):
     assert np.isfinite(o).all() and np.isfinite(dv).all()
     for grad in (dq, dk, dsink):
         np.testing.assert_array_equal(grad, np.zeros_like(grad))
+
+
+# ---------------------------------------------------------------------------
+# test_resident_backward_matches_dense (:145-181): bf16 (1, 2, T, 64) N(0,1), sink N(0,1)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("mode", ["inverse", "root", "shifted", "guarded"])
+@pytest.mark.parametrize("seq", [512, 2048])
+def test_resident_backward_matches_dense(mode, seq):
+    shape = (1, 2, seq, 64)
+    rng = np.random.default_rng(67 + seq + len(mode))
+    q, k, v, g = (_normal(rng, shape, "bf16") for _ in range(4))
+    sink = rng.standard_normal((1, 2, 1, 1)).astype(np.float32)
+    opts = dict(n=16, c=8.0, block=512, compact_stat=mode != "root", resident_bwd=True, diagonal_bwd=True,
+                shift=mode == "shifted", inv_stat=mode not in ("root", "shifted"), range_guard=mode == "guarded")
+    print(f"[resident backward] mode={mode} T={seq}", flush=True)
+    res = _run(q, k, v, g, sink, "bf16", **opts)
+    o_ref, grads = _dense(q, k, v, g, sink, 16, 8.0)
+    np.testing.assert_allclose(res[0], o_ref, atol=0.012, rtol=0.012)
+    for name, a, b in zip(("dq", "dk", "dv", "dsink"), res[1:5], grads):
+        assert rel_l2(a, b) < 0.02, (mode, seq, name, rel_l2(a, b))
+    if seq == 2048 and mode == "guarded":
+        # The reference also checks that its automatic dispatch (resident_bwd=None) gives the
+        # same gradients bit for bit; the HIP path takes the schedule knobs as hints.
+        auto = _run(q, k, v, g, sink, "bf16", **{**opts, "resident_bwd": None, "diagonal_bwd": None})
+        for a, b in zip(res[1:5], auto[1:5]):
+            np.testing.assert_array_equal(a, b)
 
 
 # ---------------------------------------------------------------------------

@@ -41,6 +41,10 @@ def test_flash_validation():
         flash_attention(q, k, v, kind="asinh", resident_bwd=True)  # needs T in {512,1024,2048}
     with pytest.raises(ValueError):
         flash_attention(q, k, v, kind="asinh", poly_rho=True, range_guard=True)
+    # test_whole_head_residency_rejects_unsupported_shape (test_flash_kernel_tpu.py:337-341).
+    x = torch.ones((1, 1, 512, 64), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="whole-head residency"):
+        flash_attention(x, x, x, kind="asinh", c=8.0, head_resident=True)
     with pytest.raises(NotImplementedError):
         flash_attention(q, k, v, kind="softmax")
     q16, k16, v16 = qkv(dtype=torch.float16)
