@@ -104,6 +104,25 @@ def make_steps(torch, x):
     return attn_step, head_step, full_step
 
 
+def make_attn_step(torch, dev, B, H, T, D, seed=1):
+    """Guarded bf16 attention fwd+bwd at another shape, inputs drawn as in make_inputs."""
+    from algebraic_amd.kernels.flash import flash_attention
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    rn = lambda *s: torch.randn(*s, device=dev, generator=g, dtype=torch.float32)
+    q = rms_norm(rn(B, H, T, D)).to(torch.bfloat16).requires_grad_(True)
+    k = rms_norm(rn(B, H, T, D)).to(torch.bfloat16).requires_grad_(True)
+    v = rn(B, H, T, D).to(torch.bfloat16).requires_grad_(True)
+    sink = (rn(1, H, 1, 1) * 0.1).requires_grad_(True)
+    do = rn(B, H, T, D).to(torch.bfloat16)
+
+    def step():
+        o = flash_attention(q, k, v, sink, kind="asinh", n=ATTN["n"], c=ATTN["c"], block=512, range_guard=True)
+        return torch.autograd.grad(o, (q, k, v, sink), do)
+
+    return step
+
+
 PEAK_FP32_TFLOPS = 157.3   # MI355X dense fp32 MFMA
 
 # The other BASELINE.json configs, reported beside the headline (timed unit: the wrapper call).
@@ -532,8 +551,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip timing BASELINE configs 1, 2, 3 and 5 beside the headline")
-    ap.add_argument("--only", choices=["attn", "head", "step", "neighbours"],
+    ap.add_argument("--only", choices=["attn", "head", "step", "neighbours", "c3"],
                     help="run only W+K launches of one part (for profiler runs) and print its time; "
+                         "'c3' is the attention fwd+bwd of BASELINE config 3 (D = 64); "
                          "'neighbours' runs the timings of the fused prologue, eval head, final norm "
                          "and feed-forward")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -562,7 +582,9 @@ def main():
         print(json.dumps(out), flush=True)
         return 0
     if args.only:
-        fn = {"attn": attn_step, "head": head_step, "step": full_step}[args.only]
+        if args.only == "c3":
+            attn_step = make_attn_step(torch, dev, **{k: OTHER_CONFIGS["C3"][k] for k in "BHTD"})
+        fn = {"attn": attn_step, "c3": attn_step, "head": head_step, "step": full_step}[args.only]
         t = timed(torch, fn, K, W)
         res = {"only": args.only, "steps": K, "warmup": W, "ms": round(t * 1e3, 4)}
         if args.copy_mib:
