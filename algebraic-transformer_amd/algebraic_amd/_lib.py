@@ -27,6 +27,8 @@ _SIGNATURES = {
     "alg_attn_workspace_size": (_S, [_I, _I, _I, _I, _I]),
     "alg_attn_prepare": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _F, _I, _I, _P, _P, _P, _P, _S]),
     "alg_attn_fwd": (_I, [_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _P, _F, _I, _I, _P, _P, _P]),
+    "alg_attn_fwd_guarded": (_I, [_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _F, _I, _P, _P, _P, _P, _P, _P,
+                                  _P, _S]),
     "alg_attn_bwd": (_I, [_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P, _F, _I, _I, _F,
                           _P, _P, _P, _P, _P, _P, _S]),
     "alg_attn_bwd_noalloc": (_I, [_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P, _F, _I, _I,

@@ -117,16 +117,24 @@ class _FlashFn(torch.autograd.Function):
         q_s = torch.empty_like(q)
         sink = torch.empty(H, dtype=torch.float32, device=dev) if has_sink else None
         flag = torch.empty(1, dtype=torch.int32, device=dev)
-        _lib.check(lib.alg_attn_prepare(
-            st, dt, B, H, T, D, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink_in),
-            sink_in.numel() if has_sink else 0, plan.c, plan.n, int(plan.range_guard),
-            _lib.ptr(q_s), _lib.ptr(sink), _lib.ptr(flag), _lib.ptr(ws), ws_bytes), "flash_attention prologue")
         o = torch.empty_like(q)
         stat = torch.empty((B, H, T), dtype=torch.float32, device=dev)
-        _lib.check(lib.alg_attn_fwd(
-            st, dt, plan.layout, B, H, T, D, _lib.ptr(q_s), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink), plan.n, plan.variant,
-            _lib.ptr(flag), plan.clamp, int(plan.fast_rho), int(plan.inv_stat),
-            _lib.ptr(o), None, _lib.ptr(stat)), "flash_attention forward")
+        nsink = sink_in.numel() if has_sink else 0
+        if plan.variant == _lib.ATTN_GUARDED:
+            # q_s, sink/c, the guard and the guarded forward (flash.py:823-856) in one call.
+            _lib.check(lib.alg_attn_fwd_guarded(
+                st, dt, plan.layout, B, H, T, D, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink_in), nsink,
+                plan.c, plan.n, _lib.ptr(q_s), _lib.ptr(sink), _lib.ptr(flag), _lib.ptr(o), None, _lib.ptr(stat),
+                _lib.ptr(ws), ws_bytes), "flash_attention forward")
+        else:
+            _lib.check(lib.alg_attn_prepare(
+                st, dt, B, H, T, D, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink_in), nsink, plan.c, plan.n,
+                int(plan.range_guard), _lib.ptr(q_s), _lib.ptr(sink), _lib.ptr(flag), _lib.ptr(ws), ws_bytes),
+                "flash_attention prologue")
+            _lib.check(lib.alg_attn_fwd(
+                st, dt, plan.layout, B, H, T, D, _lib.ptr(q_s), _lib.ptr(k), _lib.ptr(v), _lib.ptr(sink), plan.n,
+                plan.variant, _lib.ptr(flag), plan.clamp, int(plan.fast_rho), int(plan.inv_stat),
+                _lib.ptr(o), None, _lib.ptr(stat)), "flash_attention forward")
         ctx.plan = plan
         ctx.sink_shape = None if not has_sink else tuple(sink_logit.shape)
         ctx.sink_dtype = None if not has_sink else sink_logit.dtype

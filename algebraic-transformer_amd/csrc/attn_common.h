@@ -12,6 +12,8 @@ namespace alg {
 //   SHIFTED  running-max accumulation (the guarded "high" fallback or explicit shift=True)
 enum AttnMode { MODE_INRANGE = 0, MODE_CLIPPED = 1, MODE_SHIFTED = 2 };
 
+constexpr int FWD_BQ = 128;  // queries per forward workgroup (its guard partials: one set each)
+
 struct AttnFwdParams {
   const void* q;       // (B,H,T,D) pre-scaled queries q_s = round(q * alpha)
   const void* k;       // (B,H,T,D)
@@ -27,6 +29,17 @@ struct AttnFwdParams {
   int fast_rho;        // SHIFTED: fast rho for the weights
   int inv_stat;        // CLIPPED: 1 -> stat = 1/Z, 0 -> stat = Z^(-1/n)
   int layout;          // storage of q, k, v, o (see head_base)
+  // Guarded forward from unscaled queries (the bf16 in-range kernel's FROM_Q form): q holds
+  // the raw queries; the kernel writes q_s = round(q * alpha) to q_s_out, its workgroup's
+  // guard maxima (||q_s||^2 of its queries, ||k||^2 and |v| of the keys at the same positions)
+  // to guard_part[3 * (bh * nqb + query block)], and reads the sink as sink_logit / sink_c
+  // (sink_count 1: broadcast; the guard kernel that runs next writes the same value to sink).
+  void* q_s_out = nullptr;
+  float alpha = 1.0f;
+  float* guard_part = nullptr;
+  const float* sink_logit = nullptr;
+  int sink_count = 0;
+  float sink_c = 1.0f;
 };
 
 struct AttnBwdParams {

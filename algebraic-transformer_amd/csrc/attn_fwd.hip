@@ -18,7 +18,6 @@
 
 namespace alg {
 
-constexpr int FWD_BQ = 128;  // queries per workgroup
 constexpr int FWD_BK = 64;   // keys per LDS tile
 
 template <typename T>
@@ -484,6 +483,99 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_f32_split_kernel(AttnFwdParam
   }
 }
 
+// NaN-propagating maximum of the guard (a NaN anywhere fails it, as the reference's
+// comparisons do).
+__device__ __forceinline__ float guard_max(float a, float b) { return (a > b || a != a) ? a : b; }
+
+// Guard maxima of one forward workgroup (flash.py:841-849) over the queries it owns and the
+// keys at the same positions q0 .. q0 + FWD_BQ - 1, so the workgroups of a launch cover every
+// row once. Row sums follow the chunk order of the prep kernel (8 elements per 16-byte chunk,
+// then a butterfly over the row's chunks), so the guard sees the same sums either way.
+//
+// Keys and values: the workgroup's own key rows are its two diagonal tiles, which pass
+// through LDS anyway; guard_kv_tile folds one such tile (rows past T are zero-filled there and
+// add nothing) into the thread's running maxima mk (||k||^2) and mv (|v|).
+template <int D>
+__device__ __forceinline__ void guard_kv_tile(const bf16* Ks, const bf16* Vs, float& mk, float& mv) {
+  constexpr int CPR = D / 8, RPS = 256 / CPR, NR = FWD_BK / RPS;
+  const int c = threadIdx.x % CPR, r0 = threadIdx.x / CPR;
+  uint4 kr[NR], vr[NR];
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    kr[i] = *reinterpret_cast<const uint4*>(Ks + swz_at<CPR>(r0 + RPS * i, 8 * c));
+    vr[i] = *reinterpret_cast<const uint4*>(Vs + swz_at<CPR>(r0 + RPS * i, 8 * c));
+  }
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    bf16 kv[8], vv[8];
+    *reinterpret_cast<uint4*>(kv) = kr[i];
+    *reinterpret_cast<uint4*>(vv) = vr[i];
+    float sk = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float kf = (float)kv[j];
+      sk += kf * kf;
+      mv = guard_max(mv, __builtin_fabsf((float)vv[j]));
+    }
+#pragma unroll
+    for (int m = 1; m < CPR; m <<= 1) sk += __shfl_xor(sk, m, 64);
+    mk = guard_max(mk, sk);
+  }
+}
+
+// Queries, from the fragments the kernel holds, and the workgroup's maxima: called by every
+// thread once the main loop is done; writes part[0..2].
+template <int D>
+__device__ __forceinline__ void fwd_guard_partials(const bf16x8 (&qf)[D / 16], bool live, float mk, float mv,
+                                                   float* part, float (&red)[4][3]) {
+  constexpr int NF = D / 16;
+  // The thread index and the query fragments pass through empty asm statements so the compiler
+  // forms the row sums here, after the main loop, instead of computing them early and carrying
+  // them through it (that cost the kernel 10-19 more VGPRs, and at D = 64 one wave per SIMD of
+  // occupancy).
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int lane = tid & 63, wave = tid >> 6;
+  // Chunk 2s + h of row myq is qf[s] on lane half h; chunks 2s and 2s + 1 meet across the
+  // halves, then the pair sums combine in the butterfly's order.
+  float ps[NF];
+#pragma unroll
+  for (int s = 0; s < NF; ++s) {
+    float c = 0.0f;
+    bf16x8 qv = qf[s];
+    asm volatile("" : "+v"(qv));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float f = (float)qv[j];
+      c += f * f;
+    }
+    ps[s] = c + __shfl_xor(c, 32, 64);
+  }
+#pragma unroll
+  for (int w = 1; w < NF; w <<= 1)
+#pragma unroll
+    for (int s = 0; s < NF; s += 2 * w) ps[s] = ps[s] + ps[s + w];
+  float mq = live ? ps[0] : 0.0f;
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    mq = guard_max(mq, __shfl_xor(mq, m, 64));
+    mk = guard_max(mk, __shfl_xor(mk, m, 64));
+    mv = guard_max(mv, __shfl_xor(mv, m, 64));
+  }
+  if (lane == 0) {
+    red[wave][0] = mq;
+    red[wave][1] = mk;
+    red[wave][2] = mv;
+  }
+  __syncthreads();
+  if (tid < 3) {
+    float m = red[0][tid];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) m = guard_max(m, red[w][tid]);
+    part[tid] = m;
+  }
+}
+
 // In-range forward for bf16 inputs (the guarded "low" variant): same decomposition as
 // attn_fwd_kernel (4 waves x 32 queries, lane = query, S^T = K Q^T, O^T += V^T P^T), with K/V
 // tiles in two ping-pong LDS buffer sets, each filled by range-checked buffer copies issued
@@ -494,7 +586,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_f32_split_kernel(AttnFwdParam
 //   R3  O^T over keys 0..31 | weights of 32..63 (MFMA | VALU)
 //   R4  O^T over keys 32..63                    (MFMA)
 // The two tiles that cross this workgroup's diagonal evaluate the causal mask per element.
-template <int D, int L2N, int LAYOUT>
+// FROM_Q: the guarded forward's first launch, before the guard has run (no flag to read): q
+// holds the raw queries; the kernel rounds q * alpha into its query fragments, writes them out
+// as q_s, and leaves its guard maxima for the guard kernel (fwd_guard_partials).
+template <int D, int L2N, int LAYOUT, bool FROM_Q>
 __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) {
   static_assert(D == 64 || D == 128, "head_dim");
   constexpr int BK = FWD_BK, CPR = D / 8, NDB = D / 32, NF = D / 16;
@@ -502,6 +597,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) 
   __shared__ __attribute__((aligned(16))) bf16 Ks1[BK * D];
   __shared__ __attribute__((aligned(16))) bf16 Vs0[BK * D];
   __shared__ __attribute__((aligned(16))) bf16 Vs1[BK * D];
+  __shared__ float gred[FROM_Q ? 4 : 1][3];
 
   if (p.flag && *p.flag == 0) return;  // device-side guard dispatch (flash.py:853-856)
   const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
@@ -533,6 +629,16 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) 
     const bf16x8 z = {};
     qf[s] = live ? ld8(Q + (size_t)myq * ld + 16 * s + 8 * h) : z;
   }
+  if constexpr (FROM_Q) {  // q_s = round(q * alpha) (flash.py:833)
+    const float alpha = p.alpha;
+    bf16* Qs = reinterpret_cast<bf16*>(p.q_s_out) + base + (size_t)myq * ld;
+#pragma unroll
+    for (int s = 0; s < NF; ++s) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) qf[s][j] = f2bf((float)qf[s][j] * alpha);
+      if (live) *reinterpret_cast<bf16x8*>(Qs + 16 * s + 8 * h) = qf[s];
+    }
+  }
   floatx16 oacc[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db) oacc[db] = floatx16{};
@@ -556,12 +662,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) 
   rk3[1] = ld8(Ks0 + row_off[1]);
   constexpr int VE = 10;  // VALU instructions per weight (scheduling hint)
 
+  float gmk = 0.0f, gmv = 0.0f;  // FROM_Q: guard maxima of the diagonal tiles' keys and values
   auto tile = [&](auto bufc, auto maskc, int kt) {
     constexpr int BUF = decltype(bufc)::value;
     constexpr bool MASKED = decltype(maskc)::value;
     const bf16* Ks = BUF ? Ks1 : Ks0;
     const bf16* Vs = BUF ? Vs1 : Vs0;
     const int kb0 = kt * BK;
+    if constexpr (FROM_Q && MASKED) guard_kv_tile<D>(Ks, Vs, gmk, gmv);  // this workgroup's own keys
     floatx16 s[2];
     bf16x8 pf[2][2];
     float w[16];
@@ -661,25 +769,37 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) 
     tile(std::integral_constant<int, 0>{}, std::true_type{}, kt);
     if (kt + 1 < ntiles) tile(std::integral_constant<int, 1>{}, std::true_type{}, kt + 1);
   }
-  if (!live) return;
-
   // Finalize (flash.py:271-284): Z over both lane halves (+ the sink's weight), stat = 1/Z.
-  float Z = lsum + xor32(lsum);
-  if (p.sink) Z += pow2n<L2N>(rho_fast(p.sink[head]), log2n);
-  const float inv = 1.0f / Z;
-  bf16* O = reinterpret_cast<bf16*>(p.o) + base + (size_t)myq * ld;  // (o_precise: shifted only)
-#pragma unroll
-  for (int db = 0; db < NDB; ++db) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d0 = db * 32 + 8 * g + 4 * h;
-      bf16x4 ob;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) ob[e] = f2bf(oacc[db][4 * g + e] * inv);
-      *reinterpret_cast<bf16x4*>(O + d0) = ob;
+  auto finalize = [&]() __attribute__((always_inline)) {
+    float Z = lsum + xor32(lsum);
+    if constexpr (FROM_Q) {
+      if (p.sink_logit) Z += pow2n<L2N>(rho_fast(p.sink_logit[p.sink_count == 1 ? 0 : head] / p.sink_c), log2n);
+    } else {
+      if (p.sink) Z += pow2n<L2N>(rho_fast(p.sink[head]), log2n);
     }
+    const float inv = 1.0f / Z;
+    bf16* O = reinterpret_cast<bf16*>(p.o) + base + (size_t)myq * ld;  // (o_precise: shifted only)
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = db * 32 + 8 * g + 4 * h;
+        bf16x4 ob;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ob[e] = f2bf(oacc[db][4 * g + e] * inv);
+        *reinterpret_cast<bf16x4*>(O + d0) = ob;
+      }
+    }
+    if (h == 0) p.stat[(size_t)bh * T_ + myq] = inv;
+  };
+  if constexpr (FROM_Q) {
+    // After the output (its accumulators are dead), with every lane of the workgroup.
+    if (live) finalize();
+    fwd_guard_partials<D>(qf, live, gmk, gmv, p.guard_part + 3 * ((size_t)bh * nqb + blockIdx.y), gred);
+  } else {
+    if (!live) return;
+    finalize();
   }
-  if (h == 0) p.stat[(size_t)bh * T_ + myq] = inv;
 }
 
 template <typename T, int D>
@@ -694,12 +814,20 @@ static hipError_t launch_fwd_mode(const AttnFwdParams& p, int mode, hipStream_t 
     case MODE_INRANGE: {
       KTimer t("attn_fwd_inrange", st);
       if constexpr (sizeof(T) == 2) {
-        if (p.layout) {
-          if (p.log2n == 4) hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, 4, 1>), grid, block, 0, st, p);
-          else hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, 0, 1>), grid, block, 0, st, p);
+        if (p.q_s_out) {
+          if (p.layout) {
+            if (p.log2n == 4) hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, 4, 1, true>), grid, block, 0, st, p);
+            else hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, 0, 1, true>), grid, block, 0, st, p);
+          } else {
+            if (p.log2n == 4) hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, 4, 0, true>), grid, block, 0, st, p);
+            else hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, 0, 0, true>), grid, block, 0, st, p);
+          }
+        } else if (p.layout) {
+          if (p.log2n == 4) hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, 4, 1, false>), grid, block, 0, st, p);
+          else hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, 0, 1, false>), grid, block, 0, st, p);
         } else {
-          if (p.log2n == 4) hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, 4, 0>), grid, block, 0, st, p);
-          else hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, 0, 0>), grid, block, 0, st, p);
+          if (p.log2n == 4) hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, 4, 0, false>), grid, block, 0, st, p);
+          else hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, 0, 0, false>), grid, block, 0, st, p);
         }
       } else if constexpr (D == 64) {
         // Four-way key split (32 queries per workgroup) while two-way workgroups would not

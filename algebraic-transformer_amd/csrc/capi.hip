@@ -4,6 +4,7 @@
 // (src/algebraic/kernels/flash.py:740-743, 796-797; fused_head.py:163-164, 269-272);
 // everything else is shape/pointer checking before any launch, so a bad call returns an
 // error instead of launching a kernel whose grid does not match its operands.
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -90,8 +91,11 @@ int check_n(int n) {
   return ALG_OK;
 }
 
-// Workspace layout for attention: [sink partials f32 B*H*nblk][prep partials f32 3*1024], and
-// for f32 inputs then [dq accumulator f32 B*H*T*D] (the bf16 dQ kernel needs none).
+// Workspace layout for attention: [sink partials f32 B*H*nblk][guard partials f32 3*max(1024,
+// B*H*ceil(T/128)): the prep kernel's (at most 1024 workgroups) or the guarded bf16 forward's
+// (one per 128-query workgroup)], and for f32 inputs then [dq accumulator f32 B*H*T*D] (the
+// bf16 dQ kernel needs none).
+size_t attn_fwd_workgroups(int B, int H, int T) { return (size_t)B * H * ((T + alg::FWD_BQ - 1) / alg::FWD_BQ); }
 struct AttnWs {
   size_t sink_part, prep_part, dq_acc, total;
 };
@@ -99,7 +103,7 @@ AttnWs attn_ws(int dtype, int B, int H, int T, int D) {
   AttnWs w;
   w.sink_part = 0;
   w.prep_part = align256((size_t)B * H * alg::attn_bwd_sink_blocks(T) * sizeof(float));
-  w.dq_acc = w.prep_part + align256(3 * 1024 * sizeof(float));
+  w.dq_acc = w.prep_part + align256(3 * std::max<size_t>(1024, attn_fwd_workgroups(B, H, T)) * sizeof(float));
   w.total = w.dq_acc + (dtype == ALG_DTYPE_F32 ? align256((size_t)B * H * T * D * sizeof(float)) : 0);
   return w;
 }
@@ -403,6 +407,65 @@ int alg_attn_fwd(alg_stream_t stream, int dtype, int layout, int B, int H, int T
     return hip_status(alg::launch_attn_fwd(ps, D, bf, alg::MODE_SHIFTED, st), "alg_attn_fwd");
   }
   return hip_status(alg::launch_attn_fwd(p, D, bf, variant, st), "alg_attn_fwd");
+}
+
+int alg_attn_fwd_guarded(alg_stream_t stream, int dtype, int layout, int B, int H, int T, int D, const void* q,
+                         const void* k, const void* v, const float* sink_logit, int sink_count, float c, int n,
+                         void* q_s, float* sink_scaled, int* guard_flag, void* o, float* o_precise, float* stat,
+                         void* workspace, size_t workspace_bytes) {
+  int rc = check_attn_shape(dtype, B, H, T, D);
+  if (rc) return rc;
+  if ((rc = check_layout(layout, H, T, D))) return rc;
+  if ((rc = check_n(n))) return rc;
+  if (n > 32) return fail(ALG_ERR_INVALID, "the range guard applies for n <= 32 (got %d)", n);
+  if (!(c > 0.0f) || !std::isfinite(c)) return fail(ALG_ERR_INVALID, "asinh scale c must be positive and finite");
+  if (!q || !k || !v || !q_s || !guard_flag || !o || !stat)
+    return fail(ALG_ERR_INVALID, "q, k, v, q_s, guard_flag, o and stat are required");
+  if (!aligned16({q, k, v, q_s, o, o_precise, workspace})) return fail(ALG_ERR_INVALID, "matrices must be 16-byte aligned");
+  if (sink_logit && sink_count != 1 && sink_count != H) return fail(ALG_ERR_INVALID, "sink_count must be 1 or H");
+  if (sink_logit && !sink_scaled) return fail(ALG_ERR_INVALID, "sink_scaled output required with a sink");
+  const AttnWs ws = attn_ws(dtype, B, H, T, D);
+  if (!workspace || workspace_bytes < ws.total)
+    return fail(ALG_ERR_INVALID, "workspace too small: need %zu bytes", ws.total);
+  // The guard's clamp (flash.py:747-748); the in-range and shifted kernels do not read it.
+  const double t = root_pow2(1e37 / (T + 1.0), n);
+  const float clamp = (float)(0.5 * (t - 1.0 / t));
+  if (dtype != ALG_DTYPE_BF16) {
+    rc = alg_attn_prepare(stream, dtype, B, H, T, D, q, k, v, sink_logit, sink_count, c, n, 1, q_s, sink_scaled,
+                          guard_flag, workspace, workspace_bytes);
+    if (rc) return rc;
+    return alg_attn_fwd(stream, dtype, layout, B, H, T, D, q_s, k, v, sink_scaled, n, ALG_ATTN_GUARDED, guard_flag,
+                        clamp, 1, 1, o, o_precise, stat);
+  }
+  hipStream_t st = (hipStream_t)stream;
+  float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + ws.prep_part);
+  alg::AttnFwdParams p;
+  p.q = q; p.k = k; p.v = v; p.sink = nullptr; p.flag = nullptr;
+  p.o = o; p.o_precise = nullptr; p.stat = stat;
+  p.B = B; p.H = H; p.T = T;
+  p.log2n = log2_pow2(n);
+  p.clamp = clamp; p.fast_rho = 1; p.inv_stat = 1;
+  p.layout = layout;
+  p.q_s_out = q_s;
+  p.alpha = (float)(1.0 / (std::sqrt((double)D) * (double)c));  // as alg_attn_prepare
+  p.guard_part = part;
+  p.sink_logit = sink_logit; p.sink_count = sink_count; p.sink_c = c;
+  rc = hip_status(alg::launch_attn_fwd(p, D, true, alg::MODE_INRANGE, st), "alg_attn_fwd_guarded");
+  if (rc) return rc;
+  alg::GuardParams g = guard_params(H, T, n, c, sink_logit, sink_count, sink_scaled, guard_flag, 1);
+  g.part = part;
+  g.nblocks = (int)attn_fwd_workgroups(B, H, T);
+  rc = hip_status(alg::launch_attn_guard(g, st), "alg_attn_fwd_guarded");
+  if (rc) return rc;
+  alg::AttnFwdParams ps;
+  ps.q = q_s; ps.k = k; ps.v = v; ps.flag = guard_flag;
+  ps.sink = sink_logit ? sink_scaled : nullptr;  // written by the guard kernel only with a sink
+  ps.o = o; ps.o_precise = o_precise; ps.stat = stat;
+  ps.B = B; ps.H = H; ps.T = T;
+  ps.log2n = p.log2n;
+  ps.clamp = clamp; ps.fast_rho = 0; ps.inv_stat = 1;  // the fallback uses stable rho (flash.py:851)
+  ps.layout = layout;
+  return hip_status(alg::launch_attn_fwd(ps, D, true, alg::MODE_SHIFTED, st), "alg_attn_fwd_guarded");
 }
 
 int alg_attn_bwd(alg_stream_t stream, int dtype, int layout, int B, int H, int T, int D, const void* q_s,

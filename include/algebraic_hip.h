@@ -86,6 +86,22 @@ int alg_attn_fwd(alg_stream_t stream, int dtype, int layout, int B, int H, int T
                  int n, int variant, const int* guard_flag, float clamp, int fast_rho, int inv_stat,
                  void* o, float* o_precise, float* stat);
 
+/* Guarded forward from the unscaled queries, flash.py:823-856 with range_guard=True
+ * (kind="asinh", n <= 32, where the guard applies, flash.py:834): the same outputs as
+ * alg_attn_prepare(range_guard = 1) followed by alg_attn_fwd(ALG_ATTN_GUARDED) with the
+ * guard's own clamp (q_s, sink_scaled, guard_flag, o, stat; o_precise as in alg_attn_fwd), in
+ * one call. For bf16 inputs there is no separate pass over q, k and v: the in-range forward
+ * rounds q * alpha itself, writes q_s and leaves the guard maxima of its rows, the guard runs
+ * after it, and the shifted branch (flag-checked on the device) replaces o and stat when the
+ * guard fails. sink_scaled is written, and required, only with a sink (sink_logit not NULL).
+ * f32 inputs take the two calls. */
+int alg_attn_fwd_guarded(alg_stream_t stream, int dtype, int layout, int B, int H, int T, int D,
+                         const void* q, const void* k, const void* v,
+                         const float* sink_logit, int sink_count, float c, int n,
+                         void* q_s, float* sink_scaled, int* guard_flag,
+                         void* o, float* o_precise, float* stat,
+                         void* workspace, size_t workspace_bytes);
+
 /* Backward, flash.py:333-361, 515-687, 694-726 / head_resident.py:91-119:
  * in the forward residuals (q_s, k, v, sink_scaled, o, stat) and dO; out
  * dq = round(round(n * dq_s_acc) * dq_scale) (dq_scale = 1 gives the kernel's dq_s;

@@ -115,6 +115,30 @@ def test_invalid_arguments_fail_before_launch():
         _lib.check(_lib.ALG_ERR_INVALID, "probe")
 
 
+def test_guarded_forward_validates_before_launch():
+    """alg_attn_fwd_guarded: the guard applies for n <= 32 (flash.py:834); the workspace holds
+    one set of guard maxima per 128-query workgroup; argument errors precede any launch."""
+    from algebraic_amd import _lib
+    handle = lib()
+    P = ctypes.c_void_p
+    bf = _lib.DTYPE_BF16
+    B, H, T, D = 2, 4, 3000, 128
+    ws = handle.alg_attn_workspace_size(bf, B, H, T, D)
+    assert ws >= 3 * 4 * B * H * ((T + 127) // 128)
+
+    def call(n=16, c=8.0, nsink=4, sink=P(16), q=P(16), ws_bytes=ws):
+        return handle.alg_attn_fwd_guarded(None, bf, 0, B, H, T, D, q, P(16), P(16), sink, nsink, c, n, P(16),
+                                           P(16), P(16), P(16), None, P(16), P(16), ws_bytes)
+
+    assert call(n=64) == _lib.ALG_ERR_INVALID and b"n <= 32" in handle.alg_last_error()
+    assert call(n=12) == _lib.ALG_ERR_INVALID and b"power of two" in handle.alg_last_error()
+    assert call(c=0.0) == _lib.ALG_ERR_INVALID and b"positive" in handle.alg_last_error()
+    assert call(nsink=3) == _lib.ALG_ERR_INVALID and b"sink_count" in handle.alg_last_error()
+    assert call(q=None) == _lib.ALG_ERR_INVALID and b"required" in handle.alg_last_error()
+    assert call(q=P(18)) == _lib.ALG_ERR_INVALID and b"aligned" in handle.alg_last_error()
+    assert call(ws_bytes=ws - 1) == _lib.ALG_ERR_INVALID and b"workspace" in handle.alg_last_error()
+
+
 def test_neighbour_entry_points_validate_before_launch():
     """The prologue, eval head, final norm and feed-forward entry points reject bad shapes,
     missing workspaces, non-finite scalars and misaligned matrices before any launch."""
