@@ -110,13 +110,15 @@ AttnWs attn_ws(int dtype, int B, int H, int T, int D) {
 
 // Head buffers. Workspace: [partials f32 nvt*N][obj parts] (+ bwd: dZ bf16 Npad*Vp for the
 // recompute schedule, or s*h/l bf16 N*d for the residual schedule; then, when the dh product
-// is split over the vocabulary, its f32 partials split*N*d). Residual (optional,
+// is split over the vocabulary, its f32 partials split*N*d; then, when the last round of dE
+// tiles is split over the tokens, their f32 tiles (head_de_plan)). Residual (optional,
 // forward -> backward): [U bf16 Npad*Vp][l f32 N]. dZ and U are token-major with rows of
 // Vp = V rounded up to 8 (16-byte aligned rows).
 struct HeadWs {
-  size_t partial, obj_part, bwd, dh_part, total;
+  size_t partial, obj_part, bwd, dh_part, de_part, total;
   size_t res_ut, res_l, res_total;
   int Npad, Vp, dh_split;
+  alg::HeadDePlan de;
 };
 HeadWs head_ws(int N, int d, int V, int pass, bool residual) {
   HeadWs w;
@@ -129,7 +131,11 @@ HeadWs head_ws(int N, int d, int V, int pass, bool residual) {
   w.dh_split = alg::head_dh_split(N, d, V);
   w.dh_part = w.bwd + align256(bwd_bytes);
   const size_t part_bytes = w.dh_split > 1 ? (size_t)w.dh_split * N * d * sizeof(float) : 0;
-  w.total = pass == 0 ? w.bwd : w.dh_part + align256(part_bytes);
+  w.de = alg::head_de_plan(N, d, V);
+  w.de_part = w.dh_part + align256(part_bytes);
+  const size_t de_bytes =
+      w.de.split > 1 ? (size_t)(w.de.tiles - w.de.full) * w.de.split * alg::HT_M * alg::HT_N * sizeof(float) : 0;
+  w.total = pass == 0 ? w.bwd : w.de_part + align256(de_bytes);
   w.res_ut = 0;
   w.res_l = align256((size_t)w.Npad * w.Vp * 2);
   w.res_total = w.res_l + align256((size_t)N * sizeof(float));
@@ -149,6 +155,8 @@ HeadWs head_ws_f32(int N, int d, int V, int pass) {
   w.dh_split = alg::head_f32_dh_split(N, d, V);
   w.dh_part = w.bwd + align256((size_t)N * w.Vp * sizeof(float));
   const size_t part_bytes = w.dh_split > 1 ? (size_t)w.dh_split * N * d * sizeof(float) : 0;
+  w.de = alg::HeadDePlan{0, 0, 1, 0};
+  w.de_part = 0;
   w.total = pass == 0 ? w.bwd : w.dh_part + align256(part_bytes);
   w.res_ut = w.res_l = w.res_total = 0;
   return w;
@@ -751,6 +759,10 @@ int alg_head_bwd(alg_stream_t stream, int dtype, int N, int d, int V, const void
   p.dh_split = ws.dh_split;
   p.dh_kchunk = alg::head_dh_kchunk(V, ws.dh_split);
   p.dh_part = ws.dh_split > 1 ? reinterpret_cast<float*>(w + ws.dh_part) : nullptr;
+  p.de_full = ws.de.full;
+  p.de_split = ws.de.split;
+  p.de_kchunk = ws.de.kchunk;
+  p.de_part = ws.de.split > 1 ? reinterpret_cast<float*>(w + ws.de_part) : nullptr;
   return hip_status(alg::launch_head_bwd(p, (hipStream_t)stream), "alg_head_bwd");
 }
 

@@ -590,22 +590,46 @@ __global__ __launch_bounds__(256) void head_dh_reduce_kernel(HeadParams p) {
 }
 
 // dE = (U' or dZ)^T (hs or h): A = U' stored token-major [n][v] (m-contiguous), B stored
-// [n][d] (n-contiguous).
+// [n][d] (n-contiguous). Workgroups below de_full compute whole tiles, row-major inside each
+// XCD's share (U panels streamed once); the rest compute token range (id - de_full) % de_split
+// of tile de_full + (id - de_full) / de_split into an f32 tile of de_part, which
+// head_de_tail_kernel sums.
 __global__ __launch_bounds__(NT, 1) void head_de_kernel(HeadParams p) {
   __shared__ __attribute__((aligned(16))) GemmStage<MNMAJOR, MNMAJOR, HC> s0, s1;
-  const int nbm = (p.V + HT_M - 1) / HT_M, nbn = (p.d + HT_N - 1) / HT_N;
-  int tm, tn;
-  xcd_tile_rowmajor(blockIdx.x, nbm, nbn, tm, tn);  // U panels streamed once
+  const int nbn = (p.d + HT_N - 1) / HT_N;
+  const int bid = blockIdx.x;
+  int lin, kbeg = 0, kend = p.N, unit = -1;
+  if (bid < p.de_full) {
+    lin = p.de_full % 8 == 0 ? (bid % 8) * (p.de_full / 8) + bid / 8 : bid;
+  } else {
+    unit = bid - p.de_full;
+    lin = p.de_full + unit / p.de_split;
+    kbeg = (unit % p.de_split) * p.de_kchunk;
+    kend = min(p.N, kbeg + p.de_kchunk);
+  }
+  const int tm = lin / nbn, tn = lin - tm * nbn;
   const int m0 = tm * HT_M;  // vocab
   const int n0 = tn * HT_N;  // d
   const bf16* a = p.ut ? p.ut : p.dzt;
   const bf16* b = p.ut ? p.hs : p.h;
   GemmOperand A{a, p.Vp, p.N, p.V, (long)p.Npad * p.Vp}, B{b, p.d, p.N, p.d, (long)p.N * p.d};
   floatx16 acc[HC::MB][HC::NB];
-  gemm_mainloop<MNMAJOR, MNMAJOR, HC>(s0, s1, A, B, m0, n0, 0, p.N, acc);
+  gemm_mainloop<MNMAJOR, MNMAJOR, HC>(s0, s1, A, B, m0, n0, kbeg, kend, acc);
   const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
   int wm, wn;
   wave_coords<HC>(wm, wn);
+  if (unit >= 0) {  // one token range of a split tile: the whole f32 tile, row-major
+    float* part = p.de_part + (size_t)unit * HT_M * HT_N;
+#pragma unroll
+    for (int mb = 0; mb < HC::MB; ++mb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = wm * HC::WTM + mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+#pragma unroll
+        for (int nb = 0; nb < HC::NB; ++nb) part[r * HT_N + wn * HC::WTN + nb * 32 + l32] = acc[mb][nb][i];
+      }
+    return;
+  }
   if (!p.dE_f32 && m0 + HT_M <= p.V && n0 + HT_N <= p.d) {  // interior tile, bf16 output
     __syncthreads();  // every wave is done with the pipeline buffers
     store_block_bf16(acc, wave_stage(s0, s1, wm, wn),
@@ -631,6 +655,42 @@ __global__ __launch_bounds__(NT, 1) void head_de_kernel(HeadParams p) {
   }
 }
 
+// dE of a split tile: the de_split token-range tiles summed in range order, 32 rows of the
+// tile per workgroup (grid: split tiles x HT_M / 32).
+__global__ __launch_bounds__(256) void head_de_tail_kernel(HeadParams p) {
+  const int nbn = (p.d + HT_N - 1) / HT_N;
+  const int lin = p.de_full + blockIdx.x;
+  const int tm = lin / nbn, tn = lin - tm * nbn;
+  const float* part = p.de_part + (size_t)blockIdx.x * p.de_split * HT_M * HT_N;
+#pragma unroll
+  for (int c = 0; c < 32 * HT_N / 8 / 256; ++c) {
+    const int e = (threadIdx.x + 256 * c) * 8;
+    const int r = blockIdx.y * 32 + e / HT_N, col = e % HT_N;
+    const int v = tm * HT_M + r, j0 = tn * HT_N + col;
+    if (v >= p.V || j0 >= p.d) continue;
+    const size_t o = (size_t)r * HT_N + col;
+    float4 a = *reinterpret_cast<const float4*>(part + o), b = *reinterpret_cast<const float4*>(part + o + 4);
+    for (int k = 1; k < p.de_split; ++k) {
+      const float* q = part + (size_t)k * HT_M * HT_N + o;
+      const float4 x = *reinterpret_cast<const float4*>(q), y = *reinterpret_cast<const float4*>(q + 4);
+      a.x += x.x; a.y += x.y; a.z += x.z; a.w += x.w;
+      b.x += y.x; b.y += y.y; b.z += y.z; b.w += y.w;
+    }
+    const float vals[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    const size_t out = (size_t)v * p.d + j0;  // d % 8 == 0: the 8 columns are in the row
+    if (p.dE_f32) {
+      float* dst = reinterpret_cast<float*>(p.dE) + out;
+      *reinterpret_cast<float4*>(dst) = a;
+      *reinterpret_cast<float4*>(dst + 4) = b;
+    } else {
+      bf16x8 o8;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) o8[t] = f2bf(vals[t]);
+      *reinterpret_cast<bf16x8*>(reinterpret_cast<bf16*>(p.dE) + out) = o8;
+    }
+  }
+}
+
 int head_vocab_tiles(int V) { return (V + HT_M - 1) / HT_M; }
 int head_token_pad(int N) { return ((N + HT_N - 1) / HT_N) * HT_N; }
 int head_vocab_pitch(int V) { return (V + 7) / 8 * 8; }
@@ -651,6 +711,32 @@ int head_dh_split(int N, int d, int V) {
   return best;
 }
 int head_dh_kchunk(int V, int split) { return ((V + split - 1) / split + 127) / 128 * 128; }
+
+// dE tiles past the last complete round of 256 workgroups are split over the tokens when that
+// shortens the last round: S ranges per tile finish it in ceil(tail*S/256)/S of a tile's time
+// instead of one (C2's 591 tiles: two full rounds, then 79 tiles x 3 ranges in a third of a
+// tile's time). A range keeps at least 1024 tokens, and a split must save a quarter of a round
+// (its f32 tiles are written and summed by head_de_tail_kernel); ties keep the smaller split.
+HeadDePlan head_de_plan(int N, int d, int V) {
+  HeadDePlan pl;
+  pl.tiles = head_vocab_tiles(V) * ((d + HT_N - 1) / HT_N);
+  pl.full = pl.tiles;
+  pl.split = 1;
+  pl.kchunk = 0;
+  const int full = pl.tiles / 256 * 256, tail = pl.tiles - full;
+  if (tail == 0) return pl;
+  int best = 1;
+  double best_cost = 1.0;
+  for (int s = 2; s <= 8 && N / s >= 1024; ++s) {
+    const double cost = std::ceil(tail * (double)s / 256.0) / s;
+    if (cost < best_cost - 1e-9) { best = s; best_cost = cost; }
+  }
+  if (best == 1 || best_cost > 0.75) return pl;
+  pl.full = full;
+  pl.split = best;
+  pl.kchunk = ((N + best - 1) / best + 127) / 128 * 128;
+  return pl;
+}
 
 hipError_t launch_head_fwd(const HeadParams& p, hipStream_t st) {
   const int tiles = head_vocab_tiles(p.V) * (p.Npad / HT_N);
@@ -707,7 +793,17 @@ hipError_t launch_head_bwd(const HeadParams& p, hipStream_t st) {
     KTimer t("head_dh_reduce", st);
     hipLaunchKernelGGL(head_dh_reduce_kernel, dim3(blocks), dim3(256), 0, st, p);
   }
-  { KTimer t("head_de", st); hipLaunchKernelGGL(head_de_kernel, dim3(head_vocab_tiles(p.V) * dtiles), dim3(NT), 0, st, p); }
+  const int de_tiles = head_vocab_tiles(p.V) * dtiles;
+  if (p.de_split > 1 && p.de_part) {
+    const int tail = de_tiles - p.de_full;
+    { KTimer t("head_de", st); hipLaunchKernelGGL(head_de_kernel, dim3(p.de_full + tail * p.de_split), dim3(NT), 0, st, p); }
+    { KTimer t("head_de_tail", st); hipLaunchKernelGGL(head_de_tail_kernel, dim3(tail, HT_M / 32), dim3(256), 0, st, p); }
+  } else {
+    HeadParams q = p;
+    q.de_full = de_tiles;
+    q.de_split = 1;
+    { KTimer t("head_de", st); hipLaunchKernelGGL(head_de_kernel, dim3(de_tiles), dim3(NT), 0, st, q); }
+  }
   return hipGetLastError();
 }
 

@@ -40,6 +40,11 @@ struct HeadParams {
   int dh_kchunk;        // vocabulary entries per split (a multiple of 128)
   void* dE;             // (V, d) bf16 or f32
   int dE_f32;
+  // dE tiles past the last complete round of workgroups, split over the tokens (head_de_plan):
+  float* de_part = nullptr;  // (tiles - de_full) * de_split f32 tiles of HT_M x HT_N, or nullptr
+  int de_full = 0;      // tiles computed whole (all of them when de_split is 1)
+  int de_split = 1;     // token ranges per remaining tile
+  int de_kchunk = 0;    // tokens per range (a multiple of 128)
   float* pmax;          // eval: (ceil(V/HT_M), N) per-vocab-tile maximum logit
   int* pidx;            // eval: (ceil(V/HT_M), N) its vocabulary index
   float* logprob;       // eval: (N,) log p(target)

@@ -26,6 +26,10 @@ int head_vocab_pitch(int V);
 int head_stat_blocks(int N);
 int head_dh_split(int N, int d, int V);
 int head_dh_kchunk(int V, int split);
+struct HeadDePlan {
+  int tiles, full, split, kchunk;
+};
+HeadDePlan head_de_plan(int N, int d, int V);
 hipError_t launch_head_fwd(const HeadParams& p, hipStream_t st);
 hipError_t launch_head_bwd(const HeadParams& p, hipStream_t st);
 hipError_t launch_head_eval(const HeadParams& p, hipStream_t st);

@@ -142,3 +142,31 @@ def test_residual_block_every_entry(N, d, V, n, c):
         assert len(bad) == 0, f"call {call}: {len(bad)} wrong entries, first {bad[:4].tolist()}"
         l_k = res[(Npad * Vp * 2 + 255) // 256 * 256:].view(torch.float32)[:N].cpu().numpy()
         np.testing.assert_allclose(l_k, l, rtol=1e-4)
+
+
+SPLIT_SHAPE = (2176, 264, 70000)
+
+
+@pytest.fixture(scope="module")
+def split_case():
+    N, d, V = SPLIT_SHAPE
+    h, E, t = head_inputs(N, d, V, seed=12, e_std=0.15)
+    obj_r, _ = OH.dense_forward(h, E, t, n=8, c=2.0)
+    dh_r, dE_r = OH.dense_backward(h, E, t, 1.0, n=8, c=2.0)
+    return h, E, t, obj_r, dh_r, dE_r
+
+
+@pytest.mark.parametrize("e_dtype", [torch.bfloat16, torch.float32], ids=["bf16E", "f32E"])
+def test_head_de_token_split_tail(e_dtype, schedule, split_case):
+    """dE tiles past the last complete round of 256 workgroups are split over the tokens and
+    summed by a second kernel (here 274 x 2 = 548 tiles: 512 whole, the 36 tiles of vocabulary
+    rows >= 65536 in two unequal ranges of 1152 and 1024 tokens; d = 264 leaves a ragged
+    column tile). Gradients against the float64 dense oracle, the split rows also on
+    their own, so a lost or doubled token range cannot hide in the whole-matrix norm."""
+    h, E, t, obj_r, dh_r, dE_r = split_case
+    obj, pt, dh, dE = run_hip(h, E, t, n=8, c=2.0, e_dtype=e_dtype)
+    np.testing.assert_allclose(obj, obj_r, rtol=2e-3, atol=2e-4)
+    assert rel_l2(dh, dh_r) < 1e-2
+    assert rel_l2(dE, dE_r) < 1e-2
+    assert rel_l2(dE[65536:], dE_r[65536:]) < 1e-2
+    assert rel_l2(dE[65536:, 256:], dE_r[65536:, 256:]) < 1e-2
