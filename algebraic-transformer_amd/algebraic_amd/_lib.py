@@ -20,6 +20,7 @@ _P = ctypes.c_void_p
 _I = ctypes.c_int
 _F = ctypes.c_float
 _S = ctypes.c_size_t
+_L = ctypes.c_long
 
 _SIGNATURES = {
     "alg_last_error": (ctypes.c_char_p, []),
@@ -47,6 +48,8 @@ _SIGNATURES = {
     "alg_rms_norm_workspace_size": (_S, [_I, _I]),
     "alg_ffn_alu_glu_fwd": (_I, [_P, _I, _I, _I, _P, _P, _F, _P, _P, _P]),
     "alg_ffn_alu_glu_dy": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _F, _P]),
+    "alg_ffn_gemm_workspace_size": (_S, [_I, _I, _I]),
+    "alg_ffn_gemm": (_I, [_P, _I, _I, _I, _P, _L, _I, _P, _L, _I, _P, _L, _P, _S]),
     "alg_rms_norm_fwd": (_I, [_P, _I, _I, _P, _P, _F, _P, _P]),
     "alg_rms_norm_bwd": (_I, [_P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _S]),
     "alg_timer_enable": (None, [_I]),

@@ -6,9 +6,10 @@ src/algebraic/algebraic.py:86-113), differentiable in h2 and the three weights. 
 product over the concatenated weights [w_g | w_u] carries the activation in its epilogue (one
 HIP kernel writes y = gate*alu(up) and the gate/up residuals); in the backward, the product
 dout @ w_d^T carries the activation's VJP in its epilogue (one HIP kernel writes
-[d_gate | d_up]). The four remaining products are plain GEMMs (hipBLASLt through torch),
-each one call: y @ w_d, [d_gate | d_up] @ [w_g | w_u]^T, h2^T @ [d_gate | d_up], y^T @ dout.
-bf16 only; d_ff must be a multiple of 128. No CPU fallback for the fused parts.
+[d_gate | d_up]). The four remaining products are plain GEMMs on the same MFMA core
+(``alg_ffn_gemm``), each operand read in its stored layout (no transposed copies): y @ w_d,
+[d_gate | d_up] @ [w_g | w_u]^T, h2^T @ [d_gate | d_up], y^T @ dout. bf16 only; d_ff must be a
+multiple of 128 and the widths multiples of 8. No CPU fallback.
 """
 
 import torch
@@ -16,9 +17,19 @@ import torch
 from .. import _lib
 
 
-def _t(x):
-    """Contiguous transpose (products never take a transposed view)."""
-    return x.t().contiguous()
+def _gemm(a, b, a_trans=False, b_trans=False):
+    """C = op(A) op(B) in bf16 (f32 accumulation) through alg_ffn_gemm. ``a`` is stored (M, K),
+    or (K, M) with ``a_trans``; ``b`` is stored (K, N), or (N, K) with ``b_trans``; both
+    contiguous row-major."""
+    lib = _lib.load()
+    M, K = (a.shape[1], a.shape[0]) if a_trans else a.shape
+    N = b.shape[0] if b_trans else b.shape[1]
+    c = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
+    ws_b = lib.alg_ffn_gemm_workspace_size(M, N, K)
+    ws = torch.empty(max(ws_b, 1), dtype=torch.uint8, device=a.device)
+    _lib.check(lib.alg_ffn_gemm(_lib.stream_of(a), M, N, K, _lib.ptr(a), a.shape[1], int(a_trans), _lib.ptr(b),
+                                b.shape[1], int(b_trans), _lib.ptr(c), N, _lib.ptr(ws), ws_b), "alu_glu_ffn product")
+    return c
 
 
 class _FfnFn(torch.autograd.Function):
@@ -34,7 +45,7 @@ class _FfnFn(torch.autograd.Function):
         y, gate, up = (torch.empty((N, F), dtype=torch.bfloat16, device=x.device) for _ in range(3))
         _lib.check(lib.alg_ffn_alu_glu_fwd(_lib.stream_of(x), N, d, F, _lib.ptr(x), _lib.ptr(w_gu), float(beta),
                                            _lib.ptr(y), _lib.ptr(gate), _lib.ptr(up)), "alu_glu_ffn")
-        out = torch.matmul(y, wd)
+        out = _gemm(y, wd)
         ctx.save_for_backward(x, w_gu, wd, y, gate, up)
         ctx.meta = (shape, beta, w_g.dtype, w_u.dtype, w_d.dtype)
         return out.reshape(*shape[:-1], wd.shape[1])
@@ -50,9 +61,9 @@ class _FfnFn(torch.autograd.Function):
         d_gu = torch.empty((N, 2 * F), dtype=torch.bfloat16, device=x.device)
         _lib.check(lib.alg_ffn_alu_glu_dy(_lib.stream_of(x), N, dm, F, _lib.ptr(do), _lib.ptr(wd), _lib.ptr(gate),
                                           _lib.ptr(up), float(beta), _lib.ptr(d_gu)), "alu_glu_ffn backward")
-        dh2 = torch.matmul(d_gu, _t(w_gu)).reshape(shape)
-        dw_gu = torch.matmul(_t(x), d_gu)
-        dw_d = torch.matmul(_t(y), do)
+        dh2 = _gemm(d_gu, w_gu, b_trans=True).reshape(shape)
+        dw_gu = _gemm(x, d_gu, a_trans=True)
+        dw_d = _gemm(y, do, a_trans=True)
         return dh2, dw_gu[:, :F].to(tg), dw_gu[:, F:].to(tu), dw_d.to(td), None
 
 

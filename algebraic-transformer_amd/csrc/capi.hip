@@ -694,6 +694,47 @@ int alg_ffn_alu_glu_dy(alg_stream_t stream, int N, int dm, int F, const void* do
   return hip_status(alg::launch_ffn_dy(p, (hipStream_t)stream), "alg_ffn_alu_glu_dy");
 }
 
+size_t alg_ffn_gemm_workspace_size(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return alg::ffn_gemm_workspace_bytes(alg::ffn_gemm_plan(M, N, K));
+}
+
+int alg_ffn_gemm(alg_stream_t stream, int M, int N, int K, const void* A, long lda, int a_trans, const void* B,
+                 long ldb, int b_trans, void* C, long ldc, void* workspace, size_t workspace_bytes) {
+  if (M <= 0 || N <= 0 || K <= 0) return fail(ALG_ERR_INVALID, "M, N, K must be positive (got %d, %d, %d)", M, N, K);
+  if (!A || !B || !C) return fail(ALG_ERR_INVALID, "null argument");
+  if (!aligned16({A, B, C})) return fail(ALG_ERR_INVALID, "A, B and C must be 16-byte aligned");
+  // Stored row lengths: A (M, K) or (K, M); B (K, N) or (N, K).
+  const int a_cols = a_trans ? M : K, a_rows = a_trans ? K : M;
+  const int b_cols = b_trans ? K : N, b_rows = b_trans ? N : K;
+  if (a_cols % 8 || b_cols % 8 || N % 8)
+    return fail(ALG_ERR_INVALID, "stored row lengths (%d, %d) and N = %d must be multiples of 8", a_cols, b_cols, N);
+  if (lda < a_cols || ldb < b_cols || ldc < N || lda % 8 || ldb % 8 || ldc % 8)
+    return fail(ALG_ERR_INVALID, "leading dimensions (%ld, %ld, %ld) must cover the rows and be multiples of 8", lda,
+                ldb, ldc);
+  if ((double)(a_rows - 1) * lda + a_cols > 2.0e9 || (double)(b_rows - 1) * ldb + b_cols > 2.0e9 ||
+      (double)(M - 1) * ldc + N > 2.0e9)
+    return fail(ALG_ERR_INVALID, "matrices too large");
+  const alg::FfnGemmPlan pl = alg::ffn_gemm_plan(M, N, K);
+  const size_t need = alg::ffn_gemm_workspace_bytes(pl);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(ALG_ERR_INVALID, "workspace too small: need %zu bytes", need);
+  if (need && !aligned16({workspace})) return fail(ALG_ERR_INVALID, "workspace must be 16-byte aligned");
+  alg::FfnGemmParams g;
+  std::memset(&g, 0, sizeof g);
+  g.A = alg::GemmOperand{static_cast<const bf16*>(A), lda, a_rows, a_cols, (long)(a_rows - 1) * lda + a_cols};
+  g.B = alg::GemmOperand{static_cast<const bf16*>(B), ldb, b_rows, b_cols, (long)(b_rows - 1) * ldb + b_cols};
+  g.C = static_cast<bf16*>(C);
+  g.ldc = ldc;
+  g.M = M; g.N = N; g.K = K;
+  g.full = pl.full; g.split = pl.split; g.kchunk = pl.kchunk;
+  g.part = need ? static_cast<float*>(workspace) : nullptr;
+  // A stored (M, K) is k-contiguous; B stored (N, K) is k-contiguous.
+  return hip_status(alg::launch_ffn_gemm(g, a_trans ? alg::MNMAJOR : alg::KMAJOR, b_trans ? alg::KMAJOR : alg::MNMAJOR,
+                                         (hipStream_t)stream),
+                    "alg_ffn_gemm");
+}
+
 int alg_head_eval(alg_stream_t stream, int dtype, int N, int d, int V, const void* h, const void* E,
                   const int32_t* targets, int n, float c, float* logprob, int32_t* argmax, void* workspace,
                   size_t workspace_bytes) {

@@ -77,6 +77,18 @@ struct FfnParams {
   float beta;
 };
 
+// Plain bf16 products of the feed-forward block: C (M, N) row-major = A B, f32 accumulation.
+struct FfnGemmParams {
+  GemmOperand A, B;     // A: M x K, B: K x N, each k- or m/n-contiguous as stored
+  bf16* C;              // (M, ldc)
+  long ldc;
+  int M, N, K;
+  float* part;          // f32 tiles of the split tiles (ffn_gemm_plan), or nullptr
+  int full;             // tiles computed whole
+  int split;            // k ranges per remaining tile
+  int kchunk;           // k per range (a multiple of 128)
+};
+
 // Row RMS norm with gain (the final norm before the head, model.py:208).
 struct RmsNormParams {
   const bf16* x;        // (rows, d)

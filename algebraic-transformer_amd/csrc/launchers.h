@@ -46,6 +46,12 @@ int rms_norm_blocks(int rows);
 hipError_t launch_rms_norm_fwd(const RmsNormParams& p, hipStream_t st);
 hipError_t launch_ffn_fwd(const FfnParams& p, hipStream_t st);
 hipError_t launch_ffn_dy(const FfnParams& p, hipStream_t st);
+struct FfnGemmPlan {
+  int tiles, full, split, kchunk;
+};
+FfnGemmPlan ffn_gemm_plan(int M, int N, int K);
+size_t ffn_gemm_workspace_bytes(const FfnGemmPlan& pl);
+hipError_t launch_ffn_gemm(const FfnGemmParams& g, int a_mode, int b_mode, hipStream_t st);
 hipError_t launch_rms_norm_bwd(const RmsNormParams& p, float* dgain, hipStream_t st);
 
 }  // namespace alg

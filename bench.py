@@ -413,7 +413,7 @@ def time_ffn(torch, dev, iters=10, warmup=2, seed=3):
     k_fwd, k_dy = k["ffn_gate_up"], k["ffn_dy"]
     t_f, t_p = median_ms(fused), median_ms(plain)
     fl_gu, fl_dy = 2.0 * N * d * 2 * F, 2.0 * N * d * F
-    block = 6 * 2.0 * N * d * F + 2 * 2.0 * N * d * F  # 3 products forward (gate, up, out), 6 backward
+    block = 9 * 2.0 * N * d * F  # 3 products of 2 N d F forward (gate, up, out), 6 backward
     return {"workload": "ALU-GLU FFN, 1b shape N16384 d1536 d_ff4224 bf16",
             "gate_up_ms": round(k_fwd, 4), "gate_up_tflops": round(fl_gu / (k_fwd * 1e-3) / 1e12, 1),
             "dy_ms": round(k_dy, 4), "dy_tflops": round(fl_dy / (k_dy * 1e-3) / 1e12, 1),

@@ -237,6 +237,20 @@ int alg_ffn_alu_glu_fwd(alg_stream_t stream, int N, int d, int F, const void* h2
 int alg_ffn_alu_glu_dy(alg_stream_t stream, int N, int dm, int F, const void* dout, const void* w_d,
                        const void* gate, const void* up, float beta, void* d_gu);
 
+/* The block's plain products (the matmuls of model.py:185-193 that carry no activation: y w_d,
+ * d_gu w_gu^T, h2^T d_gu, y^T dout; the reference leaves them to XLA): C (M, N) = A B in bf16,
+ * one rounding of the f32 sum, C row-major with leading dimension ldc. A is (M, K) stored
+ * row-major (a_trans = 0, lda >= K) or stored as its transpose, (K, M) row-major (a_trans = 1,
+ * lda >= M); B is (K, N) stored row-major (b_trans = 0, ldb >= N) or as its transpose (N, K)
+ * (b_trans = 1, ldb >= K). The stored rows' lengths (K, M or N as the layouts give), N and the
+ * leading dimensions are multiples of 8 and A, B, C 16-byte aligned (ALG_ERR_INVALID
+ * otherwise). When the last round of output tiles would leave CUs idle those tiles are split
+ * over k into f32 workspace tiles summed in a fixed order: the workspace holds
+ * alg_ffn_gemm_workspace_size(M, N, K) bytes (0 when there is no split). */
+size_t alg_ffn_gemm_workspace_size(int M, int N, int K);
+int alg_ffn_gemm(alg_stream_t stream, int M, int N, int K, const void* A, long lda, int a_trans, const void* B,
+                 long ldb, int b_trans, void* C, long ldc, void* workspace, size_t workspace_bytes);
+
 /* Head backward, fused_head.py:120-156, 194-216, 247-254:
  * in h, E (of dtype ALG_DTYPE_BF16 or ALG_DTYPE_F32), targets, stat, g (1) f32 on the device
  * (cotangent of obj) and optionally the forward's residual (bf16 only); out dh (N,d) in h's

@@ -192,6 +192,26 @@ def test_neighbour_entry_points_validate_before_launch():
     assert rc == _lib.ALG_ERR_INVALID and b"aligned" in err()
     rc = handle.alg_ffn_alu_glu_dy(None, 256, 128, 256, P(16), P(16), P(16), P(16), 0.5, P(20))
     assert rc == _lib.ALG_ERR_INVALID and b"aligned" in err()
+    # Plain feed-forward products: row lengths and leading dimensions, workspace of a split plan.
+    rc = handle.alg_ffn_gemm(None, 256, 100, 512, P(16), 512, 0, P(16), 104, 0, P(16), 104, None, 0)
+    assert rc == _lib.ALG_ERR_INVALID and b"multiples of 8" in err()
+    rc = handle.alg_ffn_gemm(None, 300, 256, 512, P(16), 512, 1, P(16), 256, 0, P(16), 256, None, 0)
+    assert rc == _lib.ALG_ERR_INVALID and b"multiples of 8" in err()  # A stored (K, M): M = 300
+    rc = handle.alg_ffn_gemm(None, 256, 256, 512, P(16), 256, 0, P(16), 256, 0, P(16), 256, None, 0)
+    assert rc == _lib.ALG_ERR_INVALID and b"leading" in err()  # lda < K
+    rc = handle.alg_ffn_gemm(None, 256, 256, 512, P(16), 512, 0, P(24), 256, 0, P(16), 256, None, 0)
+    assert rc == _lib.ALG_ERR_INVALID and b"aligned" in err()
+    assert handle.alg_ffn_gemm_workspace_size(256, 256, 512) == 0       # one tile, short k: no split
+    need = handle.alg_ffn_gemm_workspace_size(296, 264, 5000)           # 4 tiles, k split 4 ways
+    assert need == 4 * 4 * 256 * 256 * 4
+    rc = handle.alg_ffn_gemm(None, 296, 264, 5000, P(16), 5000, 0, P(16), 264, 0, P(16), 264, P(16), need - 1)
+    assert rc == _lib.ALG_ERR_INVALID and b"workspace" in err()
+    # The 1b block's products: y w_d and d_gu w_gu^T split their last 128 of 384 tiles in two,
+    # h2^T d_gu (198 tiles) is not split, y^T dout (102 tiles) is split five ways.
+    assert handle.alg_ffn_gemm_workspace_size(16384, 1536, 4224) == 128 * 2 * 256 * 256 * 4
+    assert handle.alg_ffn_gemm_workspace_size(16384, 1536, 8448) == 128 * 2 * 256 * 256 * 4
+    assert handle.alg_ffn_gemm_workspace_size(1536, 8448, 16384) == 0
+    assert handle.alg_ffn_gemm_workspace_size(4224, 1536, 16384) == 102 * 5 * 256 * 256 * 4
 
 
 def test_noalloc_backward_rejects_scratch_beyond_its_limit():
