@@ -905,8 +905,14 @@ __global__ __launch_bounds__(256, bwd_bf16_waves_per_simd<D>()) void attn_bwd_bf
 // di = sum_j p_ij dP_ij from a first pass over the keys with the same f32 weights p and
 // products dP that its score gradients use, so that sum_j p_ij (dP_ij - di_i) vanishes to
 // f32 rounding however the weights are spread. In exact arithmetic both are <dO_i, o_i>.
+// Waves per SIMD the dQ kernel is built for: at D = 64 the in-range kernel with n fixed at
+// compile time fits 168 VGPRs (16 bytes spilled) and runs three (C3 dQ 0.158 -> 0.152 ms,
+// measured A/B on one box); the other variants spill far more at that bound and keep two.
+template <int D, int MODE, int L2N>
+constexpr int dq_waves_per_simd() { return D == 64 && MODE == MODE_INRANGE && L2N > 0 ? 3 : 2; }
+
 template <int D, int MODE, int L2N, int LAYOUT>
-__global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnBwdParams p) {
+__global__ __launch_bounds__(256, (dq_waves_per_simd<D, MODE, L2N>())) void attn_bwd_dq_kernel(AttnBwdParams p) {
   static_assert(D == 64 || D == 128, "head_dim");
   constexpr int BK = 64, CPR = D / 8, NDB = D / 32, NF = D / 16;
   constexpr int PW = 64 * CPR / 64 / 4;  // copy instruction pairs per wave and tile
