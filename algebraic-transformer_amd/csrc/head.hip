@@ -321,8 +321,8 @@ __device__ __forceinline__ float sum_tiles(const float* part, int N, int tok, in
 // 64 tokens per workgroup (lane = token, so each tile row is read as 256 contiguous bytes);
 // the EVQ waves take consecutive ranges of the tiles, and their argmax candidates and partial
 // sums are combined in range order through LDS. One token per thread over all the tiles left
-// three quarters of the SIMDs idle at N = 16384: 48 us (kernel trace) against 27 us with four
-// ranges and 24 us with eight (HIP events, which add a few us to short kernels).
+// three quarters of the SIMDs idle at N = 16384: 48 us against 20.5 us with eight ranges in a
+// kernel trace (HIP events: 27 us with four ranges, 24 us with eight).
 constexpr int EVQ = 8;  // tile ranges (waves) per token
 __global__ __launch_bounds__(64 * EVQ) void head_eval_stats_kernel(HeadParams p, int nvt) {
   __shared__ float sm[EVQ][64];

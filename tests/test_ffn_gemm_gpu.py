@@ -67,3 +67,26 @@ def test_ffn_gemm_whole_round_then_split_tail():
     err = (outs[0].float() - ref).abs()
     bad = (err > ref.abs() * 2.0 ** -8 + slack * 2.0 ** -20) | outs[0].float().isnan()
     assert not bool(bad.any()), f"{int(bad.sum())} entries off, first {bad.nonzero()[:4].tolist()}"
+
+
+def test_ffn_gemm_1b_block_products():
+    """The 1b block's four plain products at full size (N 16384, d 1536, d_ff 4224), in their
+    stored layouts and split plans: y w_d and d_gu w_gu^T (256 whole tiles, 128 split in two),
+    h2^T d_gu (198 tiles, unsplit), y^T dout (102 tiles, split five ways)."""
+    N, d, F = 16384, 1536, 4224
+    g = torch.Generator(device="cuda").manual_seed(11)
+    rn = lambda *s: torch.randn(*s, device="cuda", generator=g).to(torch.bfloat16)
+    y, wd, dgu, wgu, x, do = rn(N, F), rn(F, d), rn(N, 2 * F), rn(d, 2 * F), rn(N, d), rn(N, d)
+    cases = {"y w_d": (y, wd, False, False, y, wd), "d_gu w_gu^T": (dgu, wgu, False, True, dgu, wgu.t()),
+             "h2^T d_gu": (x, dgu, True, False, x.t(), dgu), "y^T dout": (y, do, True, False, y.t(), do)}
+    for name, (a, b, at, bt, A, B) in cases.items():
+        M, K = A.shape
+        Nc = B.shape[1]
+        print(f"[ffn_gemm] {name}: M={M} N={Nc} K={K}", flush=True)
+        outs, _ = _run(a, b, at, bt, M, Nc, K, calls=1)
+        Af, Bf = A.float(), B.float()
+        ref = Af @ Bf
+        tol = ref.abs() * 2.0 ** -8 + (Af.abs() @ Bf.abs()) * 2.0 ** -20
+        bad = ((outs[0].float() - ref).abs() > tol) | outs[0].float().isnan()
+        assert not bool(bad.any()), f"{name}: {int(bad.sum())} entries off, first {bad.nonzero()[:4].tolist()}"
+        del ref, tol, bad, outs
