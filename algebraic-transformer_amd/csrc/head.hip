@@ -292,24 +292,10 @@ __global__ __launch_bounds__(NT, 1) void head_eval_kernel(HeadParams p) {
 }
 
 // The per-token reductions over vocabulary tiles below read one value per tile (stride N) and
-// combine them in tile order; the loads are issued TB at a time so their latencies overlap,
-// while the order of the combining steps (and so every result bit) stays that of a plain loop.
+// combine them in tile order within each wave's range of tiles; the loads are issued TB at a
+// time so their latencies overlap, while the order of the combining steps stays that of a
+// plain loop.
 constexpr int TB = 16;
-
-// sum over t in [0, nvt) of part[t * N + tok], added in increasing t.
-__device__ __forceinline__ float sum_tiles(const float* part, int N, int tok, int nvt) {
-  float l = 0.0f;
-  int t = 0;
-  for (; t + TB <= nvt; t += TB) {
-    float v[TB];
-#pragma unroll
-    for (int u = 0; u < TB; ++u) v[u] = part[(size_t)(t + u) * N + tok];
-#pragma unroll
-    for (int u = 0; u < TB; ++u) l += v[u];
-  }
-  for (; t < nvt; ++t) l += part[(size_t)t * N + tok];
-  return l;
-}
 
 // log p(target) = log_softmax(n asinh(z/c))[t] (src/algebraic/evaluation.py:13-23) from the
 // tiles' (largest logit, shifted sum) pairs: with z_m the largest logit of the row and
@@ -397,12 +383,34 @@ __global__ __launch_bounds__(64 * EVQ) void head_eval_stats_kernel(HeadParams p,
 
 // Per-token statistics and telemetry (fused_head.py:116-117, 219-229); with the residual
 // schedule also l and the target entries of U.
-__global__ __launch_bounds__(256) void head_stats_kernel(HeadParams p, int nvt) {
-  __shared__ float red[256];
-  const int tok = blockIdx.x * 256 + threadIdx.x;
+// 64 tokens per workgroup, the vocabulary tiles split over EVQ waves as in the eval statistics:
+// each wave sums its range in tile order, the ranges are added in range order.
+__global__ __launch_bounds__(64 * EVQ) void head_stats_kernel(HeadParams p, int nvt) {
+  __shared__ float sl[EVQ][64];
+  const int lane = threadIdx.x & 63, q = threadIdx.x >> 6;
+  const int tok = blockIdx.x * 64 + lane;
+  const int per = (nvt + EVQ - 1) / EVQ;
+  const int t0 = min(nvt, q * per), t1 = min(nvt, t0 + per);
+  float part = 0.0f;
+  if (tok < p.N) {
+    int t = t0;
+    for (; t + TB <= t1; t += TB) {
+      float v[TB];
+#pragma unroll
+      for (int u = 0; u < TB; ++u) v[u] = p.partial[(size_t)(t + u) * p.N + tok];
+#pragma unroll
+      for (int u = 0; u < TB; ++u) part += v[u];
+    }
+    for (; t < t1; ++t) part += p.partial[(size_t)t * p.N + tok];
+  }
+  sl[q][lane] = part;
+  __syncthreads();
+  if (q != 0) return;
   float miss = 0.0f;
   if (tok < p.N) {
-    const float l = sum_tiles(p.partial, p.N, tok, nvt);
+    float l = sl[0][lane];
+#pragma unroll
+    for (int r = 1; r < EVQ; ++r) l += sl[r][lane];
     const int n = 1 << p.log2n;
     const float st = inv_root(l, n);
     p.stat[tok] = st;
@@ -425,13 +433,9 @@ __global__ __launch_bounds__(256) void head_stats_kernel(HeadParams p, int nvt) 
       }
     }
   }
-  red[threadIdx.x] = miss;
-  __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if (threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) p.obj_part[blockIdx.x] = red[0];
+  // This workgroup's sum of 1 - pt, by a fixed butterfly over the wave.
+  for (int m = 32; m >= 1; m >>= 1) miss += __shfl_xor(miss, m, 64);
+  if (lane == 0) p.obj_part[blockIdx.x] = miss;
 }
 
 __global__ __launch_bounds__(256) void head_obj_kernel(HeadParams p, int nblocks) {
@@ -723,7 +727,7 @@ __global__ __launch_bounds__(256) void head_de_tail_kernel(HeadParams p) {
 int head_vocab_tiles(int V) { return (V + HT_M - 1) / HT_M; }
 int head_token_pad(int N) { return ((N + HT_N - 1) / HT_N) * HT_N; }
 int head_vocab_pitch(int V) { return (V + 7) / 8 * 8; }
-int head_stat_blocks(int N) { return (N + 255) / 256; }
+int head_stat_blocks(int N) { return (N + 63) / 64; }
 
 // Vocabulary splits of the dh product: minimise the rounds of 256 workgroups per unit of
 // k work (ceil(tiles*S/256)/S) for products with fewer than two rounds of tiles, keeping at
@@ -781,14 +785,14 @@ hipError_t launch_head_fwd(const HeadParams& p, hipStream_t st) {
 // vocab_tiles partial rows of N).
 hipError_t launch_head_stats(const HeadParams& p, int vocab_tiles, hipStream_t st) {
   const int nb = head_stat_blocks(p.N);
-  { KTimer t("head_stats", st); hipLaunchKernelGGL(head_stats_kernel, dim3(nb), dim3(256), 0, st, p, vocab_tiles); }
+  { KTimer t("head_stats", st); hipLaunchKernelGGL(head_stats_kernel, dim3(nb), dim3(64 * EVQ), 0, st, p, vocab_tiles); }
   { KTimer t("head_obj", st); hipLaunchKernelGGL(head_obj_kernel, dim3(1), dim3(256), 0, st, p, nb); }
   return hipGetLastError();
 }
 
 hipError_t launch_head_eval_stats(const HeadParams& p, int vocab_tiles, hipStream_t st) {
   KTimer t("head_eval_stats", st);
-  hipLaunchKernelGGL(head_eval_stats_kernel, dim3((p.N + 63) / 64), dim3(64 * EVQ), 0, st, p, vocab_tiles);
+  hipLaunchKernelGGL(head_eval_stats_kernel, dim3(head_stat_blocks(p.N)), dim3(64 * EVQ), 0, st, p, vocab_tiles);
   return hipGetLastError();
 }
 
