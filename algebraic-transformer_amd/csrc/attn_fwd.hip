@@ -314,7 +314,13 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnFwdParams p) {
 // 4 / QG. The row sum is accumulated in KS parts and added at the end, an order of f32
 // additions of its own (the mathematics is that of attn_fwd_kernel's in-range branch).
 constexpr int F32S_BK = 32;  // keys per tile
-template <int QG, int L2N>
+__device__ __forceinline__ float guard_max(float a, float b);
+// FROM_Q: the guarded forward's first launch (as attn_fwd_bf16_kernel's): q holds the raw
+// queries; the kernel forms q_s = q * alpha in its query fragments, writes it, and leaves its
+// workgroup's guard maxima (its queries' ||q_s||^2, and ||k||^2 and |v| of the key rows at its
+// own query positions) with the row sums in the prep kernel's order, so the guard decides
+// exactly as after alg_attn_prepare.
+template <int QG, int L2N, bool FROM_Q>
 __global__ __launch_bounds__(256, 2) void attn_fwd_f32_split_kernel(AttnFwdParams p) {
   static_assert(QG == 1 || QG == 2, "query groups per workgroup");
   constexpr int KS = 4 / QG, BQ = 32 * QG;
@@ -347,6 +353,18 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_f32_split_kernel(AttnFwdParam
   for (int s = 0; s < NQF; ++s) {
     const floatx4 z = {};
     qf[s] = myq < T_ ? *reinterpret_cast<const floatx4*>(Q + (size_t)myq * ld + 8 * s + 4 * h) : z;
+  }
+  if constexpr (FROM_Q) {  // q_s = q * alpha (flash.py:833; an f32 product for f32 inputs)
+    const float alpha = p.alpha;
+#pragma unroll
+    for (int s = 0; s < NQF; ++s)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) qf[s][u] = qf[s][u] * alpha;
+    if (part == 0 && myq < T_) {
+      float* Qs = reinterpret_cast<float*>(p.q_s_out) + hb + (size_t)myq * ld;
+#pragma unroll
+      for (int s = 0; s < NQF; ++s) *reinterpret_cast<floatx4*>(Qs + 8 * s + 4 * h) = qf[s];
+    }
   }
   const int log2n = p.log2n;
   floatx16 oacc[NDB];
@@ -438,6 +456,69 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_f32_split_kernel(AttnFwdParam
     __syncthreads();  // every wave is done with the tiles before the next step stores
   }
 
+  if constexpr (FROM_Q) {
+    __shared__ float gred[4][3];
+    // ||q_s||^2: chunk 2s + h (4 columns) of row myq is qf[s] on lane half h; each chunk is
+    // summed in column order, chunks 2s and 2s + 1 meet across the halves, and the pair sums
+    // combine in the prep kernel's butterfly order. Only part 0's waves hold distinct rows.
+    float ps[NQF];
+#pragma unroll
+    for (int s = 0; s < NQF; ++s) {
+      floatx4 qv = qf[s];
+      asm volatile("" : "+v"(qv));  // formed here, not carried through the main loop
+      float c = 0.0f;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) c += qv[u] * qv[u];
+      ps[s] = c + __shfl_xor(c, 32, 64);
+    }
+#pragma unroll
+    for (int w = 1; w < NQF; w <<= 1)
+#pragma unroll
+      for (int s = 0; s < NQF; s += 2 * w) ps[s] = ps[s] + ps[s + w];
+    float mq = part == 0 && myq < T_ ? ps[0] : 0.0f;
+    // ||k||^2 and |v| of the key rows at this workgroup's query positions (every row of the
+    // head once over the launch): 16 lanes per row, lane li holding columns 4 li .. 4 li + 3.
+    float mk = 0.0f, mv = 0.0f;
+    {
+      const int li = threadIdx.x & 15, rsub = threadIdx.x >> 4;
+#pragma unroll
+      for (int r = 0; r < BQ; r += 16) {
+        const int key = qb * BQ + r + rsub;
+        float sk = 0.0f;
+        if (key < T_) {
+          const floatx4 kv = *reinterpret_cast<const floatx4*>(K + (size_t)key * ld + 4 * li);
+          const floatx4 vv = *reinterpret_cast<const floatx4*>(V + (size_t)key * ld + 4 * li);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            sk += kv[u] * kv[u];
+            mv = guard_max(mv, __builtin_fabsf(vv[u]));
+          }
+        }
+#pragma unroll
+        for (int m = 1; m < 16; m <<= 1) sk += __shfl_xor(sk, m, 64);
+        mk = guard_max(mk, sk);
+      }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+      mq = guard_max(mq, __shfl_xor(mq, m, 64));
+      mk = guard_max(mk, __shfl_xor(mk, m, 64));
+      mv = guard_max(mv, __shfl_xor(mv, m, 64));
+    }
+    if (lane == 0) {
+      gred[wave][0] = mq;
+      gred[wave][1] = mk;
+      gred[wave][2] = mv;
+    }
+    __syncthreads();
+    if (threadIdx.x < 3) {
+      float m = gred[0][threadIdx.x];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) m = guard_max(m, gred[w][threadIdx.x]);
+      p.guard_part[3 * ((size_t)bh * gridDim.y + blockIdx.y) + threadIdx.x] = m;
+    }
+  }
+
   // Parts 1.. hand their O^T partials and row sums to part 0 through LDS (the tiles are free
   // after the loop's last barrier): RS floats per lane, an odd stride (no bank conflicts).
   constexpr int RS = 16 * NDB + 1;
@@ -465,7 +546,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_f32_split_kernel(AttnFwdParam
 
   // Finalize (flash.py:271-284): Z over both lane halves (+ the sink's weight), stat = 1/Z.
   float Z = lsum + xor32(lsum);
-  if (p.sink) Z += pow2n<L2N>(rho_fast(p.sink[head]), log2n);
+  if constexpr (FROM_Q) {
+    if (p.sink_logit) Z += pow2n<L2N>(rho_fast(p.sink_logit[p.sink_count == 1 ? 0 : head] / p.sink_c), log2n);
+  } else {
+    if (p.sink) Z += pow2n<L2N>(rho_fast(p.sink[head]), log2n);
+  }
   const float inv = 1.0f / Z;
   if (myq < T_) {
     float* O = reinterpret_cast<float*>(p.o) + hb + (size_t)myq * ld;
@@ -802,6 +887,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) 
   }
 }
 
+int attn_fwd_f32_query_block(int B, int H, int T);
+
 template <typename T, int D>
 static hipError_t launch_fwd_mode(const AttnFwdParams& p, int mode, hipStream_t st) {
   dim3 grid(p.B * p.H, ceil_div(p.T, FWD_BQ)), block(256);
@@ -832,14 +919,24 @@ static hipError_t launch_fwd_mode(const AttnFwdParams& p, int mode, hipStream_t 
       } else if constexpr (D == 64) {
         // Four-way key split (32 queries per workgroup) while two-way workgroups would not
         // fill two rounds of the CUs; two-way (64 queries) above that.
-        if (p.B * p.H * ceil_div(p.T, 64) < 512) {
-          const dim3 g32(p.B * p.H, ceil_div(p.T, 32));
-          if (p.log2n == 4) hipLaunchKernelGGL((attn_fwd_f32_split_kernel<1, 4>), g32, block, 0, st, p);
-          else hipLaunchKernelGGL((attn_fwd_f32_split_kernel<1, 0>), g32, block, 0, st, p);
+        const int bq = attn_fwd_f32_query_block(p.B, p.H, p.T);
+        const dim3 gq(p.B * p.H, ceil_div(p.T, bq));
+        if (bq == 32) {
+          if (p.q_s_out) {
+            if (p.log2n == 4) hipLaunchKernelGGL((attn_fwd_f32_split_kernel<1, 4, true>), gq, block, 0, st, p);
+            else hipLaunchKernelGGL((attn_fwd_f32_split_kernel<1, 0, true>), gq, block, 0, st, p);
+          } else {
+            if (p.log2n == 4) hipLaunchKernelGGL((attn_fwd_f32_split_kernel<1, 4, false>), gq, block, 0, st, p);
+            else hipLaunchKernelGGL((attn_fwd_f32_split_kernel<1, 0, false>), gq, block, 0, st, p);
+          }
         } else {
-          const dim3 g64(p.B * p.H, ceil_div(p.T, 64));
-          if (p.log2n == 4) hipLaunchKernelGGL((attn_fwd_f32_split_kernel<2, 4>), g64, block, 0, st, p);
-          else hipLaunchKernelGGL((attn_fwd_f32_split_kernel<2, 0>), g64, block, 0, st, p);
+          if (p.q_s_out) {
+            if (p.log2n == 4) hipLaunchKernelGGL((attn_fwd_f32_split_kernel<2, 4, true>), gq, block, 0, st, p);
+            else hipLaunchKernelGGL((attn_fwd_f32_split_kernel<2, 0, true>), gq, block, 0, st, p);
+          } else {
+            if (p.log2n == 4) hipLaunchKernelGGL((attn_fwd_f32_split_kernel<2, 4, false>), gq, block, 0, st, p);
+            else hipLaunchKernelGGL((attn_fwd_f32_split_kernel<2, 0, false>), gq, block, 0, st, p);
+          }
         }
       } else {
         if (p.log2n == 4) hipLaunchKernelGGL((attn_fwd_kernel<T, D, MODE_INRANGE, 4>), grid, block, 0, st, p);
@@ -858,6 +955,10 @@ static hipError_t launch_fwd_mode(const AttnFwdParams& p, int mode, hipStream_t 
   }
   return hipGetLastError();
 }
+
+// Queries per workgroup of the f32 D = 64 forward: 32 (four-way key split) while 64-query
+// workgroups would not fill two rounds of the CUs, 64 (two-way) above that.
+int attn_fwd_f32_query_block(int B, int H, int T) { return B * H * ceil_div(T, 64) < 512 ? 32 : 64; }
 
 hipError_t launch_attn_fwd(const AttnFwdParams& p, int D, bool bf16_io, int mode, hipStream_t st) {
   if (bf16_io) {

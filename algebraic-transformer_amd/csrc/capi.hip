@@ -96,6 +96,10 @@ int check_n(int n) {
 // (one per 128-query workgroup)], and for f32 inputs then [dq accumulator f32 B*H*T*D] (the
 // bf16 dQ kernel needs none).
 size_t attn_fwd_workgroups(int B, int H, int T) { return (size_t)B * H * ((T + alg::FWD_BQ - 1) / alg::FWD_BQ); }
+size_t attn_fwd_f32_workgroups(int B, int H, int T) {
+  const int bq = alg::attn_fwd_f32_query_block(B, H, T);
+  return (size_t)B * H * ((T + bq - 1) / bq);
+}
 struct AttnWs {
   size_t sink_part, prep_part, dq_acc, total;
 };
@@ -103,7 +107,10 @@ AttnWs attn_ws(int dtype, int B, int H, int T, int D) {
   AttnWs w;
   w.sink_part = 0;
   w.prep_part = align256((size_t)B * H * alg::attn_bwd_sink_blocks(T) * sizeof(float));
-  w.dq_acc = w.prep_part + align256(3 * std::max<size_t>(1024, attn_fwd_workgroups(B, H, T)) * sizeof(float));
+  // Guard maxima: one triple per forward workgroup (alg_attn_fwd_guarded) or prep workgroup.
+  size_t nwg = std::max<size_t>(1024, attn_fwd_workgroups(B, H, T));
+  if (dtype == ALG_DTYPE_F32 && D == 64) nwg = std::max(nwg, attn_fwd_f32_workgroups(B, H, T));
+  w.dq_acc = w.prep_part + align256(3 * nwg * sizeof(float));
   w.total = w.dq_acc + (dtype == ALG_DTYPE_F32 ? align256((size_t)B * H * T * D * sizeof(float)) : 0);
   return w;
 }
@@ -438,11 +445,14 @@ int alg_attn_fwd_guarded(alg_stream_t stream, int dtype, int layout, int B, int 
   // The guard's clamp (flash.py:747-748); the in-range and shifted kernels do not read it.
   const double t = root_pow2(1e37 / (T + 1.0), n);
   const float clamp = (float)(0.5 * (t - 1.0 / t));
-  if (dtype != ALG_DTYPE_BF16) {
+  const bool bf = dtype == ALG_DTYPE_BF16;
+  if (!bf && D != 64) {  // the f32 D = 128 forward has no FROM_Q form: prepare, then forward
     rc = alg_attn_prepare(stream, dtype, B, H, T, D, q, k, v, sink_logit, sink_count, c, n, 1, q_s, sink_scaled,
                           guard_flag, workspace, workspace_bytes);
     if (rc) return rc;
-    return alg_attn_fwd(stream, dtype, layout, B, H, T, D, q_s, k, v, sink_scaled, n, ALG_ATTN_GUARDED, guard_flag,
+    // sink/c exists only with a sink: a sink_scaled buffer passed without one is not read.
+    return alg_attn_fwd(stream, dtype, layout, B, H, T, D, q_s, k, v, sink_logit ? sink_scaled : nullptr, n,
+                        ALG_ATTN_GUARDED, guard_flag,
                         clamp, 1, 1, o, o_precise, stat);
   }
   hipStream_t st = (hipStream_t)stream;
@@ -458,11 +468,11 @@ int alg_attn_fwd_guarded(alg_stream_t stream, int dtype, int layout, int B, int 
   p.alpha = (float)(1.0 / (std::sqrt((double)D) * (double)c));  // as alg_attn_prepare
   p.guard_part = part;
   p.sink_logit = sink_logit; p.sink_count = sink_count; p.sink_c = c;
-  rc = hip_status(alg::launch_attn_fwd(p, D, true, alg::MODE_INRANGE, st), "alg_attn_fwd_guarded");
+  rc = hip_status(alg::launch_attn_fwd(p, D, bf, alg::MODE_INRANGE, st), "alg_attn_fwd_guarded");
   if (rc) return rc;
   alg::GuardParams g = guard_params(H, T, n, c, sink_logit, sink_count, sink_scaled, guard_flag, 1);
   g.part = part;
-  g.nblocks = (int)attn_fwd_workgroups(B, H, T);
+  g.nblocks = (int)(bf ? attn_fwd_workgroups(B, H, T) : attn_fwd_f32_workgroups(B, H, T));
   rc = hip_status(alg::launch_attn_guard(g, st), "alg_attn_fwd_guarded");
   if (rc) return rc;
   alg::AttnFwdParams ps;
@@ -473,7 +483,7 @@ int alg_attn_fwd_guarded(alg_stream_t stream, int dtype, int layout, int B, int 
   ps.log2n = p.log2n;
   ps.clamp = clamp; ps.fast_rho = 0; ps.inv_stat = 1;  // the fallback uses stable rho (flash.py:851)
   ps.layout = layout;
-  return hip_status(alg::launch_attn_fwd(ps, D, true, alg::MODE_SHIFTED, st), "alg_attn_fwd_guarded");
+  return hip_status(alg::launch_attn_fwd(ps, D, bf, alg::MODE_SHIFTED, st), "alg_attn_fwd_guarded");
 }
 
 int alg_attn_bwd(alg_stream_t stream, int dtype, int layout, int B, int H, int T, int D, const void* q_s,

@@ -7,6 +7,7 @@
 
 namespace alg {
 
+int attn_fwd_f32_query_block(int B, int H, int T);
 hipError_t launch_attn_fwd(const AttnFwdParams& p, int D, bool bf16_io, int mode, hipStream_t st);
 hipError_t launch_attn_bwd(const AttnBwdParams& p, int D, bool bf16_io, const int* modes, int nmodes,
                            hipStream_t st);

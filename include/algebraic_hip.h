@@ -90,11 +90,11 @@ int alg_attn_fwd(alg_stream_t stream, int dtype, int layout, int B, int H, int T
  * (kind="asinh", n <= 32, where the guard applies, flash.py:834): the same outputs as
  * alg_attn_prepare(range_guard = 1) followed by alg_attn_fwd(ALG_ATTN_GUARDED) with the
  * guard's own clamp (q_s, sink_scaled, guard_flag, o, stat; o_precise as in alg_attn_fwd), in
- * one call. For bf16 inputs there is no separate pass over q, k and v: the in-range forward
- * rounds q * alpha itself, writes q_s and leaves the guard maxima of its rows, the guard runs
- * after it, and the shifted branch (flag-checked on the device) replaces o and stat when the
- * guard fails. sink_scaled is written, and required, only with a sink (sink_logit not NULL).
- * f32 inputs take the two calls. */
+ * one call. For bf16 inputs, and f32 inputs at D = 64, there is no separate pass over q, k
+ * and v: the in-range forward forms q * alpha itself, writes q_s and leaves the guard maxima of
+ * its rows, the guard runs after it, and the shifted branch (flag-checked on the device)
+ * replaces o and stat when the guard fails. sink_scaled is written, and required, only with a
+ * sink (sink_logit not NULL). f32 inputs at D = 128 take the two calls. */
 int alg_attn_fwd_guarded(alg_stream_t stream, int dtype, int layout, int B, int H, int T, int D,
                          const void* q, const void* k, const void* v,
                          const float* sink_logit, int sink_count, float c, int n,

@@ -1,7 +1,7 @@
 """GPU check of alg_attn_fwd_guarded, the guarded forward from unscaled queries in one call.
 
-For bf16 inputs the in-range forward kernel rounds q * alpha itself, writes q_s and leaves
-the guard maxima of its rows; the guard runs after it and the flag-checked shifted branch
+For bf16 inputs, and f32 at D = 64, the in-range forward kernel forms q * alpha itself, writes
+q_s and leaves the guard maxima of its rows; the guard runs after it and the flag-checked shifted branch
 replaces o and stat when the guard fails (flash.py:823-856). Through the C ABI (ctypes) every
 output is compared with the two-call sequence alg_attn_prepare(range_guard=1) +
 alg_attn_fwd(GUARDED) on the same inputs: q_s, sink/c, the flag, o and stat bit-identical.
@@ -107,6 +107,7 @@ def _to_dev(a, layout, dtype):
     return t.to(device="cuda", dtype=dtype).contiguous()
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
 @pytest.mark.parametrize("layout", [0, 1])
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("case,sink_kind,shape", [
@@ -119,37 +120,28 @@ def _to_dev(a, layout, dtype):
     ("big_value_first", "none", (2, 2, 320)),
     ("nan_query_mid", "per_head", (2, 2, 256)),
 ])
-def test_one_call_matches_prepare_then_forward(layout, D, case, sink_kind, shape):
+def test_one_call_matches_prepare_then_forward(dtype, layout, D, case, sink_kind, shape):
+    """f32 at D = 64 takes the same one-launch form (the f32 split forward forms q_s and the
+    guard maxima); f32 at D = 128 is prepare + forward inside the call."""
     B, H, T = shape
     L = _lib()
-    dtype = torch.bfloat16
-    q, k, v, sink, nsink = _inputs(B, H, T, D, case, sink_kind, dtype, seed=11 + T)
-    qd, kd, vd = (_to_dev(a, layout, dtype) for a in (q, k, v))
+    tdt, dt, bits = ((torch.bfloat16, L.DTYPE_BF16, torch.int16) if dtype == "bf16"
+                     else (torch.float32, L.DTYPE_F32, torch.int32))
+    q, k, v, sink, nsink = _inputs(B, H, T, D, case, sink_kind, tdt, seed=11 + T)
+    qd, kd, vd = (_to_dev(a, layout, tdt) for a in (q, k, v))
     sd = None if sink is None else torch.from_numpy(np.ascontiguousarray(sink)).float().cuda()
-    print(f"alg_attn_fwd_guarded case={case} sink={sink_kind} B,H,T,D={B},{H},{T},{D} layout={layout}", flush=True)
-    ref = _two_calls(qd, kd, vd, sd, nsink, layout, B, H, T, D, L.DTYPE_BF16)
-    got = _one_call(qd, kd, vd, sd, nsink, layout, B, H, T, D, L.DTYPE_BF16)
+    print(f"alg_attn_fwd_guarded {dtype} case={case} sink={sink_kind} B,H,T,D={B},{H},{T},{D} layout={layout}",
+          flush=True)
+    ref = _two_calls(qd, kd, vd, sd, nsink, layout, B, H, T, D, dt)
+    got = _one_call(qd, kd, vd, sd, nsink, layout, B, H, T, D, dt)
     expect_flag = 1 if case == "in_range" else 0
     assert int(ref["flag"].item()) == expect_flag
     assert int(got["flag"].item()) == expect_flag
-    assert torch.equal(got["q_s"].view(torch.int16), ref["q_s"].view(torch.int16))
+    assert torch.equal(got["q_s"].view(bits), ref["q_s"].view(bits))
     if nsink:
         assert torch.equal(got["sink_s"], ref["sink_s"])
     # Bit-identical outputs; NaN rows (the NaN-query case) compare as equal bit patterns.
-    assert torch.equal(got["o"].view(torch.int16), ref["o"].view(torch.int16))
+    assert torch.equal(got["o"].view(bits), ref["o"].view(bits))
     assert torch.equal(got["stat"].view(torch.int32), ref["stat"].view(torch.int32))
     if case in ("in_range", "tail", "big_key_last"):
         assert torch.isfinite(got["o"].float()).all()
-
-
-def test_f32_inputs_take_the_two_calls():
-    B, H, T, D = 1, 2, 200, 64
-    L = _lib()
-    q, k, v, sink, nsink = _inputs(B, H, T, D, "in_range", "per_head", torch.float32, seed=5)
-    qd, kd, vd = (_to_dev(a, 0, torch.float32) for a in (q, k, v))
-    sd = torch.from_numpy(np.ascontiguousarray(sink)).float().cuda()
-    ref = _two_calls(qd, kd, vd, sd, nsink, 0, B, H, T, D, L.DTYPE_F32)
-    got = _one_call(qd, kd, vd, sd, nsink, 0, B, H, T, D, L.DTYPE_F32)
-    assert int(got["flag"].item()) == 1
-    for key in ("q_s", "sink_s", "o", "stat"):
-        assert torch.equal(got[key], ref[key]), key
