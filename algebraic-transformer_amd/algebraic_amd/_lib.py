@@ -11,6 +11,8 @@ from pathlib import Path
 _HERE = Path(__file__).resolve().parent
 LIB_PATH = Path(os.environ.get("ALGEBRAIC_HIP_LIB", _HERE / "libalgebraic_hip.so"))
 
+ABI_VERSION = 2  # ALG_ABI_VERSION of include/algebraic_hip.h these signatures follow
+
 ALG_OK, ALG_ERR_INVALID, ALG_ERR_UNSUPPORTED, ALG_ERR_HIP = 0, 1, 2, 3
 DTYPE_BF16, DTYPE_F32 = 0, 1
 ATTN_INRANGE, ATTN_CLIPPED, ATTN_SHIFTED, ATTN_GUARDED = 0, 1, 2, 3
@@ -25,6 +27,7 @@ _L = ctypes.c_long
 _SIGNATURES = {
     "alg_last_error": (ctypes.c_char_p, []),
     "alg_version": (ctypes.c_char_p, []),
+    "alg_abi_version": (_I, []),
     "alg_attn_workspace_size": (_S, [_I, _I, _I, _I, _I]),
     "alg_attn_prepare": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _F, _I, _I, _P, _P, _P, _P, _S]),
     "alg_attn_fwd": (_I, [_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _P, _F, _I, _I, _P, _P, _P]),
@@ -75,6 +78,13 @@ def load():
             f"{LIB_PATH} not found: build it with `python algebraic-transformer_amd/build_lib.py` "
             "(or __graft_entry__.build()); the algebraic kernels have no CPU fallback")
     lib = ctypes.CDLL(str(LIB_PATH))
+    if not hasattr(lib, "alg_abi_version"):
+        raise HipLibraryMissing(f"{LIB_PATH} predates ABI version {ABI_VERSION}: rebuild it")
+    lib.alg_abi_version.restype = ctypes.c_int
+    lib.alg_abi_version.argtypes = []
+    if lib.alg_abi_version() != ABI_VERSION:
+        raise HipLibraryMissing(f"{LIB_PATH} has ABI version {lib.alg_abi_version()}, these bindings "
+                                f"expect {ABI_VERSION}: rebuild it")
     for name, (res, args) in _SIGNATURES.items():
         fn = getattr(lib, name)
         fn.restype = res

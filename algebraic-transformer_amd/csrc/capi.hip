@@ -289,7 +289,8 @@ int noalloc_scratch(void** out) {
 extern "C" {
 
 const char* alg_last_error(void) { return g_err.c_str(); }
-const char* alg_version(void) { return "algebraic_hip 0.1 gfx950"; }
+const char* alg_version(void) { return "algebraic_hip 0.2 gfx950 (ABI 2)"; }
+int alg_abi_version(void) { return ALG_ABI_VERSION; }
 
 size_t alg_attn_workspace_size(int dtype, int B, int H, int T, int D) {
   if (B <= 0 || H <= 0 || T <= 0 || D <= 0) return 0;

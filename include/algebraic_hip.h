@@ -5,7 +5,12 @@
  * Every entry point is a pure function over caller-owned device buffers: plain pointers,
  * sizes, scalars and a HIP stream. No entry point allocates device memory; scratch comes
  * from a caller workspace sized by the *_workspace_size queries. Calls are asynchronous
- * on `stream` and reentrant (no global mutable state besides the thread-local error text).
+ * on `stream` and reentrant (no global mutable state besides the thread-local error text),
+ * with one exception: alg_attn_bwd_noalloc keeps its scratch in one library-held device
+ * array per GPU, so calls of it that overlap on one GPU (two streams, two host threads)
+ * race and must be serialised by the caller.
+ * ABI: alg_abi_version() returns ALG_ABI_VERSION of the header the library was built from;
+ * a caller compares it with its own before binding (signatures change between versions).
  * Return value: ALG_OK or an error code; alg_last_error() describes the last failure on
  * the calling thread.
  *
@@ -55,8 +60,13 @@ enum { ALG_LAYOUT_BHTD = 0, ALG_LAYOUT_BTHD = 1 };
  *   GUARDED  INRANGE or SHIFTED chosen on the device by guard_flag (range_guard=True) */
 enum { ALG_ATTN_INRANGE = 0, ALG_ATTN_CLIPPED = 1, ALG_ATTN_SHIFTED = 2, ALG_ATTN_GUARDED = 3 };
 
+/* Version 2: alg_attn_workspace_size and alg_head_* take a leading dtype argument and
+ * alg_attn_bwd has no o_precise argument (version 1 had one). */
+#define ALG_ABI_VERSION 2
+
 const char* alg_last_error(void);
 const char* alg_version(void);
+int alg_abi_version(void);
 
 /* Bytes of workspace alg_attn_prepare / alg_attn_bwd need for this dtype and shape: the sink
  * gradient's and the guard's partials, and for ALG_DTYPE_F32 also an f32 dQ accumulator

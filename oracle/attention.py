@@ -266,22 +266,33 @@ def kernel_backward(q_s, k, v, sink, o, stat, do, *, n=16, alpha=None, dtype="bf
     return out
 
 
-def flash_attention_oracle(q, k, v, sink_logit, do=None, *, n=16, c=8.0, dtype="bf16"):
+def flash_attention_oracle(q, k, v, sink_logit, do=None, *, n=16, c=8.0, dtype="bf16", di_rule=None):
     """Full guarded path: prologue, guard, kernel fwd (and bwd when ``do`` is given).
 
     Returns a dict with o, stat, q_s, in_range and, with ``do``: dq, dk, dv, dsink_logit.
     Mirrors flash_attention(kind="asinh", range_guard=True) (flash.py:763-857).
+    ``di_rule`` picks how the shifted fallback's backward forms di: "precise_output" is the
+    reference's (di = <dO, o_precise> over the f32 output it keeps, flash.py:73, 322, 852),
+    "weights" the HIP bf16 fallback's (di = sum_j p_ij dP_ij, no f32 output kept). The
+    default is what the HIP path does: "weights" for bf16, "precise_output" for f32.
+    In range both rules read di from the rounded output (flash.py:633).
     """
+    if di_rule is None:
+        di_rule = "weights" if dtype == "bf16" else "precise_output"
+    if di_rule not in ("weights", "precise_output"):
+        raise ValueError(f"di_rule {di_rule!r}")
     q_s, sink, alpha = prologue(q, sink_logit, c=c, dtype=dtype)
     ok = guard_in_range(q_s, k, v, sink if sink is not None else np.zeros(1, F32), n=n,
                         has_sink=sink is not None)
     o, stat, o_precise = kernel_forward(q_s, k, v, sink, n=n, dtype=dtype, shifted=not ok)
     res = dict(o=o, stat=stat, q_s=q_s, in_range=ok, o_precise=o_precise)
     if do is not None:
-        # The f32 output is exact; the bf16 fallback forms di from its weights.
-        dq_s, dk, dv, di, dbeta, dq = kernel_backward(q_s, k, v, sink, o, stat, do, n=n, alpha=alpha,
+        # In range di comes from the rounded output; on the fallback from the f32 output
+        # (the reference) or from the weights (the HIP bf16 kernels).
+        o_di = o if ok else o_precise
+        dq_s, dk, dv, di, dbeta, dq = kernel_backward(q_s, k, v, sink, o_di, stat, do, n=n, alpha=alpha,
                                                        dtype=dtype, shifted=not ok,
-                                                       di_from_weights=dtype == "bf16" and not ok)
+                                                       di_from_weights=di_rule == "weights" and not ok)
         res.update(dq=dq, dk=dk, dv=dv, di=di)
         if sink_logit is not None:
             shape = np.shape(sink_logit)

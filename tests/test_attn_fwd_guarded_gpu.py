@@ -145,3 +145,30 @@ def test_one_call_matches_prepare_then_forward(dtype, layout, D, case, sink_kind
     assert torch.equal(got["stat"].view(torch.int32), ref["stat"].view(torch.int32))
     if case in ("in_range", "tail", "big_key_last"):
         assert torch.isfinite(got["o"].float()).all()
+
+
+@pytest.mark.parametrize("case,sink_kind", [("in_range", "per_head"), ("tail", "none"), ("big_key_last", "per_head"),
+                                            ("nan_query_mid", "broadcast")])
+@pytest.mark.parametrize("T", [200, 256])
+def test_one_call_f32_two_query_groups(case, sink_kind, T):
+    """f32 at D = 64 with B H ceil(T/64) >= 512 takes the split forward's 64-query form (two
+    query groups per workgroup, two-way key split, guard partials per 64-query block): its
+    flag, q_s, o and stat are checked bit for bit against prepare + forward, and the flag
+    against the expected branch, so a guard maximum it missed or misplaced fails here."""
+    B, H, D, layout = 8, 16, 64, 0
+    assert B * H * math.ceil(T / 64) >= 512
+    L = _lib()
+    q, k, v, sink, nsink = _inputs(B, H, T, D, case, sink_kind, torch.float32, seed=5 + T)
+    qd, kd, vd = (_to_dev(a, layout, torch.float32) for a in (q, k, v))
+    sd = None if sink is None else torch.from_numpy(np.ascontiguousarray(sink)).float().cuda()
+    print(f"alg_attn_fwd_guarded f32 two query groups case={case} sink={sink_kind} T={T}", flush=True)
+    ref = _two_calls(qd, kd, vd, sd, nsink, layout, B, H, T, D, L.DTYPE_F32)
+    got = _one_call(qd, kd, vd, sd, nsink, layout, B, H, T, D, L.DTYPE_F32)
+    expect_flag = 1 if case == "in_range" else 0
+    assert int(ref["flag"].item()) == expect_flag
+    assert int(got["flag"].item()) == expect_flag
+    assert torch.equal(got["q_s"].view(torch.int32), ref["q_s"].view(torch.int32))
+    if nsink:
+        assert torch.equal(got["sink_s"], ref["sink_s"])
+    assert torch.equal(got["o"].view(torch.int32), ref["o"].view(torch.int32))
+    assert torch.equal(got["stat"].view(torch.int32), ref["stat"].view(torch.int32))

@@ -43,6 +43,16 @@ def test_library_exports_every_declared_symbol():
     assert set(declared_functions()) == set(_lib.EXPORTS)
 
 
+def test_abi_version_matches_the_header():
+    """The library reports the ALG_ABI_VERSION of the header it was built from, and the
+    Python bindings (whose signatures follow that header) expect the same version."""
+    from algebraic_amd import _lib
+    m = re.search(r"#define\s+ALG_ABI_VERSION\s+(\d+)", HEADER.read_text())
+    assert m, "ALG_ABI_VERSION missing from the header"
+    assert lib().alg_abi_version() == int(m.group(1)) == _lib.ABI_VERSION
+    assert f"ABI {_lib.ABI_VERSION}" in lib().alg_version().decode()
+
+
 def test_workspace_sizes():
     from algebraic_amd import _lib
     handle = lib()

@@ -4,8 +4,9 @@
 Only addressing differs between the two layouts (the same tiles, in the same order, feed the
 same arithmetic), so bf16 results are compared bit for bit; the f32 path adds dq over key
 blocks with atomics, whose order varies run to run, so its dq is compared at 1e-6.
-The (B, H, T, D) results themselves are pinned to the oracle by test_attention_gpu.py,
-test_prologue_gpu.py and test_full_size_gpu.py.
+The (B, T, H, D) results are also compared with the oracle directly (dense float64 and the
+cast-faithful kernel restatement) for the guarded, shifted-fallback, clipped and explicitly
+shifted variants, ragged T included.
 """
 
 import math
@@ -124,3 +125,94 @@ def test_flash_layouts_agree_full_size_c4a():
     o = flash_attention(_bthd(q), _bthd(k), _bthd(v), sink, layout="bthd", **kw)
     flat = o.reshape(B, T, H * D)
     assert flat.data_ptr() == o.data_ptr() and flat.is_contiguous()
+
+
+# ---------------------------------------------------------------------------
+# (B, T, H, D) storage against the oracle itself (model.py:167-169, 182 feed attention the
+# projection layout): the inputs are drawn (B, H, T, D), stored (B, T, H, D) on the device,
+# and every output and gradient, read back into (B, H, T, D), is compared with the float64
+# dense oracle (algebraic.py:186-216) and, for the guarded path, with the cast-faithful
+# restatement of the kernels (flash.py:763-857).
+# ---------------------------------------------------------------------------
+BF16_DENSE, BF16_KERNEL, F32_DENSE = 2e-2, 1e-2, 1e-5
+
+
+def _np_bthd(a):
+    return np.ascontiguousarray(np.transpose(a, (0, 2, 1, 3)))
+
+
+def _run_bthd(q, k, v, do, sink, dtype, **kw):
+    from algebraic_amd.kernels.flash import flash_attention
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    dev = lambda a: torch.tensor(_np_bthd(a), device="cuda").to(tdt)
+    tq, tk, tv = (dev(a).requires_grad_(True) for a in (q, k, v))
+    ts = None if sink is None else torch.tensor(sink, device="cuda", requires_grad=True)
+    o = flash_attention(tq, tk, tv, ts, kind="asinh", n=16, c=8.0, layout="bthd", **kw)
+    assert o.shape == tq.shape  # (B, T, H, D)
+    o.backward(dev(do))
+    torch.cuda.synchronize()
+    back = lambda t: np.transpose(t.detach().float().cpu().numpy().astype(np.float64), (0, 2, 1, 3))
+    out = [back(o), back(tq.grad), back(tk.grad), back(tv.grad)]
+    out.append(None if ts is None else ts.grad.detach().cpu().numpy().astype(np.float64))
+    return out
+
+
+def _check_dense(res, q, k, v, do, sink, tol):
+    from helpers import rel_l2
+    from oracle import attention as OA
+    want = [OA.dense_forward(q, k, v, sink, n=16, c=8.0), *OA.dense_backward(q, k, v, sink, do, n=16, c=8.0)]
+    names = ["o", "dq", "dk", "dv", "dsink"]
+    errs = {nm: rel_l2(a, b) for nm, a, b in zip(names, res, want) if b is not None and a is not None}
+    bad = {nm: e for nm, e in errs.items() if not e < tol}
+    assert not bad, f"(B, T, H, D) vs dense oracle: {bad} (all {errs})"
+
+
+def _check_kernel(res, q, k, v, do, sink, dtype, tol, in_range):
+    from helpers import rel_l2
+    from oracle import attention as OA
+    ref = OA.flash_attention_oracle(q, k, v, sink, do, n=16, c=8.0, dtype=dtype)
+    assert ref["in_range"] == in_range
+    names = ["o", "dq", "dk", "dv", "dsink"]
+    errs = {nm: rel_l2(a, ref[nm]) for nm, a in zip(names, res) if a is not None and nm in ref}
+    bad = {nm: e for nm, e in errs.items() if not e < tol}
+    assert not bad, f"(B, T, H, D) vs kernel restatement: {bad} (all {errs})"
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("shape", [(2, 3, 100, 64), (1, 2, 160, 128), (2, 2, 33, 128)])
+@pytest.mark.parametrize("with_sink", [True, False])
+def test_bthd_guarded_matches_oracle(shape, dtype, with_sink):
+    """Guarded path in range (the model's call), ragged T included."""
+    from helpers import attention_inputs
+    q, k, v, do, sink = attention_inputs(*shape, seed=47, dtype=dtype, sink=with_sink)
+    print(f"[layout-oracle] guarded {shape} {dtype} sink={with_sink}", flush=True)
+    res = _run_bthd(q, k, v, do, sink, dtype, range_guard=True, block=shape[2])
+    _check_dense(res, q, k, v, do, sink, BF16_DENSE if dtype == "bf16" else F32_DENSE)
+    if dtype == "bf16":
+        _check_kernel(res, q, k, v, do, sink, dtype, BF16_KERNEL, in_range=True)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_bthd_shifted_fallback_matches_oracle(dtype):
+    """Scores past the guard's bound (q, k x 5: ||q_s||^2 ||k||^2 = 5^4 D / 64 > (16/1.01)^2)
+    take the shifted fallback chosen on the device."""
+    from helpers import attention_inputs
+    shape = (2, 3, 100, 64)
+    q, k, v, do, sink = attention_inputs(*shape, seed=53, dtype=dtype, scale=5.0)
+    print(f"[layout-oracle] shifted fallback {shape} {dtype}", flush=True)
+    res = _run_bthd(q, k, v, do, sink, dtype, range_guard=True, block=shape[2])
+    _check_dense(res, q, k, v, do, sink, BF16_DENSE if dtype == "bf16" else 1e-4)
+    _check_kernel(res, q, k, v, do, sink, dtype, BF16_KERNEL if dtype == "bf16" else 1e-4, in_range=False)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("variant", ["clipped", "explicit_shift"])
+def test_bthd_unguarded_variants_match_dense(variant, dtype):
+    """range_guard=False (the clipped unshifted default, flash.py:749-754) and shift=True."""
+    from helpers import attention_inputs
+    shape = (1, 2, 160, 128) if variant == "clipped" else (2, 3, 100, 64)
+    q, k, v, do, sink = attention_inputs(*shape, seed=59, dtype=dtype)
+    kw = dict(range_guard=False, block=32) if variant == "clipped" else dict(shift=True, block=shape[2])
+    print(f"[layout-oracle] {variant} {shape} {dtype}", flush=True)
+    res = _run_bthd(q, k, v, do, sink, dtype, **kw)
+    _check_dense(res, q, k, v, do, sink, BF16_DENSE if dtype == "bf16" else F32_DENSE)

@@ -18,6 +18,7 @@ from helpers import attention_inputs, head_inputs, rel_l2
 from oracle import attention as OA
 from oracle import closed_form as CF
 from oracle import head as OH
+from oracle.numerics import round_bf16
 from oracle import numerics as N
 
 torch = pytest.importorskip("torch")
@@ -145,6 +146,40 @@ def test_shifted_di_from_weights_centres_equal_keys():
     dq_bad = OA.kernel_backward(q_s, q, v, None, op * np.float32(1 + 2.0 ** -12), stat, do, dtype="f32",
                                 shifted=True)[0]
     assert np.linalg.norm(dq_w) < 1e-2 * np.linalg.norm(dq_bad)
+
+
+@pytest.mark.parametrize("case", ["scale4.5", "scale6", "tail+", "tail-"])
+@pytest.mark.parametrize("D", [64, 128])
+def test_shifted_di_rules_gap_is_bounded(case, D):
+    """The bf16 shifted fallback's two di rules side by side: the reference's
+    di = <dO, o_precise> over the f32 output (flash.py:73, 322, 852) and the HIP kernels'
+    di = sum_j p_ij dP_ij from the weights. Guard-tripping random inputs (q, k x 4.5 or 6):
+    the gradients of the two differ by at most 5e-3 relative L2 (measured about 2e-3, the
+    size of one bf16 rounding), well inside what either keeps from the float64 dense
+    gradients. The reference's bf16 guarded tails (q = k = +-sqrt(1000),
+    test_flash_kernel_tpu.py:238-255, whose exact dq is 0): the gradients of the two rules
+    differ by less than 1e-3 of the reference test's 0.012 tolerance."""
+    if case.startswith("scale"):
+        q, k, v, do, sink = attention_inputs(2, 2, 200, D, seed=9, dtype="bf16", scale=float(case[5:]))
+    else:
+        shape = (1, 2, 256, D)
+        q = np.full(shape, np.sqrt(1000.0), np.float32)
+        k = q * (1.0 if case == "tail+" else -1.0)
+        rng = np.random.default_rng(3)
+        v, do = (round_bf16(rng.standard_normal(shape).astype(np.float32)) for _ in range(2))
+        sink = np.zeros((1, 2, 1, 1), np.float32)
+    ref = OA.flash_attention_oracle(q, k, v, sink, do, dtype="bf16", di_rule="precise_output")
+    hip = OA.flash_attention_oracle(q, k, v, sink, do, dtype="bf16", di_rule="weights")
+    assert not ref["in_range"] and not hip["in_range"]
+    dense = dict(zip(("dq", "dk", "dv", "dsink"), OA.dense_backward(q, k, v, sink, do)))
+    for name in ("dq", "dk", "dv", "dsink"):
+        a, b = ref[name].astype(np.float64), hip[name].astype(np.float64)
+        if case.startswith("scale"):
+            gap = rel_l2(b, a)
+            assert gap < 5e-3, (name, gap)
+            assert gap < max(rel_l2(a, dense[name]), rel_l2(b, dense[name])) + 1e-3, name
+        else:
+            assert np.max(np.abs(a - b)) < 0.012 * 1e-3, name
 
 
 def test_planted_mistakes_fail_the_pins():
