@@ -884,6 +884,268 @@ __global__ __launch_bounds__(256, bwd_bf16_waves_per_simd<D>()) void attn_bwd_bf
   if (blockIdx.x == gridDim.x - 1) attn_sink_grad(p, ceil_div(T_, SINK_ROWS));
 }
 
+// dK/dV kernel for bf16 inputs at D = 128 built for two waves per SIMD: 16 keys per wave on
+// v_mfma_f32_16x16x32_bf16, NW waves per workgroup (16 NW keys of one head). A wave's dK/dV
+// accumulators take 64 registers (16 keys x 128 d x 2 / 64 lanes) and its K/V fragments 32,
+// so with one 64-query tile's S and dP (32) it fits the 256 registers of a two-wave SIMD,
+// where the 32-key kernel above needs about 410 and runs one wave per SIMD. The price is LDS
+// traffic: every wave reads the whole Q and dO tile twice (row fragments for S and dP,
+// transposed fragments for dK and dV), twice the bytes per MFMA of the 32-key form.
+// Orientation: S = Q K^T with M = 16 queries, N = the wave's 16 keys, K = 32 d, so lane l owns
+// key l % 16; P^T and dS^T feed dV += P^T dO and dK += dS^T Q as A operands (M = keys, K = 32
+// queries: slots 0..3 from block 2c, 4..7 from block 2c + 1), with dO and Q read transposed
+// (ds_read_b64_tr_b16). MFMA row m of query block b is tile row 16 b + sigma(m), sigma taking
+// m = 0..7 to rows {0..3, 8..11} and 8..15 to {4..7, 12..15}: lane group g (l / 16) then owns
+// queries 16 b + qoff(g) + i in register i, qoff = 0, 8, 4, 12, so each 32-lane half of a
+// transposed read covers 8 rows whose swizzles differ in their upper three bits and its 16
+// (row, chunk) pairs land on 16 distinct bank groups (with sigma the identity they collide in
+// pairs); the row-fragment reads still cover 16 rows of one aligned group, the four lane groups
+// at chunks 4 apart (4 g + s: adjacent chunks 4 s + g cost four extra cycles per read on the
+// bank-conflict counter).
+// Per 64-query tile: 16 steps of S, dP (one query block and 32 d each; the weights of block b
+// run under the steps of block b + 1), then 16 steps of dV, dK (one 32-query half and 16 d
+// each; block 3's weights under the first half), the next tile's copy spread over the first
+// steps, one barrier. Same work items (bwd_block_coords), tile streaming, masking and
+// outputs as attn_bwd_bf16_kernel. Built with NW = 4 (64 keys per workgroup, two per CU):
+// at C4a 0.326-0.335 ms against 0.339-0.357 ms for the 32-key kernel in the same calls, and
+// 0.339-0.346 ms with NW = 8 (128 keys, one workgroup per CU, its two waves per SIMD in step).
+template <int NW, int MODE, int L2N, int LAYOUT>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void attn_bwd_dkdv16_kernel(AttnBwdParams p) {
+  constexpr int D = 128, BQ = BF_BQ, CPR = D / 8, NS = D / 32, NDB = D / 16;
+  constexpr int PF = 2;                       // LDS fragments read PF steps ahead (3: no faster)
+  constexpr int KB = 16 * NW;                 // keys per workgroup
+  constexpr int NMASK = KB / BQ;              // query tiles that cross the diagonal
+  constexpr int PW = BQ * CPR / 64 / NW;      // copy instruction pairs per wave and tile
+  static_assert(KB % BQ == 0 && PW >= 1, "work split");
+  __shared__ __attribute__((aligned(16))) bf16 Qs0[BQ * D];
+  __shared__ __attribute__((aligned(16))) bf16 Qs1[BQ * D];
+  __shared__ __attribute__((aligned(16))) bf16 dOs0[BQ * D];
+  __shared__ __attribute__((aligned(16))) bf16 dOs1[BQ * D];
+  __shared__ __attribute__((aligned(16))) float st0[BQ];
+  __shared__ __attribute__((aligned(16))) float st1[BQ];
+  __shared__ __attribute__((aligned(16))) float di0[BQ];
+  __shared__ __attribute__((aligned(16))) float di1[BQ];
+
+  if (p.flag) {
+    const bool in_range = *p.flag != 0;
+    if ((MODE == MODE_SHIFTED) == in_range) return;
+  }
+  const int lane = threadIdx.x & 63, g = lane >> 4, l16 = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int T_ = p.T;
+  const int nbh = p.B * p.H, nkb = ceil_div(T_, KB);
+  int bh, kblk;
+  bwd_block_coords(blockIdx.x, nbh, nkb, bh, kblk);
+  const int k0 = kblk * KB;
+  const size_t base = head_base(bh, p.H, T_, D, LAYOUT);
+  const int ld = LAYOUT ? p.H * D : D;  // elements between positions
+  const bf16* Q = reinterpret_cast<const bf16*>(p.q) + base;
+  const bf16* K = reinterpret_cast<const bf16*>(p.k) + base;
+  const bf16* V = reinterpret_cast<const bf16*>(p.v) + base;
+  const bf16* dO = reinterpret_cast<const bf16*>(p.dO) + base;
+  const int nbytes = head_bytes(T_, ld, D, 2);
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)Q, (short)0, nbytes, BUF_RSRC_WORD3);
+  const __amdgpu_buffer_rsrc_t rdo = __builtin_amdgcn_make_buffer_rsrc((void*)dO, (short)0, nbytes, BUF_RSRC_WORD3);
+  const __amdgpu_buffer_rsrc_t rst =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(p.stat + (size_t)bh * T_), (short)0, T_ * 4, BUF_RSRC_WORD3);
+  const __amdgpu_buffer_rsrc_t rdi =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(p.di + (size_t)bh * T_), (short)0, T_ * 4, BUF_RSRC_WORD3);
+  const int wk0 = k0 + wave * 16;  // this wave's first key
+  const int mykey = wk0 + l16;
+  const int log2n = p.log2n;
+  const int nq = ceil_div(T_, BQ);
+  const int qstart = k0 / BQ;
+
+  tile_dma2<D, BQ, NW>(Qs0, dOs0, rq, rdo, qstart * BQ, wave, lane, ld);
+  bwd_stat_dma(st0, di0, rst, rdi, qstart * BQ, wave, lane);
+  // K and V fragments of this wave's keys (B operands of S = Q K^T and dP = dO V^T): at step
+  // s lane group g covers d = 32 g + 8 s .. + 7 (the k order of the 32-deep steps is free as
+  // long as both operands share it; with the groups' chunks 4 apart rather than adjacent the
+  // row-fragment reads are free of bank conflicts), so lane l holds K[mykey][32 g + 8 s + j].
+  // Keys past T are zero and always masked.
+  bf16x8 kf[NS], vf[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const bf16x8 z = {};
+    const size_t o = (size_t)mykey * ld + 32 * g + 8 * s;
+    kf[s] = mykey < T_ ? ld8(K + o) : z;
+    vf[s] = mykey < T_ ? ld8(V + o) : z;
+  }
+  floatx4 dk[NDB], dv[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+    dk[db] = floatx4{};
+    dv[db] = floatx4{};
+  }
+  // Per-lane swizzled offsets (the swizzle repeats every 16 rows): row fragments of Q / dO
+  // for S and dP (row sigma(l16) of a query block, chunk 4 g + s) and transposed fragments for dV
+  // and dK (rows 4 g + (0..3) of a 16-row half, columns 16 db + (0..15)).
+  const int qoff = 4 * (((g & 1) << 1) | (g >> 1));             // qoff(g): 0, 8, 4, 12
+  const int arow = (l16 & 3) | ((l16 & 4) << 1) | ((l16 & 8) >> 1);  // sigma(l16)
+  int a_off[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) a_off[s] = swz_at<CPR>(arow, 32 * g + 8 * s);
+  int t_off[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) t_off[db] = swz_at<CPR>(qoff + (l16 >> 2), 16 * db + 4 * (lane & 3));
+
+  constexpr int RING = PF + 1;
+  bf16x8 aq[RING], ao[RING];  // row fragments of Q / dO, PF steps ahead
+  __builtin_amdgcn_s_waitcnt(VMCNT0);
+  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < PF; ++t) {
+    aq[t] = ld8(Qs0 + (t / NS) * 16 * D + a_off[t % NS]);
+    ao[t] = ld8(dOs0 + (t / NS) * 16 * D + a_off[t % NS]);
+  }
+  constexpr int VE = bwd_valu_per_elem<MODE>();
+
+  auto tile = [&](auto bufc, auto maskc, int qt) {
+    constexpr int BUF = decltype(bufc)::value;
+    constexpr bool MASKED = decltype(maskc)::value;
+    const bf16* Qs = BUF ? Qs1 : Qs0;
+    const bf16* dOs = BUF ? dOs1 : dOs0;
+    const float* sts = BUF ? st1 : st0;
+    const float* dis = BUF ? di1 : di0;
+    const int qbase = qt * BQ;
+
+    floatx4 s[4], dp[4];
+    floatx4 sv[2], dvv[2];  // stat and di of a block's queries (slot = block & 1)
+    bf16x8 pa[2], da[2];
+    float pw[4], dsx[4];
+    bf16x8 cf[RING][2];    // transposed dO / Q fragments of the dV/dK steps, PF steps ahead
+
+    auto a_step = [&](int t) {
+      const int b = t / NS, st = t % NS, tn = t + PF;
+      if (tn < 4 * NS) {
+        aq[tn % RING] = ld8(Qs + (tn / NS) * 16 * D + a_off[tn % NS]);
+        ao[tn % RING] = ld8(dOs + (tn / NS) * 16 * D + a_off[tn % NS]);
+      }
+      s[b] = mfma16_bf16(aq[t % RING], kf[st], s[b]);
+      dp[b] = mfma16_bf16(ao[t % RING], vf[st], dp[b]);
+    };
+    auto load_stats = [&](int b) {
+      sv[b & 1] = *reinterpret_cast<const floatx4*>(sts + 16 * b + qoff);
+      dvv[b & 1] = *reinterpret_cast<const floatx4*>(dis + 16 * b + qoff);
+    };
+    // Weight P and score gradient dS of element i of query block b (query 16 b + qoff + i).
+    auto elem = [&](int b, int i) {
+      const bool masked = MASKED && mykey > qbase + 16 * b + qoff + i;
+      bwd_elem<MODE, L2N>(s[b][i], dp[b][i], sv[b & 1][i], dvv[b & 1][i], masked, p, log2n, pw[i], dsx[i]);
+      const int c = b >> 1, j0 = 4 * (b & 1);
+      if (i & 1) {
+        pa[c][j0 + i - 1] = f2bf(pw[i - 1]);
+        pa[c][j0 + i] = f2bf(pw[i]);
+        da[c][j0 + i - 1] = f2bf(dsx[i - 1]);
+        da[c][j0 + i] = f2bf(dsx[i]);
+      }
+    };
+    // dV/dK step u: query half c = u / NDB (queries 32 c ..), d block db = u % NDB.
+    auto c_load = [&](int u) {
+      const int c = u / NDB, db = u % NDB;
+      cf[u % RING][0] = tr_frag_at(dOs + 32 * c * D, t_off[db], t_off[db] + 16 * D);
+      cf[u % RING][1] = tr_frag_at(Qs + 32 * c * D, t_off[db], t_off[db] + 16 * D);
+    };
+    auto c_step = [&](int u) {
+      const int c = u / NDB, db = u % NDB;
+      dv[db] = mfma16_bf16(pa[c], cf[u % RING][0], dv[db]);
+      dk[db] = mfma16_bf16(da[c], cf[u % RING][1], dk[db]);
+    };
+
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      s[b] = floatx4{};
+      dp[b] = floatx4{};
+    }
+    // S, dP steps: block b's 4 steps carry the weights of block b - 1 (one element each) and
+    // load block b's stat and di into the other slot; block 0's carry the copy of the next
+    // tile (issued unconditionally: past the last tile its rows lie beyond the descriptors'
+    // ranges and zeros land in the unused buffer set).
+    load_stats(0);
+#pragma unroll
+    for (int t = 0; t < 4 * NS; ++t) {
+      const int b = t / NS, st = t % NS;
+      if (st == 0 && b >= 1) load_stats(b);
+      a_step(t);
+      if (b == 0) {
+        if (st < PW) {
+          if constexpr (BUF) tile_dma2_part<D, BQ, NW>(Qs0, dOs0, rq, rdo, qbase + BQ, wave, lane, st, ld);
+          else tile_dma2_part<D, BQ, NW>(Qs1, dOs1, rq, rdo, qbase + BQ, wave, lane, st, ld);
+        }
+        if (st == NS - 1) {
+          if constexpr (BUF) bwd_stat_dma(st0, di0, rst, rdi, qbase + BQ, wave, lane);
+          else bwd_stat_dma(st1, di1, rst, rdi, qbase + BQ, wave, lane);
+        }
+        step_order_r<2, 0>(t + PF < 4 * NS ? 2 : 0);
+      } else {
+        elem(b - 1, st);
+        if (t >= 4 * NS - PF) c_load(t - (4 * NS - PF));
+        // LDS reads: the fragments PF steps ahead (2), the block's stats (2) at its first
+        // step, the first dV/dK fragments (4) at the last PF steps.
+        step_order_r<2, VE>((t + PF < 4 * NS ? 2 : 0) + (st == 0 ? 2 : 0) + (t >= 4 * NS - PF ? 4 : 0));
+      }
+    }
+    // dV, dK steps: the first half (blocks 0, 1) under the weights of block 3.
+#pragma unroll
+    for (int u = 0; u < 2 * NDB; ++u) {
+      if (u + PF < 2 * NDB) c_load(u + PF);
+      c_step(u);
+      if (u < NDB && (u & 1) == 0) {
+        elem(3, u >> 1);
+        step_order_r<2, VE>(u + PF < 2 * NDB ? 4 : 0);
+      } else {
+        step_order_r<2, 0>(u + PF < 2 * NDB ? 4 : 0);
+      }
+    }
+
+    __builtin_amdgcn_s_waitcnt(VMCNT0);  // this wave's copies of the next tile have landed
+    __syncthreads();                     // the next buffer set is complete; this one is free
+    {
+      const bf16* Qn = BUF ? Qs0 : Qs1;
+      const bf16* dOn = BUF ? dOs0 : dOs1;
+#pragma unroll
+      for (int t = 0; t < PF; ++t) {
+        aq[t] = ld8(Qn + (t / NS) * 16 * D + a_off[t % NS]);
+        ao[t] = ld8(dOn + (t / NS) * 16 * D + a_off[t % NS]);
+      }
+    }
+  };
+
+  // The first NMASK tiles cross the diagonal; the rest alternate buffer sets.
+  int qt = qstart;
+  tile(std::integral_constant<int, 0>{}, std::true_type{}, qt);
+  if constexpr (NMASK == 2) {
+    if (qt + 1 < nq) tile(std::integral_constant<int, 1>{}, std::true_type{}, qt + 1);
+  }
+  qt += NMASK;
+  while (qt < nq) {
+    tile(std::integral_constant<int, NMASK & 1>{}, std::false_type{}, qt);
+    if (++qt >= nq) break;
+    tile(std::integral_constant<int, (NMASK + 1) & 1>{}, std::false_type{}, qt);
+    ++qt;
+  }
+
+  // dK = n * acc, dV = acc (flash.py:591-597), rounded to bf16: register i of d block db
+  // holds key wk0 + 4 g + i, column 16 db + l16.
+  const float slope = (float)(1 << log2n);
+  bf16* DK = reinterpret_cast<bf16*>(p.dk) + base;
+  bf16* DV = reinterpret_cast<bf16*>(p.dv) + base;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int key = wk0 + 4 * g + i;
+    if (key < T_) {
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const size_t o = (size_t)key * ld + 16 * db + l16;
+        DK[o] = f2bf(dk[db][i] * slope);
+        DV[o] = f2bf(dv[db][i]);
+      }
+    }
+  }
+  // The last workgroup (the lightest causal key block) also forms the sink gradient.
+  if (blockIdx.x == gridDim.x - 1) attn_sink_grad(p, ceil_div(T_, SINK_ROWS));
+}
+
 // dQ kernel for bf16 inputs (query-stationary; no atomics): one workgroup = 4 waves = 128
 // queries of one (b, h), 32 per wave. Scores are formed transposed, S^T = K Q^T and
 // dP^T = V dO^T (Q and dO fragments held in registers, so each lane owns one query and its
@@ -990,6 +1252,7 @@ __global__ __launch_bounds__(256, (dq_waves_per_simd<D, MODE, L2N>())) void attn
     }
     diq = s + xor32(s);
   }
+  const float nsdi = -stq * diq;  // in range: -stat di of this lane's query
   floatx16 dqa[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db) dqa[db] = floatx16{};
@@ -1028,7 +1291,17 @@ __global__ __launch_bounds__(256, (dq_waves_per_simd<D, MODE, L2N>())) void attn
     // the first pass of the shifted fallback, the weight times dP instead.
     auto elem = [&](int blk, int i) {
       const bool masked = MASKED && kb0 + blk * 32 + 8 * (i >> 2) + 4 * h + (i & 3) > myq;
-      bwd_elem<MODE, L2N>(s[blk][i], dp[blk][i], stq, diq, masked, p, log2n, pv[i], dsv[i]);
+      if constexpr (MODE == MODE_INRANGE) {
+        // dS = p (dP - di) r with p = w stat (flash.py:350-356), formed as
+        // (w r) fma(stat, dP, -stat di): the lane's query fixes stat and di, so the product
+        // takes one instruction less per score (the same real number, f32 operations in
+        // another order).
+        float r;
+        const float w = pow2n<L2N>(rho_fast(s[blk][i], r), log2n);
+        dsv[i] = masked ? 0.0f : (w * r) * __builtin_fmaf(stq, dp[blk][i], nsdi);
+      } else {
+        bwd_elem<MODE, L2N>(s[blk][i], dp[blk][i], stq, diq, masked, p, log2n, pv[i], dsv[i]);
+      }
       if constexpr (DIPASS) {
         di_acc += pv[i] * dp[blk][i];
       } else if (i & 1) {
@@ -1256,6 +1529,13 @@ static hipError_t launch_bwd_bf16_l(const AttnBwdParams& p, int mode, bool dq, h
     switch (mode) {
       case MODE_INRANGE: {
         KTimer t("attn_bwd_inrange", st);
+        if (D == 128) {
+          // 16 keys per wave, two waves per SIMD (two 4-wave workgroups of 64 keys per CU).
+          dim3 grid16(nbh * ceil_div(p.T, 64)), block16(256);
+          if (p.log2n == 4) hipLaunchKernelGGL((attn_bwd_dkdv16_kernel<4, MODE_INRANGE, 4, LAYOUT>), grid16, block16, 0, st, p);
+          else hipLaunchKernelGGL((attn_bwd_dkdv16_kernel<4, MODE_INRANGE, 0, LAYOUT>), grid16, block16, 0, st, p);
+          break;
+        }
         dim3 grid(nbh * nkb);
         if (p.log2n == 4) hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_INRANGE, 4, LAYOUT>), grid, block, 0, st, p);
         else hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_INRANGE, 0, LAYOUT>), grid, block, 0, st, p);

@@ -153,11 +153,11 @@ constexpr int F32_PAD = 4;
 // Both matrices have rows `ld` elements apart (ld = D for (B, H, T, D) storage, H*D for
 // (B, T, H, D)); the descriptors' ranges end at the head's last row (head_bytes).
 // ROWS (64 by default, or 32) is the tile height; the four waves share the copy instructions.
-template <int D, int ROWS = 64>
+template <int D, int ROWS = 64, int NW = 4>
 __device__ __forceinline__ void tile_dma2(bf16* la, bf16* lb, __amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
                                           int r0, int wave, int lane, int ld = D) {
-  constexpr int CPR = D / 8, RPI = 64 / CPR, PW = ROWS * CPR / 64 / 4;  // PW instructions per wave
-  static_assert(PW >= 1 && PW * 4 * RPI == ROWS, "tile height");
+  constexpr int CPR = D / 8, RPI = 64 / CPR, PW = ROWS * CPR / 64 / NW;  // PW instructions per wave
+  static_assert(PW >= 1 && PW * NW * RPI == ROWS, "tile height");
   auto lla = LDS_PTR(bf16, la);
   auto llb = LDS_PTR(bf16, lb);
   asm volatile("" : "+s"(lla), "+s"(llb));
@@ -174,12 +174,12 @@ __device__ __forceinline__ void tile_dma2(bf16* la, bf16* lb, __amdgpu_buffer_rs
   }
 }
 // Instruction pair j of tile_dma2 alone (lets a kernel spread a tile copy over several
-// pipeline steps).
-template <int D, int ROWS = 64>
+// pipeline steps). NW waves share the copy instructions (4 by default).
+template <int D, int ROWS = 64, int NW = 4>
 __device__ __forceinline__ void tile_dma2_part(bf16* la, bf16* lb, __amdgpu_buffer_rsrc_t ra,
                                                __amdgpu_buffer_rsrc_t rb, int r0, int wave, int lane, int j,
                                                int ld = D) {
-  constexpr int CPR = D / 8, RPI = 64 / CPR, PW = ROWS * CPR / 64 / 4;
+  constexpr int CPR = D / 8, RPI = 64 / CPR, PW = ROWS * CPR / 64 / NW;
   auto lla = LDS_PTR(bf16, la);
   auto llb = LDS_PTR(bf16, lb);
   asm volatile("" : "+s"(lla), "+s"(llb));
@@ -206,6 +206,19 @@ __device__ __forceinline__ void step_order() {
     if (WP > 0 && i * WP < W) __builtin_amdgcn_sched_group_barrier(0x200, WP, 0);
   }
   __builtin_amdgcn_sched_barrier(0);
+}
+
+// step_order with the LDS read count given as a value that folds to a constant once the
+// caller's loop is unrolled.
+template <int NM, int V>
+__device__ __forceinline__ void step_order_r(int r) {
+  switch (r) {
+    case 0: step_order<NM, V, 0, 0>(); break;
+    case 2: step_order<NM, V, 2, 0>(); break;
+    case 4: step_order<NM, V, 4, 0>(); break;
+    case 6: step_order<NM, V, 6, 0>(); break;
+    default: step_order<NM, V, 8, 0>(); break;
+  }
 }
 
 }  // namespace alg

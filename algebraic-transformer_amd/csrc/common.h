@@ -5,6 +5,9 @@
 //                             B: lane l holds B[k = 8*(l/32) + j][n = l%32]
 //                             C: lane l, reg i holds C[m = 8*(i/4) + 4*(l/32) + i%4][n = l%32]
 //   v_mfma_f32_32x32x2f32     A: A[m = l%32][k = l/32], B: B[k = l/32][n = l%32], C as above.
+//   v_mfma_f32_16x16x32_bf16  A: lane l holds A[m = l%16][k = 8*(l/16) + j], j < 8
+//                             B: lane l holds B[k = 8*(l/16) + j][n = l%16]
+//                             C: lane l, reg i holds C[m = 4*(l/16) + i][n = l%16]
 // Any bijection of k onto (lane half, slot) gives the same product as long as A and B use
 // the same one; the kernels exploit this to feed a C tile straight back as an operand.
 //
@@ -44,6 +47,9 @@ namespace alg {
 
 __device__ __forceinline__ floatx16 mfma_bf16(const bf16x8& a, const bf16x8& b, const floatx16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ floatx4 mfma16_bf16(const bf16x8& a, const bf16x8& b, const floatx4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 __device__ __forceinline__ floatx16 mfma_f32(float a, float b, const floatx16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);

@@ -5,7 +5,8 @@ Through the C ABI (ctypes), each call is checked against alg_attn_bwd with a cal
 on the same forward residuals, for two calls in a row, the second with a smaller input (the
 scratch keeps the first call's contents): bf16 results bit-identical (the same kernels, no
 atomics); f32 dk, dv, di and dsink bit-identical and dq within 1e-6 (it is added with f32
-atomics, whose order varies).
+atomics, whose order varies). The device's free memory (hipMemGetInfo) is the same before
+and after each checked call.
 """
 
 import ctypes
@@ -51,25 +52,37 @@ def _forward(q, k, v, sink, dtype, n=16, c=8.0):
                 alpha=1.0 / (math.sqrt(D) * c))
 
 
-def _backward(r, k, v, do, noalloc):
+def _outputs(k, v):
+    B, H, T, D = k.shape
+    return [torch.empty_like(k), torch.empty_like(k), torch.empty_like(v),
+            torch.empty((B, H, T), dtype=torch.float32, device="cuda"), torch.empty(H, dtype=torch.float32, device="cuda")]
+
+
+def _backward(r, k, v, do, noalloc, out=None):
+    """One backward through the C ABI into `out` (allocated here if not given). For the
+    no-alloc entry point the device's free memory (hipMemGetInfo) is read before the call and
+    after it has finished; the difference is returned with the results."""
     L = _lib()
     lib = L.load()
     B, H, T, D = k.shape
     st = L.stream_of(k)
-    dq, dk, dv = torch.empty_like(k), torch.empty_like(k), torch.empty_like(v)
-    di = torch.empty((B, H, T), dtype=torch.float32, device="cuda")
-    dsink = torch.empty(H, dtype=torch.float32, device="cuda")
+    dq, dk, dv, di, dsink = out if out is not None else _outputs(k, v)
     args = [st, r["dt"], 0, B, H, T, D, L.ptr(r["q_s"]), L.ptr(k), L.ptr(v), L.ptr(r["sink_s"]), L.ptr(r["o"]),
             L.ptr(r["stat"]), L.ptr(do), r["n"], L.ATTN_GUARDED, L.ptr(r["flag"]), r["clamp"], 1, 1, r["alpha"],
             L.ptr(dq), L.ptr(dk), L.ptr(dv), L.ptr(di), L.ptr(dsink)]
+    freed = 0
     if noalloc:
+        torch.cuda.synchronize()
+        free0 = torch.cuda.mem_get_info()[0]
         L.check(lib.alg_attn_bwd_noalloc(*args), "alg_attn_bwd_noalloc")
+        torch.cuda.synchronize()
+        freed = free0 - torch.cuda.mem_get_info()[0]
     else:
         ws_bytes = lib.alg_attn_workspace_size(r["dt"], B, H, T, D)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
         L.check(lib.alg_attn_bwd(*args, L.ptr(ws), ws_bytes), "alg_attn_bwd")
     torch.cuda.synchronize()
-    return [x.float().cpu().numpy() for x in (dq, dk, dv, di, dsink)]
+    return [x.float().cpu().numpy() for x in (dq, dk, dv, di, dsink)], freed
 
 
 @pytest.mark.parametrize("dtype,shapes", [
@@ -77,15 +90,25 @@ def _backward(r, k, v, do, noalloc):
     (torch.float32, [(1, 3, 512, 64), (1, 2, 100, 64)]),
 ])
 def test_noalloc_backward_matches_the_workspace_entry_point(dtype, shapes):
+    """Both calls match the workspace entry point, and neither changes the device's free
+    memory: everything the calls need (inputs, outputs, the library's code and its static
+    scratch array) exists before them. A first call on a smaller shape sets up the scratch
+    address (hipGetSymbolAddress, once per device) before the calls that are checked."""
+    cases = []
     for call, (B, H, T, D) in enumerate(shapes):
-        print(f"[noalloc] call {call}: {dtype} B{B} H{H} T{T} D{D}", flush=True)
         q, k, v, do, sink = attention_inputs(B, H, T, D, seed=40 + call, dtype="bf16" if dtype == torch.bfloat16
                                              else "f32")
         tq, tk, tv, tdo = (torch.tensor(a, device="cuda").to(dtype) for a in (q, k, v, do))
         tsink = torch.tensor(sink.reshape(-1), device="cuda")
         res = _forward(tq, tk, tv, tsink, dtype)
-        want = _backward(res, tk, tv, tdo, noalloc=False)
-        got = _backward(res, tk, tv, tdo, noalloc=True)
+        want = _backward(res, tk, tv, tdo, noalloc=False)[0]
+        cases.append((res, tk, tv, tdo, want, _outputs(tk, tv)))
+    res, tk, tv, tdo, _, out = cases[-1]
+    _backward(res, tk, tv, tdo, noalloc=True, out=out)  # set-up call
+    for call, (res, tk, tv, tdo, want, out) in enumerate(cases):
+        print(f"[noalloc] call {call}: {dtype} {tuple(tk.shape)}", flush=True)
+        got, freed = _backward(res, tk, tv, tdo, noalloc=True, out=out)
+        assert freed == 0, f"call {call}: device free memory fell by {freed} bytes"
         names = ("dq", "dk", "dv", "di", "dsink")
         for name, a, b in zip(names, got, want):
             if dtype == torch.float32 and name == "dq":
