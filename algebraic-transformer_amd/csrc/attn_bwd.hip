@@ -13,12 +13,14 @@
 //         accumulates dQ^T += K^T dS^T in registers, written once. No atomics and no
 //         per-key-block dQ partials (unlike flash.py:537-544): f32 atomics run at about a
 //         sixth of the store bandwidth on this GPU, so recomputing two products is cheaper.
-//   dkdv  key-stationary: one workgroup = 4 waves = 128 keys of one (b,h); dK/dV accumulate
-//         in registers while the kernel streams 64-query tiles of Q, dO, stat and di through
-//         LDS. Scores are formed as S = Q K^T so a lane owns one key column; P^T and dS^T
-//         feed dV += P^T dO and dK += dS^T Q directly as MFMA A operands, with dO/Q
-//         fragments transposed by ds_read_b64_tr_b16. Its last workgroup also reduces the
-//         dQ kernel's partials into the per-head sink gradient (no separate launch).
+//   dkdv  key-stationary: dK/dV accumulate in registers while the kernel streams 64-query
+//         tiles of Q, dO, stat and di through LDS. Scores are formed as S = Q K^T so a lane
+//         owns one key column; P^T and dS^T feed dV += P^T dO and dK += dS^T Q directly as
+//         MFMA A operands, with dO/Q fragments transposed by ds_read_b64_tr_b16. In range:
+//         attn_bwd_dkdv16_kernel, 16 keys per wave on 16x16x32 MFMAs (4 waves = 64 keys per
+//         workgroup, two or three waves per SIMD); clipped and shifted: attn_bwd_bf16_kernel,
+//         32 keys per wave on 32x32x16 MFMAs (4 waves = 128 keys). The last workgroup also
+//         reduces the dQ kernel's partials into the per-head sink gradient (no separate launch).
 // f32 launches: pre (di from the f32 output, sink partials, zeroed dQ accumulator), one
 // key-stationary kernel adding dQ to an f32 accumulator with atomics, post (dq from the
 // accumulator: round(round(n * acc) * dq_scale), and the sink gradient).
@@ -597,7 +599,8 @@ constexpr int bwd_valu_per_elem() { return MODE == MODE_INRANGE ? 14 : 20; }
 template <int D>
 constexpr int bwd_bf16_waves_per_simd() { return D == 64 ? 2 : 1; }
 
-// dK/dV kernel for bf16 inputs: 128 keys per workgroup, 32 per wave (lane = key), dK/dV
+// dK/dV kernel for bf16 inputs (the clipped and shifted variants; the in-range path runs
+// attn_bwd_dkdv16_kernel below): 128 keys per workgroup, 32 per wave (lane = key), dK/dV
 // accumulated in registers over the 64-query tiles of the causal range. dQ is formed by
 // attn_bwd_dq_kernel, so this kernel stages nothing for it. Arranged for one wave per SIMD
 // as a software pipeline of fixed steps; each step's MFMAs use LDS fragments read two steps
@@ -884,39 +887,70 @@ __global__ __launch_bounds__(256, bwd_bf16_waves_per_simd<D>()) void attn_bwd_bf
   if (blockIdx.x == gridDim.x - 1) attn_sink_grad(p, ceil_div(T_, SINK_ROWS));
 }
 
-// dK/dV kernel for bf16 inputs at D = 128 built for two waves per SIMD: 16 keys per wave on
-// v_mfma_f32_16x16x32_bf16, NW waves per workgroup (16 NW keys of one head). A wave's dK/dV
-// accumulators take 64 registers (16 keys x 128 d x 2 / 64 lanes) and its K/V fragments 32,
-// so with one 64-query tile's S and dP (32) it fits the 256 registers of a two-wave SIMD,
-// where the 32-key kernel above needs about 410 and runs one wave per SIMD. The price is LDS
-// traffic: every wave reads the whole Q and dO tile twice (row fragments for S and dP,
-// transposed fragments for dK and dV), twice the bytes per MFMA of the 32-key form.
+// LDS layout of the 16-key dK/dV kernel's Q / dO tiles (64 rows of D bf16) and the lane
+// mapping of its fragments, chosen with the bank-conflict counter so that both kinds of
+// fragment read are conflict-free (each alternative listed cost 2-4 extra cycles per read):
+//   D = 128: chunk c of row r at c ^ (4(r&3) + ((r>>2)&3)) (the attention kernels' swizzle);
+//            MFMA row m of a 16-query block is tile row sigma(m) (0..7 -> {0..3, 8..11}, 8..15
+//            -> {4..7, 12..15}); lane group g reads k chunk 4g + s at step s (not 4s + g);
+//            the transposed reads' row quads are qoff(g) = 0, 8, 4, 12 (not 4g);
+//   D = 64:  chunk c of row r at c ^ (r & 7) (the attention kernels' D = 64 swizzle costs 4
+//            extra cycles per row-fragment read with every mapping tried); identity rows, k
+//            chunk 4s + g, quads 4g.
+// Lane group g then owns queries 16 b + quad(g) + i in register i of query block b.
+template <int D>
+struct Dkdv16Lay;
+template <>
+struct Dkdv16Lay<128> {
+  static __device__ __forceinline__ int swz(int r) { return swz_chunk<16>(r); }
+  static __device__ __forceinline__ int arow(int m) { return (m & 3) | ((m & 4) << 1) | ((m & 8) >> 1); }
+  static __device__ __forceinline__ int dcol(int g, int s) { return 32 * g + 8 * s; }
+  static __device__ __forceinline__ int quad(int g) { return 4 * (((g & 1) << 1) | (g >> 1)); }
+};
+template <>
+struct Dkdv16Lay<64> {
+  static __device__ __forceinline__ int swz(int r) { return r & 7; }
+  static __device__ __forceinline__ int arow(int m) { return m; }
+  static __device__ __forceinline__ int dcol(int g, int s) { return 32 * s + 8 * g; }
+  static __device__ __forceinline__ int quad(int g) { return 4 * g; }
+};
+
+// dK/dV kernel for bf16 inputs built for two or more waves per SIMD: 16 keys per wave on
+// v_mfma_f32_16x16x32_bf16, NW waves per workgroup (16 NW keys of one head). At D = 128 a
+// wave's dK/dV accumulators take 64 registers (16 keys x 128 d x 2 / 64 lanes) and its K/V
+// fragments 32, so with one 64-query tile's S and dP (32) it fits the 256 registers of a
+// two-wave SIMD, where the 32-key kernel above needs about 410 and runs one wave per SIMD; at
+// D = 64 half that, three waves per SIMD. The price is LDS traffic: every wave reads the whole
+// Q and dO tile twice (row fragments for S and dP, transposed fragments for dK and dV), twice
+// the bytes per MFMA of the 32-key form.
 // Orientation: S = Q K^T with M = 16 queries, N = the wave's 16 keys, K = 32 d, so lane l owns
 // key l % 16; P^T and dS^T feed dV += P^T dO and dK += dS^T Q as A operands (M = keys, K = 32
 // queries: slots 0..3 from block 2c, 4..7 from block 2c + 1), with dO and Q read transposed
-// (ds_read_b64_tr_b16). MFMA row m of query block b is tile row 16 b + sigma(m), sigma taking
-// m = 0..7 to rows {0..3, 8..11} and 8..15 to {4..7, 12..15}: lane group g (l / 16) then owns
-// queries 16 b + qoff(g) + i in register i, qoff = 0, 8, 4, 12, so each 32-lane half of a
-// transposed read covers 8 rows whose swizzles differ in their upper three bits and its 16
-// (row, chunk) pairs land on 16 distinct bank groups (with sigma the identity they collide in
-// pairs); the row-fragment reads still cover 16 rows of one aligned group, the four lane groups
-// at chunks 4 apart (4 g + s: adjacent chunks 4 s + g cost four extra cycles per read on the
-// bank-conflict counter).
-// Per 64-query tile: 16 steps of S, dP (one query block and 32 d each; the weights of block b
-// run under the steps of block b + 1), then 16 steps of dV, dK (one 32-query half and 16 d
-// each; block 3's weights under the first half), the next tile's copy spread over the first
-// steps, one barrier. Same work items (bwd_block_coords), tile streaming, masking and
-// outputs as attn_bwd_bf16_kernel. Built with NW = 4 (64 keys per workgroup, two per CU):
-// at C4a 0.326-0.335 ms against 0.339-0.357 ms for the 32-key kernel in the same calls, and
-// 0.339-0.346 ms with NW = 8 (128 keys, one workgroup per CU, its two waves per SIMD in step).
-template <int NW, int MODE, int L2N, int LAYOUT>
-__global__ __launch_bounds__(64 * NW, 8 / NW) void attn_bwd_dkdv16_kernel(AttnBwdParams p) {
-  constexpr int D = 128, BQ = BF_BQ, CPR = D / 8, NS = D / 32, NDB = D / 16;
+// (ds_read_b64_tr_b16); row order, k order and quads as in Dkdv16Lay.
+// Per 64-query tile: 4 D / 32 steps of S, dP (one query block and 32 d each; the weights of
+// block b run under the steps of block b + 1), then 2 D / 16 steps of dV, dK (one 32-query
+// half and 16 d each; block 3's weights under the first half), the next tile's copy spread over
+// the first steps, one barrier. Same work items (bwd_block_coords), tile streaming, masking
+// and outputs as attn_bwd_bf16_kernel.
+// Built with NW = 4 (64 keys per workgroup). At C4a 0.326-0.335 ms against 0.339-0.357 ms for
+// the 32-key kernel in the same calls, and 0.339-0.346 ms with NW = 8 (128 keys, one workgroup
+// per CU, its two waves per SIMD in step); at C3 (D = 64) 0.182-0.183 ms against 0.190-0.197.
+// The 32-key kernel stays for the clipped and shifted variants.
+template <int D>
+constexpr int dkdv16_waves_per_simd() { return D == 64 ? 3 : 2; }
+template <int D, int NW, int MODE, int L2N, int LAYOUT>
+__global__ __launch_bounds__(64 * NW, dkdv16_waves_per_simd<D>() * 4 / NW) void attn_bwd_dkdv16_kernel(AttnBwdParams p) {
+  static_assert(D == 64 || D == 128, "head_dim");
+  typedef Dkdv16Lay<D> Lay;
+  constexpr int BQ = BF_BQ, CPR = D / 8, NS = D / 32, NDB = D / 16;
   constexpr int PF = 2;                       // LDS fragments read PF steps ahead (3: no faster)
   constexpr int KB = 16 * NW;                 // keys per workgroup
   constexpr int NMASK = KB / BQ;              // query tiles that cross the diagonal
-  constexpr int PW = BQ * CPR / 64 / NW;      // copy instruction pairs per wave and tile
-  static_assert(KB % BQ == 0 && PW >= 1, "work split");
+  constexpr int RPI = 64 / CPR;               // tile rows per copy instruction
+  constexpr int PW = BQ / RPI / NW;           // copy instruction pairs per wave and tile
+  constexpr int EA = 4 / NS;                  // weights per S/dP step (block b - 1)
+  constexpr int CE = NDB / 4;                 // dV/dK steps per weight of block 3
+  static_assert(KB % BQ == 0 && PW >= 1 && PW <= NS && EA >= 1 && CE >= 1, "work split");
   __shared__ __attribute__((aligned(16))) bf16 Qs0[BQ * D];
   __shared__ __attribute__((aligned(16))) bf16 Qs1[BQ * D];
   __shared__ __attribute__((aligned(16))) bf16 dOs0[BQ * D];
@@ -956,18 +990,35 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_bwd_dkdv16_kernel(AttnBw
   const int nq = ceil_div(T_, BQ);
   const int qstart = k0 / BQ;
 
-  tile_dma2<D, BQ, NW>(Qs0, dOs0, rq, rdo, qstart * BQ, wave, lane, ld);
+  // Copy instruction pair j of a 64-row Q / dO tile into LDS in this layout (as tile_dma2_part:
+  // lane l of an instruction writes 16 bytes at base + 16 l, rows past T land as zeros; both
+  // swizzles satisfy swz(RPI J + r) = swz(r) ^ swz(RPI J) for r < RPI).
+  int dma_rowb = (lane / CPR) * ld * 2;
+  int dma_chunkb = 16 * ((lane % CPR) ^ Lay::swz(lane / CPR));
+  asm volatile("" : "+v"(dma_rowb), "+v"(dma_chunkb));
+  auto dma_part = [&](bf16* la, bf16* lb, int r0, int j) {
+    auto lla = LDS_PTR(bf16, la);
+    auto llb = LDS_PTR(bf16, lb);
+    asm volatile("" : "+s"(lla), "+s"(llb));
+    const int J = wave * PW + j;
+    const int voff = (r0 + RPI * J) * ld * 2 + dma_rowb + (dma_chunkb ^ (16 * Lay::swz(RPI * J)));
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, lla + J * 512, 16, voff, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rdo, llb + J * 512, 16, voff, 0, 0, 0);
+  };
+  auto lds_at = [](int row, int col) { return row * D + (((col >> 3) ^ Lay::swz(row)) << 3) + (col & 7); };
+
+#pragma unroll
+  for (int j = 0; j < PW; ++j) dma_part(Qs0, dOs0, qstart * BQ, j);
   bwd_stat_dma(st0, di0, rst, rdi, qstart * BQ, wave, lane);
   // K and V fragments of this wave's keys (B operands of S = Q K^T and dP = dO V^T): at step
-  // s lane group g covers d = 32 g + 8 s .. + 7 (the k order of the 32-deep steps is free as
-  // long as both operands share it; with the groups' chunks 4 apart rather than adjacent the
-  // row-fragment reads are free of bank conflicts), so lane l holds K[mykey][32 g + 8 s + j].
-  // Keys past T are zero and always masked.
+  // s lane group g covers d = dcol(g, s) .. + 7 (the k order of the 32-deep steps is free as
+  // long as both operands share it), so lane l holds K[mykey][dcol(g, s) + j]. Keys past T
+  // are zero and always masked.
   bf16x8 kf[NS], vf[NS];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     const bf16x8 z = {};
-    const size_t o = (size_t)mykey * ld + 32 * g + 8 * s;
+    const size_t o = (size_t)mykey * ld + Lay::dcol(g, s);
     kf[s] = mykey < T_ ? ld8(K + o) : z;
     vf[s] = mykey < T_ ? ld8(V + o) : z;
   }
@@ -977,17 +1028,16 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_bwd_dkdv16_kernel(AttnBw
     dk[db] = floatx4{};
     dv[db] = floatx4{};
   }
-  // Per-lane swizzled offsets (the swizzle repeats every 16 rows): row fragments of Q / dO
-  // for S and dP (row sigma(l16) of a query block, chunk 4 g + s) and transposed fragments for dV
-  // and dK (rows 4 g + (0..3) of a 16-row half, columns 16 db + (0..15)).
-  const int qoff = 4 * (((g & 1) << 1) | (g >> 1));             // qoff(g): 0, 8, 4, 12
-  const int arow = (l16 & 3) | ((l16 & 4) << 1) | ((l16 & 8) >> 1);  // sigma(l16)
+  // Per-lane LDS offsets (both swizzles repeat every 16 rows): row fragments of Q / dO for S
+  // and dP (row arow(l16) of a query block, d = dcol(g, s)) and transposed fragments for dV and
+  // dK (rows quad(g) + (0..3) of a 16-row half, columns 16 db + (0..15)).
+  const int qoff = Lay::quad(g);
   int a_off[NS];
 #pragma unroll
-  for (int s = 0; s < NS; ++s) a_off[s] = swz_at<CPR>(arow, 32 * g + 8 * s);
+  for (int s = 0; s < NS; ++s) a_off[s] = lds_at(Lay::arow(l16), Lay::dcol(g, s));
   int t_off[NDB];
 #pragma unroll
-  for (int db = 0; db < NDB; ++db) t_off[db] = swz_at<CPR>(qoff + (l16 >> 2), 16 * db + 4 * (lane & 3));
+  for (int db = 0; db < NDB; ++db) t_off[db] = lds_at(qoff + (l16 >> 2), 16 * db + 4 * (lane & 3));
 
   constexpr int RING = PF + 1;
   bf16x8 aq[RING], ao[RING];  // row fragments of Q / dO, PF steps ahead
@@ -1057,7 +1107,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_bwd_dkdv16_kernel(AttnBw
       s[b] = floatx4{};
       dp[b] = floatx4{};
     }
-    // S, dP steps: block b's 4 steps carry the weights of block b - 1 (one element each) and
+    // S, dP steps: block b's NS steps carry the weights of block b - 1 (EA elements each) and
     // load block b's stat and di into the other slot; block 0's carry the copy of the next
     // tile (issued unconditionally: past the last tile its rows lie beyond the descriptors'
     // ranges and zeros land in the unused buffer set).
@@ -1069,8 +1119,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_bwd_dkdv16_kernel(AttnBw
       a_step(t);
       if (b == 0) {
         if (st < PW) {
-          if constexpr (BUF) tile_dma2_part<D, BQ, NW>(Qs0, dOs0, rq, rdo, qbase + BQ, wave, lane, st, ld);
-          else tile_dma2_part<D, BQ, NW>(Qs1, dOs1, rq, rdo, qbase + BQ, wave, lane, st, ld);
+          if constexpr (BUF) dma_part(Qs0, dOs0, qbase + BQ, st);
+          else dma_part(Qs1, dOs1, qbase + BQ, st);
         }
         if (st == NS - 1) {
           if constexpr (BUF) bwd_stat_dma(st0, di0, rst, rdi, qbase + BQ, wave, lane);
@@ -1078,11 +1128,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_bwd_dkdv16_kernel(AttnBw
         }
         step_order_r<2, 0>(t + PF < 4 * NS ? 2 : 0);
       } else {
-        elem(b - 1, st);
+#pragma unroll
+        for (int e = 0; e < EA; ++e) elem(b - 1, EA * st + e);
         if (t >= 4 * NS - PF) c_load(t - (4 * NS - PF));
         // LDS reads: the fragments PF steps ahead (2), the block's stats (2) at its first
         // step, the first dV/dK fragments (4) at the last PF steps.
-        step_order_r<2, VE>((t + PF < 4 * NS ? 2 : 0) + (st == 0 ? 2 : 0) + (t >= 4 * NS - PF ? 4 : 0));
+        step_order_r<2, VE * EA>((t + PF < 4 * NS ? 2 : 0) + (st == 0 ? 2 : 0) + (t >= 4 * NS - PF ? 4 : 0));
       }
     }
     // dV, dK steps: the first half (blocks 0, 1) under the weights of block 3.
@@ -1090,8 +1141,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void attn_bwd_dkdv16_kernel(AttnBw
     for (int u = 0; u < 2 * NDB; ++u) {
       if (u + PF < 2 * NDB) c_load(u + PF);
       c_step(u);
-      if (u < NDB && (u & 1) == 0) {
-        elem(3, u >> 1);
+      if (u < NDB && u % CE == 0) {
+        elem(3, u / CE);
         step_order_r<2, VE>(u + PF < 2 * NDB ? 4 : 0);
       } else {
         step_order_r<2, 0>(u + PF < 2 * NDB ? 4 : 0);
@@ -1528,17 +1579,11 @@ static hipError_t launch_bwd_bf16_l(const AttnBwdParams& p, int mode, bool dq, h
   } else {
     switch (mode) {
       case MODE_INRANGE: {
+        // 16 keys per wave, 4-wave workgroups of 64 keys (two per CU at D = 128, three at 64).
         KTimer t("attn_bwd_inrange", st);
-        if (D == 128) {
-          // 16 keys per wave, two waves per SIMD (two 4-wave workgroups of 64 keys per CU).
-          dim3 grid16(nbh * ceil_div(p.T, 64)), block16(256);
-          if (p.log2n == 4) hipLaunchKernelGGL((attn_bwd_dkdv16_kernel<4, MODE_INRANGE, 4, LAYOUT>), grid16, block16, 0, st, p);
-          else hipLaunchKernelGGL((attn_bwd_dkdv16_kernel<4, MODE_INRANGE, 0, LAYOUT>), grid16, block16, 0, st, p);
-          break;
-        }
-        dim3 grid(nbh * nkb);
-        if (p.log2n == 4) hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_INRANGE, 4, LAYOUT>), grid, block, 0, st, p);
-        else hipLaunchKernelGGL((attn_bwd_bf16_kernel<D, MODE_INRANGE, 0, LAYOUT>), grid, block, 0, st, p);
+        dim3 grid16(nbh * ceil_div(p.T, 64));
+        if (p.log2n == 4) hipLaunchKernelGGL((attn_bwd_dkdv16_kernel<D, 4, MODE_INRANGE, 4, LAYOUT>), grid16, block, 0, st, p);
+        else hipLaunchKernelGGL((attn_bwd_dkdv16_kernel<D, 4, MODE_INRANGE, 0, LAYOUT>), grid16, block, 0, st, p);
       } break;
       case MODE_CLIPPED: {
         KTimer t("attn_bwd_clipped", st);
