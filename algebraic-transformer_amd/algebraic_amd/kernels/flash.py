@@ -195,7 +195,31 @@ def flash_attention(q, k, v, sink_logit=None, *, kind: str = "softmax",
     """
     plan = _make_plan(q, k, v, kind, n, c, block, block_q, block_k, shift, fast_rho, inv_stat, compact_stat,
                       poly_rho, range_guard, resident_bwd, diagonal_bwd, diagonal_fwd, head_resident, layout)
-    return _FlashFn.apply(q, k, v, sink_logit, plan)
+    D = q.shape[-1]
+    if D in _BUILT_D:
+        return _FlashFn.apply(q, k, v, sink_logit, plan)
+    return _padded(q, k, v, sink_logit, plan, D)
+
+
+# Head widths the gfx950 kernels are built for. The reference's generic kernels take any D
+# (flash.py:189-326); other widths up to 128 run here on the next built width with zero
+# columns appended to q, k and v: a zero column adds nothing to any q.k product, so the
+# scores, weights and row statistics are those of the unpadded call, the padded columns of
+# o, dq, dk and dv come out exactly zero, and they are dropped. Two scalars must see the
+# logical width: alpha = 1/(sqrt(D) c) (flash.py:823) and sink/c. The padded call therefore
+# runs with c' = c sqrt(D / Dp), whose alpha 1/(sqrt(Dp) c') is the reference's, and with the
+# sink scaled by c'/c so that sink'/c' = sink/c; the gradients flow back through the
+# padding, the slice and that scaling. The C ABI itself takes D in {64, 128}.
+_BUILT_D = (64, 128)
+
+
+def _padded(q, k, v, sink_logit, plan, D):
+    Dp = next(w for w in _BUILT_D if w >= D)
+    c_pad = plan.c * math.sqrt(D / Dp)
+    pad = lambda t: torch.nn.functional.pad(t, (0, Dp - D))
+    sink_pad = None if sink_logit is None else sink_logit * (c_pad / plan.c)
+    o = _FlashFn.apply(pad(q), pad(k), pad(v), sink_pad, plan._replace(c=c_pad))
+    return o[..., :D].contiguous()
 
 
 _LAYOUTS = {"bhtd": 0, "bthd": 1}
@@ -256,6 +280,8 @@ def _make_plan(q, k, v, kind, n, c, block, block_q, block_k, shift, fast_rho, in
             if not var.fast_rho:
                 raise NotImplementedError("unshifted accumulation is built with fast rho (the default)")
             plan = _Plan(_lib.ATTN_CLIPPED, var.n, float(c), var.clamp, True, var.inv_stat, False, lay)
+    if D > 128:
+        raise NotImplementedError(f"head_dim {D}: gfx950 kernels are built for head_dim <= 128")
     if not q.is_cuda:
         raise RuntimeError("flash_attention needs GPU tensors (no CPU fallback)")
     return plan

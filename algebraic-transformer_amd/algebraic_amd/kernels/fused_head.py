@@ -55,7 +55,10 @@ class _HeadFn(torch.autograd.Function):
         pt = torch.empty(N, dtype=torch.float32, device=dev)
         obj = torch.empty((), dtype=torch.float32, device=dev)
         residual = None
-        if SCHEDULE == "residual" and dt == _lib.DTYPE_BF16 and any(ctx.needs_input_grad[:2]):
+        # n = 1 takes the recompute schedule: fused_head.py:59-65 forms l^(-1/n) as rsqrt(l)
+        # for n = 1 (not 1/l), which the kernels reproduce, and the residual schedule's
+        # U' = (l / s) dz needs stat^n = 1/l.
+        if SCHEDULE == "residual" and dt == _lib.DTYPE_BF16 and n > 1 and any(ctx.needs_input_grad[:2]):
             residual = torch.empty(lib.alg_head_residual_size(N, d, V), dtype=torch.uint8, device=dev)
         _lib.check(lib.alg_head_fwd(st, dt, N, d, V, _lib.ptr(h), _lib.ptr(e), _lib.ptr(t), n, c, _lib.ptr(stat),
                                     _lib.ptr(zt), _lib.ptr(pt), _lib.ptr(obj), _lib.ptr(residual),
@@ -100,10 +103,6 @@ def fused_head(h, embed, targets, *, kind="ce", n=16, c=16.0, block_n=128, block
         raise ValueError(kind)
     if kind == "alg_ce" and (n & (n - 1)):
         raise ValueError("n must be a power of two")
-    if kind == "alg_ce" and n == 1:
-        # fused_head.py:59-65 forms l^(-1/n) as rsqrt(l) then y * rsqrt(y) while n/2 > 1,
-        # which for n = 1 is rsqrt(l), not 1/l: the reference's fused head is wrong there.
-        raise NotImplementedError("n = 1: the fused head's statistic l^(-1/n) is built for n >= 2")
     N = h.shape[0]
     bn = min(block_n, N)
     if N % bn:

@@ -199,12 +199,15 @@ int check_head(int N, int d, int V, int n, float c) {
 
 // The training head's statistic is l^(-1/n), formed as the reference's _inv_root does
 // (fused_head.py:59-65: rsqrt, then y * rsqrt(y) while k = n/2 > 1). For n = 1 that loop gives
-// rsqrt(l) rather than 1/l, so the reference's fused head returns a wrong probability and
-// gradient there; the training head here takes n >= 2 (the evaluation head, which works in
-// the log domain, takes n = 1 too).
-int check_train_head_n(int n) {
-  if (n == 1)
-    return fail(ALG_ERR_UNSUPPORTED, "n = 1: the training head needs n >= 2 (l^(-1/n) by repeated rsqrt)");
+// rsqrt(l) rather than 1/l, and the reference's fused head then computes p = rho * rsqrt(l)
+// and its gradient from it; the kernels here form the same quantities (stat = inv_root(l, n),
+// p = (rho stat)^n), so n = 1 returns what the reference returns. The residual schedule
+// alone cannot take it: its U' = (l / s) dz rests on stat^n = 1 / l.
+int check_train_head_n(int n, const void* residual) {
+  if (n == 1 && residual)
+    return fail(ALG_ERR_UNSUPPORTED,
+                "n = 1: the residual schedule needs stat^n = 1/l, which the reference's l^(-1/n) "
+                "(rsqrt(l) at n = 1) does not give; pass no residual (recompute schedule)");
   return ALG_OK;
 }
 
@@ -601,7 +604,7 @@ int alg_head_fwd(alg_stream_t stream, int dtype, int N, int d, int V, const void
                  const int32_t* targets, int n, float c, float* stat, float* zt, float* pt, float* obj,
                  void* residual, void* workspace, size_t workspace_bytes) {
   int rc = check_head(N, d, V, n, c);
-  if (!rc) rc = check_train_head_n(n);
+  if (!rc) rc = check_train_head_n(n, residual);
   if (!rc) rc = check_head_dtype(dtype, residual);
   if (rc) return rc;
   const bool f32 = dtype == ALG_DTYPE_F32;
@@ -776,7 +779,7 @@ int alg_head_bwd(alg_stream_t stream, int dtype, int N, int d, int V, const void
                  const int32_t* targets, const float* stat, const float* g, int n, float c, const void* residual,
                  void* dh, void* dE, int dE_dtype, void* workspace, size_t workspace_bytes) {
   int rc = check_head(N, d, V, n, c);
-  if (!rc) rc = check_train_head_n(n);
+  if (!rc) rc = check_train_head_n(n, residual);
   if (!rc) rc = check_head_dtype(dtype, residual);
   if (rc) return rc;
   const bool f32 = dtype == ALG_DTYPE_F32;

@@ -175,3 +175,57 @@ def test_rows_sum_to_one_minus_sink_mass():
     p, psink, _ = OA._dense_probs(q.astype(np.float64), k.astype(np.float64), 16, 8.0,
                                   OA._sink_vector(sink, H))
     np.testing.assert_allclose(o[..., 0], 1.0 - psink, rtol=2e-6, atol=2e-6)
+
+
+# Head widths other than the built 64 and 128 (the reference's generic kernels take any D,
+# flash.py:189-326): the mirror runs them zero-padded to the next built width with c and the
+# sink rescaled so that alpha = 1/(sqrt(D) c) and sink/c are the logical width's.
+@pytest.mark.parametrize("D", [32, 48, 80, 96])
+@pytest.mark.parametrize("with_sink", [True, False])
+def test_guarded_bf16_other_head_dims(D, with_sink):
+    q, k, v, do, sink = attention_inputs(2, 3, 100, D, seed=61 + D, sink=with_sink)
+    print(f"[head_dim] bf16 D={D} sink={with_sink}", flush=True)
+    res = run_hip(q, k, v, do, sink, "bf16", range_guard=True, block=100)
+    assert res[0].shape[-1] == D
+    check_dense(res, q, k, v, do, sink, BF16_DENSE)
+    ref = OA.flash_attention_oracle(q, k, v, sink, do, dtype="bf16")
+    assert ref["in_range"]
+    for got, key in zip(res, ("o", "dq", "dk", "dv", "dsink")):
+        if got is not None and key in ref:
+            assert rel_l2(got, ref[key]) < BF16_KERNEL, key
+
+
+@pytest.mark.parametrize("D", [16, 96])
+def test_guarded_fp32_other_head_dims(D):
+    q, k, v, do, sink = attention_inputs(1, 2, 160, D, seed=67 + D, dtype="f32")
+    print(f"[head_dim] f32 D={D}", flush=True)
+    res = run_hip(q, k, v, do, sink, "f32", range_guard=True, block=160)
+    check_dense(res, q, k, v, do, sink, F32_DENSE)
+
+
+@pytest.mark.parametrize("variant", ["shifted_fallback", "clipped", "bthd"])
+def test_other_head_dim_variants(variant):
+    """D = 96 on the guard's shifted fallback (q, k x 4.5), the clipped unguarded default and
+    the (B, T, H, D) projection layout."""
+    D = 96
+    scale = 4.5 if variant == "shifted_fallback" else 1.0
+    q, k, v, do, sink = attention_inputs(2, 2, 128, D, seed=73, scale=scale)
+    print(f"[head_dim] D={D} {variant}", flush=True)
+    if variant == "bthd":
+        from algebraic_amd.kernels.flash import flash_attention
+        tr = lambda a: np.ascontiguousarray(np.transpose(a, (0, 2, 1, 3)))
+        tq, tk, tv = (_to(tr(a), torch.bfloat16).requires_grad_(True) for a in (q, k, v))
+        ts = torch.tensor(sink, device="cuda", requires_grad=True)
+        o = flash_attention(tq, tk, tv, ts, kind="asinh", n=16, c=8.0, range_guard=True, layout="bthd")
+        o.backward(_to(tr(do), torch.bfloat16))
+        back = lambda t: np.transpose(t.detach().float().cpu().numpy().astype(np.float64), (0, 2, 1, 3))
+        res = (back(o), back(tq.grad), back(tk.grad), back(tv.grad), ts.grad.cpu().numpy().astype(np.float64))
+    else:
+        kw = dict(range_guard=True) if variant == "shifted_fallback" else dict(range_guard=False)
+        res = run_hip(q, k, v, do, sink, "bf16", block=128, **kw)
+    check_dense(res, q, k, v, do, sink, BF16_DENSE)
+    if variant == "shifted_fallback":
+        ref = OA.flash_attention_oracle(q, k, v, sink, do, dtype="bf16")
+        assert not ref["in_range"]
+        for got, key in zip(res, ("o", "dq", "dk", "dv", "dsink")):
+            assert rel_l2(got, ref[key]) < BF16_KERNEL, key

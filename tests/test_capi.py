@@ -111,6 +111,15 @@ def test_invalid_arguments_fail_before_launch():
     rc = handle.alg_head_bwd(None, 0, 128, 256, 1000, P(16), P(16), P(16), P(16), P(16), 8, 2.0, None, P(16),
                              P(16), 0, P(16), 16)
     assert rc == _lib.ALG_ERR_INVALID and b"workspace" in handle.alg_last_error()
+    # n = 1 (fused_head.py:269-272 accepts it): with a residual it is refused (that schedule
+    # needs stat^n = 1/l, which the reference's l^(-1/n) = rsqrt(l) at n = 1 does not give);
+    # without one it passes the n check and fails here only on the too-small workspace.
+    rc = handle.alg_head_fwd(None, 0, 128, 256, 1000, P(16), P(16), P(16), 1, 2.0, P(16), P(16), P(16), P(16),
+                             P(16), P(16), 16)
+    assert rc == _lib.ALG_ERR_UNSUPPORTED and b"n = 1" in handle.alg_last_error()
+    rc = handle.alg_head_fwd(None, 0, 128, 256, 1000, P(16), P(16), P(16), 1, 2.0, P(16), P(16), P(16), P(16),
+                             None, P(16), 16)
+    assert rc == _lib.ALG_ERR_INVALID and b"workspace" in handle.alg_last_error()
     # f32 hidden states take no residual; an unknown dtype is refused.
     rc = handle.alg_head_fwd(None, _lib.DTYPE_F32, 128, 256, 1000, P(16), P(16), P(16), 8, 2.0, P(16), P(16),
                              P(16), P(16), P(16), P(16), 1 << 30)

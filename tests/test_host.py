@@ -52,6 +52,14 @@ def test_flash_validation():
         flash_attention(q16, k16, v16, kind="asinh", range_guard=True)
     with pytest.raises(RuntimeError):
         flash_attention(q, k, v, kind="asinh", range_guard=True)   # CPU tensors: no fallback
+    # Widths other than the built 64 / 128 run zero-padded up to 128 (GPU only); above 128 the
+    # call is refused before any device work.
+    x = torch.ones((1, 1, 64, 160), dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError, match="head_dim 160"):
+        flash_attention(x, x, x, kind="asinh", range_guard=True)
+    x = torch.ones((1, 1, 64, 96), dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU"):
+        flash_attention(x, x, x, kind="asinh", range_guard=True)
 
 
 def test_fused_head_validation():
@@ -96,10 +104,10 @@ def test_neighbour_mirrors_validate_before_any_launch():
     with pytest.raises(RuntimeError):
         alu_glu_ffn(h2, wg, wg, wd)
     h, E, t = torch.zeros(16, 64, dtype=torch.bfloat16), torch.zeros(100, 64), torch.zeros(16, dtype=torch.int32)
-    # n = 1 passes the reference's power-of-two check, but its statistic l^(-1/n) is formed by
-    # repeated rsqrt (fused_head.py:59-65), which gives rsqrt(l) there: refused before the device.
+    # n = 1 passes the reference's power-of-two check (fused_head.py:269-272) and is taken
+    # (the recompute schedule); on CPU tensors it stops at the device check like any n.
     from algebraic_amd.kernels.fused_head import fused_head
-    with pytest.raises(NotImplementedError, match="n = 1"):
+    with pytest.raises(RuntimeError, match="GPU"):
         fused_head(h, E, t, kind="alg_ce", n=1, c=2.0)
     with pytest.raises(NotImplementedError):
         head_logprob(h, E, t, head="ce")

@@ -93,3 +93,32 @@ def test_eval_head_n(n, c):
     ref = OH.eval_logprob(h, E, t, n=n, c=c)
     ref = ref[0] if isinstance(ref, tuple) else ref
     np.testing.assert_allclose(logp, ref, atol=1e-4 * max(1.0, n / 16), rtol=1e-4)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_training_head_n1_matches_reference_formula(dtype):
+    """n = 1 passes the reference's power-of-two check (fused_head.py:269-272). Its statistic
+    _inv_root(l, 1) is rsqrt(l) (fused_head.py:59-65), so the reference's fused head returns
+    p_t = rho(z_t/c) rsqrt(l) and the gradient of that, not the true NLL's. The HIP head (the
+    recompute schedule) matches the cast-faithful restatement of those formulas
+    (oracle.head.kernel_forward / kernel_backward) at the head's usual bars, and, as the
+    reference does, differs from the true-NLL dense head."""
+    from algebraic_amd.kernels.fused_head import fused_head
+    N, d, V, c = 256, 128, 1000, 2.0
+    h, E, t = head_inputs(N, d, V, seed=71, e_std=0.15)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    th = torch.tensor(h, device="cuda").to(tdt).requires_grad_(True)
+    tE = torch.tensor(E, device="cuda").to(tdt).requires_grad_(True)
+    print(f"[head n=1] {dtype}", flush=True)
+    obj, tel = fused_head(th, tE, torch.tensor(t, device="cuda"), kind="alg_ce", n=1, c=c)
+    obj.backward()
+    torch.cuda.synchronize()
+    stat, _, pt_r, obj_r = OH.kernel_forward(h, E, t, n=1, c=c, dtype=dtype)
+    dh_r, dE_r = OH.kernel_backward(h, E, t, stat, 1.0, n=1, c=c, dtype=dtype, e_dtype=dtype)
+    tol = (2e-3, 2e-2, 1e-2) if dtype == "bf16" else (1e-5, 1e-5, 1e-5)
+    assert abs(obj.item() - float(obj_r)) <= tol[0] * abs(float(obj_r)), (obj.item(), float(obj_r))
+    assert rel_l2(tel.float().cpu().numpy(), pt_r) < tol[1]
+    assert rel_l2(th.grad.float().cpu().numpy(), dh_r) < tol[2]
+    assert rel_l2(tE.grad.float().cpu().numpy(), dE_r) < tol[2]
+    obj_nll, _ = OH.dense_forward(h, E, t, n=1, c=c)
+    assert abs(float(obj_r) - obj_nll) > 10 * tol[0] * abs(obj_nll)  # the reference's n = 1 deviation
