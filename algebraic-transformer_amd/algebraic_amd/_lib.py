@@ -47,6 +47,8 @@ _SIGNATURES = {
     "alg_head_residual_size": (_S, [_I, _I, _I]),
     "alg_head_fwd": (_I, [_P, _I, _I, _I, _I, _P, _P, _P, _I, _F, _P, _P, _P, _P, _P, _P, _S]),
     "alg_head_bwd": (_I, [_P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _I, _F, _P, _P, _P, _I, _P, _S]),
+    "alg_head_streamed_workspace_size": (_S, [_I, _I, _I, _I, _I]),
+    "alg_head_bwd_streamed": (_I, [_P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _I, _F, _I, _P, _P, _I, _P, _S]),
     "alg_head_eval": (_I, [_P, _I, _I, _I, _I, _P, _P, _P, _I, _F, _P, _P, _P, _S]),
     "alg_rms_norm_workspace_size": (_S, [_I, _I]),
     "alg_ffn_alu_glu_fwd": (_I, [_P, _I, _I, _I, _P, _P, _F, _P, _P, _P]),

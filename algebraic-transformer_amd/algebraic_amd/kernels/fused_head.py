@@ -6,7 +6,8 @@ Mirrors ``fused_head(h, embed, targets, *, kind, n, c, block_n, block_v)``
 tensors on the GPU. The logits are never materialised: the forward is one tiled
 ``E h^T`` MFMA pass with the row statistics fused into its epilogue; the backward reads the
 forward's bf16 residual, or recomputes the tiles and forms the logit gradient (bf16, or f32
-for f32 hidden states) in a bounded workspace, and runs the two gradient GEMMs in HIP
+for f32 hidden states) in a workspace, whole or one vocabulary chunk at a time (the
+"streamed" schedule, which holds no (N, V) block), and runs the two gradient GEMMs in HIP
 (including the embedding gradient the reference leaves to XLA, fused_head.py:215). Returns ``(objective, telemetry)``: the mean target-miss probability
 (whose gradient is the exact NLL gradient) and the per-token target probability, which
 receives no gradient. ``kind="ce"`` (the softmax control arm) raises NotImplementedError.
@@ -20,9 +21,14 @@ from .. import _lib
 
 # Backward schedule: "residual" keeps the token-major bf16 block U = w r (and l) from the
 # forward so the backward runs 3 products; "recompute" keeps only (h, E, targets, stat) as
-# the reference does (fused_head.py:244) and recomputes the logits (4 products). f32 hidden
-# states always take the recompute schedule, in f32 throughout as the reference runs it.
+# the reference does (fused_head.py:244) and recomputes the logits (4 products) into an
+# (N, V) logit-gradient block; "streamed" recomputes them one vocabulary chunk of
+# VOCAB_CHUNK rows at a time (0: the library's default) and holds no (N, V) block at all.
+# f32 hidden states take the recompute (or streamed) schedule, in f32 throughout as the
+# reference runs it.
+SCHEDULES = ("residual", "recompute", "streamed")
 SCHEDULE = os.environ.get("ALGEBRAIC_HEAD_SCHEDULE", "residual")
+VOCAB_CHUNK = int(os.environ.get("ALGEBRAIC_HEAD_VOCAB_CHUNK", "0"))
 
 _DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float32: _lib.DTYPE_F32}
 
@@ -48,6 +54,10 @@ class _HeadFn(torch.autograd.Function):
         e = _lib.aligned16(embed.detach().to(h.dtype))        # fused_head.py:168
         t = targets.to(device=dev, dtype=torch.int32).contiguous()
         dt = _DTYPES[h.dtype]
+        if SCHEDULE not in SCHEDULES:
+            raise ValueError(f"head schedule {SCHEDULE!r}: one of {SCHEDULES}")
+        if SCHEDULE == "streamed" and (VOCAB_CHUNK < 0 or VOCAB_CHUNK % 256):
+            raise ValueError(f"vocab chunk {VOCAB_CHUNK}: 0 or a positive multiple of 256")
         ws_bytes = lib.alg_head_workspace_size(dt, N, d, V, 0)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         stat = torch.empty(N, dtype=torch.float32, device=dev)
@@ -65,6 +75,8 @@ class _HeadFn(torch.autograd.Function):
                                     _lib.ptr(ws), ws_bytes),
                    "fused_head forward")
         ctx.n, ctx.c = n, c
+        ctx.streamed = SCHEDULE == "streamed"
+        ctx.vocab_chunk = VOCAB_CHUNK
         ctx.embed_dtype = embed.dtype
         ctx.save_for_backward(h, e, t, stat, residual)
         ctx.mark_non_differentiable(pt)
@@ -80,14 +92,23 @@ class _HeadFn(torch.autograd.Function):
         st = _lib.stream_of(h)
         g = (g_obj if g_obj is not None else torch.zeros((), device=dev)).to(torch.float32).reshape(1).contiguous()
         dt = _DTYPES[h.dtype]
-        ws_bytes = lib.alg_head_workspace_size(dt, N, d, V, 2 if residual is not None else 1)
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         dh = torch.empty_like(h)
         de_f32 = ctx.embed_dtype == torch.float32
+        de_dt = _lib.DTYPE_F32 if de_f32 else _lib.DTYPE_BF16
         dE = torch.empty((V, d), dtype=torch.float32 if de_f32 else torch.bfloat16, device=dev)
+        if ctx.streamed:
+            ws_bytes = lib.alg_head_streamed_workspace_size(dt, N, d, V, ctx.vocab_chunk)
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+            _lib.check(lib.alg_head_bwd_streamed(st, dt, N, d, V, _lib.ptr(h), _lib.ptr(e), _lib.ptr(t), _lib.ptr(stat),
+                                                 _lib.ptr(g), ctx.n, ctx.c, ctx.vocab_chunk, _lib.ptr(dh), _lib.ptr(dE),
+                                                 de_dt, _lib.ptr(ws), ws_bytes),
+                       "fused_head backward (streamed)")
+            return dh, dE.to(ctx.embed_dtype), None, None, None
+        ws_bytes = lib.alg_head_workspace_size(dt, N, d, V, 2 if residual is not None else 1)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         _lib.check(lib.alg_head_bwd(st, dt, N, d, V, _lib.ptr(h), _lib.ptr(e), _lib.ptr(t), _lib.ptr(stat), _lib.ptr(g),
-                                    ctx.n, ctx.c, _lib.ptr(residual), _lib.ptr(dh), _lib.ptr(dE),
-                                    _lib.DTYPE_F32 if de_f32 else _lib.DTYPE_BF16, _lib.ptr(ws), ws_bytes),
+                                    ctx.n, ctx.c, _lib.ptr(residual), _lib.ptr(dh), _lib.ptr(dE), de_dt,
+                                    _lib.ptr(ws), ws_bytes),
                    "fused_head backward")
         return dh, dE.to(ctx.embed_dtype), None, None, None
 

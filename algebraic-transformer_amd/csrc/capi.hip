@@ -563,6 +563,51 @@ size_t alg_head_workspace_size(int dtype, int N, int d, int V, int pass) {
   return head_ws(N, d, V, pass ? 1 : 0, pass == 2).total;
 }
 
+// Streamed backward (alg_head_bwd_streamed): the vocabulary in chunks of `chunk` rows. The
+// default chunk gives one chunk's dE product at least 256 tiles of 256 x 256 (one per CU).
+// Workspace: [logit gradient of one chunk: bf16 Npad x pitch(chunk), or f32 N x pitch(chunk)]
+// (+ bf16, several chunks: [dh accumulator f32 N*d]) (+ bf16: [f32 tiles of the token-split
+// dE tail, sized for the larger of the two chunk plans]).
+struct HeadStreamWs {
+  size_t dz, acc, de_part, total;
+  int chunk;
+};
+static int head_stream_chunk(int d, int V, int vocab_chunk) {
+  int chunk = vocab_chunk;
+  if (chunk == 0) {
+    const int dtiles = (d + alg::HT_N - 1) / alg::HT_N;
+    chunk = alg::HT_M * ((256 + dtiles - 1) / dtiles);
+  }
+  return std::min(chunk, V);
+}
+static HeadStreamWs head_stream_ws(int dtype, int N, int d, int V, int vocab_chunk) {
+  HeadStreamWs w;
+  w.chunk = head_stream_chunk(d, V, vocab_chunk);
+  const int nchunks = (V + w.chunk - 1) / w.chunk;
+  const size_t pitch = (size_t)alg::head_vocab_pitch(w.chunk);
+  w.dz = 0;
+  if (dtype == ALG_DTYPE_F32) {
+    w.acc = w.de_part = w.total = align256((size_t)N * pitch * sizeof(float));
+    return w;
+  }
+  w.acc = align256((size_t)alg::head_token_pad(N) * pitch * 2);
+  w.de_part = w.acc + (nchunks > 1 ? align256((size_t)N * d * sizeof(float)) : 0);
+  size_t de_bytes = 0;
+  for (int vc : {w.chunk, V - (nchunks - 1) * w.chunk}) {
+    const alg::HeadDePlan pl = alg::head_de_plan(N, d, vc);
+    if (pl.split > 1)
+      de_bytes = std::max(de_bytes, (size_t)(pl.tiles - pl.full) * pl.split * alg::HT_M * alg::HT_N * sizeof(float));
+  }
+  w.total = w.de_part + align256(de_bytes);
+  return w;
+}
+
+size_t alg_head_streamed_workspace_size(int dtype, int N, int d, int V, int vocab_chunk) {
+  if (N <= 0 || d <= 0 || V <= 0 || vocab_chunk < 0 || vocab_chunk % alg::HT_M) return 0;
+  if (dtype != ALG_DTYPE_BF16 && dtype != ALG_DTYPE_F32) return 0;
+  return head_stream_ws(dtype, N, d, V, vocab_chunk).total;
+}
+
 size_t alg_head_residual_size(int N, int d, int V) {
   if (N <= 0 || d <= 0 || V <= 0) return 0;
   return head_ws(N, d, V, 0, true).res_total;
@@ -819,6 +864,45 @@ int alg_head_bwd(alg_stream_t stream, int dtype, int N, int d, int V, const void
   p.de_kchunk = ws.de.kchunk;
   p.de_part = ws.de.split > 1 ? reinterpret_cast<float*>(w + ws.de_part) : nullptr;
   return hip_status(alg::launch_head_bwd(p, (hipStream_t)stream), "alg_head_bwd");
+}
+
+int alg_head_bwd_streamed(alg_stream_t stream, int dtype, int N, int d, int V, const void* h, const void* E,
+                          const int32_t* targets, const float* stat, const float* g, int n, float c, int vocab_chunk,
+                          void* dh, void* dE, int dE_dtype, void* workspace, size_t workspace_bytes) {
+  int rc = check_head(N, d, V, n, c);
+  if (!rc) rc = check_head_dtype(dtype, nullptr);
+  if (rc) return rc;
+  if (vocab_chunk < 0 || vocab_chunk % alg::HT_M)
+    return fail(ALG_ERR_INVALID, "vocab_chunk %d: 0 (the default) or a positive multiple of %d", vocab_chunk,
+                alg::HT_M);
+  const bool f32 = dtype == ALG_DTYPE_F32;
+  if (!h || !E || !targets || !stat || !g || !dh || !dE) return fail(ALG_ERR_INVALID, "null argument");
+  if (!aligned16({h, E, dh, dE, workspace})) return fail(ALG_ERR_INVALID, "matrices must be 16-byte aligned");
+  if (dE_dtype != ALG_DTYPE_BF16 && dE_dtype != ALG_DTYPE_F32) return fail(ALG_ERR_INVALID, "dE dtype must be bf16 or f32");
+  const HeadStreamWs ws = head_stream_ws(dtype, N, d, V, vocab_chunk);
+  if (!workspace || workspace_bytes < ws.total)
+    return fail(ALG_ERR_INVALID, "workspace too small: need %zu bytes", ws.total);
+  HeadWs hw;
+  std::memset(&hw, 0, sizeof hw);
+  hw.Npad = f32 ? N : alg::head_token_pad(N);
+  hw.Vp = alg::head_vocab_pitch(V);
+  alg::HeadParams p = head_params(dtype, N, d, V, h, E, targets, n, c, workspace, hw);
+  p.partial = p.obj_part = nullptr;  // forward buffers
+  p.stat = const_cast<float*>(stat);
+  p.g = g;
+  p.dE = dE;
+  p.dE_f32 = dE_dtype == ALG_DTYPE_F32;
+  char* w = static_cast<char*>(workspace);
+  if (f32) {
+    p.dz32 = reinterpret_cast<float*>(w + ws.dz);
+    p.dh32 = static_cast<float*>(dh);
+    return hip_status(alg::launch_head_bwd_f32_streamed(p, ws.chunk, (hipStream_t)stream), "alg_head_bwd_streamed");
+  }
+  p.dzt = reinterpret_cast<bf16*>(w + ws.dz);
+  p.dh = static_cast<bf16*>(dh);
+  p.dh_part = ws.de_part > ws.acc ? reinterpret_cast<float*>(w + ws.acc) : nullptr;
+  p.de_part = ws.total > ws.de_part ? reinterpret_cast<float*>(w + ws.de_part) : nullptr;
+  return hip_status(alg::launch_head_bwd_streamed(p, ws.chunk, (hipStream_t)stream), "alg_head_bwd_streamed");
 }
 
 }  // extern "C"

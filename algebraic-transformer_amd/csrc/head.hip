@@ -41,6 +41,44 @@ __device__ __forceinline__ float head_w(float z, const HeadParams& p, float& r) 
   return t;
 }
 
+// Token-major staging of a wave's WTM (v) x WTN (tok) block of a bf16 (tok, v) matrix (the
+// forward's residual U, the recompute schedules' logit gradient dZ): the wave writes its block
+// into its own share of the idle pipeline buffers as [tok][v] rows, 16-byte chunks
+// XOR-swizzled by the token, then stores it with 16-byte stores that cover whole token rows
+// (full cache lines) per instruction.
+constexpr int UCH = HC::WTM / 8;          // 16-byte chunks per staged token row
+constexpr int UWAVE = HC::WTM * HC::WTN;  // staged elements per wave
+static_assert(UCH <= 64 && 64 % UCH == 0 && (UCH & (UCH - 1)) == 0, "staged row width");
+__device__ __forceinline__ int ustage_at(int tl, int vl) {
+  return tl * HC::WTM + (((vl >> 3) ^ (tl & (UCH - 1))) << 3) + (vl & 7);
+}
+
+// Stores the staged block: token rows tok0 + (0..WTN-1), vocabulary entries v0 + (0..WTM-1) of
+// out (row pitch Vp, Npad rows). AUX is the store's cache policy.
+template <int AUX>
+__device__ __forceinline__ void store_staged_tokmajor(const bf16* ub, bf16* out, int Npad, int Vp, int tok0, int v0,
+                                                      int lane) {
+  const size_t ubase = (size_t)tok0 * Vp + v0;
+  const size_t rest = ((size_t)Npad * Vp - ubase) * 2;  // bytes of out from the base
+  const __amdgpu_buffer_rsrc_t urs = __builtin_amdgcn_make_buffer_rsrc(
+      out + ubase, (short)0, (int)std::min<size_t>(rest, 0x7fffffff), BUF_RSRC_WORD3);
+  constexpr int RPS = 64 / UCH;  // token rows per store instruction
+  const int ch = lane % UCH;
+  const int voff = ((lane / UCH) * Vp + ch * 8) * 2;
+  // The row offset goes into the per-lane offset and the scalar offset stays the constant
+  // 0. A 16-byte store needs one wait state before a VALU instruction may overwrite its
+  // data registers; the compiler inserts it only when the scalar offset is not an SGPR.
+  // With the row offset in an SGPR (an earlier form of this loop) the next instruction
+  // reused the data registers of the store just issued, and on gfx950 the store wrote the
+  // new values (measured: about 0.1 % of the U entries replaced by address arithmetic).
+#pragma unroll
+  for (int j = 0; j < HC::WTN / RPS; ++j) {
+    const int tl = RPS * j + lane / UCH;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(ub + ustage_at(tl, ch * 8));
+    __builtin_amdgcn_raw_buffer_store_b128(v, urs, voff + RPS * j * Vp * 2, 0, AUX);
+  }
+}
+
 // z^T = E h^T with the forward epilogue (row sums, target logit, optional U residual).
 // L2N > 0 fixes n = 2^L2N at compile time (0: taken from the parameters).
 // acc[mb][nb][4g + e] for the row offset dt = mb*32 + 8g + e (bit 2 of dt, the lane half,
@@ -72,15 +110,10 @@ __global__ __launch_bounds__(NT, 1) void head_fwd_kernel(HeadParams p) {
   const float inv_c = p.inv_c, clamp = p.clamp;
   const int vrow0 = m0 + wm * HC::WTM;  // first vocab row of this wave
   // Interior tile (every row and column live); WITH_U also stores the residual. U is
-  // token-major (element (tok, v) at tok * Vp + v). Each wave stages its WTM (v) x WTN (tok)
-  // block of U in its own share of the (now idle) pipeline buffers as [tok][v] rows,
-  // 16-byte chunks XOR-swizzled by the token, then writes it back with 16-byte stores that
-  // cover whole token rows (full cache lines) per instruction, marked non-temporal so the
-  // 1 GB stream of U does not evict the E / h panels the GEMM is reusing from L2.
-  constexpr int UCH = HC::WTM / 8;          // 16-byte chunks per staged token row
-  constexpr int UWAVE = HC::WTM * HC::WTN;  // staged elements per wave
+  // token-major (element (tok, v) at tok * Vp + v), staged per wave and written with 16-byte
+  // stores marked non-temporal so the 1 GB stream of U does not evict the E / h panels the
+  // GEMM is reusing from L2.
   constexpr int NWAVES = HC::THREADS / 64;
-  static_assert(UCH <= 64 && 64 % UCH == 0 && (UCH & (UCH - 1)) == 0, "staged row width");
   static_assert(NWAVES * UWAVE * 2 <= 2 * (int)sizeof(s0), "staging fits the pipeline buffers");
   static_assert((NWAVES / 2) * UWAVE * 2 <= (int)sizeof(s0) || NWAVES == 1, "half the waves per stage");
   auto interior = [&](auto with_u) {
@@ -92,7 +125,6 @@ __global__ __launch_bounds__(NT, 1) void head_fwd_kernel(HeadParams p) {
       ub = reinterpret_cast<bf16*>(wi < NWAVES / 2 ? static_cast<void*>(&s0) : static_cast<void*>(&s1)) +
            (wi % (NWAVES / 2)) * UWAVE;
     }
-    auto ub_at = [](int tl, int vl) { return tl * HC::WTM + (((vl >> 3) ^ (tl & (UCH - 1))) << 3) + (vl & 7); };
 #pragma unroll
     for (int nb = 0; nb < HC::NB; ++nb) {
       const int col = wn * HC::WTN + nb * 32 + l32;
@@ -117,7 +149,7 @@ __global__ __launch_bounds__(NT, 1) void head_fwd_kernel(HeadParams p) {
             u32x2 pk;
             pk[0] = pack_bf16x2(u[0], u[1]);
             pk[1] = pack_bf16x2(u[2], u[3]);
-            *reinterpret_cast<u32x2*>(ub + ub_at(nb * 32 + l32, mb * 32 + 8 * g + 4 * h)) = pk;
+            *reinterpret_cast<u32x2*>(ub + ustage_at(nb * 32 + l32, mb * 32 + 8 * g + 4 * h)) = pk;
           }
         }
       }
@@ -135,28 +167,8 @@ __global__ __launch_bounds__(NT, 1) void head_fwd_kernel(HeadParams p) {
       part += xor32(part);
       if (h == 0) red[wm][col] = part;
     }
-    if constexpr (WITH_U) {
-      // Rows of this wave's block: tokens n0 + wn*64 + (0..63), vocabulary vrow0 + (0..127).
-      const size_t ubase = (size_t)(n0 + wn * HC::WTN) * p.Vp + vrow0;
-      const size_t rest = ((size_t)p.Npad * p.Vp - ubase) * 2;  // bytes of U from the base
-      const __amdgpu_buffer_rsrc_t urs = __builtin_amdgcn_make_buffer_rsrc(
-          p.ut + ubase, (short)0, (int)std::min<size_t>(rest, 0x7fffffff), BUF_RSRC_WORD3);
-      constexpr int RPS = 64 / UCH;  // token rows per store instruction
-      const int ch = lane % UCH;
-      const int voff = ((lane / UCH) * p.Vp + ch * 8) * 2;
-      // The row offset goes into the per-lane offset and the scalar offset stays the constant
-      // 0. A 16-byte store needs one wait state before a VALU instruction may overwrite its
-      // data registers; the compiler inserts it only when the scalar offset is not an SGPR.
-      // With the row offset in an SGPR (an earlier form of this loop) the next instruction
-      // reused the data registers of the store just issued, and on gfx950 the store wrote the
-      // new values (measured: about 0.1 % of the U entries replaced by address arithmetic).
-#pragma unroll
-      for (int j = 0; j < HC::WTN / RPS; ++j) {
-        const int tl = RPS * j + lane / UCH;
-        const u32x4 v = *reinterpret_cast<const u32x4*>(ub + ub_at(tl, ch * 8));
-        __builtin_amdgcn_raw_buffer_store_b128(v, urs, voff + RPS * j * p.Vp * 2, 0, BUF_NT);
-      }
-    }
+    // Rows of this wave's block: tokens n0 + wn*64 + (0..63), vocabulary vrow0 + (0..127).
+    if constexpr (WITH_U) store_staged_tokmajor<BUF_NT>(ub, p.ut, p.Npad, p.Vp, n0 + wn * HC::WTN, vrow0, lane);
   };
   if (m0 + HT_M <= p.V && n0 + HT_N <= p.N) {
     if (p.ut) interior(std::true_type{});
@@ -451,7 +463,22 @@ __global__ __launch_bounds__(256) void head_obj_kernel(HeadParams p, int nblocks
   if (threadIdx.x == 0) p.obj[0] = red[0] / (float)p.N;
 }
 
-// Recompute schedule: z^T again, dZ^T = bf16(s (p - y) r).
+// This wave's share of the pipeline buffers (idle after the main loop; the caller has passed
+// a barrier after which no wave reads them): half the waves stage in s0, half in s1.
+template <class Stage>
+__device__ __forceinline__ bf16* wave_stage(Stage& s0, Stage& s1, int wm, int wn) {
+  constexpr int NWAVES = HC::THREADS / 64, UWAVE = HC::WTM * HC::WTN;
+  static_assert((NWAVES / 2) * UWAVE * 2 <= (int)sizeof(Stage), "half the waves per stage");
+  const int wi = wm * HC::WN + wn;
+  return reinterpret_cast<bf16*>(wi < NWAVES / 2 ? static_cast<void*>(&s0) : static_cast<void*>(&s1)) +
+         (wi % (NWAVES / 2)) * UWAVE;
+}
+
+// Recompute schedules: z^T again, dZ^T = bf16(s (p - y) r), token-major. L2N > 0 fixes
+// n = 2^L2N at compile time (0: taken from the parameters). Interior tiles stage each wave's
+// block and write whole token rows with 16-byte stores (default cache policy: the dh and dE
+// products read dZ right after); edge tiles store element by element.
+template <int L2N>
 __global__ __launch_bounds__(NT, 1) void head_dz_kernel(HeadParams p) {
   __shared__ __attribute__((aligned(16))) GemmStage<KMAJOR, KMAJOR, HC> s0, s1;
   const int nbm = (p.V + HT_M - 1) / HT_M, nbn = p.Npad / HT_N;
@@ -465,6 +492,39 @@ __global__ __launch_bounds__(NT, 1) void head_dz_kernel(HeadParams p) {
   int wm, wn;
   wave_coords<HC>(wm, wn);
   const float scale = head_grad_scale(p);
+  const float inv_c = p.inv_c, clamp = p.clamp;
+  const int vrow0 = m0 + wm * HC::WTM;  // first vocab row of this wave
+  if (m0 + HT_M <= p.V && n0 + HT_N <= p.N) {
+    __syncthreads();  // every wave is done reading the pipeline buffers
+    bf16* ub = wave_stage(s0, s1, wm, wn);
+#pragma unroll
+    for (int nb = 0; nb < HC::NB; ++nb) {
+      const int tok = n0 + wn * HC::WTN + nb * 32 + l32;
+      const int dt = p.targets[tok] - p.v_off - vrow0 - 4 * h;  // target row relative to this lane's rows
+      const float st = p.stat[tok];
+#pragma unroll
+      for (int mb = 0; mb < HC::MB; ++mb) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float u[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float x = fminf(acc[mb][nb][4 * g + e] * inv_c, clamp);
+            float r;
+            const float t = pow2n<L2N>(rho_fast(x, r) * st, p.log2n);
+            const float y = dt == mb * 32 + 8 * g + e ? 1.0f : 0.0f;
+            u[e] = (t - y) * r * scale;
+          }
+          u32x2 pk;
+          pk[0] = pack_bf16x2(u[0], u[1]);
+          pk[1] = pack_bf16x2(u[2], u[3]);
+          *reinterpret_cast<u32x2*>(ub + ustage_at(nb * 32 + l32, mb * 32 + 8 * g + 4 * h)) = pk;
+        }
+      }
+    }
+    store_staged_tokmajor<0>(ub, p.dzt, p.Npad, p.Vp, n0 + wn * HC::WTN, vrow0, lane);
+    return;
+  }
 #pragma unroll
   for (int nb = 0; nb < HC::NB; ++nb) {
     const int tok = n0 + wn * HC::WTN + nb * 32 + l32;
@@ -475,13 +535,12 @@ __global__ __launch_bounds__(NT, 1) void head_dz_kernel(HeadParams p) {
     for (int mb = 0; mb < HC::MB; ++mb) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int v = m0 + wm * HC::WTM + mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+        const int v = vrow0 + mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
         if (v >= p.V) continue;
-        const float x = fminf(acc[mb][nb][i] * p.inv_c, p.clamp);
+        const float x = fminf(acc[mb][nb][i] * inv_c, clamp);
         float r;
-        float t = rho_fast(x, r) * st;
-        for (int e = 0; e < p.log2n; ++e) t = t * t;
-        const float y = (v == tgt) ? 1.0f : 0.0f;
+        const float t = pow2n<L2N>(rho_fast(x, r) * st, p.log2n);
+        const float y = (v + p.v_off == tgt) ? 1.0f : 0.0f;
         if (live) p.dzt[(size_t)tok * p.Vp + v] = f2bf((t - y) * r * scale);  // token-major
       }
     }
@@ -536,22 +595,16 @@ __device__ __forceinline__ void store_block_bf16(const floatx16 (&acc)[HC::MB][H
   }
 }
 
-// This wave's share of the pipeline buffers (idle after the main loop; the caller has passed
-// a barrier after which no wave reads them): half the waves stage in s0, half in s1.
-template <class Stage>
-__device__ __forceinline__ bf16* wave_stage(Stage& s0, Stage& s1, int wm, int wn) {
-  constexpr int NWAVES = HC::THREADS / 64, UWAVE = HC::WTM * HC::WTN;
-  static_assert((NWAVES / 2) * UWAVE * 2 <= (int)sizeof(Stage), "half the waves per stage");
-  const int wi = wm * HC::WN + wn;
-  return reinterpret_cast<bf16*>(wi < NWAVES / 2 ? static_cast<void*>(&s0) : static_cast<void*>(&s1)) +
-         (wi % (NWAVES / 2)) * UWAVE;
-}
 
 // dh = (U' or dZ) E: A stored token-major [n][v] (k-contiguous), B = E stored [v][d]
 // (n-contiguous). The residual schedule scales token rows by s/l. When the product has too
 // few output tiles to fill the chip (small N*d, long V) the vocabulary is split into
 // dh_split ranges: each workgroup writes its f32 partial and head_dh_reduce_kernel sums them
-// in a fixed order before the scale and the rounding.
+// in a fixed order before the scale and the rounding. ACC (the streamed schedule's later
+// vocabulary chunks, p.dh_accum 1 or 2): the tile of the f32 accumulator p.dh_part is read
+// whole after the main loop (all loads issued before the first add) and added to the product,
+// which then goes back to the accumulator (dh_accum 1) or, rounded, to dh (dh_accum 2).
+template <bool ACC>
 __global__ __launch_bounds__(NT, 1) void head_dh_kernel(HeadParams p) {
   __shared__ __attribute__((aligned(16))) GemmStage<KMAJOR, MNMAJOR, HC> s0, s1;
   const int nbm = p.Npad / HT_M, nbn = (p.d + HT_N - 1) / HT_N;
@@ -563,14 +616,40 @@ __global__ __launch_bounds__(NT, 1) void head_dh_kernel(HeadParams p) {
   const int kbeg = min(p.V, split * p.dh_kchunk), kend = min(p.V, kbeg + p.dh_kchunk);
   const bf16* a = p.ut ? p.ut : p.dzt;
   GemmOperand A{a, p.Vp, p.N, p.V, (long)p.Npad * p.Vp}, B{p.E, p.d, p.V, p.d, (long)p.V * p.d};
-  floatx16 acc[HC::MB][HC::NB];
-  gemm_mainloop<KMAJOR, MNMAJOR, HC>(s0, s1, A, B, m0, n0, kbeg, kend, acc);
   const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
   int wm, wn;
   wave_coords<HC>(wm, wn);
-  const float s = p.ut ? head_grad_scale(p) : 1.0f;
   float* part = p.dh_part ? p.dh_part + (size_t)split * p.N * p.d : nullptr;
-  if (!part && m0 + HT_M <= p.N && n0 + HT_N <= p.d) {
+  floatx16 acc[HC::MB][HC::NB];
+  gemm_mainloop<KMAJOR, MNMAJOR, HC>(s0, s1, A, B, m0, n0, kbeg, kend, acc);
+  if constexpr (ACC) {
+    // One 32 x 32 block at a time: its 16 loads are issued together, then added, and (dh_accum
+    // 1) stored back to the accumulator.
+    const bool back = p.dh_accum == 1;
+#pragma unroll
+    for (int mb = 0; mb < HC::MB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < HC::NB; ++nb) {
+        const int r0 = m0 + wm * HC::WTM + mb * 32 + 4 * h, col = n0 + wn * HC::WTN + nb * 32 + l32;
+        float* blk = part + (size_t)r0 * p.d + col;
+        float pv[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int dr = 8 * (i >> 2) + (i & 3);
+          pv[i] = r0 + dr < p.N && col < p.d ? blk[dr * p.d] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int dr = 8 * (i >> 2) + (i & 3);
+          acc[mb][nb][i] += pv[i];
+          if (back && r0 + dr < p.N && col < p.d) blk[dr * p.d] = acc[mb][nb][i];
+        }
+      }
+    if (back) return;
+  }
+  const float s = p.ut ? head_grad_scale(p) : 1.0f;
+  const bool to_dh = !part || ACC;  // bf16 output (ACC here: the last chunk)
+  if (to_dh && m0 + HT_M <= p.N && n0 + HT_N <= p.d) {
     // Interior tile, bf16 output: the row scales s/l once per row (the expression of
     // head_hscale_kernel), then the staged 16-byte stores.
     __shared__ float fsc[HT_M];
@@ -592,8 +671,9 @@ __global__ __launch_bounds__(NT, 1) void head_dh_kernel(HeadParams p) {
       for (int nb = 0; nb < HC::NB; ++nb) {
         const int col = n0 + wn * HC::WTN + nb * 32 + l32;
         if (col >= p.d) continue;
-        if (part) part[(size_t)tok * p.d + col] = acc[mb][nb][i];
-        else p.dh[(size_t)tok * p.d + col] = f2bf(acc[mb][nb][i] * f);
+        const size_t o = (size_t)tok * p.d + col;
+        if (to_dh) p.dh[o] = f2bf(acc[mb][nb][i] * f);
+        else part[o] = acc[mb][nb][i];
       }
     }
   }
@@ -806,27 +886,26 @@ hipError_t launch_head_eval(const HeadParams& p, hipStream_t st) {
   return launch_head_eval_stats(p, head_vocab_tiles(p.V), st);
 }
 
-hipError_t launch_head_bwd(const HeadParams& p, hipStream_t st) {
-  if (p.ut) {
-    const size_t chunks = (size_t)p.N * p.d / 8;
-    const int blocks = (int)std::min<size_t>((chunks + 255) / 256, 8192);
-    { KTimer t("head_hscale", st); hipLaunchKernelGGL(head_hscale_kernel, dim3(blocks), dim3(256), 0, st, p); }
-  } else {
-    const int tiles = head_vocab_tiles(p.V) * (p.Npad / HT_N);
-    { KTimer t("head_dz", st); hipLaunchKernelGGL(head_dz_kernel, dim3(tiles), dim3(NT), 0, st, p); }
-  }
+// dh = (U' or dZ) E, and the sum over vocabulary splits when the product is split.
+static void launch_head_dh(const HeadParams& p, hipStream_t st) {
   const int dtiles = (p.d + HT_N - 1) / HT_N;
   {
     KTimer t("head_dh", st);
-    hipLaunchKernelGGL(head_dh_kernel, dim3((p.Npad / HT_M) * dtiles * p.dh_split), dim3(NT), 0, st, p);
+    const dim3 grid((p.Npad / HT_M) * dtiles * p.dh_split);
+    if (p.dh_accum) hipLaunchKernelGGL(head_dh_kernel<true>, grid, dim3(NT), 0, st, p);
+    else hipLaunchKernelGGL(head_dh_kernel<false>, grid, dim3(NT), 0, st, p);
   }
-  if (p.dh_part) {
+  if (p.dh_split > 1) {
     const size_t chunks = (size_t)p.N * p.d / 8;
     const int blocks = (int)std::min<size_t>((chunks + 255) / 256, 4096);
     KTimer t("head_dh_reduce", st);
     hipLaunchKernelGGL(head_dh_reduce_kernel, dim3(blocks), dim3(256), 0, st, p);
   }
-  const int de_tiles = head_vocab_tiles(p.V) * dtiles;
+}
+
+// dE = (U' or dZ)^T (hs or h), with the token split of head_de_plan when p carries one.
+static void launch_head_de(const HeadParams& p, hipStream_t st) {
+  const int de_tiles = head_vocab_tiles(p.V) * ((p.d + HT_N - 1) / HT_N);
   if (p.de_split > 1 && p.de_part) {
     const int tail = de_tiles - p.de_full;
     { KTimer t("head_de", st); hipLaunchKernelGGL(head_de_kernel, dim3(p.de_full + tail * p.de_split), dim3(NT), 0, st, p); }
@@ -836,6 +915,56 @@ hipError_t launch_head_bwd(const HeadParams& p, hipStream_t st) {
     q.de_full = de_tiles;
     q.de_split = 1;
     { KTimer t("head_de", st); hipLaunchKernelGGL(head_de_kernel, dim3(de_tiles), dim3(NT), 0, st, q); }
+  }
+}
+
+static void launch_head_dz(const HeadParams& p, hipStream_t st) {
+  const int tiles = head_vocab_tiles(p.V) * (p.Npad / HT_N);
+  KTimer t("head_dz", st);
+  if (p.log2n == 3) hipLaunchKernelGGL(head_dz_kernel<3>, dim3(tiles), dim3(NT), 0, st, p);
+  else hipLaunchKernelGGL(head_dz_kernel<0>, dim3(tiles), dim3(NT), 0, st, p);
+}
+
+hipError_t launch_head_bwd(const HeadParams& p, hipStream_t st) {
+  if (p.ut) {
+    const size_t chunks = (size_t)p.N * p.d / 8;
+    const int blocks = (int)std::min<size_t>((chunks + 255) / 256, 8192);
+    { KTimer t("head_hscale", st); hipLaunchKernelGGL(head_hscale_kernel, dim3(blocks), dim3(256), 0, st, p); }
+  } else {
+    launch_head_dz(p, st);
+  }
+  launch_head_dh(p, st);
+  launch_head_de(p, st);
+  return hipGetLastError();
+}
+
+HeadParams head_vocab_chunk(const HeadParams& p, int v0, int vc) {
+  HeadParams q = p;
+  q.V = vc;
+  q.Vp = head_vocab_pitch(vc);
+  q.v_off = v0;
+  const size_t rows = (size_t)v0 * p.d;
+  if (p.E) q.E = p.E + rows;
+  if (p.E32) q.E32 = p.E32 + rows;
+  q.dE = p.dE_f32 ? static_cast<void*>(static_cast<float*>(p.dE) + rows) : static_cast<void*>(static_cast<bf16*>(p.dE) + rows);
+  return q;
+}
+
+hipError_t launch_head_bwd_streamed(const HeadParams& p, int chunk, hipStream_t st) {
+  const int nchunks = (p.V + chunk - 1) / chunk;
+  for (int k = 0; k < nchunks; ++k) {
+    HeadParams q = head_vocab_chunk(p, k * chunk, std::min(chunk, p.V - k * chunk));
+    q.dh_split = 1;
+    q.dh_kchunk = head_dh_kchunk(q.V, 1);
+    q.dh_part = nchunks > 1 ? p.dh_part : nullptr;
+    q.dh_accum = k == 0 ? 0 : (k == nchunks - 1 ? 2 : 1);
+    const HeadDePlan de = head_de_plan(p.N, p.d, q.V);
+    q.de_full = de.full;
+    q.de_split = de.split;
+    q.de_kchunk = de.kchunk;
+    launch_head_dz(q, st);
+    launch_head_dh(q, st);
+    launch_head_de(q, st);
   }
   return hipGetLastError();
 }

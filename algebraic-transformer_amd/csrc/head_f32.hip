@@ -224,7 +224,7 @@ __global__ __launch_bounds__(F_NT) void head_dz_f32_kernel(HeadParams p) {
         if (v >= p.V) continue;
         float r;
         const float t = pow2n<0>(rho_fast(fminf(acc[mb][nb][i] * p.inv_c, p.clamp), r) * st, p.log2n);
-        const float y = v == tgt ? 1.0f : 0.0f;
+        const float y = v + p.v_off == tgt ? 1.0f : 0.0f;
         p.dz32[(size_t)tok * p.Vp + v] = (t - y) * r * scale;
       }
     }
@@ -254,7 +254,9 @@ __global__ __launch_bounds__(F_NT) void head_dh_f32_kernel(HeadParams p) {
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
         const int col = n0 + w.wn * F_WT + nb * 32 + w.l32;
-        if (col < p.d) out[(size_t)tok * p.d + col] = acc[mb][nb][i];
+        if (col >= p.d) continue;
+        if (p.dh_accum) out[(size_t)tok * p.d + col] += acc[mb][nb][i];  // a later vocabulary chunk
+        else out[(size_t)tok * p.d + col] = acc[mb][nb][i];
       }
     }
 }
@@ -419,6 +421,26 @@ hipError_t launch_head_bwd_f32(const HeadParams& p, hipStream_t st) {
   {
     KTimer t("head_de_f32", st);
     hipLaunchKernelGGL(head_de_f32_kernel, dim3(head_f32_vocab_tiles(p.V) * nd), dim3(F_NT), 0, st, p);
+  }
+  return hipGetLastError();
+}
+
+// Streamed backward in f32: per vocabulary chunk of `chunk` rows the logit gradient (N,
+// pitch(chunk)) in p.dz32, then the chunk's dh product added into dh32 (written by the first
+// chunk) and its dE rows.
+hipError_t launch_head_bwd_f32_streamed(const HeadParams& p, int chunk, hipStream_t st) {
+  const int ntok = (p.N + F_TM - 1) / F_TM, nd = (p.d + F_TN - 1) / F_TN;
+  const int nchunks = (p.V + chunk - 1) / chunk;
+  for (int k = 0; k < nchunks; ++k) {
+    HeadParams q = head_vocab_chunk(p, k * chunk, std::min(chunk, p.V - k * chunk));
+    q.dh_split = 1;
+    q.dh_kchunk = head_f32_dh_kchunk(q.V, 1);
+    q.dh_part = nullptr;
+    q.dh_accum = k > 0;
+    const int vt = head_f32_vocab_tiles(q.V);
+    { KTimer t("head_dz_f32", st); hipLaunchKernelGGL(head_dz_f32_kernel, dim3(ntok * vt), dim3(F_NT), 0, st, q); }
+    { KTimer t("head_dh_f32", st); hipLaunchKernelGGL(head_dh_f32_kernel, dim3(ntok * nd), dim3(F_NT), 0, st, q); }
+    { KTimer t("head_de_f32", st); hipLaunchKernelGGL(head_de_f32_kernel, dim3(vt * nd), dim3(F_NT), 0, st, q); }
   }
   return hipGetLastError();
 }

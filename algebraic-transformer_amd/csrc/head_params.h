@@ -45,6 +45,12 @@ struct HeadParams {
   int de_full = 0;      // tiles computed whole (all of them when de_split is 1)
   int de_split = 1;     // token ranges per remaining tile
   int de_kchunk = 0;    // tokens per range (a multiple of 128)
+  // Streamed backward (one vocabulary chunk per launch group): E, dE and the logit gradient
+  // cover rows [v_off, v_off + V) of the vocabulary, and the dh product accumulates over
+  // the chunks in an f32 (N, d) buffer.
+  int v_off = 0;        // vocabulary index of E's first row (targets are compared with v + v_off)
+  int dh_accum = 0;     // dh product: 0 writes, 1 adds into the f32 accumulator (dh_part, or
+                        // dh32 for f32 hidden states), 2 writes bf16(accumulator + product)
   float* pmax;          // eval: (ceil(V/HT_M), N) per-vocab-tile maximum logit
   int* pidx;            // eval: (ceil(V/HT_M), N) its vocabulary index
   float* logprob;       // eval: (N,) log p(target)

@@ -33,6 +33,10 @@ struct HeadDePlan {
 HeadDePlan head_de_plan(int N, int d, int V);
 hipError_t launch_head_fwd(const HeadParams& p, hipStream_t st);
 hipError_t launch_head_bwd(const HeadParams& p, hipStream_t st);
+// Rows [v0, v0 + vc) of the vocabulary as a head of its own: E, E32 and dE offset, V = vc,
+// targets compared with v + v0.
+HeadParams head_vocab_chunk(const HeadParams& p, int v0, int vc);
+hipError_t launch_head_bwd_streamed(const HeadParams& p, int chunk, hipStream_t st);
 hipError_t launch_head_eval(const HeadParams& p, hipStream_t st);
 hipError_t launch_head_stats(const HeadParams& p, int vocab_tiles, hipStream_t st);
 hipError_t launch_head_eval_stats(const HeadParams& p, int vocab_tiles, hipStream_t st);
@@ -41,6 +45,7 @@ int head_f32_dh_split(int N, int d, int V);
 int head_f32_dh_kchunk(int V, int split);
 hipError_t launch_head_fwd_f32(const HeadParams& p, hipStream_t st);
 hipError_t launch_head_bwd_f32(const HeadParams& p, hipStream_t st);
+hipError_t launch_head_bwd_f32_streamed(const HeadParams& p, int chunk, hipStream_t st);
 hipError_t launch_head_eval_f32(const HeadParams& p, hipStream_t st);
 int rms_norm_max_d();
 int rms_norm_blocks(int rows);

@@ -338,6 +338,57 @@ def time_eval_head(torch, x, iters=20, warmup=3):
             "stats_ms": round(k["head_eval_stats"], 4)}
 
 
+def time_head_schedules(torch, x, iters=10, warmup=2):
+    """The head's three backward schedules at the C4b shape, fwd+bwd each: "residual" (the
+    default: a bf16 (N, V) residual from the forward, 3 products), "recompute" (the logits
+    recomputed into an (N, V) bf16 logit-gradient workspace, 4 products) and "streamed" (the
+    logits recomputed one vocabulary chunk at a time, no (N, V) block). `peak_extra_bytes` is
+    the device memory the call allocates beyond its inputs at its peak (torch's allocator
+    statistics), `nv_block_bytes` the (N, V)-sized buffer the schedule keeps."""
+    from algebraic_amd import _lib
+    from algebraic_amd.kernels import fused_head as FH
+    lib = _lib.load()
+    h, E, t = (x[k].detach() for k in ("h", "E", "t"))
+    h = h.clone().requires_grad_(True)
+    E = E.clone().requires_grad_(True)
+    N, d, V = HEAD["N"], HEAD["d"], HEAD["V"]
+
+    def call():
+        obj, _ = FH.fused_head(h, E, t, kind="alg_ce", n=HEAD["n"], c=HEAD["c"])
+        return torch.autograd.grad(obj, (h, E))
+    saved = FH.SCHEDULE, FH.VOCAB_CHUNK
+    out = {"workload": "fused alg_ce head fwd+bwd N16384 d2048 V32000 (C4b shape) per backward schedule"}
+    nv = {"residual": lib.alg_head_residual_size(N, d, V),
+          "recompute": lib.alg_head_workspace_size(_lib.DTYPE_BF16, N, d, V, 1),
+          "streamed": 0}
+    try:
+        for sched in FH.SCHEDULES:
+            FH.SCHEDULE, FH.VOCAB_CHUNK = sched, 0
+            for _ in range(warmup):
+                call()
+            torch.cuda.synchronize()
+            base = torch.cuda.memory_allocated()
+            torch.cuda.reset_peak_memory_stats()
+            call()
+            torch.cuda.synchronize()
+            peak = torch.cuda.max_memory_allocated() - base
+            ts = []
+            for _ in range(iters):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                call()
+                e1.record()
+                e1.synchronize()
+                ts.append(e0.elapsed_time(e1))
+            ms = sorted(ts)[len(ts) // 2]
+            out[sched] = {"ms": round(ms, 4), "tflops": round(head_flops(**HEAD) / (ms * 1e-3) / 1e12, 3),
+                          "peak_extra_bytes": int(peak), "nv_block_bytes": int(nv[sched])}
+        out["streamed"]["workspace_bytes"] = int(lib.alg_head_streamed_workspace_size(_lib.DTYPE_BF16, N, d, V, 0))
+    finally:
+        FH.SCHEDULE, FH.VOCAB_CHUNK = saved
+    return out
+
+
 def time_final_norm(torch, x, iters=20, warmup=3):
     """Final RMS norm with gain ahead of the head (model.py:208) at the C4b shape (16384 rows of
     2048): forward reads x, writes y (+ 1/rms); the VJP reads x, dy, writes dx (+ gain partials)."""
@@ -564,7 +615,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip timing BASELINE configs 1, 2, 3 and 5 beside the headline")
-    ap.add_argument("--only", choices=["attn", "head", "step", "neighbours", "c3"],
+    ap.add_argument("--only", choices=["attn", "head", "step", "neighbours", "c3", "head_schedules"],
                     help="run only W+K launches of one part (for profiler runs) and print its time; "
                          "'c3' is the attention fwd+bwd of BASELINE config 3 (D = 64); "
                          "'neighbours' runs the timings of the fused prologue, eval head, final norm "
@@ -589,6 +640,9 @@ def main():
 
     K, W = args.steps, args.warmup
     log = lambda msg: print(f"bench: {msg}", file=sys.stderr, flush=True)
+    if args.only == "head_schedules":
+        print(json.dumps({"only": "head_schedules", **time_head_schedules(torch, x, iters=K, warmup=W)}), flush=True)
+        return 0
     if args.only == "neighbours":
         out = {"only": "neighbours", "prologue": time_prologue(torch, dev), "eval_head": time_eval_head(torch, x),
                "final_norm": time_final_norm(torch, x), "ffn": time_ffn(torch, dev)}
@@ -696,6 +750,7 @@ def main():
         out["layout_bthd"] = time_layout_bthd(torch, x, K, 1)
         out["layout_bthd"]["vs_bhtd"] = round(out["attn"]["ms"] / out["layout_bthd"]["ms"], 4)
         out["eval_head"] = time_eval_head(torch, x)
+        out["head_schedules"] = time_head_schedules(torch, x)
         out["final_norm"] = time_final_norm(torch, x)
         out["ffn"] = time_ffn(torch, dev)
     if not args.no_cpu_baseline:

@@ -272,6 +272,22 @@ int alg_head_bwd(alg_stream_t stream, int dtype, int N, int d, int V,
                  const float* g, int n, float c, const void* residual, void* dh, void* dE, int dE_dtype,
                  void* workspace, size_t workspace_bytes);
 
+/* Head backward with the vocabulary streamed, fused_head.py:120-156, 194-216, 247-254 without
+ * the (N, V) logit-gradient block the reference writes (dz_ref, fused_head.py:145-146) and
+ * feeds to XLA's dE product (:215). Arguments as alg_head_bwd without a residual (the forward
+ * ran with residual NULL). The vocabulary is processed in chunks of vocab_chunk rows (0: the
+ * default, enough rows for one chunk's dE product to fill the chip, 8192 at d = 2048; else a
+ * positive multiple of 256, ALG_ERR_INVALID otherwise): per chunk the logits are recomputed,
+ * the chunk's logit gradient is formed in the workspace, its dh product is accumulated in f32
+ * and its rows of dE are written. Workspace: alg_head_streamed_workspace_size bytes, bounded
+ * by the chunk (bf16: Npad x chunk bf16 + N x d f32 for the dh accumulator; f32: N x chunk f32)
+ * instead of V. */
+size_t alg_head_streamed_workspace_size(int dtype, int N, int d, int V, int vocab_chunk);
+int alg_head_bwd_streamed(alg_stream_t stream, int dtype, int N, int d, int V,
+                          const void* h, const void* E, const int32_t* targets, const float* stat,
+                          const float* g, int n, float c, int vocab_chunk, void* dh, void* dE, int dE_dtype,
+                          void* workspace, size_t workspace_bytes);
+
 /* Measurement hook (no counterpart in the reference; for benchmarks and profilers):
  * while enabled, every kernel launch of this library records a HIP event pair on its
  * stream. alg_timer_report() waits for those events, writes a JSON object

@@ -77,6 +77,21 @@ def test_workspace_sizes():
     assert handle.alg_head_workspace_size(f32, 16384, 2048, 32000, 2) == 0
     assert handle.alg_head_workspace_size(f32, 512, 256, 1000, 3) > 0
     assert handle.alg_head_workspace_size(7, 512, 256, 1000, 0) == 0
+    # Streamed backward at C4b: the default chunk is 8192 vocabulary rows (32 x 8 = 256 dE
+    # tiles), so the workspace holds one 16384 x 8192 bf16 block and the f32 dh accumulator,
+    # no (N, V) block.
+    sw = handle.alg_head_streamed_workspace_size(bf, 16384, 2048, 32000, 0)
+    assert sw == 16384 * 8192 * 2 + 16384 * 2048 * 4
+    assert sw < 0.4 * (bwd - fwd)
+    # 4096-row chunks: the last chunk (3328 rows, 104 dE tiles) splits its dE tiles over 7
+    # token ranges, whose f32 tiles the workspace holds as well.
+    assert (handle.alg_head_streamed_workspace_size(bf, 16384, 2048, 32000, 4096)
+            == 16384 * 4096 * 2 + 16384 * 2048 * 4 + 104 * 7 * 256 * 256 * 4)
+    assert handle.alg_head_streamed_workspace_size(bf, 16384, 2048, 32000, 32768) == 16384 * 32000 * 2  # one chunk
+    assert handle.alg_head_streamed_workspace_size(f32, 16384, 2048, 32000, 4096) == 16384 * 4096 * 4
+    assert handle.alg_head_streamed_workspace_size(bf, 16384, 2048, 32000, 300) == 0   # not a multiple of 256
+    assert handle.alg_head_streamed_workspace_size(bf, 16384, 2048, 32000, -256) == 0
+    assert handle.alg_head_streamed_workspace_size(7, 16384, 2048, 32000, 0) == 0
 
 
 def test_invalid_arguments_fail_before_launch():
@@ -110,6 +125,12 @@ def test_invalid_arguments_fail_before_launch():
     assert rc == _lib.ALG_ERR_UNSUPPORTED and b"d_model" in handle.alg_last_error()
     rc = handle.alg_head_bwd(None, 0, 128, 256, 1000, P(16), P(16), P(16), P(16), P(16), 8, 2.0, None, P(16),
                              P(16), 0, P(16), 16)
+    assert rc == _lib.ALG_ERR_INVALID and b"workspace" in handle.alg_last_error()
+    rc = handle.alg_head_bwd_streamed(None, 0, 128, 256, 1000, P(16), P(16), P(16), P(16), P(16), 8, 2.0, 300,
+                                      P(16), P(16), 0, P(16), 1 << 30)
+    assert rc == _lib.ALG_ERR_INVALID and b"vocab_chunk" in handle.alg_last_error()
+    rc = handle.alg_head_bwd_streamed(None, 0, 128, 256, 1000, P(16), P(16), P(16), P(16), P(16), 1, 2.0, 256,
+                                      P(16), P(16), 0, P(16), 16)  # n = 1 is fine: no residual
     assert rc == _lib.ALG_ERR_INVALID and b"workspace" in handle.alg_last_error()
     # n = 1 (fused_head.py:269-272 accepts it): with a residual it is refused (that schedule
     # needs stat^n = 1/l, which the reference's l^(-1/n) = rsqrt(l) at n = 1 does not give);

@@ -194,12 +194,17 @@ def test_attention_rows_normalised_long_context():
     assert err <= 2.0 ** -9 + 2.0 ** -8, f"max |o - 1| = {err}"
 
 
+@pytest.mark.parametrize("schedule", ["residual", "streamed"])
 @pytest.mark.parametrize("config", list(HEAD_CONFIGS))
-def test_head_full_size(config):
+def test_head_full_size(config, schedule, monkeypatch):
+    """The default (residual) schedule and the streamed one at its default vocabulary chunk."""
+    from algebraic_amd.kernels import fused_head as FH
     from algebraic_amd.kernels.fused_head import fused_head
+    monkeypatch.setattr(FH, "SCHEDULE", schedule)
+    monkeypatch.setattr(FH, "VOCAB_CHUNK", 0)
     N, d, V = shape = HEAD_CONFIGS[config]
     h, E, tg = head_inputs(N, d, V, seed=2)
-    print(f"[full-size] head {config} {shape}", flush=True)
+    print(f"[full-size] head {config} {shape} {schedule}", flush=True)
     th = _dev(h).requires_grad_(True)
     tE = _dev(E).requires_grad_(True)
     tt = torch.from_numpy(tg).to("cuda")

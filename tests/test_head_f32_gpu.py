@@ -50,12 +50,17 @@ SHAPES = [  # (N, d, V)
 ]
 
 
+@pytest.mark.parametrize("schedule", ["recompute", "streamed"])
 @pytest.mark.parametrize("n,c", [(8, 2.0), (16, 16.0)])
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
-def test_head_f32_matches_dense(shape, n, c):
+def test_head_f32_matches_dense(shape, n, c, schedule, monkeypatch):
+    """"streamed" runs 256-row vocabulary chunks, dh accumulated over them in f32."""
+    from algebraic_amd.kernels import fused_head as FH
+    monkeypatch.setattr(FH, "SCHEDULE", schedule)
+    monkeypatch.setattr(FH, "VOCAB_CHUNK", 256)
     N, d, V = shape
     h, E, t = _inputs(N, d, V, seed=N + d + V + n)
-    print(f"f32 head N{N} d{d} V{V} n{n}", flush=True)
+    print(f"f32 head N{N} d{d} V{V} n{n} {schedule}", flush=True)
     obj, pt, dh, dE = _run(h, E, t, n, c, g=0.7)
     obj_r, pt_r = OH.dense_forward(h, E, t, n=n, c=c)
     dh_r, dE_r = OH.dense_backward(h, E, t, 0.7, n=n, c=c)

@@ -38,10 +38,14 @@ CASES = [  # (N, d, V)
 ]
 
 
-@pytest.fixture(params=["residual", "recompute"])
+@pytest.fixture(params=["residual", "recompute", "streamed"])
 def schedule(request, monkeypatch):
+    """The three backward schedules; "streamed" with 256-row vocabulary chunks, so every
+    case runs several chunks (a ragged last one where V % 256 != 0)."""
     from algebraic_amd.kernels import fused_head as FH
     monkeypatch.setattr(FH, "SCHEDULE", request.param)
+    if request.param == "streamed":
+        monkeypatch.setattr(FH, "VOCAB_CHUNK", 256)
     return request.param
 
 
@@ -170,3 +174,38 @@ def test_head_de_token_split_tail(e_dtype, schedule, split_case):
     assert rel_l2(dE, dE_r) < 1e-2
     assert rel_l2(dE[65536:], dE_r[65536:]) < 1e-2
     assert rel_l2(dE[65536:, 256:], dE_r[65536:, 256:]) < 1e-2
+
+
+@pytest.mark.parametrize("chunk", [0, 512, 1280, 4096])
+def test_head_streamed_chunks(chunk, monkeypatch):
+    """Streamed backward at several chunk sizes (0: the library's default, here one chunk;
+    1280: a ragged last chunk of 720 rows) against the float64 dense oracle and the recompute
+    schedule: the logit-gradient entries are formed by the same expression, so the gradients
+    differ only by the chunked f32 accumulation of dh."""
+    from algebraic_amd.kernels import fused_head as FH
+    N, d, V = 640, 256, 4560
+    h, E, t = head_inputs(N, d, V, seed=33, e_std=0.15)
+    print(f"[head streamed] chunk {chunk}", flush=True)
+    monkeypatch.setattr(FH, "SCHEDULE", "recompute")
+    _, _, dh_rc, dE_rc = run_hip(h, E, t, n=8, c=2.0, g=0.6)
+    monkeypatch.setattr(FH, "SCHEDULE", "streamed")
+    monkeypatch.setattr(FH, "VOCAB_CHUNK", chunk)
+    obj, pt, dh, dE = run_hip(h, E, t, n=8, c=2.0, g=0.6)
+    obj_r, _ = OH.dense_forward(h, E, t, n=8, c=2.0)
+    dh_r, dE_r = OH.dense_backward(h, E, t, 0.6, n=8, c=2.0)
+    np.testing.assert_allclose(obj, obj_r, rtol=2e-3, atol=2e-4)
+    assert rel_l2(dh, dh_r) < 1e-2
+    assert rel_l2(dE, dE_r) < 1e-2
+    assert rel_l2(dh, dh_rc) < 2e-3
+    assert rel_l2(dE, dE_rc) < 2e-3
+    last = (V - 1) // chunk * chunk if chunk else 0
+    assert rel_l2(dE[last:], dE_r[last:]) < 1e-2  # the last (ragged) chunk on its own
+
+
+def test_head_streamed_rejects_bad_chunk(monkeypatch):
+    from algebraic_amd.kernels import fused_head as FH
+    monkeypatch.setattr(FH, "SCHEDULE", "streamed")
+    monkeypatch.setattr(FH, "VOCAB_CHUNK", 300)
+    h, E, t = head_inputs(128, 128, 600, seed=1, e_std=0.15)
+    with pytest.raises(ValueError, match="multiple of 256"):
+        run_hip(h, E, t)

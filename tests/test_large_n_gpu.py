@@ -95,21 +95,26 @@ def test_eval_head_n(n, c):
     np.testing.assert_allclose(logp, ref, atol=1e-4 * max(1.0, n / 16), rtol=1e-4)
 
 
+@pytest.mark.parametrize("schedule", ["recompute", "streamed"])
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
-def test_training_head_n1_matches_reference_formula(dtype):
+def test_training_head_n1_matches_reference_formula(dtype, schedule, monkeypatch):
     """n = 1 passes the reference's power-of-two check (fused_head.py:269-272). Its statistic
     _inv_root(l, 1) is rsqrt(l) (fused_head.py:59-65), so the reference's fused head returns
     p_t = rho(z_t/c) rsqrt(l) and the gradient of that, not the true NLL's. The HIP head (the
     recompute schedule) matches the cast-faithful restatement of those formulas
     (oracle.head.kernel_forward / kernel_backward) at the head's usual bars, and, as the
-    reference does, differs from the true-NLL dense head."""
+    reference does, differs from the true-NLL dense head. The streamed schedule (256-row
+    vocabulary chunks) is held to the same bars."""
+    from algebraic_amd.kernels import fused_head as FH
     from algebraic_amd.kernels.fused_head import fused_head
+    monkeypatch.setattr(FH, "SCHEDULE", schedule)
+    monkeypatch.setattr(FH, "VOCAB_CHUNK", 256)
     N, d, V, c = 256, 128, 1000, 2.0
     h, E, t = head_inputs(N, d, V, seed=71, e_std=0.15)
     tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
     th = torch.tensor(h, device="cuda").to(tdt).requires_grad_(True)
     tE = torch.tensor(E, device="cuda").to(tdt).requires_grad_(True)
-    print(f"[head n=1] {dtype}", flush=True)
+    print(f"[head n=1] {dtype} {schedule}", flush=True)
     obj, tel = fused_head(th, tE, torch.tensor(t, device="cuda"), kind="alg_ce", n=1, c=c)
     obj.backward()
     torch.cuda.synchronize()
