@@ -579,9 +579,14 @@ __device__ __forceinline__ float guard_max(float a, float b) { return (a > b || 
 //
 // Keys and values: the workgroup's own key rows are its two diagonal tiles, which pass
 // through LDS anyway; guard_kv_tile folds one such tile (rows past T are zero-filled there and
-// add nothing) into the thread's running maxima mk (||k||^2) and mv (|v|).
+// add nothing) into the thread's running maxima mk (||k||^2) and mvb (|v|). |v| is tracked on
+// the bf16 bit patterns: with the sign cleared they order as the magnitudes do, every NaN
+// above infinity, so a packed 16-bit integer maximum over (bits & 0x7fff) pairs is the
+// NaN-propagating maximum of |v| (guard_v_max turns it back into a float) at one instruction
+// per two values.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 template <int D>
-__device__ __forceinline__ void guard_kv_tile(const bf16* Ks, const bf16* Vs, float& mk, float& mv) {
+__device__ __forceinline__ void guard_kv_tile(const bf16* Ks, const bf16* Vs, float& mk, u16x2& mvb) {
   constexpr int CPR = D / 8, RPS = 256 / CPR, NR = FWD_BK / RPS;
   const int c = threadIdx.x % CPR, r0 = threadIdx.x / CPR;
   uint4 kr[NR], vr[NR];
@@ -592,20 +597,28 @@ __device__ __forceinline__ void guard_kv_tile(const bf16* Ks, const bf16* Vs, fl
   }
 #pragma unroll
   for (int i = 0; i < NR; ++i) {
-    bf16 kv[8], vv[8];
+    bf16 kv[8];
     *reinterpret_cast<uint4*>(kv) = kr[i];
-    *reinterpret_cast<uint4*>(vv) = vr[i];
     float sk = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float kf = (float)kv[j];
       sk += kf * kf;
-      mv = guard_max(mv, __builtin_fabsf((float)vv[j]));
     }
+    const unsigned vw[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      mvb = __builtin_elementwise_max(mvb, __builtin_bit_cast(u16x2, vw[j] & 0x7fff7fffu));
 #pragma unroll
     for (int m = 1; m < CPR; m <<= 1) sk += __shfl_xor(sk, m, 64);
     mk = guard_max(mk, sk);
   }
+}
+
+// |v| maximum from guard_kv_tile's bit patterns: the larger half; NaN above 0x7f80 (infinity).
+__device__ __forceinline__ float guard_v_max(u16x2 mvb) {
+  const unsigned m = mvb.x > mvb.y ? mvb.x : mvb.y;
+  return m > 0x7f80u ? __builtin_nanf("") : __uint_as_float(m << 16);
 }
 
 // Queries, from the fragments the kernel holds, and the workgroup's maxima: called by every
@@ -701,6 +714,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) 
   const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)K, (short)0, nbytes, BUF_RSRC_WORD3);
   const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)V, (short)0, nbytes, BUF_RSRC_WORD3);
   const int myq = qb * FWD_BQ + wave * 32 + l32;
+  const int wave_qmax = qb * FWD_BQ + wave * 32 + 31;  // this wave's last query (wave-uniform)
   const int log2n = p.log2n;
   const int ntiles = min(qb * FWD_BQ + FWD_BQ - 1, T_ - 1) / BK + 1;  // key tiles up to the last query
 
@@ -747,7 +761,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) 
   rk3[1] = ld8(Ks0 + row_off[1]);
   constexpr int VE = 10;  // VALU instructions per weight (scheduling hint)
 
-  float gmk = 0.0f, gmv = 0.0f;  // FROM_Q: guard maxima of the diagonal tiles' keys and values
+  float gmk = 0.0f;  // FROM_Q: guard maxima of the diagonal tiles' keys and values
+  u16x2 gmv = {0, 0};
   auto tile = [&](auto bufc, auto maskc, int kt) {
     constexpr int BUF = decltype(bufc)::value;
     constexpr bool MASKED = decltype(maskc)::value;
@@ -755,6 +770,25 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) 
     const bf16* Vs = BUF ? Vs1 : Vs0;
     const int kb0 = kt * BK;
     if constexpr (FROM_Q && MASKED) guard_kv_tile<D>(Ks, Vs, gmk, gmv);  // this workgroup's own keys
+    if constexpr (MASKED) {
+      if (kb0 > wave_qmax) {
+        // Every key of the tile lies after this wave's queries: all its weights are zero, so
+        // the wave only takes part in the copies (none are left after the last tile) and the
+        // barrier.
+        const int rn = kt + 1 < ntiles ? kb0 + BK : T_ + BK;
+#pragma unroll
+        for (int g = 0; g < PW; ++g) {
+          if constexpr (BUF) tile_dma2_part<D>(Ks0, Vs0, rk, rv, rn, wave, lane, g, ld);
+          else tile_dma2_part<D>(Ks1, Vs1, rk, rv, rn, wave, lane, g, ld);
+        }
+        __builtin_amdgcn_s_waitcnt(VMCNT0);
+        __syncthreads();
+        const bf16* Kn = BUF ? Ks0 : Ks1;
+        rk3[0] = ld8(Kn + row_off[0]);
+        rk3[1] = ld8(Kn + row_off[1]);
+        return;
+      }
+    }
     floatx16 s[2];
     bf16x8 pf[2][2];
     float w[16];
@@ -880,7 +914,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnFwdParams p) 
   if constexpr (FROM_Q) {
     // After the output (its accumulators are dead), with every lane of the workgroup.
     if (live) finalize();
-    fwd_guard_partials<D>(qf, live, gmk, gmv, p.guard_part + 3 * ((size_t)bh * nqb + blockIdx.y), gred);
+    fwd_guard_partials<D>(qf, live, gmk, guard_v_max(gmv), p.guard_part + 3 * ((size_t)bh * nqb + blockIdx.y), gred);
   } else {
     if (!live) return;
     finalize();
