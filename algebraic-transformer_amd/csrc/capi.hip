@@ -670,7 +670,9 @@ int alg_head_fwd(alg_stream_t stream, int dtype, int N, int d, int V, const void
 
 size_t alg_rms_norm_workspace_size(int rows, int d) {
   if (rows <= 0 || d <= 0) return 0;
-  return align256((size_t)d * alg::rms_norm_blocks(rows) * sizeof(float));
+  // Per-workgroup gain partials (blocks x d), then their group sums (groups x d).
+  return align256((size_t)d * alg::rms_norm_blocks(rows) * sizeof(float)) +
+         align256((size_t)d * alg::rms_norm_gain_groups(rows) * sizeof(float));
 }
 
 static int check_rms_norm(int rows, int d, float eps) {

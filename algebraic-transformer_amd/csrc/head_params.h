@@ -103,7 +103,7 @@ struct RmsNormParams {
   float* tau;           // (rows,) 1/rms, written by the forward, read by the VJP
   const bf16* dy;       // VJP: cotangent of y
   bf16* dx;             // VJP: (rows, d)
-  float* gpart;         // VJP: (d, nblocks) gain-gradient partials, or nullptr
+  float* gpart;         // VJP: (nblocks, d) gain-gradient partials and their group sums, or nullptr
   int rows, d;
   float eps;
 };

@@ -49,6 +49,7 @@ hipError_t launch_head_bwd_f32_streamed(const HeadParams& p, int chunk, hipStrea
 hipError_t launch_head_eval_f32(const HeadParams& p, hipStream_t st);
 int rms_norm_max_d();
 int rms_norm_blocks(int rows);
+int rms_norm_gain_groups(int rows);
 hipError_t launch_rms_norm_fwd(const RmsNormParams& p, hipStream_t st);
 hipError_t launch_ffn_fwd(const FfnParams& p, hipStream_t st);
 hipError_t launch_ffn_dy(const FfnParams& p, hipStream_t st);

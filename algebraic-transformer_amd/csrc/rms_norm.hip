@@ -31,23 +31,41 @@ __device__ __forceinline__ float wave_sum(float s) {
   return s;
 }
 
-// Row chunk c of this lane (chunk lane + 64 c), or zeros past the row's end.
+// Row chunk c of this lane (chunk lane + 64 c), or zeros past the row's end: buffer loads over
+// the row's range, which return zeros past it, so every lane loads unconditionally and the
+// row's loads issue back to back under one wait (a load per lane behind a range check
+// compiles to a branch and a wait around each).
 template <int NC>
 __device__ __forceinline__ void load_row(const bf16* r, int lane, int nch, uint4 (&raw)[NC]) {
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)r, (short)0, nch * 16, BUF_RSRC_WORD3);
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
-    const int ch = lane + 64 * c;
-    raw[c] = ch < nch ? *reinterpret_cast<const uint4*>(r + 8 * ch) : make_uint4(0, 0, 0, 0);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * (lane + 64 * c), 0, 0);
+    raw[c] = make_uint4(v[0], v[1], v[2], v[3]);
   }
 }
 
+// Gain of this lane's chunks (1 without a gain; zeros past the row's end, where x is zero).
 template <int NC>
 __device__ __forceinline__ void load_gain(const float* gain, int lane, int nch, float (&g)[NC][8]) {
+  if (!gain) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) g[c][e] = 1.0f;
+    return;
+  }
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)gain, (short)0, nch * 32, BUF_RSRC_WORD3);
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
-    const int ch = lane + 64 * c;
+    const int off = 32 * (lane + 64 * c);
+    const auto lo = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+    const auto hi = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16, 0, 0);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) g[c][e] = (ch < nch && gain) ? gain[8 * ch + e] : 1.0f;
+    for (int e = 0; e < 4; ++e) {
+      g[c][e] = __uint_as_float(lo[e]);
+      g[c][4 + e] = __uint_as_float(hi[e]);
+    }
   }
 }
 
@@ -58,7 +76,7 @@ __device__ __forceinline__ void load_gain(const float* gain, int lane, int nch, 
 template <int NC>
 __global__ __launch_bounds__(256) void rms_norm_fwd_kernel(RmsNormParams p) {
   const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int row = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   if (row >= p.rows) return;
   const int nch = p.d / 8;
   uint4 raw[NC];
@@ -89,93 +107,133 @@ __global__ __launch_bounds__(256) void rms_norm_fwd_kernel(RmsNormParams p) {
   if (lane == 0) p.tau[row] = tau;
 }
 
-// Rows in a grid-stride loop (the gain gradient is a per-workgroup partial); the next row's
-// x and dy are loaded while the current one is reduced and written.
+// Rows in a grid-stride loop, one row per wave at a time (the gain gradient is a
+// per-workgroup partial). The gain sits in LDS and the per-element values (x, dy, a = g dy)
+// are formed again from the raw row for the output, so a wave holds only its row's raw
+// chunks and its gain-gradient accumulators: about 100 registers at d = 2048, four waves
+// per SIMD, whose row loads keep enough bytes in flight without a software prefetch.
 template <int NC>
 __global__ __launch_bounds__(256) void rms_norm_bwd_kernel(RmsNormParams p) {
-  __shared__ float red[4][NC * 512];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __shared__ __attribute__((aligned(16))) float gs[NC * 512];
+  __shared__ float red[NC * 512];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nch = p.d / 8;
-  float g[NC][8], acc[NC][8];
-  load_gain<NC>(p.gain, lane, nch, g);
+  {
+    float g[NC][8];  // chunk lane + 64 c of the gain, as the rows are laid out
+    load_gain<NC>(p.gain, lane, nch, g);
+    if (wave == 0) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) gs[8 * (lane + 64 * c) + e] = g[c][e];
+    }
+  }
+  __syncthreads();
+  float acc[NC][8];
 #pragma unroll
   for (int c = 0; c < NC; ++c)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[c][e] = 0.0f;
   const float inv_d = 1.0f / (float)p.d;
   const int stride = gridDim.x * 4;
-  int row = blockIdx.x * 4 + wave;
-  uint4 xr[NC], dyr[NC];
-  if (row < p.rows) {
+  for (int row = blockIdx.x * 4 + wave; row < p.rows; row += stride) {
+    uint4 xr[NC], dyr[NC];
     load_row<NC>(p.x + (size_t)row * p.d, lane, nch, xr);
     load_row<NC>(p.dy + (size_t)row * p.d, lane, nch, dyr);
-  }
-  for (; row < p.rows; row += stride) {
     const float tau = p.tau[row];
-    float x[NC][8], a[NC][8];
     float s = 0.0f;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      float dy[8];
-      cvt8(xr[c], x[c]);
+      float x[8], dy[8];
+      cvt8(xr[c], x);
       cvt8(dyr[c], dy);
+      const float* g = gs + 8 * (lane + 64 * c);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        acc[c][e] += __fmul_rn(dy[e], __fmul_rn(x[c][e], tau));
-        a[c][e] = __fmul_rn(g[c][e], dy[e]);
-        s += __fmul_rn(a[c][e], x[c][e]);
+        acc[c][e] += __fmul_rn(dy[e], __fmul_rn(x[e], tau));
+        s += __fmul_rn(__fmul_rn(g[e], dy[e]), x[e]);
       }
-    }
-    const int next = row + stride;
-    if (next < p.rows) {
-      load_row<NC>(p.x + (size_t)next * p.d, lane, nch, xr);
-      load_row<NC>(p.dy + (size_t)next * p.d, lane, nch, dyr);
+      __builtin_amdgcn_sched_barrier(0);  // one chunk's temporaries live at a time
     }
     s = wave_sum(s);
     const float coef = __fmul_rn(__fmul_rn(__fmul_rn(tau, tau), tau), s) * inv_d;
     bf16* dxr = p.dx + (size_t)row * p.d;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
+      // Re-convert from the raw chunks (keeping the converted values live across the row sum
+      // would double the registers).
+      asm volatile("" : "+v"(xr[c].x), "+v"(xr[c].y), "+v"(xr[c].z), "+v"(xr[c].w));
+      asm volatile("" : "+v"(dyr[c].x), "+v"(dyr[c].y), "+v"(dyr[c].z), "+v"(dyr[c].w));
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
       const int ch = lane + 64 * c;
       if (ch < nch) {
+        float x[8], dy[8];
+        cvt8(xr[c], x);
+        cvt8(dyr[c], dy);
+        const float* g = gs + 8 * ch;
         bf16 out[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) out[e] = f2bf(__fsub_rn(__fmul_rn(a[c][e], tau), __fmul_rn(x[c][e], coef)));
+        for (int e = 0; e < 8; ++e)
+          out[e] = f2bf(__fsub_rn(__fmul_rn(__fmul_rn(g[e], dy[e]), tau), __fmul_rn(x[e], coef)));
         *reinterpret_cast<uint4*>(dxr + 8 * ch) = *reinterpret_cast<uint4*>(out);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   if (!p.gpart) return;
+  // The workgroup's partial: the waves' accumulators added in wave order.
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const int ch = lane + 64 * c;
-    if (ch < nch) {
+  for (int w = 0; w < 4; ++w) {
+    if (wave == w) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) red[wave][8 * ch + e] = acc[c][e];
+      for (int c = 0; c < NC; ++c) {
+        const int ch = lane + 64 * c;
+        if (ch < nch) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) red[8 * ch + e] = w == 0 ? acc[c][e] : red[8 * ch + e] + acc[c][e];
+        }
+      }
     }
-  }
-  __syncthreads();
-  for (int i = threadIdx.x; i < p.d; i += 256)
-    p.gpart[(size_t)i * gridDim.x + blockIdx.x] = red[0][i] + red[1][i] + red[2][i] + red[3][i];
-}
-
-// dgain[i] = sum over blocks of gpart[i][block], one workgroup per column, fixed-order tree.
-__global__ __launch_bounds__(256) void rms_norm_gain_reduce_kernel(const float* gpart, int nblocks, float* dgain) {
-  __shared__ float red[256];
-  const int i = blockIdx.x;
-  float s = 0.0f;
-  for (int b = threadIdx.x; b < nblocks; b += 256) s += gpart[(size_t)i * nblocks + b];
-  red[threadIdx.x] = s;
-  __syncthreads();
-  for (int w = 128; w > 0; w >>= 1) {
-    if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
     __syncthreads();
   }
-  if (threadIdx.x == 0) dgain[i] = red[0];
+  for (int i = threadIdx.x; i < p.d; i += 256) p.gpart[(size_t)blockIdx.x * p.d + i] = red[i];  // row per block
+}
+
+// dgain[i] = sum over blocks of gpart[block][i], in two fixed-order stages with a thread per
+// column (coalesced rows): the blocks in groups of RN_GROUP summed in block order into
+// tmp[group][i], then the groups in group order (at most RN_GROUP groups: 1024 blocks).
+// Each stage issues its RN_GROUP loads together (rows past the end are read clamped and not
+// added) and then sums them in order.
+constexpr int RN_GROUP = 32;
+__device__ __forceinline__ float rn_sum_rows(const float* a, int r0, int r1, int d, int i) {
+  float v[RN_GROUP];
+#pragma unroll
+  for (int k = 0; k < RN_GROUP; ++k) v[k] = a[(size_t)min(r0 + k, r1 - 1) * d + i];
+  float s = v[0];
+#pragma unroll
+  for (int k = 1; k < RN_GROUP; ++k)
+    if (r0 + k < r1) s += v[k];
+  return s;
+}
+__global__ __launch_bounds__(256) void rms_norm_gain_part_kernel(const float* gpart, int nblocks, int d, float* tmp) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= d) return;
+  const int b0 = blockIdx.y * RN_GROUP;
+  tmp[(size_t)blockIdx.y * d + i] = rn_sum_rows(gpart, b0, min(nblocks, b0 + RN_GROUP), d, i);
+}
+
+__global__ __launch_bounds__(256) void rms_norm_gain_reduce_kernel(const float* tmp, int ngroups, int d, float* dgain) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= d) return;
+  dgain[i] = rn_sum_rows(tmp, 0, ngroups, d, i);
 }
 
 int rms_norm_max_d() { return RN_MAXC * 512; }
 int rms_norm_blocks(int rows) { return rows / 4 + 1 < 1024 ? rows / 4 + 1 : 1024; }
+int rms_norm_gain_groups(int rows) { return (rms_norm_blocks(rows) + RN_GROUP - 1) / RN_GROUP; }
+static_assert(1024 <= RN_GROUP * RN_GROUP, "the groups of the largest grid fit one second stage");
 
 // Chunks per lane for width d: ceil(d / 512), 1..RN_MAXC (the width is checked by the caller).
 static int rms_norm_nc(int d) { return (d / 8 + 63) / 64; }
@@ -206,8 +264,12 @@ hipError_t launch_rms_norm_bwd(const RmsNormParams& p, float* dgain, hipStream_t
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !dgain) return e;
+  // Workspace: gpart (nb rows of d) then, 256-byte aligned, the group sums (ngroups rows of d).
+  const int ng = rms_norm_gain_groups(p.rows);
+  float* tmp = p.gpart + ((size_t)nb * p.d + 63) / 64 * 64;
   KTimer t("rms_norm_gain_reduce", st);
-  hipLaunchKernelGGL(rms_norm_gain_reduce_kernel, dim3(p.d), dim3(256), 0, st, p.gpart, nb, dgain);
+  hipLaunchKernelGGL(rms_norm_gain_part_kernel, dim3((p.d + 255) / 256, ng), dim3(256), 0, st, p.gpart, nb, p.d, tmp);
+  hipLaunchKernelGGL(rms_norm_gain_reduce_kernel, dim3((p.d + 255) / 256), dim3(256), 0, st, tmp, ng, p.d, dgain);
   return hipGetLastError();
 }
 
