@@ -92,6 +92,19 @@ __device__ __forceinline__ void load_f32(const float* p, float (&x)[CH]) {
   for (int e = 0; e < CH; e += 4) *reinterpret_cast<float4*>(&x[e]) = *reinterpret_cast<const float4*>(p + e);
 }
 
+// Gain entries c0 .. c0 + CH - 1 of both halves (1 without a gain): one uniform branch around
+// the vector loads, so they issue together.
+template <int CH>
+__device__ __forceinline__ void load_gain_halves(const float* g, int c0, int half, float (&ga)[CH], float (&gb)[CH]) {
+  if (g) {
+    load_f32<CH>(g + c0, ga);
+    load_f32<CH>(g + half + c0, gb);
+  } else {
+#pragma unroll
+    for (int e = 0; e < CH; ++e) ga[e] = gb[e] = 1.0f;
+  }
+}
+
 template <int LPR>
 __device__ __forceinline__ float row_sum(float s) {
 #pragma unroll
@@ -102,7 +115,7 @@ __device__ __forceinline__ float row_sum(float s) {
 // One tensor's row: y = rot(round((x tau) g)) in the I/O dtype (as f32 values), tau out.
 template <typename T, int CH, int LPR>
 __device__ __forceinline__ float norm_rotate(float (&a)[CH], float (&b)[CH], const float (&ga)[CH],
-                                             const float (&gb)[CH], bool has_gain, const float (&ca)[CH],
+                                             const float (&gb)[CH], const float (&ca)[CH],
                                              const float (&sa)[CH], bool rotate, float inv_d, float eps) {
   float ss = 0.0f;
 #pragma unroll
@@ -112,7 +125,8 @@ __device__ __forceinline__ float norm_rotate(float (&a)[CH], float (&b)[CH], con
 #pragma unroll
   for (int e = 0; e < CH; ++e) {
     float ya = mul_rn(a[e], tau), yb = mul_rn(b[e], tau);
-    if (has_gain) { ya = mul_rn(ya, ga[e]); yb = mul_rn(yb, gb[e]); }
+    ya = mul_rn(ya, ga[e]);  // gain 1 when there is none: the product is exact
+    yb = mul_rn(yb, gb[e]);
     ya = rnd<T>(ya);
     yb = rnd<T>(yb);
     if (rotate) {
@@ -157,7 +171,9 @@ __global__ __launch_bounds__(256) void cayley_tables_kernel(const float* w, int 
   sin_out[idx] = mul_rn(os, inv);
 }
 
-template <typename T, int D>
+// ROT: the Cayley rotation (cos/sin tables given); GUARD: the guard's |v| maxima (v read). Both
+// are template parameters so that every load of a row sits in one block and issues together.
+template <typename T, int D, bool ROT, bool GUARD>
 __global__ __launch_bounds__(256) void attn_qk_prologue_kernel(QkPrologueParams p) {
   constexpr int CH = 16 / sizeof(T), HALF = D / 2, LPR = HALF / CH, RPW = 64 / LPR;
   static_assert(HALF % CH == 0 && 64 % LPR == 0, "row split");
@@ -165,14 +181,9 @@ __global__ __launch_bounds__(256) void attn_qk_prologue_kernel(QkPrologueParams 
   const int sub = lane / LPR, li = lane - sub * LPR;
   const int c0 = li * CH;
   float gqa[CH], gqb[CH], gka[CH], gkb[CH];
-#pragma unroll
-  for (int e = 0; e < CH; ++e) {
-    gqa[e] = p.q_gain ? p.q_gain[c0 + e] : 1.0f;
-    gqb[e] = p.q_gain ? p.q_gain[HALF + c0 + e] : 1.0f;
-    gka[e] = p.k_gain ? p.k_gain[c0 + e] : 1.0f;
-    gkb[e] = p.k_gain ? p.k_gain[HALF + c0 + e] : 1.0f;
-  }
-  const bool rotate = p.cos != nullptr;
+  load_gain_halves<CH>(p.q_gain, c0, HALF, gqa, gqb);
+  load_gain_halves<CH>(p.k_gain, c0, HALF, gka, gkb);
+  constexpr bool rotate = ROT;
   const float inv_d = 1.0f / (float)D;
   float mq = 0.0f, mk = 0.0f, mv = 0.0f;
   const RowAddr ra = head_rows(p.H, p.T, D, p.layout);
@@ -195,11 +206,11 @@ __global__ __launch_bounds__(256) void attn_qk_prologue_kernel(QkPrologueParams 
       rq[u][1] = ld16<T>(p.q, in + HALF);
       rk[u][0] = ld16<T>(p.k, in);
       rk[u][1] = ld16<T>(p.k, in + HALF);
-      if (p.want_guard) {
+      if constexpr (GUARD) {
         rv[u][0] = ld16<T>(p.v, in);
         rv[u][1] = ld16<T>(p.v, in + HALF);
       }
-      if (rotate) {
+      if constexpr (ROT) {
         load_f32<CH>(p.cos + (size_t)tt[u] * HALF + c0, ca[u]);
         load_f32<CH>(p.sin + (size_t)tt[u] * HALF + c0, sa[u]);
       }
@@ -215,7 +226,7 @@ __global__ __launch_bounds__(256) void attn_qk_prologue_kernel(QkPrologueParams 
       // a sum of v*0, which is NaN exactly when some v is NaN or infinite (either fails the
       // guard's |v| bound, as the reference's comparison with a NaN maximum does).
       float av = 0.0f;
-      if (p.want_guard) {
+      if constexpr (GUARD) {
         float va[CH], vb[CH], nan_acc = 0.0f;
         cvt_chunk<T, CH>(rv[u][0], va);
         cvt_chunk<T, CH>(rv[u][1], vb);
@@ -226,10 +237,8 @@ __global__ __launch_bounds__(256) void attn_qk_prologue_kernel(QkPrologueParams 
         }
         if (nan_acc != nan_acc) av = nan_acc;
       }
-      const float tq =
-          norm_rotate<T, CH, LPR>(qa, qb, gqa, gqb, p.q_gain != nullptr, ca[u], sa[u], rotate, inv_d, p.eps);
-      const float tk =
-          norm_rotate<T, CH, LPR>(ka, kb, gka, gkb, p.k_gain != nullptr, ca[u], sa[u], rotate, inv_d, p.eps);
+      const float tq = norm_rotate<T, CH, LPR>(qa, qb, gqa, gqb, ca[u], sa[u], rotate, inv_d, p.eps);
+      const float tk = norm_rotate<T, CH, LPR>(ka, kb, gka, gkb, ca[u], sa[u], rotate, inv_d, p.eps);
       float sq = 0.0f, sk = 0.0f;
 #pragma unroll
       for (int e = 0; e < CH; ++e) {
@@ -306,7 +315,7 @@ __device__ __forceinline__ void norm_rotate_vjp(float (&a)[CH], float (&b)[CH], 
   }
 }
 
-template <typename T, int D>
+template <typename T, int D, bool ROT>
 __global__ __launch_bounds__(256) void attn_qk_prologue_bwd_kernel(QkPrologueBwdParams p) {
   constexpr int CH = 16 / sizeof(T), HALF = D / 2, LPR = HALF / CH, RPW = 64 / LPR;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -314,15 +323,11 @@ __global__ __launch_bounds__(256) void attn_qk_prologue_bwd_kernel(QkPrologueBwd
   const int c0 = li * CH;
   float gqa[CH], gqb[CH], gka[CH], gkb[CH];
   float aq_a[CH], aq_b[CH], ak_a[CH], ak_b[CH];  // gain-gradient accumulators
+  load_gain_halves<CH>(p.q_gain, c0, HALF, gqa, gqb);
+  load_gain_halves<CH>(p.k_gain, c0, HALF, gka, gkb);
 #pragma unroll
-  for (int e = 0; e < CH; ++e) {
-    gqa[e] = p.q_gain ? p.q_gain[c0 + e] : 1.0f;
-    gqb[e] = p.q_gain ? p.q_gain[HALF + c0 + e] : 1.0f;
-    gka[e] = p.k_gain ? p.k_gain[c0 + e] : 1.0f;
-    gkb[e] = p.k_gain ? p.k_gain[HALF + c0 + e] : 1.0f;
-    aq_a[e] = aq_b[e] = ak_a[e] = ak_b[e] = 0.0f;
-  }
-  const bool rotate = p.cos != nullptr;
+  for (int e = 0; e < CH; ++e) aq_a[e] = aq_b[e] = ak_a[e] = ak_b[e] = 0.0f;
+  constexpr bool rotate = ROT;
   const float inv_d = 1.0f / (float)D;
   const RowAddr ra = head_rows(p.H, p.T, D, p.layout);
   const int t0 = blockIdx.y * (4 * RPW * PRO_ITER) + wave * RPW + sub;
@@ -351,7 +356,7 @@ __global__ __launch_bounds__(256) void attn_qk_prologue_bwd_kernel(QkPrologueBwd
       const size_t row = (size_t)blockIdx.x * p.T + tc;
       tq[u] = p.tau_q[row];
       tk[u] = p.tau_k[row];
-      if (rotate) {
+      if constexpr (ROT) {
         load_f32<CH>(p.cos + (size_t)tc * HALF + c0, ca[u]);
         load_f32<CH>(p.sin + (size_t)tc * HALF + c0, sa[u]);
       }
@@ -458,12 +463,21 @@ hipError_t launch_attn_qk_prologue(const QkPrologueParams& p, bool bf16_io, Guar
   const dim3 grid(p.B * p.H, (p.T + attn_qk_rows_per_wg(p.D, bf16_io) - 1) / attn_qk_rows_per_wg(p.D, bf16_io));
   {
     KTimer t("attn_qk_prologue", st);
+    auto go = [&](auto tc, auto dc) {
+      typedef decltype(tc) T;
+      constexpr int D = decltype(dc)::value;
+      const bool rot = p.cos != nullptr, guard = p.want_guard != 0;
+      if (rot && guard) hipLaunchKernelGGL((attn_qk_prologue_kernel<T, D, true, true>), grid, dim3(256), 0, st, p);
+      else if (rot) hipLaunchKernelGGL((attn_qk_prologue_kernel<T, D, true, false>), grid, dim3(256), 0, st, p);
+      else if (guard) hipLaunchKernelGGL((attn_qk_prologue_kernel<T, D, false, true>), grid, dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((attn_qk_prologue_kernel<T, D, false, false>), grid, dim3(256), 0, st, p);
+    };
     if (bf16_io) {
-      if (p.D == 128) hipLaunchKernelGGL((attn_qk_prologue_kernel<bf16, 128>), grid, dim3(256), 0, st, p);
-      else hipLaunchKernelGGL((attn_qk_prologue_kernel<bf16, 64>), grid, dim3(256), 0, st, p);
+      if (p.D == 128) go(bf16{}, std::integral_constant<int, 128>{});
+      else go(bf16{}, std::integral_constant<int, 64>{});
     } else {
-      if (p.D == 128) hipLaunchKernelGGL((attn_qk_prologue_kernel<float, 128>), grid, dim3(256), 0, st, p);
-      else hipLaunchKernelGGL((attn_qk_prologue_kernel<float, 64>), grid, dim3(256), 0, st, p);
+      if (p.D == 128) go(float{}, std::integral_constant<int, 128>{});
+      else go(float{}, std::integral_constant<int, 64>{});
     }
   }
   hipError_t e = hipGetLastError();
@@ -479,12 +493,18 @@ hipError_t launch_attn_qk_prologue_bwd(const QkPrologueBwdParams& p, bool bf16_i
   const dim3 grid(p.B * p.H, (p.T + attn_qk_rows_per_wg(p.D, bf16_io) - 1) / attn_qk_rows_per_wg(p.D, bf16_io));
   {
     KTimer t("attn_qk_prologue_bwd", st);
+    auto go = [&](auto tc, auto dc) {
+      typedef decltype(tc) T;
+      constexpr int D = decltype(dc)::value;
+      if (p.cos) hipLaunchKernelGGL((attn_qk_prologue_bwd_kernel<T, D, true>), grid, dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((attn_qk_prologue_bwd_kernel<T, D, false>), grid, dim3(256), 0, st, p);
+    };
     if (bf16_io) {
-      if (p.D == 128) hipLaunchKernelGGL((attn_qk_prologue_bwd_kernel<bf16, 128>), grid, dim3(256), 0, st, p);
-      else hipLaunchKernelGGL((attn_qk_prologue_bwd_kernel<bf16, 64>), grid, dim3(256), 0, st, p);
+      if (p.D == 128) go(bf16{}, std::integral_constant<int, 128>{});
+      else go(bf16{}, std::integral_constant<int, 64>{});
     } else {
-      if (p.D == 128) hipLaunchKernelGGL((attn_qk_prologue_bwd_kernel<float, 128>), grid, dim3(256), 0, st, p);
-      else hipLaunchKernelGGL((attn_qk_prologue_bwd_kernel<float, 64>), grid, dim3(256), 0, st, p);
+      if (p.D == 128) go(float{}, std::integral_constant<int, 128>{});
+      else go(float{}, std::integral_constant<int, 64>{});
     }
   }
   hipError_t e = hipGetLastError();
