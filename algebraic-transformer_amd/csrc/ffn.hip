@@ -130,17 +130,31 @@ __global__ __launch_bounds__(FNT, 1) void ffn_dy_kernel(FfnParams p) {
       for (int nb = 0; nb < FC::NB; ++nb) stg[stage_at(row, nb * 32 + l32)] = f2bf(acc[mb][nb][i]);
     }
   }
-  // 128 rows x 8 chunks of 8 columns: lane -> (row, chunk).
+  // 128 rows x 8 chunks of 8 columns: lane -> (row, chunk), in groups of GRP chunks per lane
+  // whose gate/up loads are issued together (out-of-range chunks read chunk 0 and are not
+  // stored): behind a per-chunk range check each load got a branch and a wait of its own.
   const int f0 = n0 + wn * FC::WTN;
-#pragma unroll 4
-  for (int it = 0; it < 16; ++it) {
-    const int idx = it * 64 + lane, row = idx >> 3, ch = idx & 7;
+  constexpr int GRP = 8;
+#pragma unroll 1
+  for (int g0 = 0; g0 < 16; g0 += GRP) {
+    bf16x8 gvs[GRP], uvs[GRP];
+#pragma unroll
+    for (int k = 0; k < GRP; ++k) {
+      const int idx = (g0 + k) * 64 + lane, row = idx >> 3, ch = idx & 7;
+      const int tok = m0 + wm * FC::WTM + row, f = f0 + 8 * ch;
+      const size_t o = tok < p.N && f < p.F ? (size_t)tok * p.F + f : 0;
+      gvs[k] = *reinterpret_cast<const bf16x8*>(p.gate + o);
+      uvs[k] = *reinterpret_cast<const bf16x8*>(p.up + o);
+    }
+#pragma unroll
+    for (int k = 0; k < GRP; ++k) asm volatile("" : "+v"(gvs[k]), "+v"(uvs[k]));  // loads before the checks
+#pragma unroll
+  for (int k = 0; k < GRP; ++k) {
+    const int idx = (g0 + k) * 64 + lane, row = idx >> 3, ch = idx & 7;
     const int tok = m0 + wm * FC::WTM + row, f = f0 + 8 * ch;
     if (tok >= p.N || f >= p.F) continue;  // F is a multiple of 128: chunks are whole
-    const size_t o = (size_t)tok * p.F + f;
     const bf16x8 dyv = *reinterpret_cast<const bf16x8*>(stg + stage_at(row, 8 * ch));
-    const bf16x8 gv = *reinterpret_cast<const bf16x8*>(p.gate + o);
-    const bf16x8 uv = *reinterpret_cast<const bf16x8*>(p.up + o);
+    const bf16x8 gv = gvs[k], uv = uvs[k];
     bf16x8 dg, du;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -155,6 +169,7 @@ __global__ __launch_bounds__(FNT, 1) void ffn_dy_kernel(FfnParams p) {
     const size_t od = (size_t)tok * 2 * p.F + f;
     *reinterpret_cast<bf16x8*>(p.d_gu + od) = dg;
     *reinterpret_cast<bf16x8*>(p.d_gu + od + p.F) = du;
+  }
   }
 }
 
