@@ -1015,12 +1015,15 @@ __global__ __launch_bounds__(64 * NW, dkdv16_waves_per_simd<D>() * 4 / NW) void 
   // long as both operands share it), so lane l holds K[mykey][dcol(g, s) + j]. Keys past T
   // are zero and always masked.
   bf16x8 kf[NS], vf[NS];
+  {
+    const size_t row = (size_t)min(mykey, T_ - 1) * ld;
 #pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    const bf16x8 z = {};
-    const size_t o = (size_t)mykey * ld + Lay::dcol(g, s);
-    kf[s] = mykey < T_ ? ld8(K + o) : z;
-    vf[s] = mykey < T_ ? ld8(V + o) : z;
+    for (int s = 0; s < NS; ++s) {
+      kf[s] = ld8(K + row + Lay::dcol(g, s));
+      vf[s] = ld8(V + row + Lay::dcol(g, s));
+    }
+    keep_own_row<NS>(kf, mykey < T_);
+    keep_own_row<NS>(vf, mykey < T_);
   }
   floatx4 dk[NDB], dv[NDB];
 #pragma unroll
@@ -1280,26 +1283,31 @@ __global__ __launch_bounds__(256, (dq_waves_per_simd<D, MODE, L2N>())) void attn
   // queries past T carry stat = 0, so their weights and score gradients are zero.
   bf16x8 qf[NF], of[NF];
   const bool live = myq < T_;
+  {
+    const size_t row = (size_t)min(myq, T_ - 1) * ld + 8 * h;
 #pragma unroll
-  for (int s = 0; s < NF; ++s) {
-    const bf16x8 z = {};
-    const size_t o = (size_t)myq * ld + 16 * s + 8 * h;
-    qf[s] = live ? ld8(Q + o) : z;
-    of[s] = live ? ld8(dO + o) : z;
+    for (int s = 0; s < NF; ++s) {
+      qf[s] = ld8(Q + row + 16 * s);
+      of[s] = ld8(dO + row + 16 * s);
+    }
+    keep_own_row<NF>(qf, live);
+    keep_own_row<NF>(of, live);
   }
   const float stq = live ? p.stat[(size_t)bh * T_ + myq] : 0.0f;
   float diq = 0.0f;
   if constexpr (MODE != MODE_SHIFTED) {
     // di = sum_d dO o over the rounded output (flash.py:633); the two lane halves hold
     // alternate 8-element chunks of the row.
-    const bf16* O = reinterpret_cast<const bf16*>(p.o) + base + (size_t)myq * ld;
+    const bf16* O = reinterpret_cast<const bf16*>(p.o) + base + (size_t)min(myq, T_ - 1) * ld;
+    bf16x8 ovs[NF];
+#pragma unroll
+    for (int st = 0; st < NF; ++st) ovs[st] = ld8(O + 16 * st + 8 * h);
+    keep_own_row<NF>(ovs, live);
     float s = 0.0f;
 #pragma unroll
     for (int st = 0; st < NF; ++st) {
-      const bf16x8 z = {};
-      const bf16x8 ov = live ? ld8(O + 16 * st + 8 * h) : z;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) s += (float)of[st][j] * (float)ov[j];
+      for (int j = 0; j < 8; ++j) s += (float)of[st][j] * (float)ovs[st][j];
     }
     diq = s + xor32(s);
   }

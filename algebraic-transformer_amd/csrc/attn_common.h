@@ -221,4 +221,17 @@ __device__ __forceinline__ void step_order_r(int r) {
   }
 }
 
+// Fragments of a lane's own row that may lie past T: the caller loads them from the row clamped
+// to T - 1 (so every lane loads unconditionally and the loads issue together), and
+// keep_own_row zeroes them on lanes whose row is past T. The empty asm keeps the compiler from
+// moving the loads behind the lane check (a load per fragment behind a branch, each with a
+// wait of its own).
+template <int N>
+__device__ __forceinline__ void keep_own_row(bf16x8 (&f)[N], bool live) {
+#pragma unroll
+  for (int s = 0; s < N; ++s) asm volatile("" : "+v"(f[s]));
+  const bf16x8 z = {};
+#pragma unroll
+  for (int s = 0; s < N; ++s) f[s] = live ? f[s] : z;
+}
 }  // namespace alg
