@@ -1553,7 +1553,6 @@ __global__ __launch_bounds__(256) void attn_bwd_post_kernel(AttnBwdParams p, siz
 // Grid of a fallback (grid-stride) kernel: every work item gets its own workgroup when the
 // variant was chosen on the host; when it is one branch of the device guard it usually exits
 // at once, so it is launched as a small grid (a multiple of 8, so work item % 8 stays the XCD).
-constexpr int FALLBACK_GRID = 512;
 static int fallback_grid(const AttnBwdParams& p, int items) {
   return p.flag ? std::min(items, FALLBACK_GRID) : items;
 }

@@ -6,6 +6,13 @@
 
 namespace alg {
 
+#ifndef ALG_FALLBACK_GRID
+#define ALG_FALLBACK_GRID 512
+#endif
+// Workgroups of a flag-checked fallback launch (grid-stride over its work items): with the flag
+// clear every workgroup exits at once, so the launch costs its dispatch.
+constexpr int FALLBACK_GRID = ALG_FALLBACK_GRID;
+
 // Variants of the asinh-power kernel (src/algebraic/kernels/flash.py:59-73, 732-760, 850-852):
 //   INRANGE  unshifted, unclipped, stat = 1/Z (the guarded "low" variant, bounded_scores)
 //   CLIPPED  unshifted with x = min(s, clamp) (range_guard=False defaults); stat 1/Z or Z^(-1/n)

@@ -930,7 +930,7 @@ static hipError_t launch_fwd_mode(const AttnFwdParams& p, int mode, hipStream_t 
   // the variant, a small grid (a multiple of 8) when it is the branch the device guard
   // usually skips.
   const int items = p.B * p.H * ceil_div(p.T, FWD_BQ);
-  const int fallback_items = p.flag ? std::min(items, 512) : items;
+  const int fallback_items = p.flag ? std::min(items, FALLBACK_GRID) : items;
   switch (mode) {
     case MODE_INRANGE: {
       KTimer t("attn_fwd_inrange", st);
