@@ -10,7 +10,7 @@
 // stat = l^(-1/n) (fused_head.py:116), telemetry pt = (rho(min(zt/c, X)) stat)^n and the
 // objective mean(1 - pt) (fused_head.py:219-229).
 //
-// Backward, two schedules over the same GEMM core:
+// Backward, three schedules over the same GEMM core:
 //  * residual (3 products): with p = w/l the logit gradient is
 //        dz = s (p - y) r = (s/l) U',  U' = w r except U'_t = (w_t - l) r_t,
 //    so the forward epilogue also stores U = bf16(w r) token-major and the statistics kernel
@@ -19,6 +19,9 @@
 //  * recompute (4 products, the reference's schedule, fused_head.py:120-156, 194-216): the
 //    backward recomputes z, writes bf16(s (p - y) r) token-major, then dh = dZ E and
 //    dE = dZ^T h.
+//  * streamed (the recompute schedule one vocabulary chunk at a time, launch_head_bwd_streamed):
+//    per chunk dZ of the chunk only, its dh product accumulated in f32 across the chunks and its
+//    rows of dE, so no (N, V) block is held at all.
 // Every product reads its operands in their natural layout (k-contiguous fragments via
 // ds_read_b128, transposed ones via ds_read_b64_tr_b16).
 #include <cmath>
