@@ -35,6 +35,8 @@ CASES = [  # (N, d, V)
     (100, 128, 260),     # N < 128 (single ragged token tile)
     (512, 512, 2304),    # several k-step pairs in every product
     (256, 72, 333),      # d not a multiple of the k step or of a tile
+    (1, 8, 300),         # one token, the narrowest rows
+    (5, 16, 513),        # a few tokens, a vocabulary just past two 256-row chunks
 ]
 
 
