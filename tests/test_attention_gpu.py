@@ -64,6 +64,9 @@ CASES = [  # (B, H, T, D)
     (1, 2, 256, 128),
     (1, 1, 33, 128),     # T just past one 32-row block
     (2, 2, 384, 64),
+    (1, 2, 1, 64),       # one position
+    (2, 1, 2, 128),      # two positions
+    (1, 3, 17, 64),      # a partial first tile
 ]
 
 
@@ -73,6 +76,16 @@ def test_guarded_bf16_matches_oracle(shape, with_sink):
     B, H, T, D = shape
     q, k, v, do, sink = attention_inputs(B, H, T, D, seed=3, sink=with_sink)
     res = run_hip(q, k, v, do, sink, "bf16", range_guard=True, block=T)
+    if T == 1 and not with_sink:
+        # One key and no sink: p = 1, o = v, and every exact gradient of q is 0 (the score
+        # gradient p (dP - di) vanishes); di from the bf16 output leaves rounding noise, so
+        # dq is held to an absolute bar on the scale of dO . k, the rest to the usual ones.
+        assert np.abs(res[1]).max() <= 1e-2 * np.abs(do).max() * np.abs(k).max()
+        o_ref = OA.dense_forward(q, k, v, sink)
+        _, dk_r, dv_r, _ = OA.dense_backward(q, k, v, sink, do)
+        assert rel_l2(res[0], o_ref) < BF16_DENSE and rel_l2(res[3], dv_r) < BF16_DENSE
+        assert np.abs(res[2]).max() <= 1e-2 * np.abs(do).max() * np.abs(q).max()
+        return
     check_dense(res, q, k, v, do, sink, BF16_DENSE)
     ref = OA.flash_attention_oracle(q, k, v, sink, do, dtype="bf16")
     assert ref["in_range"]
