@@ -570,7 +570,8 @@ size_t alg_head_workspace_size(int dtype, int N, int d, int V, int pass) {
 // dE tail, sized for the larger of the two chunk plans]).
 struct HeadStreamWs {
   size_t dz, acc, de_part, total;
-  int chunk;
+  int chunk, nchunks;
+  bool has_de_part;  // some chunk's dE tail is token-split
 };
 static int head_stream_chunk(int d, int V, int vocab_chunk) {
   int chunk = vocab_chunk;
@@ -584,9 +585,11 @@ static HeadStreamWs head_stream_ws(int dtype, int N, int d, int V, int vocab_chu
   HeadStreamWs w;
   w.chunk = head_stream_chunk(d, V, vocab_chunk);
   const int nchunks = (V + w.chunk - 1) / w.chunk;
+  w.nchunks = nchunks;
+  w.has_de_part = false;
   const size_t pitch = (size_t)alg::head_vocab_pitch(w.chunk);
   w.dz = 0;
-  if (dtype == ALG_DTYPE_F32) {
+  if (dtype == ALG_DTYPE_F32) {  // dh accumulates in place in the f32 output; no dE split
     w.acc = w.de_part = w.total = align256((size_t)N * pitch * sizeof(float));
     return w;
   }
@@ -598,6 +601,7 @@ static HeadStreamWs head_stream_ws(int dtype, int N, int d, int V, int vocab_chu
     if (pl.split > 1)
       de_bytes = std::max(de_bytes, (size_t)(pl.tiles - pl.full) * pl.split * alg::HT_M * alg::HT_N * sizeof(float));
   }
+  w.has_de_part = de_bytes > 0;
   w.total = w.de_part + align256(de_bytes);
   return w;
 }
@@ -902,8 +906,8 @@ int alg_head_bwd_streamed(alg_stream_t stream, int dtype, int N, int d, int V, c
   }
   p.dzt = reinterpret_cast<bf16*>(w + ws.dz);
   p.dh = static_cast<bf16*>(dh);
-  p.dh_part = ws.de_part > ws.acc ? reinterpret_cast<float*>(w + ws.acc) : nullptr;
-  p.de_part = ws.total > ws.de_part ? reinterpret_cast<float*>(w + ws.de_part) : nullptr;
+  p.dh_part = ws.nchunks > 1 ? reinterpret_cast<float*>(w + ws.acc) : nullptr;
+  p.de_part = ws.has_de_part ? reinterpret_cast<float*>(w + ws.de_part) : nullptr;
   return hip_status(alg::launch_head_bwd_streamed(p, ws.chunk, (hipStream_t)stream), "alg_head_bwd_streamed");
 }
 
