@@ -389,6 +389,36 @@ def time_head_schedules(torch, x, iters=10, warmup=2):
     return out
 
 
+def time_step_graph(torch, x, full_step, steps, eager_ms):
+    """The headline step captured once in a HIP graph (torch.cuda.CUDAGraph) and replayed
+    `steps` times back to back: the launch-overhead-free time of the same kernels (the library
+    reads no device data on the host and records no memset, and the range guard branches on
+    the device, so the whole step replays). Reported beside the headline, not as it."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            full_step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        full_step()
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        graph.replay()
+    e1.record()
+    e1.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    del graph
+    torch.cuda.synchronize()
+    return {"workload": "the headline step (same kernels and shapes) replayed from one captured HIP graph",
+            "ms": round(ms, 4), "eager_ms": round(eager_ms, 4), "eager_over_graph": round(eager_ms / ms, 4)}
+
+
 def time_final_norm(torch, x, iters=20, warmup=3):
     """Final RMS norm with gain ahead of the head (model.py:208) at the C4b shape (16384 rows of
     2048): forward reads x, writes y (+ 1/rms); the VJP reads x, dy, writes dx (+ gain partials)."""
@@ -753,6 +783,7 @@ def main():
         out["head_schedules"] = time_head_schedules(torch, x)
         out["final_norm"] = time_final_norm(torch, x)
         out["ffn"] = time_ffn(torch, dev)
+        out["step_graph"] = time_step_graph(torch, x, full_step, K, step_s * 1e3)
     if not args.no_cpu_baseline:
         log("timing the CPU baseline sample")
         c1_ms = out.get("other_configs", {}).get("C1", {}).get("ms")
