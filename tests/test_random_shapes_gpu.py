@@ -1,0 +1,148 @@
+"""Seeded random configurations through both mirrors, against the float64 dense oracles.
+
+The fixed-shape tests pick edge cases by hand. This sweep draws the shape, dtype, layout,
+sink form, guard setting, head schedule and vocabulary chunk from fixed seeds, so combinations
+that no hand-written case lists meet the same bars:
+  attention (flash.py:763-857 and its VJP) against oracle.attention.dense_forward /
+  dense_backward: bf16 within 2e-2 relative L2 (the sink gradient excepted, below) and within
+  1e-2 of the cast-faithful restatement, f32 within 1e-5 (tests/test_flash_kernel_tpu.py);
+  head (fused_head.py:232-275) against oracle.head.dense_forward / dense_backward: bf16
+  objective within 2e-3 relative, telemetry 2e-2 and gradients 1e-2 relative L2
+  (tests/test_fused_head_tpu.py); f32 hidden states 1e-5 throughout.
+Each draw prints its configuration before it runs on the GPU.
+"""
+
+import numpy as np
+import pytest
+
+from helpers import rel_l2, rms_norm
+from oracle import attention as OA
+from oracle import head as OH
+from oracle.numerics import round_bf16
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+ATTN_DRAWS = 24
+HEAD_DRAWS = 24
+
+
+def _attn_config(i):
+    rng = np.random.default_rng(7000 + i)
+    B, H = int(rng.integers(1, 4)), int(rng.integers(1, 5))
+    T = int(rng.integers(1, 700)) if i % 3 else int(rng.integers(1, 80))
+    D = int(rng.choice([64, 128, 64, 128, 32, 96]))
+    dtype = "f32" if rng.random() < 0.3 else "bf16"
+    layout = "bthd" if rng.random() < 0.4 else "bhtd"
+    sink = str(rng.choice(["head", "head", "scalar", "none"]))
+    if T == 1 and sink == "none":
+        sink = "head"  # one key and no sink: p = 1 and the exact q, k gradients are 0 (no relative bar)
+    guard = bool(rng.random() < 0.8)
+    return dict(B=B, H=H, T=T, D=D, dtype=dtype, layout=layout, sink=sink, guard=guard, seed=7000 + i)
+
+
+@pytest.mark.parametrize("i", range(ATTN_DRAWS))
+def test_attention_random_config(i):
+    from algebraic_amd.kernels.flash import flash_attention
+    cfg = _attn_config(i)
+    print(f"[random attention] {cfg}", flush=True)
+    B, H, T, D = cfg["B"], cfg["H"], cfg["T"], cfg["D"]
+    rng = np.random.default_rng(cfg["seed"])
+    q, k, v, do = (rng.standard_normal((B, H, T, D)).astype(np.float32) for _ in range(4))
+    q, k = rms_norm(q), rms_norm(k)
+    if cfg["dtype"] == "bf16":
+        q, k, v, do = (round_bf16(a).astype(np.float32) for a in (q, k, v, do))
+    sink = {"head": (rng.standard_normal((1, H, 1, 1)) * 0.1).astype(np.float32),
+            "scalar": (rng.standard_normal((1,)) * 0.1).astype(np.float32), "none": None}[cfg["sink"]]
+    tdt = torch.bfloat16 if cfg["dtype"] == "bf16" else torch.float32
+    bthd = cfg["layout"] == "bthd"
+    lay = (lambda a: np.ascontiguousarray(a.transpose(0, 2, 1, 3))) if bthd else (lambda a: a)
+    tq, tk, tv = (torch.tensor(lay(a), device="cuda").to(tdt).requires_grad_(True) for a in (q, k, v))
+    ts = None if sink is None else torch.tensor(sink, device="cuda", requires_grad=True)
+    o = flash_attention(tq, tk, tv, ts, kind="asinh", n=16, c=8.0, block=T, range_guard=cfg["guard"],
+                        layout=cfg["layout"])
+    o.backward(torch.tensor(lay(do), device="cuda").to(tdt))
+    torch.cuda.synchronize()
+    back = (lambda a: a.transpose(0, 2, 1, 3)) if bthd else (lambda a: a)
+    f = lambda t: back(t.detach().float().cpu().numpy().astype(np.float64))
+    got = {"o": f(o), "dq": f(tq.grad), "dk": f(tk.grad), "dv": f(tv.grad)}
+    sink_o = None if sink is None else np.broadcast_to(sink.reshape(-1), (H,)).reshape(1, H, 1, 1)
+    want = {"o": OA.dense_forward(q, k, v, sink_o)}
+    want["dq"], want["dk"], want["dv"], ds_r = OA.dense_backward(q, k, v, sink_o, do)
+    if sink is not None:
+        ds = ts.grad.detach().cpu().numpy().astype(np.float64)
+        ds_r = np.asarray(ds_r).reshape(-1)
+        got["dsink"] = ds.reshape(-1)
+        want["dsink"] = ds_r if sink.size == H else np.array([ds_r.sum()])
+    if cfg["dtype"] == "f32":
+        errs = {key: rel_l2(got[key], want[key]) for key in got}
+        bad = {key: e for key, e in errs.items() if not e < 1e-5}
+        assert not bad, (cfg, errs)
+        return
+    # bf16: the dense oracle at 2e-2 and the cast-faithful restatement (the reference's rounding
+    # points, oracle.attention.flash_attention_oracle) at 1e-2. The sink gradient is one number
+    # per head, a sum over B T rows of terms of both signs in di = <dO, o>, which the reference
+    # forms from the bf16 output (flash.py:633): that rounding alone moves it by a few percent of
+    # itself in some draws (2.7 % in draw 19, restatement against dense), so it is held to the
+    # restatement only.
+    ref = OA.flash_attention_oracle(q, k, v, sink_o, do, dtype="bf16")
+    assert ref["in_range"], cfg
+    if sink is not None:
+        ref_ds = np.asarray(ref["dsink"], dtype=np.float64).reshape(-1)
+        ref["dsink"] = ref_ds if sink.size == H else np.array([ref_ds.sum()])
+    errs = {key: rel_l2(got[key], want[key]) for key in ("o", "dq", "dk", "dv")}
+    errs_k = {key: rel_l2(got[key], ref[key]) for key in got}
+    bad = {key: e for key, e in errs.items() if not e < 2e-2}
+    bad.update({key + " (restatement)": e for key, e in errs_k.items() if not e < 1e-2})
+    assert not bad, (cfg, errs, errs_k)
+
+
+def _head_config(i):
+    rng = np.random.default_rng(9000 + i)
+    N = int(rng.integers(1, 700))
+    d = int(rng.choice([64, 72, 128, 192, 256]))
+    V = int(rng.integers(2, 3000))
+    dtype = "f32" if rng.random() < 0.25 else "bf16"
+    schedule = str(rng.choice(["residual", "recompute", "streamed"]))
+    chunk = int(rng.choice([0, 256, 512, 768]))
+    n, c = ((8, 2.0), (8, 2.0), (16, 16.0), (4, 2.0))[int(rng.integers(0, 4))]
+    e_f32 = bool(dtype == "bf16" and rng.random() < 0.3)  # f32 E with bf16 h: cast, dE back in f32
+    return dict(N=N, d=d, V=V, dtype=dtype, schedule=schedule, chunk=chunk, n=n, c=c, e_f32=e_f32,
+                seed=9000 + i)
+
+
+@pytest.mark.parametrize("i", range(HEAD_DRAWS))
+def test_head_random_config(i, monkeypatch):
+    from algebraic_amd.kernels import fused_head as FH
+    cfg = _head_config(i)
+    print(f"[random head] {cfg}", flush=True)
+    monkeypatch.setattr(FH, "SCHEDULE", cfg["schedule"])
+    monkeypatch.setattr(FH, "VOCAB_CHUNK", cfg["chunk"])
+    N, d, V = cfg["N"], cfg["d"], cfg["V"]
+    rng = np.random.default_rng(cfg["seed"])
+    h = rms_norm(rng.standard_normal((N, d)).astype(np.float32))
+    E = (rng.standard_normal((V, d)) * 0.15).astype(np.float32)
+    t = rng.integers(0, V, N).astype(np.int32)
+    bf = cfg["dtype"] == "bf16"
+    hdt = torch.bfloat16 if bf else torch.float32
+    edt = torch.float32 if (cfg["e_f32"] or not bf) else torch.bfloat16
+    if bf:
+        h = round_bf16(h).astype(np.float32)
+        if not cfg["e_f32"]:
+            E = round_bf16(E).astype(np.float32)
+    th = torch.tensor(h, device="cuda").to(hdt).requires_grad_(True)
+    tE = torch.tensor(E, device="cuda").to(edt).requires_grad_(True)
+    obj, tel = FH.fused_head(th, tE, torch.tensor(t, device="cuda"), kind="alg_ce", n=cfg["n"], c=cfg["c"],
+                             block_n=N)  # the reference requires N % block_n == 0
+    (obj * 0.8).backward()
+    torch.cuda.synchronize()
+    assert tE.grad.dtype == edt and th.grad.dtype == hdt
+    E_seen = round_bf16(E).astype(np.float32) if bf else E  # the mirror casts E to h's dtype
+    obj_r, pt_r = OH.dense_forward(h, E_seen, t, n=cfg["n"], c=cfg["c"])
+    dh_r, dE_r = OH.dense_backward(h, E_seen, t, 0.8, n=cfg["n"], c=cfg["c"])
+    f = lambda x: x.detach().float().cpu().numpy().astype(np.float64)
+    o_tol, p_tol, g_tol = (2e-3, 2e-2, 1e-2) if bf else (1e-5, 1e-5, 1e-5)
+    errs = {"obj": abs(float(obj.detach()) - obj_r), "pt": rel_l2(f(tel), pt_r),
+            "dh": rel_l2(f(th.grad), dh_r), "dE": rel_l2(f(tE.grad), dE_r)}
+    assert errs["obj"] <= o_tol * abs(obj_r) + (2e-4 if bf else 1e-7), (cfg, obj_r, errs)
+    assert errs["pt"] < p_tol and errs["dh"] < g_tol and errs["dE"] < g_tol, (cfg, errs)
