@@ -146,3 +146,77 @@ def test_head_random_config(i, monkeypatch):
             "dh": rel_l2(f(th.grad), dh_r), "dE": rel_l2(f(tE.grad), dE_r)}
     assert errs["obj"] <= o_tol * abs(obj_r) + (2e-4 if bf else 1e-7), (cfg, obj_r, errs)
     assert errs["pt"] < p_tol and errs["dh"] < g_tol and errs["dE"] < g_tol, (cfg, errs)
+
+
+NORM_DRAWS = 12
+EVAL_DRAWS = 12
+
+
+def _norm_config(i):
+    rng = np.random.default_rng(11000 + i)
+    rows = int(rng.integers(1, 3000))
+    d = 8 * int(rng.integers(1, 513))  # 8 .. 4096, the kernels' 16-byte rows
+    return dict(rows=rows, d=d, gain=bool(rng.random() < 0.7), scale=float(rng.choice([0.05, 1.0, 30.0])),
+                seed=11000 + i)
+
+
+@pytest.mark.parametrize("i", range(NORM_DRAWS))
+def test_final_norm_random_config(i):
+    """The final RMS norm (model.py:208) and its VJP against oracle.prologue.rms_norm /
+    rms_norm_vjp at the bars of tests/test_rms_norm_gpu.py (y, dx 1e-4; dgain 1e-5)."""
+    from algebraic_amd.kernels.norm import rms_norm as norm
+    from oracle import prologue as OP
+    cfg = _norm_config(i)
+    print(f"[random norm] {cfg}", flush=True)
+    rng = np.random.default_rng(cfg["seed"])
+    x = round_bf16((rng.standard_normal((cfg["rows"], cfg["d"])) * cfg["scale"]).astype(np.float32))
+    dy = round_bf16(rng.standard_normal((cfg["rows"], cfg["d"])).astype(np.float32))
+    g = (1 + 0.2 * rng.standard_normal(cfg["d"])).astype(np.float32) if cfg["gain"] else None
+    tx = torch.tensor(x, device="cuda").to(torch.bfloat16).requires_grad_(True)
+    tg = None if g is None else torch.tensor(g, device="cuda", requires_grad=True)
+    y = norm(tx, tg)
+    y.backward(torch.tensor(dy, device="cuda").to(torch.bfloat16))
+    torch.cuda.synchronize()
+    y_ref, tau = OP.rms_norm(x, g, 1e-5, "bf16")
+    dx_ref, dg_ref = OP.rms_norm_vjp(x, g, tau, dy, "bf16")
+    errs = {"y": rel_l2(y.detach().float().cpu().numpy(), y_ref), "dx": rel_l2(tx.grad.float().cpu().numpy(), dx_ref)}
+    if g is not None:
+        errs["dgain"] = rel_l2(tg.grad.cpu().numpy(), dg_ref)
+    assert errs["y"] < 1e-4 and errs["dx"] < 1e-4 and errs.get("dgain", 0) < 1e-5, (cfg, errs)
+
+
+def _eval_config(i):
+    rng = np.random.default_rng(13000 + i)
+    return dict(N=int(rng.integers(1, 900)), d=int(rng.choice([64, 72, 128, 256, 512])), V=int(rng.integers(2, 5000)),
+                nc=((8, 2.0), (16, 16.0), (1, 2.0), (4, 2.0))[int(rng.integers(0, 4))],
+                dtype="f32" if rng.random() < 0.25 else "bf16", seed=13000 + i)
+
+
+@pytest.mark.parametrize("i", range(EVAL_DRAWS))
+def test_eval_head_random_config(i):
+    """The streamed evaluation head (benchmarking.py:178-188, evaluation.py:13-23) against
+    oracle.head.eval_logprob: log p within 1e-4 absolute for bf16 hidden states and 1e-5 for
+    f32 (scaled with n above 16 as in tests/test_large_n_gpu.py), the argmax a maximum of the
+    float64 logits up to a near-tie."""
+    from algebraic_amd.kernels.fused_head import head_logprob
+    cfg = _eval_config(i)
+    print(f"[random eval head] {cfg}", flush=True)
+    N, d, V = cfg["N"], cfg["d"], cfg["V"]
+    n, c = cfg["nc"]
+    rng = np.random.default_rng(cfg["seed"])
+    h = rms_norm(rng.standard_normal((N, d)).astype(np.float32))
+    E = (rng.standard_normal((V, d)) * 0.05).astype(np.float32)
+    t = rng.integers(0, V, N).astype(np.int32)
+    bf = cfg["dtype"] == "bf16"
+    if bf:
+        h, E = round_bf16(h).astype(np.float32), round_bf16(E).astype(np.float32)
+    tdt = torch.bfloat16 if bf else torch.float32
+    lp, am = head_logprob(torch.tensor(h, device="cuda").to(tdt), torch.tensor(E, device="cuda").to(tdt),
+                          torch.tensor(t, device="cuda"), n=n, c=c)
+    torch.cuda.synchronize()
+    lp_ref, _, z = OH.eval_logprob(h, E, t, n=n, c=c)
+    err = float(np.max(np.abs(lp.cpu().numpy().astype(np.float64) - lp_ref)))
+    assert err < (1e-4 if bf else 1e-5), (cfg, err)
+    am = am.cpu().numpy()
+    best = z.max(axis=1)
+    assert np.all(z[np.arange(N), am] >= best - 1e-5 * (np.abs(best) + 1)), cfg
