@@ -220,3 +220,97 @@ def test_eval_head_random_config(i):
     am = am.cpu().numpy()
     best = z.max(axis=1)
     assert np.all(z[np.arange(N), am] >= best - 1e-5 * (np.abs(best) + 1)), cfg
+
+
+PROLOGUE_DRAWS = 12
+
+
+def _prologue_config(i):
+    rng = np.random.default_rng(15000 + i)
+    return dict(B=int(rng.integers(1, 3)), H=int(rng.integers(1, 4)), T=int(rng.integers(2, 400)),
+                D=int(rng.choice([64, 128])), dtype="f32" if rng.random() < 0.3 else "bf16",
+                gain=bool(rng.random() < 0.7), rotate=bool(rng.random() < 0.7), sink=bool(rng.random() < 0.7),
+                seed=15000 + i)
+
+
+@pytest.mark.parametrize("i", range(PROLOGUE_DRAWS))
+def test_prologue_random_config(i):
+    """The fused attention prologue (model.py:170-174: QK RMS norm + gain, Cayley rotation,
+    q alpha and the guard) with attention and its VJP, against the oracle chain
+    (oracle.prologue then oracle.attention) at the bars of tests/test_prologue_gpu.py: bf16
+    1e-2, f32 1e-5 (gain gradients 1e-4)."""
+    from algebraic_amd.kernels.prologue import qk_norm_rotary_flash_attention
+    from oracle import prologue as OP
+    cfg = _prologue_config(i)
+    print(f"[random prologue] {cfg}", flush=True)
+    B, H, T, D, dtype = cfg["B"], cfg["H"], cfg["T"], cfg["D"], cfg["dtype"]
+    rng = np.random.default_rng(cfg["seed"])
+    q, k, v, do = (rng.standard_normal((B, H, T, D)).astype(np.float32) for _ in range(4))
+    q, k = q * 3.0, k * 0.6
+    if dtype == "bf16":
+        q, k, v, do = (round_bf16(a).astype(np.float32) for a in (q, k, v, do))
+    gq = (1 + 0.2 * rng.standard_normal(D)).astype(np.float32) if cfg["gain"] else None
+    gk = (1 + 0.2 * rng.standard_normal(D)).astype(np.float32) if cfg["gain"] else None
+    cos, sin = OP.cayley_table_geometric(D, T) if cfg["rotate"] else (None, None)
+    sink = (rng.standard_normal((1, H, 1, 1)) * 0.1).astype(np.float32) if cfg["sink"] else None
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    dev = lambda a: torch.tensor(a, device="cuda").to(tdt).requires_grad_(True)
+    tq, tk, tv = dev(q), dev(k), dev(v)
+    f32 = lambda a: None if a is None else torch.tensor(a, device="cuda", requires_grad=True)
+    ts, tgq, tgk = f32(sink), f32(gq), f32(gk)
+    tc = None if cos is None else torch.tensor(cos, device="cuda")
+    tsn = None if sin is None else torch.tensor(sin, device="cuda")
+    o = qk_norm_rotary_flash_attention(tq, tk, tv, ts, tgq, tgk, tc, tsn, kind="asinh", n=16, c=8.0,
+                                       range_guard=True, block=T)
+    o.backward(torch.tensor(do, device="cuda").to(tdt))
+    torch.cuda.synchronize()
+    g = lambda t: t.detach().float().cpu().numpy()
+    got = dict(o=g(o), dq=g(tq.grad), dk=g(tk.grad), dv=g(tv.grad))
+    _, k_r, q_r, tau_q, tau_k = OP.prologue_forward(q, k, gq, gk, cos, sin, c=8.0, dtype=dtype)
+    res = OA.flash_attention_oracle(q_r, k_r, v, sink, do, n=16, c=8.0, dtype=dtype)
+    assert res["in_range"], cfg
+    dq, dk, dgq, dgk = OP.prologue_backward(q, k, gq, gk, cos, sin, tau_q, tau_k, res["dq"], res["dk"], dtype=dtype)
+    ref = dict(o=res["o"], dq=dq, dk=dk, dv=res["dv"])
+    if gq is not None:
+        got.update(dq_gain=g(tgq.grad), dk_gain=g(tgk.grad))
+        ref.update(dq_gain=dgq, dk_gain=dgk)
+    if sink is not None:
+        got["dsink"], ref["dsink"] = g(ts.grad), res["dsink"]
+    tol = 1e-2 if dtype == "bf16" else 1e-5
+    errs = {n: rel_l2(np.reshape(got[n], -1), np.reshape(ref[n], -1)) for n in ref}
+    bad = {n: e for n, e in errs.items() if not e < (1e-4 if dtype == "f32" and "gain" in n else tol)}
+    assert not bad, (cfg, errs)
+
+
+FFN_DRAWS = 10
+
+
+def _ffn_config(i):
+    rng = np.random.default_rng(17000 + i)
+    return dict(N=int(rng.integers(1, 700)), d=8 * int(rng.integers(1, 97)), F=128 * int(rng.integers(1, 9)),
+                beta=float(rng.choice([0.5, 0.8, 1.0])), seed=17000 + i)
+
+
+@pytest.mark.parametrize("i", range(FFN_DRAWS))
+def test_ffn_random_config(i):
+    """The ALU-GLU feed-forward with fused activation epilogues (model.py:185-193,
+    algebraic.py:86-113) against oracle.ffn at the bar of tests/test_ffn_gpu.py (1e-2 relative
+    L2 for the output and every gradient)."""
+    from algebraic_amd.kernels.ffn import alu_glu_ffn
+    from oracle import ffn as OF
+    cfg = _ffn_config(i)
+    print(f"[random ffn] {cfg}", flush=True)
+    N, d, F, beta = cfg["N"], cfg["d"], cfg["F"], cfg["beta"]
+    rng = np.random.default_rng(cfg["seed"])
+    r = lambda *s, sc=1.0: round_bf16((rng.standard_normal(s) * sc).astype(np.float32)).astype(np.float32)
+    h2, w_g, w_u, w_d, dout = r(N, d), r(d, F, sc=d ** -0.5), r(d, F, sc=d ** -0.5), r(F, d, sc=F ** -0.5), r(N, d)
+    t = [torch.tensor(a, device="cuda").to(torch.bfloat16).requires_grad_(True) for a in (h2, w_g, w_u, w_d)]
+    out = alu_glu_ffn(*t, beta=beta)
+    out.backward(torch.tensor(dout, device="cuda").to(torch.bfloat16))
+    torch.cuda.synchronize()
+    o_ref, _, _, _ = OF.ffn_forward(h2, w_g, w_u, w_d, beta)
+    dh2, dw_g, dw_u, dw_d, _, _ = OF.ffn_backward(h2, w_g, w_u, w_d, dout, beta)
+    g = lambda x: x.detach().float().cpu().numpy()
+    errs = {"out": rel_l2(g(out), o_ref), "dh2": rel_l2(g(t[0].grad), dh2), "dw_g": rel_l2(g(t[1].grad), dw_g),
+            "dw_u": rel_l2(g(t[2].grad), dw_u), "dw_d": rel_l2(g(t[3].grad), dw_d)}
+    assert max(errs.values()) < 1e-2, (cfg, errs)
