@@ -515,14 +515,25 @@ __global__ __launch_bounds__(NT, 1) void head_dz_kernel(HeadParams p) {
             const float x = fminf(acc[mb][nb][4 * g + e] * inv_c, clamp);
             float r;
             const float t = pow2n<L2N>(rho_fast(x, r) * st, p.log2n);
-            const float y = dt == mb * 32 + 8 * g + e ? 1.0f : 0.0f;
-            u[e] = (t - y) * r * scale;
+            u[e] = t * r * scale;  // (t - y) r s with y = 0; the target entry is patched below
           }
           u32x2 pk;
           pk[0] = pack_bf16x2(u[0], u[1]);
           pk[1] = pack_bf16x2(u[2], u[3]);
           *reinterpret_cast<u32x2*>(ub + ustage_at(nb * 32 + l32, mb * 32 + 8 * g + 4 * h)) = pk;
         }
+      }
+      // The target entry, (t - 1) r s (y = 1): rare (WTM of V rows per token), so it is formed
+      // again behind a wave-uniform branch, as the forward selects the target logit, and
+      // overwrites its staged slot (the same lane wrote it above; LDS keeps a wave's order).
+      const bool mine = (unsigned)dt < (unsigned)HC::WTM && !(dt & 4);
+      if (__builtin_amdgcn_ballot_w64(mine)) {
+        int dsel = dt;
+        asm volatile("" : "+v"(dsel));  // keeps the select inside the branch (not speculated)
+        const float x = fminf(select_row(acc, nb, dsel) * inv_c, clamp);
+        float r;
+        const float t = pow2n<L2N>(rho_fast(x, r) * st, p.log2n);
+        if (mine) ub[ustage_at(nb * 32 + l32, dsel + 4 * h)] = f2bf((t - 1.0f) * r * scale);
       }
     }
     store_staged_tokmajor<0>(ub, p.dzt, p.Npad, p.Vp, n0 + wn * HC::WTN, vrow0, lane);
