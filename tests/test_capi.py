@@ -282,3 +282,24 @@ def test_hot_path_entry_points_reject_misaligned_matrices():
     rc = handle.alg_head_fwd(None, 0, 128, 256, 1000, P(16), P(40), P(16), 8, 2.0, P(16), P(16), P(16), P(16),
                              None, P(16), 1 << 30)
     assert rc == _lib.ALG_ERR_INVALID and b"aligned" in handle.alg_last_error()
+
+
+def test_sources_stay_capture_safe():
+    """The entry points must stay safe under stream capture (tests/test_graph_gpu.py replays the
+    whole step from one graph): no device allocation, no memset or copy (a memset recorded
+    into a graph is a hazard of its own), no host synchronisation in the library's sources.
+    The one exception is the opt-in kernel timer's report, which the host calls outside any
+    step (alg_timer_report)."""
+    banned = re.compile(r"\b(hipMalloc\w*|hipFree\w*|hipMemset\w*|hipMemcpy\w*|hipDeviceSynchronize|"
+                        r"hipStreamSynchronize|hipStreamQuery|hipEventQuery|hipHostMalloc|hipExtMallocWithFlags)\s*\(")
+    found = []
+    for path in sorted((ROOT / "algebraic-transformer_amd" / "csrc").glob("*")):
+        if path.suffix not in (".hip", ".h", ".cpp"):
+            continue
+        for i, line in enumerate(path.read_text().splitlines(), 1):
+            code = line.split("//", 1)[0]
+            if banned.search(code):
+                found.append(f"{path.name}:{i}: {line.strip()}")
+    assert not found, found
+    timer = (ROOT / "algebraic-transformer_amd" / "csrc" / "ktimer.hip").read_text()
+    assert timer.count("hipEventSynchronize(") == 1, "the timer report is the only synchronising call"
