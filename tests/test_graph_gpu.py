@@ -120,3 +120,64 @@ def test_step_graph_replays_match_eager():
     for name, got, ref in zip(names, static_out, want):
         assert torch.equal(got, ref), ("back in range", name)
     assert not math.isnan(float(static_out[5].item()))
+
+
+def test_noalloc_backward_in_a_graph():
+    """alg_attn_bwd_noalloc (no counterpart in the reference; for callers that cannot allocate,
+    such as code under graph capture) captured in a graph through the C ABI and replayed for
+    three upstream gradients: every replay bit-identical (bf16) to the workspace entry point
+    alg_attn_bwd run eagerly on the same inputs. One eager call first sets up the library's
+    scratch address (once per device, outside the capture)."""
+    from algebraic_amd import _lib as L
+    lib = L.load()
+    Bb, Hb, Tb, Db = 2, 4, 384, 128
+    dt = L.DTYPE_BF16
+    x = _case(4)
+    q, k, v = (x[n][:Bb, :Hb, :Tb].contiguous() for n in ("q", "k", "v"))
+    sink_in = x["sink"][:, :Hb].reshape(-1).contiguous()
+    st = L.stream_of(q)
+    ws_bytes = lib.alg_attn_workspace_size(dt, Bb, Hb, Tb, Db)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    q_s, o = torch.empty_like(q), torch.empty_like(q)
+    sink_s = torch.empty(Hb, dtype=torch.float32, device="cuda")
+    flag = torch.empty(1, dtype=torch.int32, device="cuda")
+    stat = torch.empty((Bb, Hb, Tb), dtype=torch.float32, device="cuda")
+    L.check(lib.alg_attn_fwd_guarded(st, dt, 0, Bb, Hb, Tb, Db, L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(sink_in), Hb,
+                                     C, N_EXP, L.ptr(q_s), L.ptr(sink_s), L.ptr(flag), L.ptr(o), None, L.ptr(stat),
+                                     L.ptr(ws), ws_bytes), "guarded forward")
+    t = 1e37 / (Tb + 1.0)
+    for _ in range(4):
+        t = math.sqrt(t)
+    clamp, alpha = 0.5 * (t - 1.0 / t), 1.0 / (math.sqrt(Db) * C)
+    do = torch.empty_like(q)
+
+    def outputs():
+        return [torch.empty_like(k), torch.empty_like(k), torch.empty_like(v),
+                torch.empty((Bb, Hb, Tb), dtype=torch.float32, device="cuda"),
+                torch.empty(Hb, dtype=torch.float32, device="cuda")]
+
+    def args(out, stream):
+        return [stream, dt, 0, Bb, Hb, Tb, Db, L.ptr(q_s), L.ptr(k), L.ptr(v), L.ptr(sink_s), L.ptr(o), L.ptr(stat),
+                L.ptr(do), N_EXP, L.ATTN_GUARDED, L.ptr(flag), clamp, 1, 1, alpha, *(L.ptr(a) for a in out)]
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+    do.copy_(torch.randn(do.shape, device="cuda", generator=g).to(torch.bfloat16))
+    static = outputs()
+    L.check(lib.alg_attn_bwd_noalloc(*args(static, st)), "set-up call")
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        L.check(lib.alg_attn_bwd_noalloc(*args(static, L.stream_of(q))), "captured call")
+    torch.cuda.synchronize()
+    for rep in range(3):
+        print(f"[graph] no-alloc backward replay {rep}", flush=True)
+        do.copy_(torch.randn(do.shape, device="cuda", generator=g).to(torch.bfloat16))
+        want = outputs()
+        L.check(lib.alg_attn_bwd(*args(want, st), L.ptr(ws), ws_bytes), "eager workspace backward")
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, a, b in zip(("dq", "dk", "dv", "di", "dsink"), static, want):
+            assert torch.isfinite(b.float()).all(), (rep, name)
+            assert torch.equal(a, b), (rep, name)
