@@ -315,8 +315,14 @@ __device__ __forceinline__ void gemm_mainloop(GemmStage<AM, BM, C>& s0, GemmStag
       };
       copy_tile(s0, 0);
       copy_tile(s1, 1);
-      __builtin_amdgcn_s_waitcnt(VMCNT0);
-      __syncthreads();
+      // Wait for tile 0's copies only (tile 1's NG copy instructions are the younger ones):
+      // tile 1 is first read after the barrier inside the first step, which waits for every
+      // copy, so its load overlaps tile 0's first three sub-steps. The barrier is a plain
+      // s_barrier: __syncthreads() would add a release fence, which waits for every copy.
+      // Each wave has waited for its own tile-0 copies before it, so after it all of tile 0
+      // is in LDS; the memory clobber keeps the fragment reads after it.
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(NG));
+      asm volatile("s_barrier" ::: "memory");
       load(s0, 0, f0);
       int kt = 0;
       for (; kt + 2 < nk; kt += 2) {
